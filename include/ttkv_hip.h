@@ -1,0 +1,129 @@
+/* C ABI of the MI355X compressed-KV attention library (libttkv_hip.so).
+ *
+ * Drop-in boundary for the hot path of ttkv-vllm's `vllm_ttkv` AttentionImpl. Every entry point
+ * takes raw device pointers, sizes and the caller's HIP stream, allocates nothing, never
+ * synchronises, and returns 0 on success or a TTKV_E_* code (message via ttkv_last_error(),
+ * thread-local). Geometry/shape errors the host can see are refused before any launch; conditions
+ * only the device can see (a block id outside the cache, a request without a registered decoder,
+ * a padded slot id) set bits in the caller's `error_word` and leave the affected rows NaN-filled
+ * or unwritten, never silently plausible.
+ *
+ * Byte format: the reference's slot layout, bit for bit (vllm_ttkv/layout.py:56-261;
+ * codec/ttkv_packed_cache.py:50-271; vllm_ttkv/select_triton.py:24-91).
+ */
+#ifndef TTKV_HIP_H
+#define TTKV_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* ttkv_stream_t; /* == hipStream_t */
+
+enum {
+  TTKV_DTYPE_F32 = 0,
+  TTKV_DTYPE_F16 = 1,
+  TTKV_DTYPE_BF16 = 2,
+};
+
+enum {
+  TTKV_OK = 0,
+  TTKV_E_INVALID = 1,     /* bad geometry / argument, refused before launch */
+  TTKV_E_UNSUPPORTED = 2, /* a geometry the compiled kernels do not cover */
+  TTKV_E_LAUNCH = 3,      /* hipLaunch / HIP runtime error */
+  TTKV_E_WORKSPACE = 4,   /* workspace too small */
+};
+
+/* Device-side condition bits written (OR-ed) into `error_word`. */
+enum {
+  TTKV_ERR_NO_DECODER = 1,   /* block_table[r,0] maps to no decoder slot */
+  TTKV_ERR_BAD_BLOCK = 2,    /* a block id outside [0, num_blocks) inside a request's used prefix */
+  TTKV_ERR_BAD_SLOT = 4,     /* slot_mapping entry is PAD (<0) or past the cache */
+  TTKV_ERR_SEQ_LEN = 8,      /* seq_lens[r] > the max_seq_len the call was sized for (clamped) */
+};
+
+/* One layer's allocation. Mirrors TTKLayout(H, d, r1, qbits, res_k, res_bits, v_lanes, v_bits)
+ * (vllm_ttkv/layout.py:56-74); all byte offsets are derived from these by layout.py:98-157's
+ * formulas. The kernels are built for d == 128, qbits == 8, res_bits/v_bits in {3, 4}. */
+typedef struct ttkv_layout {
+  int32_t H, d, r1, qbits, res_k, res_bits, v_lanes, v_bits;
+} ttkv_layout;
+
+/* Bytes of one token's blob (K slot + V slot) for `lay`, or -1 if the geometry is invalid.
+ * Replaces TTKLayout.compressed_bytes_per_token (vllm_ttkv/layout.py:152-154). */
+int64_t ttkv_blob_bytes(const ttkv_layout* lay);
+
+/* Workspace bytes `ttkv_decode_paged` needs for this batch shape. The workspace must be
+ * zero-filled before its first use; every call leaves its counter region zero again. */
+int64_t ttkv_decode_workspace_bytes(const ttkv_layout* lay, int32_t num_heads,
+                                    int32_t num_reqs, int32_t max_seq_len);
+
+/* K1 -- fused paged decode read, ONE launch for the whole batch of decode requests.
+ *
+ * Replaces, per layer and step, the reference's per-request loop (vllm_ttkv/impl.py:452-493)
+ * of `_decode_one` (impl.py:511-540): block_slots + gather_slots + split_blob +
+ * cos_sin_from_cache (decode.py:54-122, 160-197, 286-339), `krt_from_slots`
+ * (krt_triton.py:320-371), softmax(scores * scale) (impl.py:538) and `v_out_from_slots`
+ * (v_out_triton.py:121-155). Semantics are vllm_ttkv/reference.py:149-163 per request:
+ *   K_pre[t] = (cq[t] * float(cs16[t])) @ decoder_f[:, h*d:(h+1)*d] + residual[h, t]
+ *   s[p, t]  = scale * q[p] . RoPE_t(K_pre[t])           (t = 0 .. seq_len-1, absolute position t)
+ *   out[p]   = sum_t softmax_t(s[p, :]) * V[h(p), t]      h(p) = p / (num_heads / H)
+ *
+ * query        [N, num_heads, d] (dtype q_dtype), row of request r at query_start_loc[r].
+ * page         per-layer cache viewed as bytes; slot s at page + s*slot_stride (>= blob bytes).
+ * block_table  [num_reqs, bt_row_stride] int32; slot of position t = bt[r, t/bs]*bs + t%bs.
+ * dec_slot_of_block [num_blocks] int32: the registry rope_store.register_decoder keys by
+ *              block_table[r, 0] (rope_store.py:148-237), as a device map; -1 = none.
+ * dec_pool     [n_dec_slots, r1, H*d] fp32 decoder_f rows (encode.py:178-211).
+ * cos_sin_cache [max_position, d] fp32, vLLM layout: cos in columns [0,d/2), sin in [d/2,d)
+ *              (decode.py:54-122).
+ * out          [N, num_heads, d] (dtype out_dtype); only the decode rows are written. */
+int ttkv_decode_paged(const ttkv_layout* lay, int32_t num_heads, float scale,
+                      const void* query, int32_t q_dtype, int64_t q_row_stride,
+                      const uint8_t* page, int64_t n_slots, int64_t slot_stride,
+                      int32_t block_size, const int32_t* block_table, int64_t bt_row_stride,
+                      int32_t max_blocks, const int32_t* seq_lens,
+                      const int32_t* query_start_loc, int32_t num_reqs, int32_t max_seq_len,
+                      const int32_t* dec_slot_of_block, int64_t num_blocks,
+                      const float* dec_pool, int64_t n_dec_slots,
+                      const float* cos_sin_cache, int64_t max_position,
+                      void* out, int32_t out_dtype, int64_t out_row_stride,
+                      void* workspace, int64_t workspace_bytes, int32_t* error_word,
+                      ttkv_stream_t stream);
+
+/* K3 -- write/encode of `num_tokens` new tokens into their slots, one launch per layer.
+ *
+ * Replaces the reference's per-request write (vllm_ttkv/impl.py:543-653): `encode_frozen(_batch)`
+ * (encode.py:301-428) + `pack_and_write` / `_fused_write` (encode.py:511-603) with the coefficient
+ * index_put (encode.py:570-573) and `select_triton.write_k_residual` / `write_v_rows`
+ * (select_triton.py:235-303). Per token i of request r (query_start_loc[r] <= i < [r+1]):
+ *   c   = M_i @ pinv                      (M_i = key[i] flattened h*d + j; pinv [H*d, r1])
+ *   cs  = max|c| * fp32(1/127), 1 if 0;   cq = clamp(rint(c / cs), -128, 127)
+ *   R   = key[i] - (cq * cs) @ decoder_f   -> K residual rows; value[i] -> V rows
+ * written at slot_mapping[i] as the reference slot bytes (layout.py:161-239), padding zeroed.
+ * When coeff_q_in/coeff_scale_in ([N, r1] int8, [N] fp32) are given, they replace the projection
+ * (a first chunk written with its fit's own coefficients, encode.py:257-298).
+ * Bytes are bit-exact functions of R and value (select_triton.py:24-91): exact top-k by magnitude
+ * (ties -> lowest lane), ruler = rowmax * fp32(1/(2^(b-1)-1)), q = rint(x / ruler) (IEEE div).
+ * coeff_out [N, r1] and resid_out [N, H*d] (optional, fp32) receive c and R.
+ * key/value: [N, H, d] rows with the given element stride between tokens. */
+int ttkv_write_paged(const ttkv_layout* lay, const void* key, int32_t k_dtype, int64_t k_row_stride,
+                     const void* value, int32_t v_dtype, int64_t v_row_stride,
+                     const int64_t* slot_mapping, int32_t num_tokens,
+                     const int32_t* query_start_loc, int32_t num_reqs, const int32_t* block_table,
+                     int64_t bt_row_stride, const int32_t* dec_slot_of_block, int64_t num_blocks,
+                     const float* dec_pool, const float* pinv_pool, int64_t n_dec_slots,
+                     const int8_t* coeff_q_in, const float* coeff_scale_in, uint8_t* page,
+                     int64_t n_slots, int64_t slot_stride, float* coeff_out, float* resid_out,
+                     int32_t* error_word, ttkv_stream_t stream);
+
+/* Message for the last nonzero return on this thread. */
+const char* ttkv_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TTKV_HIP_H */

@@ -1,0 +1,136 @@
+"""K3 (write/encode) on the GPU against the CPU oracle.
+
+Bytes are pinned bit-exactly from the quantiser inputs on (the kernel's own projection c and
+residual R, which it can export), exactly as the reference pins its fused write against the torch
+packer from the same FittedK (tests/test_encode_triton.py:100-121 in the reference). The float
+stages (projection, reconstruction) are checked at fp32 tolerance against the oracle."""
+import pytest
+import torch
+
+from helpers import D, H
+from oracle import codec, encode
+from oracle.layout import layout_for_config, unpack_v_slots
+from oracle import attend
+from vllm_ttkv import kernels, synth
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _setup(cfg_name, n_new, seed, r1=110, fit_on=96):
+    cfg = codec.CONFIGS[cfg_name]
+    lay = layout_for_config(cfg, r1=r1)
+    K = synth.keys(fit_on + n_new, seed=seed)
+    fk = encode.fit_into_budget(K[:, :fit_on].contiguous(), lay, cfg)
+    dec = fk["decoder_f"]
+    pinv = encode.pinv(dec)
+    Knew = K[:, fit_on:].contiguous()                       # [H, n, d]
+    V = synth.values(n_new, seed=seed + 1) * 0.3
+    return lay, dec, pinv, Knew, V
+
+
+def _run(lay, dec, pinv, Knew, V, slots, n_slots, v_dtype=torch.float32, cq_in=None, cs_in=None):
+    n = Knew.shape[1]
+    C = lay.compressed_bytes_per_token()
+    page = torch.zeros(n_slots, C, dtype=torch.uint8, device=DEV)
+    bt = torch.zeros(1, 1, dtype=torch.int32, device=DEV)    # request 0 owns block 0
+    dec_map = torch.zeros(1, dtype=torch.int32, device=DEV)  # block 0 -> decoder slot 0
+    qsl = torch.tensor([0, n], dtype=torch.int32, device=DEV)
+    c_out = torch.zeros(n, lay.r1, device=DEV)
+    r_out = torch.zeros(n, H * D, device=DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    kernels.write_paged(lay, Knew.permute(1, 0, 2).contiguous().to(DEV),
+                        V.permute(1, 0, 2).contiguous().to(v_dtype).to(DEV),
+                        slots.to(DEV), qsl, bt, dec_map, dec.unsqueeze(0).to(DEV),
+                        pinv.unsqueeze(0).to(DEV), page,
+                        coeff_q_in=None if cq_in is None else cq_in.to(DEV),
+                        coeff_scale_in=None if cs_in is None else cs_in.to(DEV),
+                        coeff_out=c_out, resid_out=r_out, error_word=err)
+    torch.cuda.synchronize()
+    return page.cpu(), c_out.cpu(), r_out.cpu(), int(err.item())
+
+
+@pytest.mark.parametrize("cfg", ["safe", "tight", "campaign4x"])
+def test_write_bytes_exact_from_quantiser_inputs(cfg):
+    lay, dec, pinv, Knew, V = _setup(cfg, 9, seed=21)
+    slots = torch.tensor([5, 0, 17, 3, 30, 8, 11, 2, 25], dtype=torch.int64)
+    page, c, R, err = _run(lay, dec, pinv, Knew, V, slots, 32)
+    assert err == 0
+    # float stages at fp32 tolerance
+    c_ref = encode.project(Knew, pinv)
+    assert (c - c_ref).abs().max() <= 1e-4 * c_ref.abs().max() + 1e-7
+    cq, cs = encode.quantise_coeffs(c)                      # from the kernel's own c
+    R_ref = encode.residual(Knew, cq, cs, dec)              # [H*n, d] (head, token)
+    R_k = R.reshape(-1, H, D).permute(1, 0, 2).reshape(H * Knew.shape[1], D)
+    assert (R_k - R_ref).abs().max() <= 1e-4
+    # bytes: bit-exact from (c, R, V)
+    k_slots = encode.k_slots_from(lay, cq, cs.to(torch.float16).reshape(-1),
+                                  codec.build_rows(R_k, lay.res_k, lay.res_bits))
+    v_slots = encode.v_slots_from(lay, encode.encode_v(V, lay))
+    want = torch.cat([k_slots, v_slots], dim=1)
+    got = page[slots]
+    nbad = int((got != want).sum())
+    assert nbad == 0, f"{cfg}: {nbad} of {want.numel()} bytes differ"
+    untouched = torch.ones(32, dtype=torch.bool)
+    untouched[slots] = False
+    assert int(page[untouched].abs().sum()) == 0, "bytes outside the written slots changed"
+
+
+def test_write_bf16_value_is_exact():
+    lay, dec, pinv, Knew, V = _setup("safe", 5, seed=7)
+    V = V.to(torch.bfloat16).float()                        # values representable in bf16
+    slots = torch.arange(5, dtype=torch.int64)
+    page, c, R, err = _run(lay, dec, pinv, Knew, V, slots, 8, v_dtype=torch.bfloat16)
+    v_slots = encode.v_slots_from(lay, encode.encode_v(V, lay))
+    assert torch.equal(page[slots, lay.v_offset:], v_slots)
+
+
+def test_ties_and_zero_rows_follow_the_lowest_lane_rule():
+    """Three-value alphabet (most lanes tie) and all-zero rows: the oracle uses the same
+    tie rule (lowest lane index), so bytes must be identical, and zero rows carry the ruler
+    fp16(1 / (2^(b-1)-1)) (test_encode_triton.py:256-325 in the reference)."""
+    lay, dec, pinv, Knew, _ = _setup("safe", 6, seed=13)
+    g = torch.Generator().manual_seed(14)
+    V = torch.randint(0, 3, (H, 6, D), generator=g).float() - 1.0
+    V[:, 4] = 0.0
+    slots = torch.arange(6, dtype=torch.int64)
+    page, _, _, err = _run(lay, dec, pinv, Knew, V, slots, 8)
+    want = encode.v_slots_from(lay, encode.encode_v(V, lay))
+    assert torch.equal(page[slots, lay.v_offset:], want)
+    sc = unpack_v_slots(lay, page[slots, lay.v_offset:])[2].reshape(H, 6)
+    assert torch.all(sc[:, 4] == torch.tensor(1.0 / 3, dtype=torch.float16))
+    dense = attend.dense_v_from_slots(lay, page[slots, lay.v_offset:])
+    assert float(dense[:, 4].abs().max()) == 0.0
+
+
+def test_fit_coefficients_path():
+    """A first chunk is written with its fit's own coefficients (encode.py:257-298)."""
+    cfg = codec.CONFIGS["safe"]
+    lay = layout_for_config(cfg, r1=110)
+    K = synth.keys(40, seed=3)
+    V = synth.values(40, seed=4)
+    fk = encode.fit_into_budget(K, lay, cfg)
+    dec = fk["decoder_f"]
+    # fp32 coefficient ruler of the fit (build_k_layer keeps it fp32 for the residual)
+    cs32 = fk["coeff_scale"].float()
+    slots = torch.arange(40, dtype=torch.int64)
+    page, _, R, err = _run(lay, dec, encode.pinv(dec), K, V, slots, 40,
+                           cq_in=fk["coeff_q"], cs_in=cs32)
+    assert err == 0
+    R_k = R.reshape(-1, H, D).permute(1, 0, 2).reshape(H * 40, D)
+    R_ref = encode.residual(K, fk["coeff_q"], cs32.unsqueeze(1), dec)
+    assert (R_k - R_ref).abs().max() <= 1e-4
+    k_slots = encode.k_slots_from(lay, fk["coeff_q"], cs32.to(torch.float16),
+                                  codec.build_rows(R_k, lay.res_k, lay.res_bits))
+    assert torch.equal(page[:, :lay.k_slot_bytes], k_slots)
+
+
+def test_slot_refusals_set_the_error_word_and_write_nothing():
+    lay, dec, pinv, Knew, V = _setup("safe", 3, seed=5)
+    for bad in ([0, -1, 2], [0, 1, 99]):
+        page, _, _, err = _run(lay, dec, pinv, Knew, V, torch.tensor(bad, dtype=torch.int64), 8)
+        assert err & 4, f"{bad}: error word {err}"
+        bad_i = 1 if bad[1] == -1 else 2
+        ok_rows = [j for j in range(3) if j != bad_i]
+        assert int(page.abs().sum()) > 0
+        assert all(int(page[bad[j]].abs().sum()) > 0 for j in ok_rows)

@@ -1,0 +1,91 @@
+// extern "C" entry points of libttkv_hip (declared in include/ttkv_hip.h).
+#include <mutex>
+#include <vector>
+
+#include "ttkv_host.h"
+
+namespace ttkv {
+
+static thread_local std::string t_err;
+
+int host_fail(int code, const std::string& msg) {
+  t_err = msg;
+  return code;
+}
+
+int device_cu_count() {
+  static std::mutex mu;
+  static std::vector<int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  std::lock_guard<std::mutex> lk(mu);
+  if ((int)cache.size() <= dev) cache.resize(dev + 1, 0);
+  if (!cache[dev]) {
+    int cu = 0;
+    if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cu <= 0)
+      cu = 256;
+    cache[dev] = cu;
+  }
+  return cache[dev];
+}
+
+}  // namespace ttkv
+
+using namespace ttkv;
+
+extern "C" {
+
+const char* ttkv_last_error(void) { return t_err.c_str(); }
+
+int64_t ttkv_blob_bytes(const ttkv_layout* lay) {
+  Geom g;
+  return make_geom(lay, &g) ? g.blob : -1;
+}
+
+int64_t ttkv_decode_workspace_bytes(const ttkv_layout* lay, int32_t num_heads, int32_t num_reqs,
+                                    int32_t max_seq_len) {
+  Geom g;
+  if (!make_geom(lay, &g) || num_heads <= 0 || num_heads % g.H || num_reqs < 0) return -1;
+  return decode_workspace_bytes(g, num_heads / g.H, num_reqs, max_seq_len);
+}
+
+int ttkv_decode_paged(const ttkv_layout* lay, int32_t num_heads, float scale, const void* query,
+                      int32_t q_dtype, int64_t q_row_stride, const uint8_t* page, int64_t n_slots,
+                      int64_t slot_stride, int32_t block_size, const int32_t* block_table,
+                      int64_t bt_row_stride, int32_t max_blocks, const int32_t* seq_lens,
+                      const int32_t* query_start_loc, int32_t num_reqs, int32_t max_seq_len,
+                      const int32_t* dec_slot_of_block, int64_t num_blocks,
+                      const float* dec_pool, int64_t n_dec_slots, const float* cos_sin_cache,
+                      int64_t max_position, void* out, int32_t out_dtype, int64_t out_row_stride,
+                      void* workspace, int64_t workspace_bytes, int32_t* error_word,
+                      ttkv_stream_t stream) {
+  Geom g;
+  if (!make_geom(lay, &g)) return host_fail(TTKV_E_INVALID, "invalid layout");
+  return decode_paged(g, num_heads, scale, query, q_dtype, q_row_stride, page, n_slots,
+                      slot_stride, block_size, block_table, bt_row_stride, max_blocks, seq_lens,
+                      query_start_loc, num_reqs, max_seq_len, dec_slot_of_block, num_blocks,
+                      dec_pool, n_dec_slots, cos_sin_cache, max_position, out, out_dtype,
+                      out_row_stride, workspace, workspace_bytes, error_word,
+                      (hipStream_t)stream);
+}
+
+int ttkv_write_paged(const ttkv_layout* lay, const void* key, int32_t k_dtype, int64_t k_row_stride,
+                     const void* value, int32_t v_dtype, int64_t v_row_stride,
+                     const int64_t* slot_mapping, int32_t num_tokens,
+                     const int32_t* query_start_loc, int32_t num_reqs, const int32_t* block_table,
+                     int64_t bt_row_stride, const int32_t* dec_slot_of_block, int64_t num_blocks,
+                     const float* dec_pool, const float* pinv_pool, int64_t n_dec_slots,
+                     const int8_t* coeff_q_in, const float* coeff_scale_in, uint8_t* page,
+                     int64_t n_slots, int64_t slot_stride, float* coeff_out, float* resid_out,
+                     int32_t* error_word, ttkv_stream_t stream) {
+  Geom g;
+  if (!make_geom(lay, &g)) return host_fail(TTKV_E_INVALID, "invalid layout");
+  return write_paged(g, key, k_dtype, k_row_stride, value, v_dtype, v_row_stride, slot_mapping,
+                     num_tokens, query_start_loc, num_reqs, block_table, bt_row_stride,
+                     dec_slot_of_block, num_blocks, dec_pool, pinv_pool, n_dec_slots, coeff_q_in,
+                     coeff_scale_in, page, n_slots, slot_stride, coeff_out, resid_out, error_word,
+                     (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,110 @@
+// Shared device helpers for the compressed-KV kernels (gfx950 / CDNA4).
+//
+// Slot format (reference: vllm_ttkv/layout.py:56-261, codec/ttkv_packed_cache.py:50-271):
+//   token blob = [K slot | V slot], each zero-padded to 16 bytes
+//   K slot = r1 int8 coefficients, fp16 coefficient ruler (LE), H rows of
+//            [bitmap d/8 B | MSB-first code stream ceil(k*bits/8) B | fp16 ruler (LE)]
+//   V slot = H rows of the same shape
+// Bitmap: lane j <-> byte j>>3, bit 7-(j&7). The stream holds the kept lanes in increasing lane
+// order, `bits` bits each, MSB first; the stored code is q + 2^(bits-1). Decoded value
+// (code - 2^(bits-1)) * float(ruler) on kept lanes, 0 elsewhere.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/ttkv_hip.h"
+
+namespace ttkv {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+
+constexpr int kD = 128;           // head dim the kernels are built for
+constexpr int kBitmapBytes = kD / 8;
+
+// Byte geometry of one layer, derived exactly as layout.py:98-157.
+struct Geom {
+  int H, d, r1, qbits, res_k, res_bits, v_lanes, v_bits;
+  int coeff_bytes;   // r1 * qbits / 8
+  int k_pb, v_pb;    // packed code bytes per row
+  int k_row, v_row;  // bytes per head row
+  int k_field;       // offset of head 0's K row in the slot
+  int k_slot, v_slot, blob;
+};
+
+__host__ inline int align_up16(int n) { return (n + 15) / 16 * 16; }
+
+__host__ inline bool make_geom(const ttkv_layout* l, Geom* g) {
+  if (!l) return false;
+  g->H = l->H; g->d = l->d; g->r1 = l->r1; g->qbits = l->qbits;
+  g->res_k = l->res_k; g->res_bits = l->res_bits; g->v_lanes = l->v_lanes; g->v_bits = l->v_bits;
+  if (g->d <= 0 || g->d % 8 || g->H <= 0 || g->r1 <= 0) return false;
+  if ((g->r1 * g->qbits) % 8) return false;
+  if (g->res_k < 0 || g->res_k > g->d || g->v_lanes < 1 || g->v_lanes > g->d) return false;
+  g->coeff_bytes = g->r1 * g->qbits / 8;
+  g->k_pb = (g->res_k * g->res_bits + 7) / 8;
+  g->v_pb = (g->v_lanes * g->v_bits + 7) / 8;
+  g->k_row = g->d / 8 + g->k_pb + 2;
+  g->v_row = g->d / 8 + g->v_pb + 2;
+  g->k_field = g->coeff_bytes + 2;
+  g->k_slot = align_up16(g->coeff_bytes + 2 + g->H * g->k_row);
+  g->v_slot = align_up16(g->H * g->v_row);
+  g->blob = g->k_slot + g->v_slot;
+  return true;
+}
+
+__device__ __forceinline__ float f16_bits_to_float(uint32_t bits16) {
+  _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)bits16);
+  return (float)h;
+}
+
+__device__ __forceinline__ float bf16_bits_to_float(uint32_t bits16) {
+  return __builtin_bit_cast(float, bits16 << 16);
+}
+
+// Load element `i` of a q/out-style tensor of dtype `dt` as fp32.
+__device__ __forceinline__ float load_act(const void* p, int dt, int64_t i) {
+  if (dt == TTKV_DTYPE_F32) return ((const float*)p)[i];
+  uint32_t b = ((const uint16_t*)p)[i];
+  return dt == TTKV_DTYPE_F16 ? f16_bits_to_float(b) : bf16_bits_to_float(b);
+}
+
+// Round-to-nearest-even fp32 -> bf16 bits (NaN kept quiet).
+__device__ __forceinline__ uint16_t float_to_bf16_bits(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ void store_act(void* p, int dt, int64_t i, float v) {
+  if (dt == TTKV_DTYPE_F32) {
+    ((float*)p)[i] = v;
+  } else if (dt == TTKV_DTYPE_F16) {
+    ((_Float16*)p)[i] = (_Float16)v;
+  } else {
+    ((uint16_t*)p)[i] = float_to_bf16_bits(v);
+  }
+}
+
+// Copy `nbytes` bytes starting at an arbitrary global byte address `src` into LDS at a 4-byte
+// aligned `dst`, realigned so dst[0] == src[0]. Uses only aligned dword loads that stay inside
+// [floor4(src), ceil4(src + nbytes)), so it never reads past a 16-byte-aligned blob end.
+// `part`/`nparts` split the dwords of one row between cooperating threads.
+__device__ __forceinline__ void copy_row_realign(const uint8_t* src, int nbytes, uint32_t* dst,
+                                                 int part, int nparts) {
+  const uintptr_t a = (uintptr_t)src;
+  const uint32_t* base = (const uint32_t*)(a & ~(uintptr_t)3);
+  const int sh = (int)(a & 3);
+  const int nsrc = (sh + nbytes + 3) >> 2;           // source dwords that hold the row
+  const int ndst = (nbytes + 3) >> 2;
+  for (int dw = part; dw < ndst; dw += nparts) {
+    uint32_t lo = base[dw];
+    uint32_t hi = (dw + 1 < nsrc) ? base[dw + 1] : 0u;
+    // bytes [sh, sh+4) of the 8-byte little-endian pair (hi:lo)
+    dst[dw] = sh ? __builtin_amdgcn_alignbyte(hi, lo, sh) : lo;
+  }
+}
+
+}  // namespace ttkv

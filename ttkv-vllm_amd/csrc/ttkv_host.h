@@ -1,0 +1,36 @@
+// Host-side shared state of libttkv_hip: thread-local error text and device properties.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <string>
+
+#include "ttkv_common.h"
+
+namespace ttkv {
+
+int host_fail(int code, const std::string& msg);
+int device_cu_count();
+
+int decode_chunk_for(int num_reqs, int H, int max_seq_len);
+int64_t decode_workspace_bytes(const Geom& g, int G, int num_reqs, int max_seq_len);
+int decode_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype,
+                 int64_t q_row_stride, const uint8_t* page, int64_t n_slots, int64_t slot_stride,
+                 int block_size, const int32_t* bt, int64_t bt_row_stride, int max_blocks,
+                 const int32_t* seq_lens, const int32_t* qsl, int num_reqs, int max_seq_len,
+                 const int32_t* dec_map, int64_t num_blocks, const float* dec_pool,
+                 int64_t n_dec_slots, const float* cs_cache, int64_t max_pos, void* out,
+                 int out_dtype, int64_t out_row_stride, void* ws, int64_t ws_bytes, int32_t* err,
+                 hipStream_t st);
+
+}  // namespace ttkv
+
+namespace ttkv {
+int write_paged(const Geom& g, const void* key, int k_dtype, int64_t k_row_stride, const void* val,
+                int v_dtype, int64_t v_row_stride, const int64_t* slot_mapping, int num_tokens,
+                const int32_t* qsl, int num_reqs, const int32_t* bt, int64_t bt_row_stride,
+                const int32_t* dec_map, int64_t num_blocks, const float* dec_pool,
+                const float* pinv_pool, int64_t n_dec_slots, const int8_t* cq_in,
+                const float* cs_in, uint8_t* page, int64_t n_slots, int64_t slot_stride,
+                float* c_out, float* r_out, int32_t* err, hipStream_t st);
+}  // namespace ttkv

@@ -1,0 +1,334 @@
+// K3: write/encode of new tokens into compressed slots, one launch for all tokens of a layer.
+// gfx950 / CDNA4.
+//
+// One 256-thread workgroup per token:
+//   project   c[a] = sum_m M[m] * pinv[m][a], M = the token's raw key flattened m = h*d + j
+//             (encode.py:322-324), fp32 in a fixed order          -- or take (cq, cs) from a fit
+//   quantise  cs = max|c| * fp32(1/127) (1 if 0); cq = clamp(rint(c / cs), -128, 127)
+//             (encode.py:328-332; the fp32 reciprocal multiply is torch-CUDA's scalar division,
+//             select_triton.py:76-84; c/cs is a correctly rounded division)
+//   residual  R[h][j] = K[h][j] - sum_a (cq[a]*cs) * decoder_f[a][h*d+j]   (encode.py:334-336)
+//   rows      for every head: K residual row from R, V row from the value; each row picks exactly
+//             k lanes by magnitude (ties -> lowest lane, select_triton.py:181-193), ruler =
+//             rowmax * fp32(1/(2^(b-1)-1)) (1 * that if rowmax == 0), q = clamp(rint(x / ruler)),
+//             bitmap MSB-first, codes MSB-first in lane order, fp16 ruler LE
+//             (ttkv_packed_cache.py:203-231, select_triton.py:195-232)
+//   store     coefficients, fp16 coefficient ruler, H K rows, H V rows, zero padding: the
+//             bytes layout.pack_k_slots/pack_v_slots produce (layout.py:161-239), written at
+//             slot_mapping[i] (encode.py:471-508).
+// Selection, quantisation and packing are bit-exact functions of their float inputs (R and the
+// value); the projection and reconstruction sums are fp32 with an implementation-defined order,
+// as in the reference. Optional outputs expose c and R so tests can pin the bytes from there.
+#include <math.h>
+
+#include "ttkv_host.h"
+
+namespace ttkv {
+
+constexpr int kWThreads = 256;
+
+struct WriteArgs {
+  Geom g;
+  const void* key;
+  int k_dtype;
+  int64_t k_row_stride;
+  const void* val;
+  int v_dtype;
+  int64_t v_row_stride;
+  const int64_t* slot_mapping;
+  int num_tokens;
+  const int32_t* qsl;
+  int num_reqs;
+  const int32_t* bt;
+  int64_t bt_row_stride;
+  const int32_t* dec_map;
+  int64_t num_blocks;
+  const float* dec_pool;
+  const float* pinv_pool;
+  int64_t n_dec_slots;
+  const int8_t* cq_in;
+  const float* cs_in;
+  uint8_t* page;
+  int64_t n_slots, slot_stride;
+  float* c_out;
+  float* r_out;
+  int* err;
+  float inv127, inv_rk, inv_rv;
+};
+
+struct WriteSmem {
+  float kraw[8 * kD];   // the token's raw key, flattened m = h*d + j (H <= 8)
+  float resid[8 * kD];  // R
+  float c[256];         // projection / coefficients (r1 <= 256)
+  float cpart[256];
+  float cqs[256];       // cq * cs (fp32)
+  float red[kWThreads / 64];
+  uint8_t codes[4][kD];  // per-wave code bytes by rank
+  int req;
+  int dslot;
+};
+
+// Exact top-k select + quantise + pack of one 128-lane row held as lane l: x0 = dim l,
+// x1 = dim l+64. Writes bitmap, codes and fp16 ruler at dst (any alignment). `codes` is this
+// wave's LDS scratch. Every lane of the wave must call it.
+template <int BITS>
+__device__ void pack_row(float x0, float x1, int k, float inv_ruler, uint8_t* dst,
+                         uint8_t* codes) {
+  constexpr int OFF = 1 << (BITS - 1);
+  const int lane = threadIdx.x & 63;
+  const uint32_t u0 = __builtin_bit_cast(uint32_t, fabsf(x0));
+  const uint32_t u1 = __builtin_bit_cast(uint32_t, fabsf(x1));
+  // k-th largest magnitude by bit construction on the (monotone) magnitude bit pattern.
+  uint32_t t = 0;
+  for (int b = 30; b >= 0; --b) {
+    const uint32_t cand = t | (1u << b);
+    const int cnt = __builtin_popcountll(__ballot(u0 >= cand)) +
+                    __builtin_popcountll(__ballot(u1 >= cand));
+    if (cnt >= k) t = cand;
+  }
+  const uint64_t above0 = __ballot(u0 > t), above1 = __ballot(u1 > t);
+  const int need = k - (__builtin_popcountll(above0) + __builtin_popcountll(above1));
+  const uint64_t tie0 = __ballot(u0 == t), tie1 = __ballot(u1 == t);
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  const int tr0 = __builtin_popcountll(tie0 & below);
+  const int tr1 = __builtin_popcountll(tie0) + __builtin_popcountll(tie1 & below);
+  const bool s0 = (u0 > t) || (u0 == t && tr0 < need);
+  const bool s1 = (u1 > t) || (u1 == t && tr1 < need);
+  const uint64_t sel0 = __ballot(s0), sel1 = __ballot(s1);
+  // Row max (always kept when k >= 1), as bits: non-negative floats order like their bits.
+  uint32_t mx = u0 > u1 ? u0 : u1;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint32_t other = __shfl_xor(mx, o);
+    mx = other > mx ? other : mx;
+  }
+  const float rmax = __builtin_bit_cast(float, mx);
+  const float sc = (rmax == 0.f ? 1.f : rmax) * inv_ruler;
+  // Codes, by rank (lane order).
+  const int rank0 = __builtin_popcountll(sel0 & below);
+  const int rank1 = __builtin_popcountll(sel0) + __builtin_popcountll(sel1 & below);
+  if (s0) {
+    const float q = fminf(fmaxf(rintf(__fdiv_rn(x0, sc)), (float)-OFF), (float)(OFF - 1));
+    codes[rank0] = (uint8_t)((int)q + OFF);
+  }
+  if (s1) {
+    const float q = fminf(fmaxf(rintf(__fdiv_rn(x1, sc)), (float)-OFF), (float)(OFF - 1));
+    codes[rank1] = (uint8_t)((int)q + OFF);
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int pb = (k * BITS + 7) / 8;
+  // Bitmap: byte m holds dims 8m..8m+7, dim 8m at bit 7.
+  if (lane < 16) {
+    const uint64_t sel = lane < 8 ? sel0 : sel1;
+    const uint32_t byte = (uint32_t)(sel >> (8 * (lane & 7))) & 0xffu;
+    dst[lane] = (uint8_t)(__builtin_bitreverse32(byte) >> 24);
+  }
+  // Code stream: byte b = stream bits [8b, 8b+8), MSB first, zero beyond k codes.
+  if (lane < pb) {
+    uint32_t byte = 0;
+#pragma unroll
+    for (int bit = 0; bit < 8; ++bit) {
+      const int p = 8 * lane + bit;
+      const int ci = p / BITS;
+      const uint32_t code = ci < k ? codes[ci] : 0u;
+      byte |= ((code >> (BITS - 1 - (p - ci * BITS))) & 1u) << (7 - bit);
+    }
+    dst[16 + lane] = (uint8_t)byte;
+  }
+  if (lane == 0) {
+    const uint16_t hb = __builtin_bit_cast(uint16_t, (_Float16)sc);
+    dst[16 + pb] = (uint8_t)(hb & 0xff);
+    dst[16 + pb + 1] = (uint8_t)(hb >> 8);
+  }
+}
+
+template <int RB, int VB>
+__global__ __launch_bounds__(kWThreads) void write_paged_kernel(WriteArgs a) {
+  __shared__ WriteSmem S;
+  const Geom& g = a.g;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = tid >> 6;
+  const int i = blockIdx.x;
+  const int HD = g.H * kD;
+
+  if (tid == 0) {
+    // request of token i: qsl[r] <= i < qsl[r+1]
+    int lo = 0, hi = a.num_reqs - 1, r = -1;
+    while (lo <= hi) {
+      const int mid = (lo + hi) >> 1;
+      if (a.qsl[mid] <= i) {
+        r = mid;
+        lo = mid + 1;
+      } else {
+        hi = mid - 1;
+      }
+    }
+    int ds = -1;
+    if (r >= 0 && i < a.qsl[r + 1]) {
+      const int blk0 = a.bt[(int64_t)r * a.bt_row_stride];
+      if (blk0 >= 0 && blk0 < a.num_blocks) ds = a.dec_map[blk0];
+    }
+    if (ds < 0 || ds >= a.n_dec_slots) {
+      atomicOr(a.err, TTKV_ERR_NO_DECODER);
+      ds = -1;
+    }
+    S.req = r;
+    S.dslot = ds;
+  }
+  const int64_t slot = a.slot_mapping[i];
+  const bool slot_ok = slot >= 0 && slot < a.n_slots;
+  if (!slot_ok && tid == 0) atomicOr(a.err, TTKV_ERR_BAD_SLOT);
+  for (int m = tid; m < HD; m += kWThreads)
+    S.kraw[m] = load_act(a.key, a.k_dtype, (int64_t)i * a.k_row_stride + m);
+  __syncthreads();
+  const int ds = S.dslot;
+  if (ds < 0 || !slot_ok) return;
+  const float* dec = a.dec_pool + (int64_t)ds * g.r1 * HD;
+
+  // ---- coefficients
+  if (a.cq_in) {
+    for (int ar = tid; ar < g.r1; ar += kWThreads) S.c[ar] = (float)a.cq_in[(int64_t)i * g.r1 + ar];
+    __syncthreads();
+  } else {
+    const float* pinv = a.pinv_pool + (int64_t)ds * HD * g.r1;
+    // thread (ar, half): half of the 1024-long dot product, fixed order, then combined.
+    const int nh = kWThreads / 128 > 0 ? 2 : 1;
+    const int ar = tid & 127;
+    const int part = tid >> 7;
+    for (int a0 = 0; a0 < g.r1; a0 += 128) {
+      const int aa = a0 + ar;
+      float acc = 0.f;
+      if (aa < g.r1) {
+        const int m0 = part * (HD / nh), m1 = m0 + HD / nh;
+        for (int m = m0; m < m1; ++m) acc = fmaf(S.kraw[m], pinv[(int64_t)m * g.r1 + aa], acc);
+      }
+      if (part == 1 && aa < g.r1) S.cpart[aa] = acc;
+      __syncthreads();
+      if (part == 0 && aa < g.r1) S.c[aa] = acc + S.cpart[aa];
+      __syncthreads();
+    }
+    // max |c|
+    float mx = 0.f;
+    for (int ar2 = tid; ar2 < g.r1; ar2 += kWThreads) mx = fmaxf(mx, fabsf(S.c[ar2]));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if (lane == 0) S.red[wv] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(S.red[0], S.red[1]), fmaxf(S.red[2], S.red[3]));
+    float cs = mx * a.inv127;
+    if (cs == 0.f) cs = 1.f;
+    if (a.c_out)
+      for (int ar2 = tid; ar2 < g.r1; ar2 += kWThreads) a.c_out[(int64_t)i * g.r1 + ar2] = S.c[ar2];
+    __syncthreads();
+    for (int ar2 = tid; ar2 < g.r1; ar2 += kWThreads)
+      S.c[ar2] = fminf(fmaxf(rintf(__fdiv_rn(S.c[ar2], cs)), -128.f), 127.f);
+    if (tid == 0) S.red[0] = cs;
+    __syncthreads();
+  }
+  const float cs = a.cq_in ? a.cs_in[i] : S.red[0];
+  uint8_t* base = a.page + slot * a.slot_stride;
+  for (int ar = tid; ar < g.r1; ar += kWThreads) {
+    S.cqs[ar] = S.c[ar] * cs;
+    base[ar] = (uint8_t)(int8_t)(int)S.c[ar];
+  }
+  if (tid == 0) {
+    const uint16_t hb = __builtin_bit_cast(uint16_t, (_Float16)cs);
+    base[g.coeff_bytes] = (uint8_t)(hb & 0xff);
+    base[g.coeff_bytes + 1] = (uint8_t)(hb >> 8);
+  }
+  // zero padding after the last K row and after the last V row
+  for (int b = g.k_field + g.H * g.k_row + tid; b < g.k_slot; b += kWThreads) base[b] = 0;
+  for (int b = g.k_slot + g.H * g.v_row + tid; b < g.blob; b += kWThreads) base[b] = 0;
+  __syncthreads();
+
+  // ---- residual R = K - (cq*cs) @ decoder_f
+  for (int m = tid; m < HD; m += kWThreads) {
+    float acc = 0.f;
+    for (int ar = 0; ar < g.r1; ++ar) acc = fmaf(S.cqs[ar], dec[(int64_t)ar * HD + m], acc);
+    const float R = S.kraw[m] - acc;
+    S.resid[m] = R;
+    if (a.r_out) a.r_out[(int64_t)i * HD + m] = R;
+  }
+  __syncthreads();
+
+  // ---- rows: wave wv packs heads wv, wv+4 (K residual, then V)
+  for (int h = wv; h < g.H; h += 4) {
+    pack_row<RB>(S.resid[h * kD + lane], S.resid[h * kD + 64 + lane], g.res_k, a.inv_rk,
+                 base + g.k_field + h * g.k_row, S.codes[wv]);
+    __builtin_amdgcn_wave_barrier();
+    const int64_t vb = (int64_t)i * a.v_row_stride + h * kD;
+    pack_row<VB>(load_act(a.val, a.v_dtype, vb + lane), load_act(a.val, a.v_dtype, vb + 64 + lane),
+                 g.v_lanes, a.inv_rv, base + g.k_slot + h * g.v_row, S.codes[wv]);
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+static float inv_ruler_f32(int bits) { return (float)(1.0 / (double)((1 << (bits - 1)) - 1)); }
+
+int write_paged(const Geom& g, const void* key, int k_dtype, int64_t k_row_stride, const void* val,
+                int v_dtype, int64_t v_row_stride, const int64_t* slot_mapping, int num_tokens,
+                const int32_t* qsl, int num_reqs, const int32_t* bt, int64_t bt_row_stride,
+                const int32_t* dec_map, int64_t num_blocks, const float* dec_pool,
+                const float* pinv_pool, int64_t n_dec_slots, const int8_t* cq_in,
+                const float* cs_in, uint8_t* page, int64_t n_slots, int64_t slot_stride,
+                float* c_out, float* r_out, int32_t* err, hipStream_t st) {
+  if (g.d != kD) return host_fail(TTKV_E_UNSUPPORTED, "head dim must be 128");
+  if (g.H > 8) return host_fail(TTKV_E_UNSUPPORTED, "H > 8 KV heads is not built");
+  if (g.qbits != 8) return host_fail(TTKV_E_UNSUPPORTED, "coefficient width must be 8 bits");
+  if (g.r1 > 256) return host_fail(TTKV_E_UNSUPPORTED, "r1 > 256 is not built");
+  if (g.res_k < 1) return host_fail(TTKV_E_UNSUPPORTED, "res_k must be >= 1");
+  if (!((g.res_bits == 3 && g.v_bits == 3) || (g.res_bits == 4 && g.v_bits == 4)))
+    return host_fail(TTKV_E_UNSUPPORTED, "res_bits/v_bits must be 3/3 or 4/4");
+  if (!key || !val || !slot_mapping || !qsl || !bt || !dec_map || !dec_pool || !page || !err)
+    return host_fail(TTKV_E_INVALID, "null pointer argument");
+  if (!cq_in && !pinv_pool) return host_fail(TTKV_E_INVALID, "need pinv_pool or coeff_q_in");
+  if (cq_in && !cs_in) return host_fail(TTKV_E_INVALID, "coeff_q_in needs coeff_scale_in");
+  if (slot_stride < g.blob) return host_fail(TTKV_E_INVALID, "slot stride smaller than the blob");
+  if (k_dtype < 0 || k_dtype > 2 || v_dtype < 0 || v_dtype > 2)
+    return host_fail(TTKV_E_INVALID, "dtype code");
+  if (num_tokens < 0 || num_reqs < 0) return host_fail(TTKV_E_INVALID, "negative size");
+  if (num_tokens == 0) return TTKV_OK;
+  WriteArgs a{};
+  a.g = g;
+  a.key = key;
+  a.k_dtype = k_dtype;
+  a.k_row_stride = k_row_stride;
+  a.val = val;
+  a.v_dtype = v_dtype;
+  a.v_row_stride = v_row_stride;
+  a.slot_mapping = slot_mapping;
+  a.num_tokens = num_tokens;
+  a.qsl = qsl;
+  a.num_reqs = num_reqs;
+  a.bt = bt;
+  a.bt_row_stride = bt_row_stride;
+  a.dec_map = dec_map;
+  a.num_blocks = num_blocks;
+  a.dec_pool = dec_pool;
+  a.pinv_pool = pinv_pool;
+  a.n_dec_slots = n_dec_slots;
+  a.cq_in = cq_in;
+  a.cs_in = cs_in;
+  a.page = page;
+  a.n_slots = n_slots;
+  a.slot_stride = slot_stride;
+  a.c_out = c_out;
+  a.r_out = r_out;
+  a.err = err;
+  a.inv127 = inv_ruler_f32(8);
+  a.inv_rk = inv_ruler_f32(g.res_bits);
+  a.inv_rv = inv_ruler_f32(g.v_bits);
+  if (g.res_bits == 3)
+    hipLaunchKernelGGL((write_paged_kernel<3, 3>), dim3(num_tokens), dim3(kWThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL((write_paged_kernel<4, 4>), dim3(num_tokens), dim3(kWThreads), 0, st, a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return host_fail(TTKV_E_LAUNCH, std::string("write launch: ") +
+                                                          hipGetErrorString(e));
+  return TTKV_OK;
+}
+
+}  // namespace ttkv

@@ -1,0 +1,167 @@
+"""torch-facing wrappers over the libttkv_hip C ABI.
+
+Each wrapper validates what the host can see, allocates nothing on its own except when the
+caller did not pass an output or workspace, and launches on torch's current stream. The tensors
+must live on a HIP device; there is no CPU path.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _hip
+from .layout import TTKLayout
+
+
+def _need_device(*ts):
+    for t in ts:
+        if t is not None and t.device.type != "cuda":
+            raise RuntimeError("libttkv_hip kernels take device tensors; got a "
+                               f"{t.device.type} tensor (there is no CPU implementation)")
+
+
+def _i32(t, name):
+    if t.dtype != torch.int32 or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous int32 tensor, got {t.dtype}")
+    return t
+
+
+def page_bytes(page: torch.Tensor, blob: int) -> torch.Tensor:
+    """`[n_slots, W]` uint8 view of a paged cache `[num_blocks, (1,) block_size, C]` in any dtype.
+
+    The last dim of a vLLM page counts MODEL-dtype elements (decode.py:125-157), so the row is
+    reinterpreted as bytes. W >= blob is accepted (vLLM rounds the row up to whole elements)."""
+    u8 = page if page.dtype == torch.uint8 else page.view(torch.uint8)
+    if u8.shape[-1] < blob:
+        raise ValueError(f"the cache row is {u8.shape[-1]} bytes but the layout needs {blob}")
+    if not u8.is_contiguous():
+        raise ValueError("the cache page must be contiguous")
+    return u8.reshape(-1, u8.shape[-1])
+
+
+def decode_workspace(lay: TTKLayout, num_heads: int, num_reqs: int, max_seq_len: int,
+                     device) -> torch.Tensor:
+    """A zero-filled workspace sized for this batch shape (the kernel keeps it zero)."""
+    n = _hip.lib().ttkv_decode_workspace_bytes(_hip.Layout.of(lay), num_heads, num_reqs,
+                                               max_seq_len)
+    if n < 0:
+        raise ValueError("invalid layout / head count for the decode workspace")
+    return torch.zeros(max(int(n), 256), dtype=torch.uint8, device=device)
+
+
+def decode_paged(lay: TTKLayout, query: torch.Tensor, page: torch.Tensor, block_size: int,
+                 block_table: torch.Tensor, seq_lens: torch.Tensor,
+                 query_start_loc: torch.Tensor, max_seq_len: int,
+                 dec_slot_of_block: torch.Tensor, dec_pool: torch.Tensor,
+                 cos_sin_cache: torch.Tensor, scale: float, out: torch.Tensor | None = None,
+                 workspace: torch.Tensor | None = None,
+                 error_word: torch.Tensor | None = None) -> torch.Tensor:
+    """K1: one launch over all decode requests. See `ttkv_decode_paged` in include/ttkv_hip.h.
+
+    query [N, HQ, d]; page: the layer's cache (bytes reinterpreted); block_table [B, max_blocks]
+    int32; seq_lens [B] int32; query_start_loc [>=B] int32 (row of request r's query);
+    dec_slot_of_block [num_blocks] int32; dec_pool [slots, r1, H*d] fp32; cos_sin_cache
+    [max_pos, d] fp32 (vLLM layout). Returns `out` [N, HQ, d] with the decode rows written."""
+    _need_device(query, page, block_table, seq_lens, query_start_loc, dec_slot_of_block,
+                 dec_pool, cos_sin_cache)
+    L = _hip.lib()
+    num_reqs = int(seq_lens.numel())
+    N, HQ, d = query.shape
+    if d != lay.d:
+        raise ValueError(f"query head dim {d} != layout d {lay.d}")
+    if query.stride(2) != 1 or query.stride(1) != d:
+        raise ValueError("query must be contiguous within a token ([HQ, d] rows)")
+    blob = lay.compressed_bytes_per_token()
+    flat = page_bytes(page, blob)
+    _i32(block_table, "block_table")
+    _i32(seq_lens, "seq_lens")
+    _i32(query_start_loc, "query_start_loc")
+    _i32(dec_slot_of_block, "dec_slot_of_block")
+    if dec_pool.dtype != torch.float32 or not dec_pool.is_contiguous():
+        raise ValueError("dec_pool must be contiguous fp32 [slots, r1, H*d]")
+    if dec_pool.dim() != 3 or dec_pool.shape[1] != lay.r1 or dec_pool.shape[2] != lay.H * lay.d:
+        raise ValueError(f"dec_pool is {tuple(dec_pool.shape)}; expected [slots, {lay.r1}, "
+                         f"{lay.H * lay.d}] (a decoder written at one rank cannot be read at "
+                         f"another)")
+    if cos_sin_cache.dtype != torch.float32 or not cos_sin_cache.is_contiguous():
+        raise ValueError("cos_sin_cache must be contiguous fp32 [max_pos, d]")
+    if cos_sin_cache.shape[-1] != lay.d:
+        raise NotImplementedError(
+            f"rotary_dim={cos_sin_cache.shape[-1]} != head_dim={lay.d} (partial rotary) is not "
+            f"supported: the kernel pairs (j, j+d/2) across the whole row")
+    if out is None:
+        out = torch.empty_like(query)
+    if out.shape != query.shape or out.stride(2) != 1 or out.stride(1) != d:
+        raise ValueError("out must match query's shape with contiguous [HQ, d] rows")
+    if out.dtype not in _hip.DTYPE_CODE or query.dtype not in _hip.DTYPE_CODE:
+        raise ValueError("query/out dtype must be fp32, fp16 or bf16")
+    if workspace is None:
+        workspace = decode_workspace(lay, HQ, num_reqs, max_seq_len, query.device)
+    if error_word is None:
+        error_word = torch.zeros(1, dtype=torch.int32, device=query.device)
+    rc = L.ttkv_decode_paged(
+        _hip.Layout.of(lay), HQ, float(scale),
+        query.data_ptr(), _hip.DTYPE_CODE[query.dtype], query.stride(0),
+        flat.data_ptr(), flat.shape[0], flat.stride(0),
+        int(block_size), block_table.data_ptr(), block_table.stride(0), block_table.shape[1],
+        seq_lens.data_ptr(), query_start_loc.data_ptr(), num_reqs, int(max_seq_len),
+        dec_slot_of_block.data_ptr(), dec_slot_of_block.numel(), dec_pool.data_ptr(),
+        dec_pool.shape[0], cos_sin_cache.data_ptr(), cos_sin_cache.shape[0],
+        out.data_ptr(), _hip.DTYPE_CODE[out.dtype], out.stride(0),
+        workspace.data_ptr(), workspace.numel(), error_word.data_ptr(),
+        _hip.stream_ptr(query.device))
+    _hip.check(rc, "ttkv_decode_paged")
+    return out
+
+
+def write_paged(lay: TTKLayout, key: torch.Tensor, value: torch.Tensor,
+                slot_mapping: torch.Tensor, query_start_loc: torch.Tensor,
+                block_table: torch.Tensor, dec_slot_of_block: torch.Tensor,
+                dec_pool: torch.Tensor, pinv_pool: torch.Tensor | None, page: torch.Tensor,
+                coeff_q_in: torch.Tensor | None = None,
+                coeff_scale_in: torch.Tensor | None = None,
+                coeff_out: torch.Tensor | None = None, resid_out: torch.Tensor | None = None,
+                error_word: torch.Tensor | None = None) -> None:
+    """K3: encode + pack `key`/`value` ([N, H, d], raw pre-RoPE keys) into their slots.
+
+    See `ttkv_write_paged` in include/ttkv_hip.h. `pinv_pool` [slots, H*d, r1] fp32 drives the
+    frozen projection; `coeff_q_in`/`coeff_scale_in` replace it with a fit's coefficients."""
+    _need_device(key, value, slot_mapping, query_start_loc, block_table, dec_slot_of_block,
+                 dec_pool, pinv_pool, page)
+    N = key.shape[0]
+    if key.dim() != 3 or key.shape[1:] != (lay.H, lay.d) or value.shape != key.shape:
+        raise ValueError(f"key/value must be [N, {lay.H}, {lay.d}], got {tuple(key.shape)} and "
+                         f"{tuple(value.shape)}")
+    for t, nm in ((key, "key"), (value, "value")):
+        if t.stride(2) != 1 or t.stride(1) != lay.d:
+            raise ValueError(f"{nm} must be contiguous within a token")
+        if t.dtype not in _hip.DTYPE_CODE:
+            raise ValueError(f"{nm} dtype must be fp32, fp16 or bf16")
+    if slot_mapping.dtype != torch.int64 or slot_mapping.numel() < N:
+        raise ValueError("slot_mapping must be int64 with one id per token")
+    _i32(query_start_loc, "query_start_loc")
+    _i32(block_table, "block_table")
+    _i32(dec_slot_of_block, "dec_slot_of_block")
+    if dec_pool.dtype != torch.float32 or tuple(dec_pool.shape[1:]) != (lay.r1, lay.H * lay.d):
+        raise ValueError("dec_pool must be fp32 [slots, r1, H*d]")
+    if pinv_pool is not None and (pinv_pool.dtype != torch.float32 or
+                                  tuple(pinv_pool.shape[1:]) != (lay.H * lay.d, lay.r1)):
+        raise ValueError("pinv_pool must be fp32 [slots, H*d, r1]")
+    flat = page_bytes(page, lay.compressed_bytes_per_token())
+    if error_word is None:
+        error_word = torch.zeros(1, dtype=torch.int32, device=key.device)
+    cq = None
+    if coeff_q_in is not None:
+        cq = coeff_q_in.to(torch.int8).contiguous()
+        if coeff_scale_in is None:
+            raise ValueError("coeff_q_in needs coeff_scale_in (fp32)")
+        coeff_scale_in = coeff_scale_in.to(torch.float32).contiguous()
+    rc = _hip.lib().ttkv_write_paged(
+        _hip.Layout.of(lay), key.data_ptr(), _hip.DTYPE_CODE[key.dtype], key.stride(0),
+        value.data_ptr(), _hip.DTYPE_CODE[value.dtype], value.stride(0),
+        slot_mapping.data_ptr(), N, query_start_loc.data_ptr(), query_start_loc.numel() - 1,
+        block_table.data_ptr(), block_table.stride(0), dec_slot_of_block.data_ptr(),
+        dec_slot_of_block.numel(), dec_pool.data_ptr(), _hip.ptr(pinv_pool), dec_pool.shape[0],
+        _hip.ptr(cq), _hip.ptr(coeff_scale_in), flat.data_ptr(), flat.shape[0], flat.stride(0),
+        _hip.ptr(coeff_out), _hip.ptr(resid_out), error_word.data_ptr(),
+        _hip.stream_ptr(key.device))
+    _hip.check(rc, "ttkv_write_paged")
