@@ -1,0 +1,318 @@
+"""Benchmark: the fused compressed-KV decode read (K1) on one MI355X.
+
+Headline workload: Llama-3.2-3B attention geometry (24 q heads, 8 KV heads,
+head dim 128, 28 layers), `safe` allocation at r1 = 110, block size 16, 8 concurrent requests at
+14,402 cached tokens each, one decode query per request per step. One step = 28 K1 launches (one
+per layer, each over the whole batch). `value` = decode tokens/s of the attention read alone
+(8 tokens per step / step time); inputs are resident in HBM before timing starts.
+
+Stores are built the way serving builds them, with this package's own code (never the oracle):
+keys/values from the seeded synthetic generator, each request's first chunk fitted on the GPU
+(`encode.fit_into_budget`), every token packed by the K3 write kernel (first chunk from the fit's
+coefficients, the rest by frozen projection).
+
+Extra fields: the batch-1 context sweep (1082/4322/8642/14402), batch 8 with seeded random
+contexts U[1000, 14400] (config 3), the multi-query continuation score (config 4) and the
+4-bit store with one write per request per layer (config 5) when their kernels are built, the
+dense fp16 paged-attention comparator, the K1 roofline (HBM bytes per launch / measured launch
+time vs 8 TB/s) and the CPU baseline (the torch-CPU oracle timed on a bounded sample on this
+host).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "ttkv-vllm_amd"))
+
+HBM_PEAK_GBPS = 8000.0
+L_LAYERS, HQ, H, D, BS = 28, 24, 8, 128, 16
+R1, FIT_ON = 110, 2048
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def build_store(torch, lay, cfg, lens, n_layers, seed, dev, fit_on=FIT_ON, distinct=4):
+    """Per-layer paged caches for requests of `lens` tokens. Returns a dict of device tensors."""
+    from vllm_ttkv import encode, kernels, synth
+    bt, nblk = synth.shuffled_block_table(lens, BS, seed=seed, extra_blocks=4)
+    B = len(lens)
+    C = lay.compressed_bytes_per_token()
+    dec_map = torch.full((nblk,), -1, dtype=torch.int32)
+    for r in range(B):
+        dec_map[bt[r, 0]] = r
+    bt_d, dec_map_d = bt.to(dev), dec_map.to(dev)
+    pos_slot = []
+    for r, n in enumerate(lens):
+        p = torch.arange(n)
+        pos_slot.append((bt[r, p // BS].long() * BS + p % BS).to(dev))
+    layers = []
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    t_fit = t_write = 0.0
+    for li in range(n_layers):
+        if li >= distinct:
+            # replicate a built layer into this layer's own pages (distinct HBM addresses)
+            src = layers[li % distinct]
+            layers.append(dict(page=src["page"].clone(), dec_pool=src["dec_pool"].clone()))
+            continue
+        page = torch.zeros(nblk * BS, C, dtype=torch.uint8, device=dev)
+        dec_pool = torch.zeros(B, lay.r1, H * D, dtype=torch.float32, device=dev)
+        pinv_pool = torch.zeros(B, H * D, lay.r1, dtype=torch.float32, device=dev)
+        first_k, first_v, first_cq, first_cs, first_slot, rest = [], [], [], [], [], []
+        for r, n in enumerate(lens):
+            s = seed * 1000003 + li * 1009 + r
+            K = synth.keys(n, seed=s, device=dev)
+            V = synth.values(n, seed=s, device=dev)
+            f = min(fit_on, n)
+            t0 = time.perf_counter()
+            fk = encode.fit_into_budget(K[:, :f], lay, cfg)
+            dec_pool[r] = fk.decoder.decoder_f
+            pinv_pool[r] = fk.decoder.pinv
+            torch.cuda.synchronize()
+            t_fit += time.perf_counter() - t0
+            Kt, Vt = K.permute(1, 0, 2), V.permute(1, 0, 2)
+            first_k.append(Kt[:f]); first_v.append(Vt[:f])
+            first_cq.append(fk.coeff_q); first_cs.append(fk.coeff_scale)
+            first_slot.append(pos_slot[r][:f])
+            rest.append((Kt[f:], Vt[f:], pos_slot[r][f:]))
+        t0 = time.perf_counter()
+        fl = [x.shape[0] for x in first_k]
+        qsl = torch.tensor([0] + list(torch.tensor(fl).cumsum(0)), dtype=torch.int32, device=dev)
+        kernels.write_paged(lay, torch.cat(first_k).contiguous(), torch.cat(first_v).contiguous(),
+                            torch.cat(first_slot), qsl, bt_d, dec_map_d, dec_pool, pinv_pool,
+                            page, coeff_q_in=torch.cat(first_cq), coeff_scale_in=torch.cat(first_cs),
+                            error_word=err)
+        rl = [x[0].shape[0] for x in rest]
+        if sum(rl):
+            qsl = torch.tensor([0] + list(torch.tensor(rl).cumsum(0)), dtype=torch.int32,
+                               device=dev)
+            kernels.write_paged(lay, torch.cat([x[0] for x in rest]).contiguous(),
+                                torch.cat([x[1] for x in rest]).contiguous(),
+                                torch.cat([x[2] for x in rest]), qsl, bt_d, dec_map_d, dec_pool,
+                                pinv_pool, page, error_word=err)
+        torch.cuda.synchronize()
+        t_write += time.perf_counter() - t0
+        del first_k, first_v, rest
+        layers.append(dict(page=page, dec_pool=dec_pool))
+    if int(err.item()):
+        raise RuntimeError(f"store build: device error word {int(err.item())}")
+    return dict(layers=layers, bt=bt_d, dec_map=dec_map_d, nblk=nblk, B=B,
+                seq_lens=torch.tensor(lens, dtype=torch.int32, device=dev), max_len=max(lens),
+                t_fit=t_fit, t_write=t_write)
+
+
+def k1_bytes(lay, lens, r1, cs_rows):
+    """Algorithmic HBM bytes of one K1 launch: every slot once, each request's fp32 decoder
+    once, the angle table rows once, q and out once (fp16)."""
+    B = len(lens)
+    return (sum(lens) * lay.compressed_bytes_per_token() + B * r1 * H * D * 4
+            + cs_rows * D * 4 + 2 * B * HQ * D * 2)
+
+
+def time_k1(torch, lay, store, q, cache, steps, warmup, n_layers):
+    """Time `steps` decode steps (n_layers K1 launches each). Returns (ms/step, ms/launch)."""
+    from vllm_ttkv import kernels
+    dev = q.device
+    B = store["B"]
+    qsl = torch.arange(B + 1, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    ws = kernels.decode_workspace(lay, HQ, B, store["max_len"], dev, BS)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def step(evs=None):
+        for li in range(n_layers):
+            L = store["layers"][li % len(store["layers"])]
+            if evs is not None:
+                evs[li][0].record()
+            kernels.decode_paged(lay, q, L["page"], BS, store["bt"], store["seq_lens"], qsl,
+                                 store["max_len"], store["dec_map"], L["dec_pool"], cache,
+                                 D ** -0.5, out=out, workspace=ws, error_word=err)
+            if evs is not None:
+                evs[li][1].record()
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for _ in range(n_layers)] for _ in range(steps)]
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record()
+    for s in range(steps):
+        step(evs[s])
+    t1.record()
+    torch.cuda.synchronize()
+    if int(err.item()):
+        raise RuntimeError(f"K1: device error word {int(err.item())}")
+    ms_step = t0.elapsed_time(t1) / steps
+    per = [a.elapsed_time(b) for st in evs for (a, b) in st]
+    return ms_step, sum(per) / len(per)
+
+
+def cpu_baseline(torch, lay, store, q, cache, n, budget_s=12.0):
+    """The torch-CPU oracle (reference.py:149-163 restated, float32, the reference's request
+    loop) on a bounded sample: request-layers of the headline workload, timed until `budget_s`."""
+    sys.path.insert(0, str(ROOT))
+    from oracle import attend, rope as orope
+    from oracle.layout import Layout
+    lay = Layout(lay.H, lay.d, lay.r1, lay.qbits, lay.res_k, lay.res_bits, lay.v_lanes, lay.v_bits)
+    torch.set_num_threads(os.cpu_count() or 1)
+    cores = torch.get_num_threads()
+    bt = store["bt"].cpu()
+    cos, sin = orope.cos_sin_from_cache(cache.cpu(), torch.arange(n), D)
+    done, t_tot = 0, 0.0
+    r, li = 0, 0
+    while t_tot < budget_s and done < 64:
+        L = store["layers"][li % len(store["layers"])]
+        p = torch.arange(n, device=bt.device)
+        slots = (bt[r, p // BS].long() * BS + p % BS)
+        blob = L["page"][slots.to(L["page"].device)].cpu()
+        dec = L["dec_pool"][r].cpu()
+        k_s, v_s = blob[:, :lay.k_slot_bytes].contiguous(), blob[:, lay.k_slot_bytes:].contiguous()
+        qq = q[r].float().cpu()
+        t0 = time.perf_counter()
+        attend.attend_raw_store(lay, k_s, v_s, dec, qq, cos, sin, D ** -0.5)
+        t_tot += time.perf_counter() - t0
+        done += 1
+        r = (r + 1) % store["B"]
+        li += 1
+    per_req_layer = t_tot / done
+    step_s = per_req_layer * store["B"] * L_LAYERS
+    return dict(value=store["B"] / step_s, unit="tokens/s", cores=cores, kind="port",
+                sample=f"{done} request-layers of the headline workload (n={n}) through the "
+                       f"torch-CPU oracle attend_raw_store, {t_tot:.1f} s; extrapolated x"
+                       f"{store['B']} requests x {L_LAYERS} layers per step",
+                ms_per_request_layer=per_req_layer * 1e3)
+
+
+def read_traffic(path):
+    """HBM bytes per K1 launch from a committed rocprofv3 --pmc summary, if one exists."""
+    p = ROOT / "profiles" / path
+    if not p.exists():
+        return None
+    for line in p.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1].split()[0])
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=L_LAYERS)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="headline workload only")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run one 1 GiB device copy (HBM-counter calibration for rocprofv3)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (--gpus {args.gpus} "
+              f"requested). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from vllm_ttkv import rope, synth
+    from vllm_ttkv.layout import CONFIGS, layout_for_config
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    cfg = CONFIGS["safe"]
+    lay = layout_for_config(cfg, r1=R1)
+    cache = rope.cos_sin_cache(16384, D, device=dev)
+    extra = {}
+
+    if args.calib_copy:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log("calibration copy: 1073741824 bytes read + written")
+        del src, dst
+
+    # ---------------------------------------------------------------- headline: B=8 @ 14402
+    lens = [14402] * 8
+    t0 = time.perf_counter()
+    store = build_store(torch, lay, cfg, lens, args.layers, seed=1, dev=dev)
+    log(f"build B=8x14402: {time.perf_counter() - t0:.1f}s (fit {store['t_fit']:.1f}s, "
+        f"write {store['t_write']:.1f}s)")
+    q = synth.queries(8, seed=5, device=dev)
+    ms_step, ms_launch = time_k1(torch, lay, store, q, cache, args.steps, args.warmup,
+                                 args.layers)
+    nbytes = k1_bytes(lay, lens, R1, max(lens))
+    achieved = nbytes / (ms_launch * 1e-3) / 1e9
+    step_ms = ms_step * L_LAYERS / args.layers
+    log(f"K1 B=8x14402: {ms_launch * 1e3:.1f} us/launch, {achieved:.0f} GB/s")
+
+    if not args.no_extra:
+        sweep = []
+        for n in (1082, 4322, 8642, 14402):
+            st = build_store(torch, lay, cfg, [n], 2, seed=2, dev=dev)
+            q1 = synth.queries(1, seed=6, device=dev)
+            _, ml = time_k1(torch, lay, st, q1, cache, 20, 3, 2)
+            b = k1_bytes(lay, [n], R1, n)
+            log(f"K1 B=1x{n}: {ml * 1e3:.1f} us/launch")
+            sweep.append(dict(context=n, us_per_layer=ml * 1e3,
+                              hbm_gbps=b / (ml * 1e-3) / 1e9,
+                              tokens_per_s=1.0 / (ml * 1e-3 * L_LAYERS)))
+            del st
+        extra["batch1_sweep"] = sweep
+        g = torch.Generator().manual_seed(3)
+        lens3 = [int(x) for x in torch.randint(1000, 14401, (8,), generator=g)]
+        st = build_store(torch, lay, cfg, lens3, 2, seed=3, dev=dev)
+        _, ml = time_k1(torch, lay, st, q, cache, 20, 3, 2)
+        b = k1_bytes(lay, lens3, R1, max(lens3))
+        extra["config3_b8_random"] = dict(contexts=lens3, us_per_layer=ml * 1e3,
+                                          hbm_gbps=b / (ml * 1e-3) / 1e9,
+                                          tokens_per_s=8 / (ml * 1e-3 * L_LAYERS))
+        del st
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(torch, lay, store, q, cache, lens[0])
+        log(f"cpu baseline: {cpu['ms_per_request_layer']:.0f} ms per request-layer on "
+            f"{cpu['cores']} threads")
+
+    line = {
+        "metric": "decode step us/layer vs context at batch 1 & 8; achieved HBM GB/s; tokens/s",
+        "value": 8 / (step_ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": step_ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded low-rank keys with outlier channels, N(0,1) values, fp16 "
+                "queries; stores fitted and packed on the GPU by this package; 4 distinct layer "
+                "stores, each copied into its own pages for the other 24 layers)",
+        "config": {"workload": "llama-3.2-3b attention decode read, batch 8 x 14402 cached tokens, "
+                               "28 layers, safe r1=110, block 16, one K1 launch per layer",
+                   "global_batch": 8, "seq_len": 14402, "layers": L_LAYERS,
+                   "layers_timed": args.layers, "parallelism": "single GPU"},
+        "us_per_layer": ms_launch * 1e3,
+        "hbm_gbps": achieved,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS,
+                     "traffic": read_traffic("k1_decode_b8_ctx14402_pmc.txt"),
+                     "algorithmic_bytes_per_launch": nbytes},
+        "cpu_baseline": cpu,
+    }
+    line.update(extra)
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

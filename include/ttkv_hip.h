@@ -58,7 +58,7 @@ int64_t ttkv_blob_bytes(const ttkv_layout* lay);
 /* Workspace bytes `ttkv_decode_paged` needs for this batch shape. The workspace must be
  * zero-filled before its first use; every call leaves its counter region zero again. */
 int64_t ttkv_decode_workspace_bytes(const ttkv_layout* lay, int32_t num_heads,
-                                    int32_t num_reqs, int32_t max_seq_len);
+                                    int32_t num_reqs, int32_t max_seq_len, int32_t block_size);
 
 /* K1 -- fused paged decode read, ONE launch for the whole batch of decode requests.
  *

@@ -44,10 +44,11 @@ int64_t ttkv_blob_bytes(const ttkv_layout* lay) {
 }
 
 int64_t ttkv_decode_workspace_bytes(const ttkv_layout* lay, int32_t num_heads, int32_t num_reqs,
-                                    int32_t max_seq_len) {
+                                    int32_t max_seq_len, int32_t block_size) {
   Geom g;
   if (!make_geom(lay, &g) || num_heads <= 0 || num_heads % g.H || num_reqs < 0) return -1;
-  return decode_workspace_bytes(g, num_heads / g.H, num_reqs, max_seq_len);
+  if (block_size <= 0) return -1;
+  return decode_workspace_bytes(g, num_heads / g.H, num_reqs, max_seq_len, block_size);
 }
 
 int ttkv_decode_paged(const ttkv_layout* lay, int32_t num_heads, float scale, const void* query,

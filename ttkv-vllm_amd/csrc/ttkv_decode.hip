@@ -2,30 +2,34 @@
 // layer for the whole decode batch. gfx950 / CDNA4.
 //
 // Work item = (request r, KV head h, token chunk c). A 256-thread workgroup (4 waves) walks its
-// chunk in 64-token tiles:
-//   stage   : coefficient bytes -> fp16 MFMA B-fragments in LDS (int8 exact in fp16); this head's
-//             K and V rows -> LDS, realigned to 4 bytes.
-//   decode  : one thread per half row (64 lanes): bitmap + MSB-first code stream -> dense values.
-//             K: (code - 2^(b-1)) * ruler as fp32; V: (code - 2^(b-1)) as fp16 (+ fp32 ruler).
+// chunk in 64-token tiles with the next tile's raw bytes prefetched into registers while the
+// current one is computed (global loads in flight across the whole tile):
+//   commit  : prefetched bytes -> LDS: coefficients as fp16 MFMA B-fragments (int8 is exact in
+//             fp16), this head's K and V rows realigned to 4 bytes.
+//   decode  : one thread per half row. Per bitmap byte, the next 8 codes are cut from the MSB-first
+//             stream, spread one per byte and scattered to their lanes with one v_perm driven by a
+//             256-entry selector table; lanes outside the bitmap get the zero code 2^(b-1).
+//             Output: one code byte per (token, lane) for K and for V.
 //   recon   : K_pre^T[128 x 16 tokens] = Dec^T[128 x r1] * coeff^T[r1 x 16] on MFMA 16x16x32 f16.
 //             The decoder is split hi + lo in fp16 and both halves are applied; decoder_f values
 //             are int8 * fp16 row rulers (<= 19 significant bits), so hi + lo is exact and the
 //             products are exact in the fp32 accumulator. Wave w owns dims {16w..16w+15} and
 //             {64+16w..64+16w+15}, so each RoPE pair (j, j+64) sits in one lane and the decoder
 //             fragments stay in registers for the whole chunk.
-//   rope+qk : k = cs * acc + residual; rotate by the row's own absolute position; fp32 dot with
-//             the G query heads of this KV head; partial dots reduced across lanes and waves.
-//   softmax : online (running max / sum), base-2 exponent with scale*log2(e) folded in.
-//   P.V     : o[p] += P[p,t] * ruler_v[t] * vcode[t] in fp32 (v_fma_mix with fp16 codes).
+//   rope+qk : k = cs * acc + ruler * (code - 2^(b-1)); rotate by the row's absolute position; fp32
+//             dot with the G query heads (pre-scaled by scale * log2 e); partial dots reduced
+//             across the 4 lane groups and the 4 waves.
+//   softmax : online, base 2, evaluated redundantly by every wave (no extra barrier).
+//   P.V     : o[p] += P[p,t] * ruler_v[t] * code; the 2^(b-1) offset is removed once at the end
+//             through the running sum of P * ruler_v.
 // Chunks of one (r, h) are combined in the same launch by the last workgroup to finish
 // (device-scope fence + counter), which also resets the counter to zero.
 //
 // Reference semantics: vllm_ttkv/reference.py:63-163 (dense K, per-row RoPE, scores, softmax,
 // V readout), vllm_ttkv/impl.py:511-540 (scale then softmax), decode.py:54-122 (vLLM cos/sin
-// half layout), decode.py:307-339 (slot = block_table[r, t/bs]*bs + t%bs).
+// half layout), decode.py:307-339 (slot = block_table[r, t/bs]*bs + t%bs); bit format
+// codec/ttkv_packed_cache.py:50-100, 138-167, 247-271.
 #include <math.h>
-
-#include <type_traits>
 
 #include "ttkv_common.h"
 
@@ -34,9 +38,9 @@ namespace ttkv {
 constexpr int kTile = 64;
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
-constexpr int kKresStride = 132;   // fp32 per K-residual row in LDS (bank stagger)
-constexpr int kVStride = 136;      // fp16 per V row in LDS
-constexpr int kRawDw = 15;         // dwords per raw head row in LDS (row + window slack)
+constexpr int kRawDw = 16;      // dwords per staged head row (49-50 B rows + window slack)
+constexpr int kCodeStride = 144;  // bytes per code row (128 + bank stagger)
+constexpr int kSegMax = 260;    // block ids staged per chunk
 
 struct DecodeArgs {
   Geom g;
@@ -73,22 +77,18 @@ template <int KSTEPS>
 struct DecodeSmem {
   static constexpr int kCoefStride = KSTEPS * 32 + 8;  // fp16 per token row
   _Float16 coef[kTile][kCoefStride];
-  float kres[kTile][kKresStride];
-  _Float16 vval[kTile][kVStride];
-  union {
-    struct {
-      uint32_t rawk[kTile][kRawDw];
-      uint32_t rawv[kTile][kRawDw];
-    } raw;
-    struct {
-      float spart[kWaves][kTile][8];
-      float pw[8][kTile];
-      float alpha[8];
-      float m[8], l[8];
-    } sm;
-  } u;
+  uint32_t rawk[kTile][kRawDw];
+  uint32_t rawv[kTile][kRawDw];
+  uint8_t kcode[kTile][kCodeStride];
+  uint8_t vcode[kTile][kCodeStride];
+  float spart[kWaves][kTile][8];  // per wave partial scores (G <= 8)
+  uint2 lut[256];
+  int32_t seg[kSegMax];
   float cs[kTile];
+  float krul[kTile];
   float vrul[kTile];
+  float qs[8][kD];  // this KV head's query rows, pre-scaled by scale * log2(e)
+  float m[8], l[8];
   int is_last;
 };
 
@@ -102,58 +102,200 @@ __device__ __forceinline__ void i8x4_to_f16(uint32_t x, uint32_t& p01, uint32_t&
   p23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, hi) - bias);
 }
 
-// Decode dims [64*half, 64*half+64) of one head row held in LDS (bitmap at byte 0, code stream
-// at byte 16, fp16 ruler after the stream). Calls emit(dim_base, codes[8]) per bitmap byte with
-// the raw code of every lane (2^(BITS-1) for lanes not in the bitmap, so value 0).
-template <int BITS, typename Emit>
-__device__ __forceinline__ void decode_half_row(const uint8_t* row, int half, Emit emit) {
-  constexpr uint32_t OFF = 1u << (BITS - 1);
-  int rank = 0;
-  if (half) {
-    const uint32_t* bw = (const uint32_t*)row;
-    rank = __builtin_popcount(bw[0]) + __builtin_popcount(bw[1]);
+__device__ __forceinline__ uint32_t bswap32(uint32_t x) {
+  return __builtin_amdgcn_perm(0u, x, 0x00010203u);
+}
+
+// Spread the 8 codes at the top of a 32-bit MSB-first window (code k at bits 31-B*k-B+1 ..
+// 31-B*k) into bytes: e0 = codes 0..3, e1 = codes 4..7 (byte i of e0 = code i).
+template <int BITS>
+__device__ __forceinline__ void spread8(uint32_t w, uint32_t& e0, uint32_t& e1) {
+  if constexpr (BITS == 4) {
+    // nibbles: code k at bits 28-4k. bytes of (w >> 4) & 0x0f0f0f0f hold codes 6,4,2,0 at bytes
+    // 0..3; bytes of w & 0x0f0f0f0f hold codes 7,5,3,1. Interleave with v_perm.
+    const uint32_t ev = (w >> 4) & 0x0f0f0f0fu;  // byte0 = c6, byte1 = c4, byte2 = c2, byte3 = c0
+    const uint32_t od = w & 0x0f0f0f0fu;         // byte0 = c7, byte1 = c5, byte2 = c3, byte3 = c1
+    // e0 = [c0, c1, c2, c3]: c0 = ev.b3, c1 = od.b3, c2 = ev.b2, c3 = od.b2  (S0 = ev: 4-7, S1 = od)
+    e0 = __builtin_amdgcn_perm(ev, od, 0x02060307u);
+    // e1 = [c4, c5, c6, c7]: c4 = ev.b1, c5 = od.b1, c6 = ev.b0, c7 = od.b0
+    e1 = __builtin_amdgcn_perm(ev, od, 0x00040105u);
+  } else {
+    e0 = __builtin_amdgcn_ubfe(w, 32 - BITS, BITS) |
+         (__builtin_amdgcn_ubfe(w, 32 - 2 * BITS, BITS) << 8) |
+         (__builtin_amdgcn_ubfe(w, 32 - 3 * BITS, BITS) << 16) |
+         (__builtin_amdgcn_ubfe(w, 32 - 4 * BITS, BITS) << 24);
+    e1 = __builtin_amdgcn_ubfe(w, 32 - 5 * BITS, BITS) |
+         (__builtin_amdgcn_ubfe(w, 32 - 6 * BITS, BITS) << 8) |
+         (__builtin_amdgcn_ubfe(w, 32 - 7 * BITS, BITS) << 16) |
+         (__builtin_amdgcn_ubfe(w, 32 - 8 * BITS, BITS) << 24);
   }
+}
+
+// Decode dims [64*half, 64*half+64) of one staged head row (bitmap dwords 0..3, MSB-first code
+// stream from dword 4) into one code byte per lane at dst[0..63]; lanes outside the bitmap get
+// 2^(BITS-1). `lut[B]` holds the v_perm selectors that move the byte-spread codes of bitmap
+// byte B onto its set lanes (0x0c -> zero byte for the others).
+template <int BITS>
+__device__ __forceinline__ void decode_half_row(const uint32_t* row, int half, const uint2* lut,
+                                                uint8_t* dst) {
+  constexpr uint32_t OFFB = (1u << (BITS - 1)) * 0x01010101u;
+  // XOR pattern that flips the top bit of each of 8 codes at the top of the window: a kept
+  // code c becomes c ^ 2^(b-1), so after the zero-filling scatter a final XOR restores c and
+  // turns the zero bytes into the zero code 2^(b-1).
+  constexpr uint32_t FLIP = BITS == 4 ? 0x88888888u : 0x92492400u;
+  int rank = 0;
+  if (half) rank = __builtin_popcount(row[0]) + __builtin_popcount(row[1]);
+  const uint32_t bm0 = row[2 * half], bm1 = row[2 * half + 1];
+  const uint32_t* st = row + 4;
 #pragma unroll
   for (int m = 0; m < 8; ++m) {
-    const uint32_t B = row[8 * half + m];
+    const uint32_t B = __builtin_amdgcn_ubfe(m < 4 ? bm0 : bm1, 8 * (m & 3), 8);
     const int bp = rank * BITS;
-    const uint8_t* s = row + 16 + (bp >> 3);
-    // Up to 8 codes (8*BITS bits) starting (bp & 7) bits into the first byte: 31 bits for
-    // 3-bit codes fit a 32-bit window, 39 bits for 4-bit codes need a 64-bit one.
-    typedef typename std::conditional<(8 * BITS + 7 > 32), uint64_t, uint32_t>::type win_t;
-    constexpr int WB = 8 * (int)sizeof(win_t);
-    win_t w = 0;
-#pragma unroll
-    for (int b = 0; b < (int)sizeof(win_t); ++b) w |= (win_t)s[b] << (WB - 8 - 8 * b);
-    w <<= (bp & 7);
-    uint32_t codes[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const bool present = (B >> (7 - k)) & 1u;
-      const uint32_t c = (uint32_t)(w >> (WB - BITS));
-      codes[k] = present ? c : OFF;
-      w = present ? (win_t)(w << BITS) : w;
-    }
-    emit(64 * half + 8 * m, codes);
+    const int wi = bp >> 5;
+    const uint64_t pair = ((uint64_t)bswap32(st[wi]) << 32) | (uint64_t)bswap32(st[wi + 1]);
+    const uint32_t w = (uint32_t)((pair << (bp & 31)) >> 32) ^ FLIP;
+    uint32_t e0, e1;
+    spread8<BITS>(w, e0, e1);
+    const uint2 sel = lut[B];
+    uint2 out;
+    out.x = __builtin_amdgcn_perm(e1, e0, sel.x) ^ OFFB;
+    out.y = __builtin_amdgcn_perm(e1, e0, sel.y) ^ OFFB;
+    *(uint2*)(dst + 8 * m) = out;
     rank += __builtin_popcount(B);
   }
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+// Cross-lane helpers on DPP and the gfx950 permlane swaps (VALU ops, no LDS round trip).
+__device__ __forceinline__ float dpp_f(float v, int ctrl_sel) {
+  const int iv = __builtin_bit_cast(int, v);
+  int r = 0;
+  switch (ctrl_sel) {  // dpp control must be a constant
+    case 0: r = __builtin_amdgcn_update_dpp(0, iv, 0xB1, 0xF, 0xF, false); break;   // xor 1
+    case 1: r = __builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xF, 0xF, false); break;   // xor 2
+    case 2: r = __builtin_amdgcn_update_dpp(0, iv, 0x124, 0xF, 0xF, false); break;  // row_ror 4
+    default: r = __builtin_amdgcn_update_dpp(0, iv, 0x128, 0xF, 0xF, false); break; // row_ror 8
+  }
+  return __builtin_bit_cast(float, r);
+}
+// Sum / max over the 16 lanes of each row (every lane gets its row's result).
+__device__ __forceinline__ float row_sum(float v) {
+  v += dpp_f(v, 0);
+  v += dpp_f(v, 1);
+  v += dpp_f(v, 2);
+  v += dpp_f(v, 3);
   return v;
 }
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+__device__ __forceinline__ float row_max(float v) {
+  v = fmaxf(v, dpp_f(v, 0));
+  v = fmaxf(v, dpp_f(v, 1));
+  v = fmaxf(v, dpp_f(v, 2));
+  v = fmaxf(v, dpp_f(v, 3));
   return v;
+}
+// Lanes l and l^16 / l^32 exchanged: returns (value of rows {0,2}, value of rows {1,3}) etc.
+__device__ __forceinline__ void swap16(float v, float& a, float& b) {
+  const int iv = __builtin_bit_cast(int, v);
+  const auto r = __builtin_amdgcn_permlane16_swap(iv, iv, false, false);
+  a = __builtin_bit_cast(float, (int)r[0]);  // rows [0,0,2,2]
+  b = __builtin_bit_cast(float, (int)r[1]);  // rows [1,1,3,3]
+}
+__device__ __forceinline__ void swap32(float v, float& a, float& b) {
+  const int iv = __builtin_bit_cast(int, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(iv, iv, false, false);
+  a = __builtin_bit_cast(float, (int)r[0]);  // halves [lo, lo]
+  b = __builtin_bit_cast(float, (int)r[1]);  // halves [hi, hi]
+}
+// Sum over lanes {l, l^16, l^32, l^48} (the four rows at the same row position).
+__device__ __forceinline__ float cross_row_sum(float v) {
+  float a, b;
+  swap16(v, a, b);
+  v = a + b;
+  swap32(v, a, b);
+  return a + b;
+}
+__device__ __forceinline__ float cross_row_max(float v) {
+  float a, b;
+  swap16(v, a, b);
+  v = fmaxf(a, b);
+  swap32(v, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float wave_max(float v) { return cross_row_max(row_max(v)); }
+__device__ __forceinline__ float wave_sum(float v) { return cross_row_sum(row_sum(v)); }
+// Broadcast row `nb` (lanes 16nb..16nb+15) of v to all four rows: out[nb].
+__device__ __forceinline__ void bcast_rows(float v, float out[4]) {
+  float r02, r13, a, b;
+  swap16(v, r02, r13);      // r02 = rows [0,0,2,2], r13 = rows [1,1,3,3]
+  swap32(r02, a, b);        // a = [r0 x4], b = [r2 x4]
+  out[0] = a;
+  out[2] = b;
+  swap32(r13, a, b);        // a = [r1 x4], b = [r3 x4]
+  out[1] = a;
+  out[3] = b;
+}
+
+// Raw bytes of one token prefetched by one of its 4 threads, plus this lane's RoPE angles for
+// the tile (4 tokens x 4 dims of cos and of sin), so that no global load is issued between the
+// prefetch and its use (vmcnt retires in order).
+template <int KSTEPS>
+struct Prefetch {
+  float4v cosv[4], sinv[4];
+  uint32_t coef[KSTEPS * 2];  // KSTEPS*8 coefficient bytes
+  uint32_t krow[5], vrow[5];  // 5 source dwords (4 output dwords + funnel)
+  uint32_t rul;               // coefficient ruler bits when outside the coefficient window
+};
+
+template <int KSTEPS>
+__device__ __forceinline__ void prefetch_angles(Prefetch<KSTEPS>& P, const float* cs_cache, int tt,
+                                                int ntile, int n, int dl) {
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) {
+    const int tok = 16 * nb + n;
+    const int pos = tok < ntile ? tt + tok : tt;
+    P.cosv[nb] = *(const float4v*)&cs_cache[(int64_t)pos * kD + dl];
+    P.sinv[nb] = *(const float4v*)&cs_cache[(int64_t)pos * kD + 64 + dl];
+  }
+}
+
+template <int KSTEPS>
+__device__ __forceinline__ void prefetch(Prefetch<KSTEPS>& P, const uint8_t* base, int part,
+                                         const Geom& g, int k_row_off, int v_row_off) {
+  constexpr int kCPP = KSTEPS * 8;
+  if (!base) {
+#pragma unroll
+    for (int i = 0; i < KSTEPS * 2; ++i) P.coef[i] = 0u;
+#pragma unroll
+    for (int i = 0; i < 5; ++i) P.krow[i] = P.vrow[i] = 0u;
+    P.rul = 0u;
+    return;
+  }
+  const uint32_t* cs = (const uint32_t*)(base + part * kCPP);
+#pragma unroll
+  for (int i = 0; i < KSTEPS * 2; ++i) P.coef[i] = cs[i];
+  {
+    const uintptr_t A = (uintptr_t)(base + k_row_off);
+    const uint32_t* src = (const uint32_t*)(A & ~(uintptr_t)3);
+    const int nsrc = (int)((A & 3) + g.k_row + 3) >> 2;
+#pragma unroll
+    for (int i = 0; i < 5; ++i) P.krow[i] = (part * 4 + i < nsrc) ? src[part * 4 + i] : 0u;
+  }
+  {
+    const uintptr_t A = (uintptr_t)(base + v_row_off);
+    const uint32_t* src = (const uint32_t*)(A & ~(uintptr_t)3);
+    const int nsrc = (int)((A & 3) + g.v_row + 3) >> 2;
+#pragma unroll
+    for (int i = 0; i < 5; ++i) P.vrow[i] = (part * 4 + i < nsrc) ? src[part * 4 + i] : 0u;
+  }
+  P.rul = 0u;
+  if (part == 0 && g.coeff_bytes + 2 > KSTEPS * 32)
+    P.rul = (uint32_t)base[g.coeff_bytes] | ((uint32_t)base[g.coeff_bytes + 1] << 8);
 }
 
 template <int G, int RB, int VB, int KSTEPS>
 __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   DecodeSmem<KSTEPS>& S = *reinterpret_cast<DecodeSmem<KSTEPS>*>(smem_raw);
+  constexpr int kCPP = KSTEPS * 8;
   const Geom& g = a.g;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -171,13 +313,16 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   const int r = rc / a.max_chunks;
   const int c = rc % a.max_chunks;
   if (r >= a.num_reqs) return;
-  int seq = a.seq_lens[r];
+  // independent per-request loads issued together (each is a full memory round trip)
+  const int seq_raw = a.seq_lens[r];
+  const int64_t qrow = a.qsl[r];
+  const int blk0 = a.bt[(int64_t)r * a.bt_row_stride];
+  int seq = seq_raw;
   if (seq > a.max_seq) {  // the host sized the grid, workspace and table checks from max_seq
     if (tid == 0 && c == 0) atomicOr(a.err, TTKV_ERR_SEQ_LEN);
     seq = a.max_seq;
   }
   const int n_chunks = (seq + a.chunk - 1) / a.chunk;
-  const int64_t qrow = a.qsl[r];
   if (c >= n_chunks) {
     if (seq <= 0 && c == 0) {  // empty context: the reference's einsum over zero rows is 0
       for (int i = tid; i < G * kD; i += kThreads)
@@ -189,7 +334,6 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   const int t1 = min(seq, t0 + a.chunk);
 
   // Decoder slot via the device registry keyed by the request's first block.
-  const int blk0 = a.bt[(int64_t)r * a.bt_row_stride];
   int dslot = -1;
   if (blk0 >= 0 && blk0 < a.num_blocks) dslot = a.dec_map[blk0];
   if (dslot < 0 || dslot >= a.n_dec_slots) {
@@ -199,6 +343,55 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
         store_act(a.out, a.out_dtype, qrow * a.out_row_stride + (int64_t)(h * G) * kD + i, NAN);
     return;
   }
+
+  // ---- selector table for the code scatter, and this chunk's block ids
+  {
+    const uint32_t B = (uint32_t)tid;
+    uint32_t s0 = 0, s1 = 0, idx = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const bool present = (B >> (7 - k)) & 1u;
+      const uint32_t sel = present ? idx : 0x0cu;
+      idx += present;
+      if (k < 4) s0 |= sel << (8 * k);
+      else s1 |= sel << (8 * (k - 4));
+    }
+    S.lut[tid] = make_uint2(s0, s1);
+  }
+  const int bfirst = t0 / a.block_size;
+  const int nseg = (t1 - 1) / a.block_size - bfirst + 1;
+  for (int i = tid; i < nseg; i += kThreads) {
+    int blk = a.bt[(int64_t)r * a.bt_row_stride + bfirst + i];
+    if (blk < 0 || blk >= a.num_blocks) {
+      atomicOr(a.err, TTKV_ERR_BAD_BLOCK);
+      blk = -1;
+    }
+    S.seg[i] = blk;
+  }
+
+  const int k_row_off = g.k_field + h * g.k_row;
+  const int v_row_off = g.k_slot + h * g.v_row;
+  const int ptok = tid >> 2;  // token / part handled by this thread in prefetch + commit
+  const int part = tid & 3;
+  const int k_sh = (k_row_off & 3), v_sh = (v_row_off & 3);  // slot bases are 16-aligned
+  const int dl = 16 * wv + 4 * gq;
+  __syncthreads();  // seg
+
+  auto slot_base = [&](int tt) -> const uint8_t* {
+    if (ptok >= min(kTile, t1 - tt)) return nullptr;
+    const int pos = tt + ptok;
+    const int bi = pos / a.block_size;
+    const int blk = S.seg[bi - bfirst];
+    if (blk < 0) return nullptr;
+    const int64_t slot = (int64_t)blk * a.block_size + (pos - bi * a.block_size);
+    if (slot >= a.n_slots) return nullptr;
+    return a.page + slot * a.slot_stride;
+  };
+
+  // first tile's bytes in flight while the decoder is loaded
+  Prefetch<KSTEPS> P;
+  prefetch<KSTEPS>(P, slot_base(t0), part, g, k_row_off, v_row_off);
+  prefetch_angles<KSTEPS>(P, a.cs_cache, t0, min(kTile, t1 - t0), n, dl);
 
   // ---- decoder fragments (A operand, M = dims, K = r1), hi/lo fp16, resident in registers.
   const int HD = g.H * kD;
@@ -220,115 +413,89 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
     }
   }
 
-  // ---- query: this lane's 8 dims for each of the G heads of KV head h.
-  const int dl = 16 * wv + 4 * gq;
-  float ql[G][4], qh[G][4];
-#pragma unroll
-  for (int p = 0; p < G; ++p) {
-    const int64_t qb = qrow * a.q_row_stride + (int64_t)(h * G + p) * kD;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      ql[p][i] = load_act(a.q, a.q_dtype, qb + dl + i);
-      qh[p][i] = load_act(a.q, a.q_dtype, qb + 64 + dl + i);
-    }
-  }
+  // ---- query rows of the G heads of KV head h, pre-scaled by scale * log2(e), into LDS.
+  for (int i = tid; i < G * kD; i += kThreads)
+    S.qs[i / kD][i % kD] =
+        load_act(a.q, a.q_dtype, qrow * a.q_row_stride + (int64_t)(h * G) * kD + i) * a.scale_log2;
 
-  float o[G][8];
-#pragma unroll
-  for (int p = 0; p < G; ++p)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o[p][i] = 0.f;
-  float m_run[G], l_run[G];  // meaningful in wave 0
+  float o[G][8], psum[G], m_run[G], l_run[G];
 #pragma unroll
   for (int p = 0; p < G; ++p) {
+    psum[p] = 0.f;
     m_run[p] = -INFINITY;
     l_run[p] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[p][i] = 0.f;
   }
 
-  constexpr int kCoefPerPart = KSTEPS * 8;  // coefficients staged per thread (4 threads/token)
-  const int k_row_off = g.k_field + h * g.k_row;
-  const int v_row_off = g.k_slot + h * g.v_row;
 
   for (int tt = t0; tt < t1; tt += kTile) {
     const int ntile = min(kTile, t1 - tt);
-    // ---------------------------------------------------------------- stage
+    // ---------------------------------------------------------------- commit prefetched bytes
     {
-      const int tok = tid >> 2;
-      const int part = tid & 3;
-      const uint8_t* base = nullptr;
-      if (tok < ntile) {
-        const int pos = tt + tok;
-        const int bi = pos / a.block_size;
-        const int blk = a.bt[(int64_t)r * a.bt_row_stride + bi];
-        const int64_t slot = (int64_t)blk * a.block_size + (pos - bi * a.block_size);
-        if (blk < 0 || blk >= a.num_blocks || slot >= a.n_slots) {
-          if (part == 0) atomicOr(a.err, TTKV_ERR_BAD_BLOCK);
-        } else {
-          base = a.page + slot * a.slot_stride;
-        }
+      uint32_t* cdst = (uint32_t*)&S.coef[ptok][part * kCPP];
+#pragma unroll
+      for (int dw = 0; dw < KSTEPS * 2; ++dw) {
+        const int b0 = part * kCPP + dw * 4;
+        uint32_t x = P.coef[dw];
+        const int keep = g.r1 - b0;  // bytes of this dword that are coefficients
+        if (keep <= 0) x = 0;
+        else if (keep < 4) x &= (1u << (8 * keep)) - 1u;
+        uint32_t p01, p23;
+        i8x4_to_f16(x, p01, p23);
+        cdst[2 * dw] = p01;
+        cdst[2 * dw + 1] = p23;
       }
-      uint32_t* cdst = (uint32_t*)&S.coef[tok][part * kCoefPerPart];
-      if (base) {
-        const uint32_t* csrc = (const uint32_t*)(base + part * kCoefPerPart);
+      // coefficient ruler (fp16 LE at byte coeff_bytes)
+      const int rb = g.coeff_bytes;
+      if (rb + 2 <= KSTEPS * 32) {
+        if (part == rb / kCPP) {
+          const int off = rb - part * kCPP;
+          const int dw = off >> 2, sh = off & 3;
+          uint32_t lo = 0u, hi = 0u;  // select without dynamic register indexing
 #pragma unroll
-        for (int dw = 0; dw < kCoefPerPart / 4; ++dw) {
-          const int b0 = part * kCoefPerPart + dw * 4;
-          uint32_t x = csrc[dw];
-          const int keep = g.r1 - b0;  // bytes of this dword that are coefficients
-          if (keep <= 0) x = 0;
-          else if (keep < 4) x &= (1u << (8 * keep)) - 1u;
-          uint32_t p01, p23;
-          i8x4_to_f16(x, p01, p23);
-          cdst[2 * dw] = p01;
-          cdst[2 * dw + 1] = p23;
+          for (int i = 0; i < KSTEPS * 2; ++i) {
+            lo = (i == dw) ? P.coef[i] : lo;
+            hi = (i == dw + 1) ? P.coef[i] : hi;
+          }
+          const uint32_t v = sh ? __builtin_amdgcn_alignbyte(hi, lo, sh) : lo;
+          S.cs[ptok] = f16_bits_to_float(v & 0xffffu);
         }
-        if (part == 0) {
-          const uint32_t lo = base[g.coeff_bytes], hi = base[g.coeff_bytes + 1];
-          S.cs[tok] = f16_bits_to_float(lo | (hi << 8));
-        }
-        copy_row_realign(base + k_row_off, g.k_row, S.u.raw.rawk[tok], part, 4);
-        copy_row_realign(base + v_row_off, g.v_row, S.u.raw.rawv[tok], part, 4);
-      } else {
+      } else if (part == 0) {
+        S.cs[ptok] = f16_bits_to_float(P.rul);
+      }
 #pragma unroll
-        for (int dw = 0; dw < kCoefPerPart / 2; ++dw) cdst[dw] = 0u;
-        if (part == 0) S.cs[tok] = 0.f;
-        for (int dw = part; dw < kRawDw; dw += 4) {
-          S.u.raw.rawk[tok][dw] = 0u;
-          S.u.raw.rawv[tok][dw] = 0u;
-        }
+      for (int i = 0; i < 4; ++i) {
+        S.rawk[ptok][part * 4 + i] =
+            k_sh ? __builtin_amdgcn_alignbyte(P.krow[i + 1], P.krow[i], k_sh) : P.krow[i];
+        S.rawv[ptok][part * 4 + i] =
+            v_sh ? __builtin_amdgcn_alignbyte(P.vrow[i + 1], P.vrow[i], v_sh) : P.vrow[i];
       }
     }
+    // ---------------------------------------------------------------- prefetch the next tile
+    if (tt + kTile < t1) prefetch<KSTEPS>(P, slot_base(tt + kTile), part, g, k_row_off, v_row_off);
     __syncthreads();
     // ---------------------------------------------------------------- decode (thread = half row)
     {
-      const int kind = tid >> 7;          // waves 0,1: K rows; waves 2,3: V rows
+      const int kind = tid >> 7;  // waves 0,1: K rows; waves 2,3: V rows
       const int tok = (tid >> 1) & 63;
       const int half = tid & 1;
       if (kind == 0) {
-        const uint8_t* row = (const uint8_t*)S.u.raw.rawk[tok];
-        const int rb = 16 + g.k_pb;
-        const float ruler = f16_bits_to_float((uint32_t)row[rb] | ((uint32_t)row[rb + 1] << 8));
-        decode_half_row<RB>(row, half, [&](int d0, const uint32_t* cd) {
-          float4v v0, v1;
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            v0[k] = (float)((int)cd[k] - (1 << (RB - 1))) * ruler;
-            v1[k] = (float)((int)cd[4 + k] - (1 << (RB - 1))) * ruler;
-          }
-          *(float4v*)&S.kres[tok][d0] = v0;
-          *(float4v*)&S.kres[tok][d0 + 4] = v1;
-        });
+        const uint32_t* row = S.rawk[tok];
+        decode_half_row<RB>(row, half, S.lut, &S.kcode[tok][64 * half]);
+        if (half == 0) {
+          const int rb = 16 + g.k_pb;
+          const uint32_t bits = __builtin_amdgcn_alignbyte(row[(rb >> 2) + 1], row[rb >> 2], rb & 3);
+          S.krul[tok] = f16_bits_to_float(bits & 0xffffu);
+        }
       } else {
-        const uint8_t* row = (const uint8_t*)S.u.raw.rawv[tok];
-        const int rb = 16 + g.v_pb;
-        if (half == 0)
-          S.vrul[tok] = f16_bits_to_float((uint32_t)row[rb] | ((uint32_t)row[rb + 1] << 8));
-        decode_half_row<VB>(row, half, [&](int d0, const uint32_t* cd) {
-          half8 v;
-#pragma unroll
-          for (int k = 0; k < 8; ++k) v[k] = (_Float16)(float)((int)cd[k] - (1 << (VB - 1)));
-          *(half8*)&S.vval[tok][d0] = v;
-        });
+        const uint32_t* row = S.rawv[tok];
+        decode_half_row<VB>(row, half, S.lut, &S.vcode[tok][64 * half]);
+        if (half == 0) {
+          const int rb = 16 + g.v_pb;
+          const uint32_t bits = __builtin_amdgcn_alignbyte(row[(rb >> 2) + 1], row[rb >> 2], rb & 3);
+          S.vrul[tok] = f16_bits_to_float(bits & 0xffffu);
+        }
       }
     }
     __syncthreads();
@@ -336,6 +503,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
       const int tok = 16 * nb + n;
+      const float4v cv = P.cosv[nb], sv = P.sinv[nb];
       float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < KSTEPS; ++s) {
@@ -346,96 +514,98 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
         acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[1][s], b, acc1, 0, 0, 0);
       }
       const float cs = S.cs[tok];
-      const float4v rl = *(const float4v*)&S.kres[tok][dl];
-      const float4v rh = *(const float4v*)&S.kres[tok][64 + dl];
-      const int pos = tok < ntile ? tt + tok : tt;
-      const float4v cv = *(const float4v*)&a.cs_cache[(int64_t)pos * kD + dl];
-      const float4v sv = *(const float4v*)&a.cs_cache[(int64_t)pos * kD + 64 + dl];
+      const float kr = S.krul[tok];
+      const float kb = -(float)(1 << (RB - 1)) * kr;
+      const uint32_t cl = *(const uint32_t*)&S.kcode[tok][dl];
+      const uint32_t ch = *(const uint32_t*)&S.kcode[tok][64 + dl];
       float yl[4], yh[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float kl = fmaf(cs, acc0[i], rl[i]);
-        const float kh = fmaf(cs, acc1[i], rh[i]);
+        const float rl = fmaf((float)((cl >> (8 * i)) & 0xffu), kr, kb);
+        const float rh = fmaf((float)((ch >> (8 * i)) & 0xffu), kr, kb);
+        const float kl = fmaf(cs, acc0[i], rl);
+        const float kh = fmaf(cs, acc1[i], rh);
         yl[i] = kl * cv[i] - kh * sv[i];
         yh[i] = kh * cv[i] + kl * sv[i];
       }
 #pragma unroll
       for (int p = 0; p < G; ++p) {
-        float part = 0.f;
+        const float4v ql = *(const float4v*)&S.qs[p][dl];
+        const float4v qh = *(const float4v*)&S.qs[p][64 + dl];
+        float sp = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          part = fmaf(ql[p][i], yl[i], part);
-          part = fmaf(qh[p][i], yh[i], part);
+          sp = fmaf(ql[i], yl[i], sp);
+          sp = fmaf(qh[i], yh[i], sp);
         }
-        part += __shfl_xor(part, 16);
-        part += __shfl_xor(part, 32);
-        if (gq == 0) S.u.sm.spart[wv][tok][p] = part;
+        sp = cross_row_sum(sp);
+        if (gq == (p & 3)) S.spart[wv][tok][p] = sp;
       }
     }
+    // next tile's angles: issued after this tile's raw-byte prefetch, needed one tile later
+    if (tt + kTile < t1)
+      prefetch_angles<KSTEPS>(P, a.cs_cache, tt + kTile, min(kTile, t1 - tt - kTile), n, dl);
     __syncthreads();
-    // ---------------------------------------------------------------- online softmax (wave 0)
-    if (wv == 0) {
+    // ---------------------------------------------------------------- online softmax (every wave)
+    float pv[G];
+    {
       const int tok = lane;
       const bool valid = tok < ntile;
+      const float vr = S.vrul[tok];
 #pragma unroll
       for (int p = 0; p < G; ++p) {
-        float s = S.u.sm.spart[0][tok][p] + S.u.sm.spart[1][tok][p] + S.u.sm.spart[2][tok][p] +
-                  S.u.sm.spart[3][tok][p];
-        s = valid ? s * a.scale_log2 : -INFINITY;
+        float s = S.spart[0][tok][p] + S.spart[1][tok][p] + S.spart[2][tok][p] +
+                  S.spart[3][tok][p];
+        s = valid ? s : -INFINITY;
         const float mt = wave_max(s);
         const float mn = fmaxf(m_run[p], mt);
         const float alpha = exp2f(m_run[p] - mn);
         const float pr = valid ? exp2f(s - mn) : 0.f;
         l_run[p] = l_run[p] * alpha + wave_sum(pr);
         m_run[p] = mn;
-        S.u.sm.pw[p][tok] = pr * S.vrul[tok];
-        if (lane == 0) S.u.sm.alpha[p] = alpha;
+        pv[p] = pr * vr;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[p][i] *= alpha;
+        psum[p] *= alpha;
       }
     }
-    __syncthreads();
     // ---------------------------------------------------------------- P.V
-    {
-      float al[G];
+    float pwb[G][4];
 #pragma unroll
-      for (int p = 0; p < G; ++p) al[p] = S.u.sm.alpha[p];
+    for (int p = 0; p < G; ++p) bcast_rows(pv[p], pwb[p]);
 #pragma unroll
-      for (int p = 0; p < G; ++p)
+    for (int nb = 0; nb < 4; ++nb) {
+      const int tok = 16 * nb + n;
+      const uint32_t cl = *(const uint32_t*)&S.vcode[tok][dl];
+      const uint32_t ch = *(const uint32_t*)&S.vcode[tok][64 + dl];
+      float v[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) o[p][i] *= al[p];
+      for (int i = 0; i < 4; ++i) {
+        v[i] = (float)((cl >> (8 * i)) & 0xffu);
+        v[4 + i] = (float)((ch >> (8 * i)) & 0xffu);
+      }
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb) {
-        const int tok = 16 * nb + n;
-        _Float16 v[8];
-        __builtin_memcpy(&v[0], &S.vval[tok][dl], 8);
-        __builtin_memcpy(&v[4], &S.vval[tok][64 + dl], 8);
+      for (int p = 0; p < G; ++p) {
+        const float pw = pwb[p][nb];
+        psum[p] += pw;
 #pragma unroll
-        for (int p = 0; p < G; ++p) {
-          const float pw = S.u.sm.pw[p][tok];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) o[p][i] = fmaf(pw, (float)v[i], o[p][i]);
-        }
+        for (int i = 0; i < 8; ++i) o[p][i] = fmaf(pw, v[i], o[p][i]);
       }
     }
-    __syncthreads();
   }
 
-  // ---- reduce o over the 16 token lanes of each lane group
+  // ---- reduce o over the 16 token lanes of each lane group; remove the 2^(b-1) code offset
 #pragma unroll
-  for (int p = 0; p < G; ++p)
+  for (int p = 0; p < G; ++p) {
+    const float off = (float)(1 << (VB - 1)) * row_sum(psum[p]);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float v = o[p][i];
-      v += __shfl_xor(v, 1);
-      v += __shfl_xor(v, 2);
-      v += __shfl_xor(v, 4);
-      v += __shfl_xor(v, 8);
-      o[p][i] = v;
-    }
-  if (wv == 0 && lane == 0) {
+    for (int i = 0; i < 8; ++i) o[p][i] = row_sum(o[p][i]) - off;
+  }
+  if (tid == 0) {
 #pragma unroll
     for (int p = 0; p < G; ++p) {
-      S.u.sm.m[p] = m_run[p];
-      S.u.sm.l[p] = l_run[p];
+      S.m[p] = m_run[p];
+      S.l[p] = l_run[p];
     }
   }
   __syncthreads();
@@ -444,7 +614,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
     if (n == 0) {
 #pragma unroll
       for (int p = 0; p < G; ++p) {
-        const float inv = 1.f / S.u.sm.l[p];
+        const float inv = 1.f / S.l[p];
         const int64_t ob = qrow * a.out_row_stride + (int64_t)(h * G + p) * kD;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -458,49 +628,59 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
 
   // ---- split-K partial: [G][kD + 2] per (r, h, c): unnormalised o, running max, running sum
   const int64_t pstride = (int64_t)G * (kD + 2);
-  float* part = a.ws_part + ((int64_t)(r * g.H + h) * a.max_chunks + c) * pstride;
+  float* partp = a.ws_part + ((int64_t)(r * g.H + h) * a.max_chunks + c) * pstride;
+  // The partial is written with agent-scope (write-through) atomic stores and waited on before
+  // the counter update, so no cache-wide release fence is needed; the combining block reads the
+  // partials with agent-scope atomic loads.
+  auto st_agent = [](float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
   if (n == 0) {
 #pragma unroll
     for (int p = 0; p < G; ++p)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        part[p * (kD + 2) + dl + i] = o[p][i];
-        part[p * (kD + 2) + 64 + dl + i] = o[p][4 + i];
+        st_agent(&partp[p * (kD + 2) + dl + i], o[p][i]);
+        st_agent(&partp[p * (kD + 2) + 64 + dl + i], o[p][4 + i]);
       }
   }
   if (tid < G) {
-    part[tid * (kD + 2) + kD] = S.u.sm.m[tid];
-    part[tid * (kD + 2) + kD + 1] = S.u.sm.l[tid];
+    st_agent(&partp[tid * (kD + 2) + kD], S.m[tid]);
+    st_agent(&partp[tid * (kD + 2) + kD + 1], S.l[tid]);
   }
-  __threadfence();
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (tid == 0) {
-    const int prev = atomicAdd(&a.ws_cnt[r * g.H + h], 1);
+    const int prev = __hip_atomic_fetch_add(&a.ws_cnt[r * g.H + h], 1, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
     S.is_last = (prev == n_chunks - 1);
   }
   __syncthreads();
   if (!S.is_last) return;
-  __threadfence();
+  auto ld_agent = [](const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
   const float* pbase = a.ws_part + (int64_t)(r * g.H + h) * a.max_chunks * pstride;
   for (int it = tid; it < G * kD; it += kThreads) {
     const int p = it / kD;
     const int dim = it - p * kD;
     float M = -INFINITY;
-    for (int cc = 0; cc < n_chunks; ++cc) M = fmaxf(M, pbase[cc * pstride + p * (kD + 2) + kD]);
+    for (int cc = 0; cc < n_chunks; ++cc) M = fmaxf(M, ld_agent(&pbase[cc * pstride + p * (kD + 2) + kD]));
     float L = 0.f, O = 0.f;
     for (int cc = 0; cc < n_chunks; ++cc) {
       const float* pc = pbase + cc * pstride + p * (kD + 2);
-      const float f = exp2f(pc[kD] - M);
-      L = fmaf(pc[kD + 1], f, L);
-      O = fmaf(pc[dim], f, O);
+      const float f = exp2f(ld_agent(&pc[kD]) - M);
+      L = fmaf(ld_agent(&pc[kD + 1]), f, L);
+      O = fmaf(ld_agent(&pc[dim]), f, O);
     }
     store_act(a.out, a.out_dtype, qrow * a.out_row_stride + (int64_t)(h * G + p) * kD + dim,
               O / L);
   }
-  if (tid == 0) a.ws_cnt[r * g.H + h] = 0;
+  if (tid == 0) __hip_atomic_store(&a.ws_cnt[r * g.H + h], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace ttkv
+
 
 // ------------------------------------------------------------------------------------ host side
 #include "ttkv_host.h"
@@ -548,16 +728,20 @@ static int dispatch_k(const DecodeArgs& a, int ksteps, int grid, hipStream_t st)
   return host_fail(TTKV_E_UNSUPPORTED, "r1 > 160 is not built");
 }
 
-int decode_chunk_for(int num_reqs, int H, int max_seq_len) {
+int decode_chunk_for(int num_reqs, int H, int max_seq_len, int block_size) {
   const int64_t work = (int64_t)num_reqs * H * std::max(max_seq_len, 1);
-  const int64_t target = 4LL * device_cu_count();
+  const int64_t target = 2LL * device_cu_count();  // one round at 2 resident blocks per CU
   int64_t chunk = (work + target - 1) / target;
   chunk = (chunk + kTile - 1) / kTile * kTile;
-  return (int)std::min<int64_t>(std::max<int64_t>(chunk, kTile), 4096);
+  chunk = std::min<int64_t>(std::max<int64_t>(chunk, kTile), 4096);
+  // the block ids of one chunk are staged in LDS: at most kSegMax of them
+  const int64_t seg_cap = (int64_t)(kSegMax - 2) * std::max(block_size, 1) / kTile * kTile;
+  return (int)std::max<int64_t>(std::min<int64_t>(chunk, seg_cap), kTile);
 }
 
-int64_t decode_workspace_bytes(const Geom& g, int G, int num_reqs, int max_seq_len) {
-  const int chunk = decode_chunk_for(num_reqs, g.H, max_seq_len);
+int64_t decode_workspace_bytes(const Geom& g, int G, int num_reqs, int max_seq_len,
+                               int block_size) {
+  const int chunk = decode_chunk_for(num_reqs, g.H, max_seq_len, block_size);
   const int max_chunks = std::max(1, (max_seq_len + chunk - 1) / chunk);
   const int64_t cnt = ((int64_t)num_reqs * g.H * 4 + 255) / 256 * 256;
   return cnt + (int64_t)num_reqs * g.H * max_chunks * G * (kD + 2) * 4;
@@ -628,10 +812,10 @@ int decode_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype,
   a.out_dtype = out_dtype;
   a.out_row_stride = out_row_stride;
   a.err = err;
-  a.chunk = decode_chunk_for(num_reqs, g.H, max_seq_len);
+  a.chunk = decode_chunk_for(num_reqs, g.H, max_seq_len, block_size);
   a.max_chunks = std::max(1, (max_seq_len + a.chunk - 1) / a.chunk);
   if (a.max_chunks > 1) {
-    const int64_t need = decode_workspace_bytes(g, G, num_reqs, max_seq_len);
+    const int64_t need = decode_workspace_bytes(g, G, num_reqs, max_seq_len, block_size);
     if (!ws || ws_bytes < need)
       return host_fail(TTKV_E_WORKSPACE, "decode workspace needs " + std::to_string(need) +
                                              " bytes, got " + std::to_string(ws_bytes));

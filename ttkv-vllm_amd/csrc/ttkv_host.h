@@ -12,8 +12,9 @@ namespace ttkv {
 int host_fail(int code, const std::string& msg);
 int device_cu_count();
 
-int decode_chunk_for(int num_reqs, int H, int max_seq_len);
-int64_t decode_workspace_bytes(const Geom& g, int G, int num_reqs, int max_seq_len);
+int decode_chunk_for(int num_reqs, int H, int max_seq_len, int block_size);
+int64_t decode_workspace_bytes(const Geom& g, int G, int num_reqs, int max_seq_len,
+                               int block_size);
 int decode_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype,
                  int64_t q_row_stride, const uint8_t* page, int64_t n_slots, int64_t slot_stride,
                  int block_size, const int32_t* bt, int64_t bt_row_stride, int max_blocks,

@@ -59,7 +59,7 @@ def lib():
     L.ttkv_blob_bytes.restype = I64
     L.ttkv_blob_bytes.argtypes = [LP]
     L.ttkv_decode_workspace_bytes.restype = I64
-    L.ttkv_decode_workspace_bytes.argtypes = [LP, I32, I32, I32]
+    L.ttkv_decode_workspace_bytes.argtypes = [LP, I32, I32, I32, I32]
     L.ttkv_decode_paged.restype = ctypes.c_int
     L.ttkv_decode_paged.argtypes = [
         LP, I32, F32,                 # layout, num_heads, scale

@@ -39,10 +39,10 @@ def page_bytes(page: torch.Tensor, blob: int) -> torch.Tensor:
 
 
 def decode_workspace(lay: TTKLayout, num_heads: int, num_reqs: int, max_seq_len: int,
-                     device) -> torch.Tensor:
+                     device, block_size: int = 16) -> torch.Tensor:
     """A zero-filled workspace sized for this batch shape (the kernel keeps it zero)."""
     n = _hip.lib().ttkv_decode_workspace_bytes(_hip.Layout.of(lay), num_heads, num_reqs,
-                                               max_seq_len)
+                                               max_seq_len, block_size)
     if n < 0:
         raise ValueError("invalid layout / head count for the decode workspace")
     return torch.zeros(max(int(n), 256), dtype=torch.uint8, device=device)
@@ -95,7 +95,7 @@ def decode_paged(lay: TTKLayout, query: torch.Tensor, page: torch.Tensor, block_
     if out.dtype not in _hip.DTYPE_CODE or query.dtype not in _hip.DTYPE_CODE:
         raise ValueError("query/out dtype must be fp32, fp16 or bf16")
     if workspace is None:
-        workspace = decode_workspace(lay, HQ, num_reqs, max_seq_len, query.device)
+        workspace = decode_workspace(lay, HQ, num_reqs, max_seq_len, query.device, block_size)
     if error_word is None:
         error_word = torch.zeros(1, dtype=torch.int32, device=query.device)
     rc = L.ttkv_decode_paged(
