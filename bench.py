@@ -157,6 +157,76 @@ def time_k1(torch, lay, store, q, cache, steps, warmup, n_layers):
     return ms_step, sum(per) / len(per)
 
 
+def time_launches(torch, fn, steps, warmup):
+    """Average ms per call of `fn` (one kernel launch on torch's current stream), HIP events."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    for a, b in evs:
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in evs) / steps
+
+
+def k2_flops(lens, qlens, r1):
+    """Algorithmic FLOPs of one K2 attention launch: causal-visible scores and P.V
+    (2*HQ*d each per visible (query, key)), and each stored key reconstructed once
+    (2*H*r1*d)."""
+    f = 0
+    for n, Q in zip(lens, qlens):
+        p0 = n - Q
+        vis = Q * p0 + Q * (Q + 1) // 2
+        f += 2 * 2 * HQ * D * vis + 2 * H * r1 * D * n
+    return f
+
+
+def bench_config4(torch, lay, cfg, cache, dev, steps=10, warmup=3):
+    """4 requests, 7400 cached tokens each plus a 256-query chunk whose keys
+    are already written (n = 7656), causal over cached + chunk positions; one K2 launch per
+    layer over the 4 chunks."""
+    from vllm_ttkv import kernels, synth
+    Q, n = 256, 7400 + 256
+    lens = [n] * 4
+    st = build_store(torch, lay, cfg, lens, 1, seed=4, dev=dev)
+    L = st["layers"][0]
+    q = synth.queries(4 * Q, seed=8, device=dev)
+    qsl = torch.arange(0, 4 * Q + 1, Q, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    ws = kernels.prefill_workspace(lay, HQ, 4, Q, n, dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def attend():
+        kernels.prefill_paged(lay, q, L["page"], BS, st["bt"], st["seq_lens"], qsl, Q, n,
+                              st["dec_map"], L["dec_pool"], cache, D ** -0.5, out=out,
+                              workspace=ws, error_word=err)
+
+    ms = time_launches(torch, attend, steps, warmup)
+    scores = torch.empty(HQ, Q, n, dtype=torch.float32, device=dev)
+
+    def score1():
+        kernels.multi_scores_paged(lay, q[:Q], L["page"], BS, st["bt"][:1], st["seq_lens"][:1],
+                                   qsl[:2], Q, n, st["dec_map"], L["dec_pool"], cache,
+                                   D ** -0.5, scores=scores, error_word=err)
+
+    ms_s = time_launches(torch, score1, steps, warmup)
+    torch.cuda.synchronize()
+    if int(err.item()):
+        raise RuntimeError(f"K2: device error word {int(err.item())}")
+    fl = k2_flops(lens, [Q] * 4, lay.r1)
+    tf = fl / (ms * 1e-3) / 1e12
+    log(f"K2 config4: {ms * 1e3:.1f} us/launch (4 chunks), {tf:.1f} TFLOP/s; scores mode "
+        f"{ms_s * 1e3:.1f} us per chunk")
+    return dict(requests=4, cached=7400, chunk=Q, us_per_launch=ms * 1e3,
+                us_per_chunk_layer=ms * 1e3 / 4, algorithmic_flop_per_launch=fl,
+                tflops=tf, mfma_peak_tflops=2500.0, mfma_frac=tf / 2500.0,
+                scores_mode_us_per_chunk_layer=ms_s * 1e3,
+                scores_mode_gbps_written=HQ * Q * n * 4 / (ms_s * 1e-3) / 1e9)
+
+
 def cpu_baseline(torch, lay, store, q, cache, n, budget_s=12.0):
     """The torch-CPU oracle (reference.py:149-163 restated, float32, the reference's request
     loop) on a bounded sample: request-layers of the headline workload, timed until `budget_s`."""
@@ -276,6 +346,7 @@ def main():
                                           hbm_gbps=b / (ml * 1e-3) / 1e9,
                                           tokens_per_s=8 / (ml * 1e-3 * L_LAYERS))
         del st
+        extra["config4_continuation"] = bench_config4(torch, lay, cfg, cache, dev)
 
     cpu = None
     if not args.no_cpu:

@@ -41,7 +41,7 @@ enum {
   TTKV_ERR_NO_DECODER = 1,   /* block_table[r,0] maps to no decoder slot */
   TTKV_ERR_BAD_BLOCK = 2,    /* a block id outside [0, num_blocks) inside a request's used prefix */
   TTKV_ERR_BAD_SLOT = 4,     /* slot_mapping entry is PAD (<0) or past the cache */
-  TTKV_ERR_SEQ_LEN = 8,      /* seq_lens[r] > the max_seq_len the call was sized for (clamped) */
+  TTKV_ERR_SEQ_LEN = 8,      /* seq_lens[r] (or a query count) beyond what the call was sized for (clamped), or a continuation with seq_len < q_len */
 };
 
 /* One layer's allocation. Mirrors TTKLayout(H, d, r1, qbits, res_k, res_bits, v_lanes, v_bits)
@@ -118,6 +118,58 @@ int ttkv_write_paged(const ttkv_layout* lay, const void* key, int32_t k_dtype, i
                      const int8_t* coeff_q_in, const float* coeff_scale_in, uint8_t* page,
                      int64_t n_slots, int64_t slot_stride, float* coeff_out, float* resid_out,
                      int32_t* error_word, ttkv_stream_t stream);
+
+/* Workspace bytes `ttkv_prefill_paged` needs for this batch shape (0 when one key split covers
+ * every query block). Zero-filled before first use; every call leaves the counters zero. */
+int64_t ttkv_prefill_workspace_bytes(const ttkv_layout* lay, int32_t num_heads, int32_t num_reqs,
+                                     int32_t max_q_len, int32_t max_seq_len);
+
+/* K2 -- multi-query read for chunked-prefill continuations, ONE launch over the batch.
+ *
+ * Replaces the reference's per-request `_prefill_continuation` (vllm_ttkv/impl.py:725-778):
+ * `krt_multi_from_slots` (krt_triton.py:268-317) with p0 = seq_len - q_len, the softmax over the
+ * materialised [num_heads, Q, n] scores (impl.py:771) and `v_out_multi_from_slots`
+ * (v_out_triton.py:249-293). Per request r with Q = qsl[r+1]-qsl[r] queries and n = seq_lens[r]
+ * stored keys (the chunk's own keys included, written before the read), p0 = n - Q:
+ *   s[p, j, t] = scale * q[qsl[r]+j, p] . RoPE_t(K_pre[t]),   -inf where t > p0 + j
+ *   out[qsl[r]+j, p] = sum_t softmax_t(s[p, j, :]) * V[h(p), t]
+ * Key tiles are reconstructed once per 64-query block and reused by all its queries and GQA
+ * heads on MFMA; the scores never leave the chip.
+ * req_index    optional [num_reqs] int32: batch rows to process (block_table / seq_lens /
+ *              query_start_loc are indexed by it); NULL = rows 0..num_reqs-1.
+ * max_q_len / max_seq_len bound Q and n over the processed rows (they size the grid).
+ * Other arguments as for ttkv_decode_paged. Refused device-side: a request whose n < Q (bit
+ * TTKV_ERR_SEQ_LEN), one without a decoder (TTKV_ERR_NO_DECODER, its rows are NaN). */
+int ttkv_prefill_paged(const ttkv_layout* lay, int32_t num_heads, float scale,
+                       const void* query, int32_t q_dtype, int64_t q_row_stride,
+                       const uint8_t* page, int64_t n_slots, int64_t slot_stride,
+                       int32_t block_size, const int32_t* block_table, int64_t bt_row_stride,
+                       int32_t max_blocks, const int32_t* seq_lens,
+                       const int32_t* query_start_loc, const int32_t* req_index,
+                       int32_t num_reqs, int32_t max_q_len, int32_t max_seq_len,
+                       const int32_t* dec_slot_of_block, int64_t num_blocks,
+                       const float* dec_pool, int64_t n_dec_slots,
+                       const float* cos_sin_cache, int64_t max_position,
+                       void* out, int32_t out_dtype, int64_t out_row_stride,
+                       void* workspace, int64_t workspace_bytes, int32_t* error_word,
+                       ttkv_stream_t stream);
+
+/* K2, scores mode -- the continuation score tensor of ONE request (num_reqs == 1), as
+ * `krt_multi_from_slots` returns it (krt_triton.py:268-317; reference.py:112-146):
+ *   scores[p * s_head_stride + j * s_q_stride + t] = s[p, j, t]   fp32, -inf where t > p0 + j
+ * for p < num_heads, j < Q, t < n. Reconstruction and rotated keys are carried at fp32 accuracy
+ * (hi + lo fp16 MFMA operands); the query is taken as fp16. */
+int ttkv_multi_scores_paged(const ttkv_layout* lay, int32_t num_heads, float scale,
+                            const void* query, int32_t q_dtype, int64_t q_row_stride,
+                            const uint8_t* page, int64_t n_slots, int64_t slot_stride,
+                            int32_t block_size, const int32_t* block_table,
+                            int64_t bt_row_stride, int32_t max_blocks, const int32_t* seq_lens,
+                            const int32_t* query_start_loc, int32_t max_q_len,
+                            int32_t max_seq_len, const int32_t* dec_slot_of_block,
+                            int64_t num_blocks, const float* dec_pool, int64_t n_dec_slots,
+                            const float* cos_sin_cache, int64_t max_position, float* scores,
+                            int64_t s_head_stride, int64_t s_q_stride, int32_t* error_word,
+                            ttkv_stream_t stream);
 
 /* Message for the last nonzero return on this thread. */
 const char* ttkv_last_error(void);

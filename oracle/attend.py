@@ -133,3 +133,24 @@ def paged_decode(lay: Layout, flat, block_table, seq_lens, query_start_loc, quer
         q = query[int(query_start_loc[r])]
         out.append(attend_raw_store(lay, k, v, decoders[r], q, cos, sin, scale, dtype))
     return torch.stack(out)
+
+
+def paged_continuation(lay: Layout, flat, block_table, seq_lens, query_start_loc, query,
+                       decoders, cos_sin_cache, block_size: int, scale: float, rows=None,
+                       dtype=torch.float32):
+    """impl.py:725-778: `_prefill_continuation` for each request in `rows` (default: all).
+
+    Request r's queries are rows query_start_loc[r]..[r+1] of query [N, HQ, d] (post-RoPE); they
+    attend over the seq_lens[r] stored keys with p0 = seq_len - q_len. Returns {r: [Q, HQ, d]}."""
+    from .rope import cos_sin_from_cache
+    rows = range(block_table.shape[0]) if rows is None else rows
+    out = {}
+    for r in rows:
+        n = int(seq_lens[r])
+        s, e = int(query_start_loc[r]), int(query_start_loc[r + 1])
+        k, v = gather_request(lay, flat, block_table[r], n, block_size)
+        cos, sin = cos_sin_from_cache(cos_sin_cache, torch.arange(n), lay.d)
+        q = query[s:e].permute(1, 0, 2)
+        o = attend_multi(lay, k, v, decoders[r], q, cos, sin, scale, p0=n - (e - s), dtype=dtype)
+        out[r] = o.permute(1, 0, 2)
+    return out

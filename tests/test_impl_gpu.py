@@ -1,0 +1,143 @@
+"""The drop-in `TTKVAttentionImpl.forward` on the GPU: first-chunk fit + write, decode steps and a
+mixed decode / continuation / first-chunk step, each checked against the CPU oracle reading the
+cache bytes the step wrote (reference test: test_impl_decode.py:259-873 -- real forward vs
+attend_raw_store, write->decode loop, continuation over the whole store, mixed batch)."""
+from dataclasses import dataclass
+
+import pytest
+import torch
+
+from helpers import HQ, H, D
+from oracle import attend
+from oracle.layout import layout_for_config as oracle_layout
+from oracle.rope import cos_sin_from_cache, rope_apply
+from vllm_ttkv import patch, rope_store, synth
+from vllm_ttkv.impl import TTKVAttentionImpl
+from vllm_ttkv.layout import CONFIGS, layout_for_config
+from vllm_ttkv.metadata import TTKVAttentionMetadata
+from vllm_ttkv.rope import cos_sin_cache
+
+pytestmark = pytest.mark.gpu
+SCALE = D ** -0.5
+BS = 16
+NAME = "model.layers.5.self_attn.attn"
+
+
+@dataclass
+class _Layer:
+    layer_name: str
+    ttkv_layout: object
+
+
+class _Seq:
+    """One request's raw K/V/q streams (positions 0..T-1)."""
+
+    def __init__(self, T, seed):
+        self.K = synth.keys(T, seed=seed).permute(1, 0, 2).contiguous()     # [T, H, d]
+        self.V = synth.values(T, seed=seed).permute(1, 0, 2).contiguous()
+        self.Q = synth.queries(T, seed=seed).float()                         # [T, HQ, d]
+
+
+def _step(im, layer, cache, csc, bt, reqs):
+    """reqs: list of (seq, start, end) -> positions [start, end) of each request this step."""
+    qsl, rows_k, rows_v, rows_q, slots, seq_lens = [0], [], [], [], [], []
+    for r, (sq, s, e) in enumerate(reqs):
+        qsl.append(qsl[-1] + e - s)
+        rows_k.append(sq.K[s:e])
+        rows_v.append(sq.V[s:e])
+        rows_q.append(sq.Q[s:e])
+        pos = torch.arange(s, e)
+        slots.append(bt[r, pos // BS].long() * BS + pos % BS)
+        seq_lens.append(e)
+    raw_k = torch.cat(rows_k)
+    positions = torch.cat([torch.arange(s, e) for _, s, e in reqs])
+    cos, sin = cos_sin_from_cache(csc, positions, D)
+    k_post = rope_apply(raw_k, cos.unsqueeze(1), sin.unsqueeze(1)).to(torch.float16)
+    N = qsl[-1]
+    dev = "cuda"
+    md = TTKVAttentionMetadata(
+        seq_lens=torch.tensor(seq_lens, dtype=torch.int32, device=dev),
+        slot_mapping=torch.cat(slots).to(dev),
+        block_table=bt[:len(reqs)].to(dev),
+        query_start_loc=torch.tensor(qsl, dtype=torch.int32, device=dev),
+        query_start_loc_cpu=torch.tensor(qsl, dtype=torch.int32), num_actual_tokens=N,
+        max_query_len=max(e - s for _, s, e in reqs), max_seq_len=max(seq_lens))
+    q = torch.cat(rows_q).to(torch.float16)
+    patch.stash_raw_k(NAME, raw_k.reshape(N, H * D).to(dev), cos_sin_cache=csc.to(dev))
+    out = torch.full((N, HQ, D), float("nan"), dtype=torch.float16, device=dev)
+    im.forward(layer, q.to(dev), k_post.reshape(N, H * D).to(dev),
+               torch.cat(rows_v).reshape(N, H * D).to(torch.float16).to(dev), cache, md,
+               output=out)
+    torch.cuda.synchronize()
+    assert int(im.error_word.item()) == 0
+    return out.float().cpu(), q, k_post, qsl, seq_lens
+
+
+def _check(got, want, what, max_abs=2e-3, mean_abs=1e-3):
+    e = (got.double() - want.double()).abs()
+    print(f"{what}: max-abs {e.max():.3e} mean-abs {e.mean():.3e}")
+    assert torch.isfinite(got).all(), what
+    assert e.max() <= max_abs and e.mean() <= mean_abs, f"{what}: {e.max():.3e} / {e.mean():.3e}"
+
+
+def _sdpa_ref(q, k_post, v):
+    """fp64 causal attention over the chunk's own (fp16) post-RoPE keys and values."""
+    q, k_post, v = q.double(), k_post.double(), v.half().double()
+    G = HQ // H
+    T = q.shape[0]
+    kk = k_post.repeat_interleave(G, dim=1).transpose(0, 1)
+    vv = v.repeat_interleave(G, dim=1).transpose(0, 1)
+    s = torch.einsum("htd,hsd->hts", q.transpose(0, 1), kk) * SCALE
+    s = s.masked_fill(torch.triu(torch.ones(T, T, dtype=torch.bool), 1), float("-inf"))
+    return torch.einsum("hts,hsd->htd", torch.softmax(s, -1), vv).transpose(0, 1)
+
+
+def test_forward_write_then_read_loop_and_mixed_batch():
+    lay = layout_for_config(CONFIGS["safe"], 110)
+    olay = oracle_layout(CONFIGS["safe"], 110)
+    rope_store.clear_stores()
+    csc = cos_sin_cache(4096)
+    seqs = [_Seq(1100, 1), _Seq(1000, 2), _Seq(400, 3)]
+    bt, nblk = synth.shuffled_block_table([1100, 1000, 400], BS, seed=9, extra_blocks=2)
+    C = lay.compressed_bytes_per_token()
+    cache = torch.zeros(nblk, 1, BS, C // 2, dtype=torch.bfloat16, device="cuda")
+    im = TTKVAttentionImpl(HQ, D, SCALE, H)
+    layer = _Layer(NAME, lay)
+
+    def oracle_inputs():
+        flat = cache.view(torch.uint8).reshape(-1, C).cpu()
+        store = rope_store.store_for_layer(NAME)
+        decs = [store.decoders[int(bt[r, 0])].decoder_f.cpu() for r in range(len(store.decoders))]
+        return flat, decs
+
+    # step 1: two first chunks (fit + write; SDPA over the chunk's own q/k/v)
+    out, q, k_post, qsl, _ = _step(im, layer, cache, csc, bt, [(seqs[0], 0, 700),
+                                                                (seqs[1], 0, 500)])
+    for r, (s, e) in enumerate([(0, 700), (0, 500)]):
+        want = _sdpa_ref(q[qsl[r]:qsl[r + 1]], k_post[qsl[r]:qsl[r + 1]], seqs[r].V[s:e])
+        _check(out[qsl[r]:qsl[r + 1]], want, f"first chunk {r}")
+    assert len(rope_store.store_for_layer(NAME).decoders) == 2
+
+    # steps 2-3: decode-only steps (K3 frozen write, then one K1 launch)
+    for t in range(2):
+        reqs = [(seqs[0], 700 + t, 701 + t), (seqs[1], 500 + t, 501 + t)]
+        out, q, _, qsl, seq_lens = _step(im, layer, cache, csc, bt, reqs)
+        flat, decs = oracle_inputs()
+        want = attend.paged_decode(olay, flat, bt[:2], torch.tensor(seq_lens), torch.tensor(qsl),
+                                   q.float(), decs, csc, BS, SCALE, dtype=torch.float64)
+        _check(out, want, f"decode step {t}")
+
+    # step 4: mixed -- a decode, a continuation chunk of 99, a new request's first chunk
+    reqs = [(seqs[0], 702, 703), (seqs[1], 502, 601), (seqs[2], 0, 300)]
+    out, q, k_post, qsl, seq_lens = _step(im, layer, cache, csc, bt, reqs)
+    flat, decs = oracle_inputs()
+    sl = torch.tensor(seq_lens)
+    want_d = attend.paged_decode(olay, flat, bt[:1], sl[:1], torch.tensor(qsl[:2]), q.float(),
+                                 decs[:1], csc, BS, SCALE, dtype=torch.float64)
+    _check(out[0:1], want_d, "mixed: decode row")
+    want_c = attend.paged_continuation(olay, flat, bt[:3], sl, torch.tensor(qsl), q.double(),
+                                       decs, csc, BS, SCALE, rows=[1], dtype=torch.float64)
+    _check(out[qsl[1]:qsl[2]], want_c[1], "mixed: continuation rows")
+    want_f = _sdpa_ref(q[qsl[2]:qsl[3]], k_post[qsl[2]:qsl[3]], seqs[2].V[0:300])
+    _check(out[qsl[2]:qsl[3]], want_f, "mixed: first chunk rows")
+    rope_store.clear_stores()

@@ -1,0 +1,155 @@
+"""K2 (multi-query continuation read) on the GPU against the CPU oracle.
+
+Scores mode vs `raw_scores_multi` (reference.py:112-146) and attention mode vs the reference's
+continuation (impl.py:725-778: scores, softmax over the store, V readout), both with the causal
+rule key t visible to query j iff t <= p0 + j, p0 = seq_len - q_len.
+
+Tolerance (north star): scores and outputs within 2e-3 max-abs / 1e-3 mean-abs against the
+float64 oracle; the masked pattern is compared exactly."""
+import pytest
+import torch
+
+from helpers import HQ, fitted_store, llama3_cache, paged
+from oracle import attend
+from oracle.rope import cos_sin_from_cache
+from vllm_ttkv import kernels, synth
+
+pytestmark = pytest.mark.gpu
+MAX_ABS, MEAN_ABS = 2e-3, 1e-3
+SCALE = 128 ** -0.5
+
+
+def _dev_inputs(stores, block_size=16, seed=0):
+    pg = paged(stores, block_size, seed)
+    B = len(stores)
+    dec_pool = torch.stack([s["decoder"] for s in stores]).cuda()
+    dec_map = torch.full((pg["num_blocks"],), -1, dtype=torch.int32)
+    for r in range(B):
+        dec_map[pg["block_table"][r, 0]] = r
+    return pg, dec_pool, dec_map.cuda()
+
+
+def _check(got, want, what, exact_inf=True):
+    got = got.double().cpu()
+    if exact_inf:
+        assert torch.equal(torch.isneginf(got), torch.isneginf(want)), f"{what}: mask pattern"
+        fin = torch.isfinite(want)
+        assert torch.isfinite(got[fin]).all(), what
+        e = (got[fin] - want[fin]).abs()
+    else:
+        assert torch.isfinite(got).all(), what
+        e = (got - want).abs()
+    print(f"{what}: max-abs {e.max():.3e} mean-abs {e.mean():.3e}")
+    assert e.max() <= MAX_ABS and e.mean() <= MEAN_ABS, f"{what}: {e.max():.3e} / {e.mean():.3e}"
+
+
+@pytest.mark.parametrize("cfg,n,Q", [("safe", 1000, 100), ("safe", 2100, 256), ("safe", 77, 5),
+                                     ("campaign4x", 900, 130), ("tight", 700, 64)])
+def test_scores_mode_vs_raw_scores_multi(cfg, n, Q):
+    st = fitted_store(cfg, n, seed=n + Q)
+    cache = llama3_cache(4096)
+    pg, dec_pool, dec_map = _dev_inputs([st])
+    q = synth.queries(Q, seed=Q).reshape(Q, HQ, 128)
+    qsl = torch.tensor([0, Q], dtype=torch.int32)
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    got = kernels.multi_scores_paged(st["lay"], q.cuda(), pg["page"].cuda(), 16,
+                                     pg["block_table"].cuda(), pg["seq_lens"].cuda(), qsl.cuda(),
+                                     Q, n, dec_map, dec_pool, cache.cuda(), SCALE,
+                                     error_word=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    cos, sin = cos_sin_from_cache(cache, torch.arange(n), 128)
+    want = attend.raw_scores_multi(st["lay"], st["k_slots"], st["decoder"],
+                                   q.permute(1, 0, 2).double(), cos, sin, SCALE, p0=n - Q,
+                                   dtype=torch.float64)
+    _check(got, want, f"scores {cfg} n={n} Q={Q}")
+
+
+def test_attend_mode_ragged_batch_with_splits():
+    """Three continuation requests of different lengths in one launch (several key splits per
+    query block, so the in-launch combine runs), fp16 queries and output."""
+    shapes = [(300, 40), (1000, 128), (2100, 257)]
+    stores = [fitted_store("safe", n, seed=7 + i) for i, (n, _) in enumerate(shapes)]
+    cache = llama3_cache(4096)
+    pg, dec_pool, dec_map = _dev_inputs(stores, seed=3)
+    qs = [synth.queries(Q, seed=100 + i).reshape(Q, HQ, 128) for i, (_, Q) in enumerate(shapes)]
+    q = torch.cat(qs)
+    qsl = torch.tensor([0] + list(torch.tensor([Q for _, Q in shapes]).cumsum(0)),
+                       dtype=torch.int32)
+    out = torch.zeros_like(q, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    kernels.prefill_paged(st_lay := stores[0]["lay"], q.cuda(), pg["page"].cuda(), 16,
+                          pg["block_table"].cuda(), pg["seq_lens"].cuda(), qsl.cuda(),
+                          max(Q for _, Q in shapes), max(n for n, _ in shapes), dec_map, dec_pool,
+                          cache.cuda(), SCALE, out=out, error_word=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    want = attend.paged_continuation(st_lay, pg["page"], pg["block_table"], pg["seq_lens"], qsl,
+                                     q.double(), [s["decoder"] for s in stores], cache, 16, SCALE,
+                                     dtype=torch.float64)
+    for r in range(len(shapes)):
+        s, e = int(qsl[r]), int(qsl[r + 1])
+        _check(out[s:e].float(), want[r], f"attend req {r} {shapes[r]}", exact_inf=False)
+
+
+def test_attend_mode_req_index_subset_bf16():
+    """`req_index` selects batch rows (decodes at the front are skipped); bf16 in and out."""
+    shapes = [(50, 1), (600, 70), (1200, 200)]
+    stores = [fitted_store("safe", n, seed=20 + i) for i, (n, _) in enumerate(shapes)]
+    cache = llama3_cache(2048)
+    pg, dec_pool, dec_map = _dev_inputs(stores, seed=5)
+    q = torch.cat([synth.queries(Q, seed=200 + i).reshape(Q, HQ, 128)
+                   for i, (_, Q) in enumerate(shapes)]).to(torch.bfloat16)
+    qsl = torch.tensor([0, 1, 71, 271], dtype=torch.int32)
+    out = torch.full(q.shape, 7.0, dtype=torch.bfloat16, device="cuda")
+    kernels.prefill_paged(stores[0]["lay"], q.cuda(), pg["page"].cuda(), 16,
+                          pg["block_table"].cuda(), pg["seq_lens"].cuda(), qsl.cuda(), 200, 1200,
+                          dec_map, dec_pool, cache.cuda(), SCALE,
+                          req_index=torch.tensor([1, 2], dtype=torch.int32, device="cuda"),
+                          out=out)
+    torch.cuda.synchronize()
+    assert torch.all(out[0].float() == 7.0), "row of an unselected request was written"
+    want = attend.paged_continuation(stores[0]["lay"], pg["page"], pg["block_table"],
+                                     pg["seq_lens"], qsl, q.double(),
+                                     [s["decoder"] for s in stores], cache, 16, SCALE,
+                                     rows=[1, 2], dtype=torch.float64)
+    for r in (1, 2):
+        s, e = int(qsl[r]), int(qsl[r + 1])
+        e_ = (out[s:e].double().cpu() - want[r]).abs()
+        print(f"bf16 req {r}: max-abs {e_.max():.3e} mean-abs {e_.mean():.3e}")
+        # bf16 output rounding alone is up to 2^-9 relative; the tolerance is on the math
+        assert e_.max() <= 2e-2 and e_.mean() <= 2e-3
+
+
+def test_single_query_continuation_equals_decode_read():
+    """Q = 1: the multi-query read of one query equals K1's decode read of it."""
+    st = fitted_store("safe", 777, seed=31)
+    cache = llama3_cache(1024)
+    pg, dec_pool, dec_map = _dev_inputs([st])
+    q = synth.queries(1, seed=31).reshape(1, HQ, 128).cuda()
+    qsl = torch.tensor([0, 1], dtype=torch.int32, device="cuda")
+    args = (pg["page"].cuda(), 16, pg["block_table"].cuda(), pg["seq_lens"].cuda(), qsl)
+    k2 = kernels.prefill_paged(st["lay"], q, *args, 1, 777, dec_map, dec_pool, cache.cuda(),
+                               SCALE, out=torch.zeros(1, HQ, 128, device="cuda"))
+    k1 = kernels.decode_paged(st["lay"], q, *args, 777, dec_map, dec_pool, cache.cuda(), SCALE,
+                              out=torch.zeros(1, HQ, 128, device="cuda"))
+    torch.cuda.synchronize()
+    e = (k1 - k2).abs().max().item()
+    print(f"Q=1 K2 vs K1: {e:.3e}")
+    assert e <= 1e-3
+
+
+def test_missing_decoder_sets_error_and_nan():
+    st = fitted_store("safe", 200, seed=41)
+    cache = llama3_cache(1024)
+    pg, dec_pool, _ = _dev_inputs([st])
+    dec_map = torch.full((pg["num_blocks"],), -1, dtype=torch.int32, device="cuda")
+    q = synth.queries(10, seed=1).reshape(10, HQ, 128).cuda()
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    out = kernels.prefill_paged(st["lay"], q, pg["page"].cuda(), 16, pg["block_table"].cuda(),
+                                pg["seq_lens"].cuda(),
+                                torch.tensor([0, 10], dtype=torch.int32, device="cuda"), 10, 200,
+                                dec_map, dec_pool, cache.cuda(), SCALE, error_word=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) & 1
+    assert torch.isnan(out).all()

@@ -89,4 +89,54 @@ int ttkv_write_paged(const ttkv_layout* lay, const void* key, int32_t k_dtype, i
                      (hipStream_t)stream);
 }
 
+int64_t ttkv_prefill_workspace_bytes(const ttkv_layout* lay, int32_t num_heads, int32_t num_reqs,
+                                     int32_t max_q_len, int32_t max_seq_len) {
+  Geom g;
+  if (!make_geom(lay, &g) || num_heads <= 0 || num_heads % g.H || num_reqs < 0) return -1;
+  return prefill_workspace_bytes(g, num_heads / g.H, num_reqs, max_q_len, max_seq_len);
+}
+
+int ttkv_prefill_paged(const ttkv_layout* lay, int32_t num_heads, float scale, const void* query,
+                       int32_t q_dtype, int64_t q_row_stride, const uint8_t* page,
+                       int64_t n_slots, int64_t slot_stride, int32_t block_size,
+                       const int32_t* block_table, int64_t bt_row_stride, int32_t max_blocks,
+                       const int32_t* seq_lens, const int32_t* query_start_loc,
+                       const int32_t* req_index, int32_t num_reqs, int32_t max_q_len,
+                       int32_t max_seq_len, const int32_t* dec_slot_of_block, int64_t num_blocks,
+                       const float* dec_pool, int64_t n_dec_slots, const float* cos_sin_cache,
+                       int64_t max_position, void* out, int32_t out_dtype, int64_t out_row_stride,
+                       void* workspace, int64_t workspace_bytes, int32_t* error_word,
+                       ttkv_stream_t stream) {
+  Geom g;
+  if (!make_geom(lay, &g)) return host_fail(TTKV_E_INVALID, "invalid layout");
+  return prefill_paged(g, num_heads, scale, query, q_dtype, q_row_stride, page, n_slots,
+                       slot_stride, block_size, block_table, bt_row_stride, max_blocks, seq_lens,
+                       query_start_loc, req_index, num_reqs, max_q_len, max_seq_len,
+                       dec_slot_of_block, num_blocks, dec_pool, n_dec_slots, cos_sin_cache,
+                       max_position, out, out_dtype, out_row_stride, nullptr, 0, 0, workspace,
+                       workspace_bytes, error_word, (hipStream_t)stream);
+}
+
+int ttkv_multi_scores_paged(const ttkv_layout* lay, int32_t num_heads, float scale,
+                            const void* query, int32_t q_dtype, int64_t q_row_stride,
+                            const uint8_t* page, int64_t n_slots, int64_t slot_stride,
+                            int32_t block_size, const int32_t* block_table,
+                            int64_t bt_row_stride, int32_t max_blocks, const int32_t* seq_lens,
+                            const int32_t* query_start_loc, int32_t max_q_len,
+                            int32_t max_seq_len, const int32_t* dec_slot_of_block,
+                            int64_t num_blocks, const float* dec_pool, int64_t n_dec_slots,
+                            const float* cos_sin_cache, int64_t max_position, float* scores,
+                            int64_t s_head_stride, int64_t s_q_stride, int32_t* error_word,
+                            ttkv_stream_t stream) {
+  Geom g;
+  if (!make_geom(lay, &g)) return host_fail(TTKV_E_INVALID, "invalid layout");
+  if (!scores) return host_fail(TTKV_E_INVALID, "scores is null");
+  return prefill_paged(g, num_heads, scale, query, q_dtype, q_row_stride, page, n_slots,
+                       slot_stride, block_size, block_table, bt_row_stride, max_blocks, seq_lens,
+                       query_start_loc, nullptr, 1, max_q_len, max_seq_len, dec_slot_of_block,
+                       num_blocks, dec_pool, n_dec_slots, cos_sin_cache, max_position, nullptr, 0,
+                       0, scores, s_head_stride, s_q_stride, nullptr, 0, error_word,
+                       (hipStream_t)stream);
+}
+
 }  // extern "C"

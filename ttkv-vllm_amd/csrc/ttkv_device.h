@@ -1,0 +1,170 @@
+// Device helpers shared by the read kernels (K1 decode, K2 multi-query): exact int8 -> fp16
+// conversion, the LUT-driven bitmap/code-stream decode of one packed head row, and cross-lane
+// reductions on DPP and the gfx950 permlane swaps. Bit format: codec/ttkv_packed_cache.py:50-100,
+// 138-167 (bitmap MSB-first per byte, lane order; codes MSB-first in lane order).
+#pragma once
+
+#include "ttkv_common.h"
+
+namespace ttkv {
+
+// int8 x4 (little-endian in a dword) -> two packed fp16 pairs, exact.
+__device__ __forceinline__ void i8x4_to_f16(uint32_t x, uint32_t& p01, uint32_t& p23) {
+  const uint32_t u = x ^ 0x80808080u;  // b + 128 as unsigned bytes
+  const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+  const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+  const half2v bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+  p01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, lo) - bias);
+  p23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, hi) - bias);
+}
+
+__device__ __forceinline__ uint32_t bswap32(uint32_t x) {
+  return __builtin_amdgcn_perm(0u, x, 0x00010203u);
+}
+
+// Spread the 8 codes at the top of a 32-bit MSB-first window (code k at bits 31-B*k-B+1 ..
+// 31-B*k) into bytes: e0 = codes 0..3, e1 = codes 4..7 (byte i of e0 = code i).
+template <int BITS>
+__device__ __forceinline__ void spread8(uint32_t w, uint32_t& e0, uint32_t& e1) {
+  if constexpr (BITS == 4) {
+    // nibbles: code k at bits 28-4k. bytes of (w >> 4) & 0x0f0f0f0f hold codes 6,4,2,0 at bytes
+    // 0..3; bytes of w & 0x0f0f0f0f hold codes 7,5,3,1. Interleave with v_perm.
+    const uint32_t ev = (w >> 4) & 0x0f0f0f0fu;  // byte0 = c6, byte1 = c4, byte2 = c2, byte3 = c0
+    const uint32_t od = w & 0x0f0f0f0fu;         // byte0 = c7, byte1 = c5, byte2 = c3, byte3 = c1
+    // e0 = [c0, c1, c2, c3]: c0 = ev.b3, c1 = od.b3, c2 = ev.b2, c3 = od.b2  (S0 = ev: 4-7, S1 = od)
+    e0 = __builtin_amdgcn_perm(ev, od, 0x02060307u);
+    // e1 = [c4, c5, c6, c7]: c4 = ev.b1, c5 = od.b1, c6 = ev.b0, c7 = od.b0
+    e1 = __builtin_amdgcn_perm(ev, od, 0x00040105u);
+  } else {
+    e0 = __builtin_amdgcn_ubfe(w, 32 - BITS, BITS) |
+         (__builtin_amdgcn_ubfe(w, 32 - 2 * BITS, BITS) << 8) |
+         (__builtin_amdgcn_ubfe(w, 32 - 3 * BITS, BITS) << 16) |
+         (__builtin_amdgcn_ubfe(w, 32 - 4 * BITS, BITS) << 24);
+    e1 = __builtin_amdgcn_ubfe(w, 32 - 5 * BITS, BITS) |
+         (__builtin_amdgcn_ubfe(w, 32 - 6 * BITS, BITS) << 8) |
+         (__builtin_amdgcn_ubfe(w, 32 - 7 * BITS, BITS) << 16) |
+         (__builtin_amdgcn_ubfe(w, 32 - 8 * BITS, BITS) << 24);
+  }
+}
+
+// Decode dims [64*half, 64*half+64) of one staged head row (bitmap dwords 0..3, MSB-first code
+// stream from dword 4) into one code byte per lane at dst[0..63]; lanes outside the bitmap get
+// 2^(BITS-1). `lut[B]` holds the v_perm selectors that move the byte-spread codes of bitmap
+// byte B onto its set lanes (0x0c -> zero byte for the others).
+template <int BITS>
+__device__ __forceinline__ void decode_half_row(const uint32_t* row, int half, const uint2* lut,
+                                                uint8_t* dst) {
+  constexpr uint32_t OFFB = (1u << (BITS - 1)) * 0x01010101u;
+  // XOR pattern that flips the top bit of each of 8 codes at the top of the window: a kept
+  // code c becomes c ^ 2^(b-1), so after the zero-filling scatter a final XOR restores c and
+  // turns the zero bytes into the zero code 2^(b-1).
+  constexpr uint32_t FLIP = BITS == 4 ? 0x88888888u : 0x92492400u;
+  int rank = 0;
+  if (half) rank = __builtin_popcount(row[0]) + __builtin_popcount(row[1]);
+  const uint32_t bm0 = row[2 * half], bm1 = row[2 * half + 1];
+  const uint32_t* st = row + 4;
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    const uint32_t B = __builtin_amdgcn_ubfe(m < 4 ? bm0 : bm1, 8 * (m & 3), 8);
+    const int bp = rank * BITS;
+    const int wi = bp >> 5;
+    const uint64_t pair = ((uint64_t)bswap32(st[wi]) << 32) | (uint64_t)bswap32(st[wi + 1]);
+    const uint32_t w = (uint32_t)((pair << (bp & 31)) >> 32) ^ FLIP;
+    uint32_t e0, e1;
+    spread8<BITS>(w, e0, e1);
+    const uint2 sel = lut[B];
+    uint2 out;
+    out.x = __builtin_amdgcn_perm(e1, e0, sel.x) ^ OFFB;
+    out.y = __builtin_amdgcn_perm(e1, e0, sel.y) ^ OFFB;
+    *(uint2*)(dst + 8 * m) = out;
+    rank += __builtin_popcount(B);
+  }
+}
+
+// Cross-lane helpers on DPP and the gfx950 permlane swaps (VALU ops, no LDS round trip).
+__device__ __forceinline__ float dpp_f(float v, int ctrl_sel) {
+  const int iv = __builtin_bit_cast(int, v);
+  int r = 0;
+  switch (ctrl_sel) {  // dpp control must be a constant
+    case 0: r = __builtin_amdgcn_update_dpp(0, iv, 0xB1, 0xF, 0xF, false); break;   // xor 1
+    case 1: r = __builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xF, 0xF, false); break;   // xor 2
+    case 2: r = __builtin_amdgcn_update_dpp(0, iv, 0x124, 0xF, 0xF, false); break;  // row_ror 4
+    default: r = __builtin_amdgcn_update_dpp(0, iv, 0x128, 0xF, 0xF, false); break; // row_ror 8
+  }
+  return __builtin_bit_cast(float, r);
+}
+// Sum / max over the 16 lanes of each row (every lane gets its row's result).
+__device__ __forceinline__ float row_sum(float v) {
+  v += dpp_f(v, 0);
+  v += dpp_f(v, 1);
+  v += dpp_f(v, 2);
+  v += dpp_f(v, 3);
+  return v;
+}
+__device__ __forceinline__ float row_max(float v) {
+  v = fmaxf(v, dpp_f(v, 0));
+  v = fmaxf(v, dpp_f(v, 1));
+  v = fmaxf(v, dpp_f(v, 2));
+  v = fmaxf(v, dpp_f(v, 3));
+  return v;
+}
+// Lanes l and l^16 / l^32 exchanged: returns (value of rows {0,2}, value of rows {1,3}) etc.
+__device__ __forceinline__ void swap16(float v, float& a, float& b) {
+  const int iv = __builtin_bit_cast(int, v);
+  const auto r = __builtin_amdgcn_permlane16_swap(iv, iv, false, false);
+  a = __builtin_bit_cast(float, (int)r[0]);  // rows [0,0,2,2]
+  b = __builtin_bit_cast(float, (int)r[1]);  // rows [1,1,3,3]
+}
+__device__ __forceinline__ void swap32(float v, float& a, float& b) {
+  const int iv = __builtin_bit_cast(int, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(iv, iv, false, false);
+  a = __builtin_bit_cast(float, (int)r[0]);  // halves [lo, lo]
+  b = __builtin_bit_cast(float, (int)r[1]);  // halves [hi, hi]
+}
+// Sum over lanes {l, l^16, l^32, l^48} (the four rows at the same row position).
+__device__ __forceinline__ float cross_row_sum(float v) {
+  float a, b;
+  swap16(v, a, b);
+  v = a + b;
+  swap32(v, a, b);
+  return a + b;
+}
+__device__ __forceinline__ float cross_row_max(float v) {
+  float a, b;
+  swap16(v, a, b);
+  v = fmaxf(a, b);
+  swap32(v, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float wave_max(float v) { return cross_row_max(row_max(v)); }
+__device__ __forceinline__ float wave_sum(float v) { return cross_row_sum(row_sum(v)); }
+// Broadcast row `nb` (lanes 16nb..16nb+15) of v to all four rows: out[nb].
+__device__ __forceinline__ void bcast_rows(float v, float out[4]) {
+  float r02, r13, a, b;
+  swap16(v, r02, r13);      // r02 = rows [0,0,2,2], r13 = rows [1,1,3,3]
+  swap32(r02, a, b);        // a = [r0 x4], b = [r2 x4]
+  out[0] = a;
+  out[2] = b;
+  swap32(r13, a, b);        // a = [r1 x4], b = [r3 x4]
+  out[1] = a;
+  out[3] = b;
+}
+
+
+// Selector table for decode_half_row: entry B holds the v_perm selectors that move the
+// byte-spread codes of bitmap byte B onto its set lanes (0x0c -> zero byte elsewhere). One entry
+// per thread of a 256-thread block.
+__device__ __forceinline__ uint2 scatter_lut_entry(uint32_t B) {
+  uint32_t s0 = 0, s1 = 0, idx = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const bool present = (B >> (7 - k)) & 1u;
+    const uint32_t sel = present ? idx : 0x0cu;
+    idx += present;
+    if (k < 4) s0 |= sel << (8 * k);
+    else s1 |= sel << (8 * (k - 4));
+  }
+  return make_uint2(s0, s1);
+}
+
+}  // namespace ttkv

@@ -35,3 +35,17 @@ int write_paged(const Geom& g, const void* key, int k_dtype, int64_t k_row_strid
                 const float* cs_in, uint8_t* page, int64_t n_slots, int64_t slot_stride,
                 float* c_out, float* r_out, int32_t* err, hipStream_t st);
 }  // namespace ttkv
+
+namespace ttkv {
+int64_t prefill_workspace_bytes(const Geom& g, int G, int num_reqs, int max_q_len,
+                                int max_seq_len);
+int prefill_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype,
+                  int64_t q_row_stride, const uint8_t* page, int64_t n_slots, int64_t slot_stride,
+                  int block_size, const int32_t* bt, int64_t bt_row_stride, int max_blocks,
+                  const int32_t* seq_lens, const int32_t* qsl, const int32_t* req_index,
+                  int num_reqs, int max_q_len, int max_seq_len, const int32_t* dec_map,
+                  int64_t num_blocks, const float* dec_pool, int64_t n_dec_slots,
+                  const float* cs_cache, int64_t max_pos, void* out, int out_dtype,
+                  int64_t out_row_stride, float* s_out, int64_t s_head_stride, int64_t s_q_stride,
+                  void* ws, int64_t ws_bytes, int32_t* err, hipStream_t st);
+}  // namespace ttkv

@@ -84,15 +84,44 @@ def lib():
         P, I64, I64,                  # page, n_slots, slot_stride
         P, P, P, P,                   # coeff_out, resid_out, error_word, stream
     ]
+    L.ttkv_prefill_workspace_bytes.restype = I64
+    L.ttkv_prefill_workspace_bytes.argtypes = [LP, I32, I32, I32, I32]
+    L.ttkv_prefill_paged.restype = ctypes.c_int
+    L.ttkv_prefill_paged.argtypes = [
+        LP, I32, F32,                 # layout, num_heads, scale
+        P, I32, I64,                  # query, q_dtype, q_row_stride
+        P, I64, I64,                  # page, n_slots, slot_stride
+        I32, P, I64, I32,             # block_size, block_table, bt_row_stride, max_blocks
+        P, P, P,                      # seq_lens, query_start_loc, req_index
+        I32, I32, I32,                # num_reqs, max_q_len, max_seq_len
+        P, I64, P, I64,               # dec_slot_of_block, num_blocks, dec_pool, n_dec_slots
+        P, I64,                       # cos_sin_cache, max_position
+        P, I32, I64,                  # out, out_dtype, out_row_stride
+        P, I64, P,                    # workspace, workspace_bytes, error_word
+        P,                            # stream
+    ]
+    L.ttkv_multi_scores_paged.restype = ctypes.c_int
+    L.ttkv_multi_scores_paged.argtypes = [
+        LP, I32, F32,                 # layout, num_heads, scale
+        P, I32, I64,                  # query, q_dtype, q_row_stride
+        P, I64, I64,                  # page, n_slots, slot_stride
+        I32, P, I64, I32,             # block_size, block_table, bt_row_stride, max_blocks
+        P, P, I32, I32,               # seq_lens, query_start_loc, max_q_len, max_seq_len
+        P, I64, P, I64,               # dec_slot_of_block, num_blocks, dec_pool, n_dec_slots
+        P, I64,                       # cos_sin_cache, max_position
+        P, I64, I64,                  # scores, s_head_stride, s_q_stride
+        P, P,                         # error_word, stream
+    ]
     for name in EXPORTS:
         getattr(L, name)  # every declared symbol must resolve
     _LIB = L
     return L
 
 
-# Every symbol include/ttkv_hip.h declares (checked by tests/test_abi_exports.py).
+# Every symbol include/ttkv_hip.h declares (checked by tests/test_abi.py).
 EXPORTS = ("ttkv_last_error", "ttkv_blob_bytes", "ttkv_decode_workspace_bytes",
-           "ttkv_decode_paged", "ttkv_write_paged")
+           "ttkv_decode_paged", "ttkv_write_paged", "ttkv_prefill_workspace_bytes",
+           "ttkv_prefill_paged", "ttkv_multi_scores_paged")
 
 
 def check(rc: int, what: str) -> None:

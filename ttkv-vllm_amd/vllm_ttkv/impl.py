@@ -1,0 +1,340 @@
+"""`AttentionImpl` for the compressed-KV cache: write this step's raw K/V into slots, then read.
+
+Drop-in for the reference's `TTKVAttentionImpl` (vllm_ttkv/impl.py:326-901): same constructor,
+same refusals, same `forward` contract (writes into `output`; the store write happens first and
+unconditionally; decodes must sit at the front of the batch). What changes is how the work is
+issued:
+
+  * the write is the HIP kernel K3 (`kernels.write_paged`) for all tokens of a step -- one launch
+    for every request that already has a decoder (the kernel resolves each token's decoder from
+    its request's first block through the device registry), plus a fit on the device for a
+    request's first chunk;
+  * the decode read is ONE K1 launch (`kernels.decode_paged`) over all decode requests of the
+    layer, instead of the reference's per-request loop of ~7 launches (impl.py:468-493, 511-540);
+  * a decode-only step reads nothing back to the host: the batch split comes from
+    `query_start_loc_cpu`, the grid from `max_seq_len`, and the kernels read block tables,
+    sequence lengths and decoder slots on the device. Device-side refusals (a block outside the
+    cache, a padded slot id, a request without a decoder) set bits in `self.error_word`;
+    `VLLM_TTKV_CHECK=1` makes every forward synchronise and raise on them.
+  * a continuation chunk (seq_len > q_len) uses the multi-query kernel K2 over the whole store;
+    a first chunk attends over its own post-RoPE q/k/v with SDPA, as in the reference
+    (impl.py:684-723, decode.py:363-389).
+"""
+from __future__ import annotations
+
+import logging
+import os
+from dataclasses import dataclass
+
+import torch
+
+from . import _hip, kernels
+from . import encode as enc
+from .layout import CONFIGS, TTKLayout
+from .patch import take_raw_k
+from .rope_store import ensure_store, layout_for_layer
+
+logger = logging.getLogger("vllm.ttkv")
+
+try:  # pragma: no cover
+    from vllm.v1.attention.backend import AttentionImpl as _ImplBase
+    from vllm.v1.attention.backend import AttentionType
+except Exception:  # noqa: BLE001
+    _ImplBase = object
+    AttentionType = None
+
+CHECK_ENV = "VLLM_TTKV_CHECK"
+
+
+@dataclass
+class BatchPlan:
+    """Which requests decode (a leading run of q_len == 1) and where each request's tokens sit."""
+
+    qsl: list
+    n_decodes: int
+    prefills: list
+
+    @property
+    def n_reqs(self) -> int:
+        return len(self.qsl) - 1
+
+    @classmethod
+    def of(cls, md) -> "BatchPlan":
+        if md.query_start_loc is None or md.seq_lens is None or md.block_table is None:
+            raise RuntimeError("the attention metadata is missing one of `query_start_loc` / "
+                               "`seq_lens` / `block_table`, so the batch cannot be split or "
+                               "addressed")
+        src = md.query_start_loc_cpu if md.query_start_loc_cpu is not None else md.query_start_loc
+        qsl = [int(x) for x in src.tolist()]
+        q_len = [qsl[i + 1] - qsl[i] for i in range(len(qsl) - 1)]
+        decodes = [r for r, q in enumerate(q_len) if q == 1]
+        nd = len(decodes)
+        if decodes != list(range(nd)):
+            raise RuntimeError(f"decode requests are not contiguous at the front of the batch "
+                               f"(decode rows {decodes}, query lengths {q_len}); vLLM's reorder "
+                               f"puts them there and the split relies on it")
+        return cls(qsl=qsl, n_decodes=nd, prefills=[r for r, q in enumerate(q_len) if q > 1])
+
+
+def as_kv_heads(x: torch.Tensor, H: int, d: int, what: str) -> torch.Tensor:
+    """`[T, H*d]` or `[T, H, d]` -> `[T, H, d]` (encode.py:131-148)."""
+    if x.dim() == 2:
+        if x.shape[-1] != H * d:
+            raise ValueError(f"{what} is [T, {x.shape[-1]}] but {H} kv heads of width {d} need "
+                             f"{H * d}")
+        return x.reshape(x.shape[0], H, d)
+    if x.dim() == 3 and tuple(x.shape[1:]) == (H, d):
+        return x
+    raise ValueError(f"{what} has shape {tuple(x.shape)}; expected [T, {H}, {d}] or [T, {H * d}]")
+
+
+class TTKVAttentionImpl(_ImplBase):
+    def __init__(self, num_heads: int, head_size: int, scale: float,
+                 num_kv_heads: int | None = None, alibi_slopes=None, sliding_window=None,
+                 kv_cache_dtype: str = "auto", logits_soft_cap=None, attn_type=None,
+                 kv_sharing_target_layer_name=None, **kwargs):
+        if alibi_slopes is not None:
+            raise NotImplementedError("TT-KV does not support ALiBi: the score kernel has no "
+                                      "bias term")
+        if logits_soft_cap is not None:
+            raise NotImplementedError("TT-KV does not support logits_soft_cap")
+        if sliding_window is not None:
+            raise NotImplementedError("TT-KV does not support a sliding window: the read attends "
+                                      "over the whole store")
+        if kv_sharing_target_layer_name is not None:
+            raise NotImplementedError("TT-KV does not support KV sharing: a shared layer would "
+                                      "read another layer's store and decoder")
+        if (AttentionType is not None and attn_type is not None
+                and attn_type != AttentionType.DECODER):  # pragma: no cover
+            raise NotImplementedError(f"TT-KV only supports decoder attention, got {attn_type!r}")
+        self.num_heads = num_heads
+        self.head_size = head_size
+        self.num_kv_heads = num_kv_heads or num_heads
+        self.scale = float(scale)
+        self.kv_cache_dtype = kv_cache_dtype
+        if num_heads % self.num_kv_heads:
+            raise ValueError(f"num_heads={num_heads} is not a multiple of "
+                             f"num_kv_heads={self.num_kv_heads}")
+        self.error_word = None
+        self._ws = None
+        self._pws = None
+
+    # ------------------------------------------------------------------ entry point
+    def forward(self, layer, query, key, value, kv_cache, attn_metadata, output=None,
+                output_scale=None, output_block_scale=None):
+        """`query`/`key` are post-RoPE (used by the first-chunk SDPA); the store is written from
+        the raw key stashed by the rotary call. Writes into `output` and returns it."""
+        if output_scale is not None or output_block_scale is not None:
+            raise NotImplementedError("TT-KV does not support fused output quantization")
+        if attn_metadata is None:
+            if output is None:
+                raise ValueError("attn_metadata and output are both None; nothing to write")
+            return output.fill_(0)
+        lay = self._layout(layer)
+        cache = self._cache_tensor(kv_cache)
+        md = attn_metadata
+        plan = BatchPlan.of(md)
+        N = plan.qsl[-1]
+        n_tokens = query.shape[0]
+        if output is None:
+            output = torch.empty(n_tokens, self.num_heads, self.head_size, dtype=query.dtype,
+                                 device=query.device)
+        actual = getattr(md, "num_actual_tokens", None)
+        if actual and int(actual) != N:
+            raise RuntimeError(f"query_start_loc says {N} query tokens but num_actual_tokens "
+                               f"says {actual}")
+        if N > n_tokens:
+            raise RuntimeError(f"metadata describes {N} query tokens but the query tensor holds "
+                               f"{n_tokens}")
+        if N == 0:
+            return output
+        if self.error_word is None or self.error_word.device != query.device:
+            self.error_word = torch.zeros(1, dtype=torch.int32, device=query.device)
+
+        name = getattr(layer, "layer_name", None)
+        stash = take_raw_k(name)                # pops: the write comes first, unconditionally
+        store = ensure_store(name, self._cos_sin_cache(layer, stash), lay, cache.shape[0])
+        self._write_store(lay, cache, stash, value, md, plan, store)
+
+        q3 = query.view(n_tokens, self.num_heads, self.head_size)
+        if plan.n_decodes:
+            nd = plan.n_decodes
+            self._decode(lay, cache, store, q3, md, nd, output)
+        if plan.prefills:
+            self._prefill(lay, cache, store, q3, key, value, md, plan, output)
+        if os.environ.get(CHECK_ENV):
+            torch.cuda.synchronize(query.device)
+            err = int(self.error_word.item())
+            if err:
+                raise RuntimeError(f"vllm_ttkv: device refusal bits {err} (1 no decoder, 2 block "
+                                   f"outside the cache, 4 padded/out-of-range slot id, 8 "
+                                   f"seq_len beyond max_seq_len) in layer {name!r}")
+        return output
+
+    # ------------------------------------------------------------------ write
+    def _write_store(self, lay, cache, stash, value, md, plan, store):
+        if value is None:
+            raise RuntimeError("no value tensor, so V cannot be stored")
+        if lay.H != self.num_kv_heads:
+            raise RuntimeError(f"the layout holds H={lay.H} head rows but this layer has "
+                               f"{self.num_kv_heads} KV heads")
+        N = plan.qsl[-1]
+        K = as_kv_heads(stash["raw_k"], lay.H, lay.d, "the captured raw key")[:N]
+        V = as_kv_heads(value, lay.H, lay.d, "value")[:N]
+        if not K.is_contiguous():
+            K = K.contiguous()
+        if not V.is_contiguous():
+            V = V.contiguous()
+        slots = md.slot_mapping[:N].to(torch.int64)
+        qsl_d = md.query_start_loc[:plan.n_reqs + 1].to(torch.int32)
+        bt = md.block_table.to(torch.int32)
+        if not plan.prefills:
+            # decode-only step: every request has a decoder; one launch, no host reads
+            kernels.write_paged(lay, K, V, slots, qsl_d, bt, store.dec_map, store.dec_pool,
+                                store.pinv_pool, cache, error_word=self.error_word)
+            return
+        # A step with prefill chunks: a request without a decoder is on its first chunk and is
+        # fitted (encode.py:257-298); one host read of the first block ids and lengths decides.
+        keys = [int(x) for x in md.block_table[:plan.n_reqs, 0].tolist()]
+        seq_lens = [int(x) for x in md.seq_lens[:plan.n_reqs].tolist()]
+        cfg = CONFIGS[os.environ.get("VLLM_TTKV_CONFIG", "safe")]
+        frozen, fitted = [], []
+        for r in range(plan.n_reqs):
+            s, e = plan.qsl[r], plan.qsl[r + 1]
+            if e <= s:
+                continue
+            if store.decoders.get(keys[r]) is None:
+                if seq_lens[r] != e - s:
+                    raise RuntimeError(
+                        f"request {keys[r]} arrives with seq_len={seq_lens[r]} but {e - s} tokens "
+                        f"in this step and has no fitted decoder: a continuation of a request "
+                        f"whose first chunk never reached the writer")
+                fk = enc.fit_into_budget(K[s:e].permute(1, 0, 2), lay, cfg)
+                store.register(keys[r], fk.decoder)
+                fitted.append((r, fk))
+            else:
+                frozen.append(r)
+        dev = K.device
+
+        def launch(reqs, cq=None, cs=None):
+            idx = torch.cat([torch.arange(plan.qsl[r], plan.qsl[r + 1], device=dev) for r in reqs])
+            starts = [0]
+            for r in reqs:
+                starts.append(starts[-1] + plan.qsl[r + 1] - plan.qsl[r])
+            sub_qsl = torch.tensor(starts, dtype=torch.int32, device=dev)
+            rows = torch.tensor(reqs, device=dev)
+            kernels.write_paged(lay, K[idx].contiguous(), V[idx].contiguous(), slots[idx], sub_qsl,
+                                bt[rows].contiguous(), store.dec_map, store.dec_pool,
+                                store.pinv_pool, cache, coeff_q_in=cq, coeff_scale_in=cs,
+                                error_word=self.error_word)
+
+        if frozen:
+            launch(frozen)
+        if fitted:
+            launch([r for r, _ in fitted], torch.cat([fk.coeff_q for _, fk in fitted]),
+                   torch.cat([fk.coeff_scale for _, fk in fitted]))
+
+    # ------------------------------------------------------------------ read
+    def _workspace(self, lay, num_reqs, max_seq_len, block_size, device):
+        need = _hip.lib().ttkv_decode_workspace_bytes(_hip.Layout.of(lay), self.num_heads,
+                                                      num_reqs, max_seq_len, block_size)
+        if self._ws is None or self._ws.numel() < need or self._ws.device != device:
+            self._ws = torch.zeros(max(int(need), 256), dtype=torch.uint8, device=device)
+        return self._ws
+
+    def _prefill_workspace(self, lay, num_reqs, max_q, max_seq, device):
+        need = _hip.lib().ttkv_prefill_workspace_bytes(_hip.Layout.of(lay), self.num_heads,
+                                                       num_reqs, max_q, max_seq)
+        if self._pws is None or self._pws.numel() < need or self._pws.device != device:
+            self._pws = torch.zeros(max(int(need), 256), dtype=torch.uint8, device=device)
+        return self._pws
+
+    def _decode(self, lay, cache, store, q3, md, nd, output):
+        bs = self._block_size(cache)
+        max_len = int(md.max_seq_len) if md.max_seq_len else int(md.seq_lens[:nd].max())
+        kernels.decode_paged(lay, q3, cache, bs, md.block_table[:nd].to(torch.int32),
+                             md.seq_lens[:nd].to(torch.int32),
+                             md.query_start_loc[:nd + 1].to(torch.int32), max_len, store.dec_map,
+                             store.dec_pool, store.cos_sin_cache, self.scale, out=output,
+                             workspace=self._workspace(lay, nd, max_len, bs, q3.device),
+                             error_word=self.error_word)
+
+    def _prefill(self, lay, cache, store, q3, key, value, md, plan, output):
+        seq_lens = [int(x) for x in md.seq_lens[:plan.n_reqs].tolist()]
+        cont = []
+        for r in plan.prefills:
+            s, e = plan.qsl[r], plan.qsl[r + 1]
+            q_len, seq = e - s, seq_lens[r]
+            if seq < q_len:
+                raise RuntimeError(f"request {r} has seq_len={seq} but {q_len} query tokens")
+            if seq == q_len:
+                output[s:e] = self._sdpa(q3[s:e], key[s:e], value[s:e]).to(output.dtype)
+            else:
+                cont.append(r)
+        if cont:
+            # every continuation chunk of the step in one K2 launch
+            max_q = max(plan.qsl[r + 1] - plan.qsl[r] for r in cont)
+            max_seq = max(seq_lens[r] for r in cont)
+            dev = q3.device
+            kernels.prefill_paged(
+                lay, q3, cache, self._block_size(cache), md.block_table.to(torch.int32),
+                md.seq_lens.to(torch.int32), md.query_start_loc.to(torch.int32), max_q, max_seq,
+                store.dec_map, store.dec_pool, store.cos_sin_cache, self.scale,
+                req_index=torch.tensor(cont, dtype=torch.int32, device=dev), out=output,
+                workspace=self._prefill_workspace(lay, len(cont), max_q, max_seq, dev),
+                error_word=self.error_word)
+
+    def _sdpa(self, q, k, v):
+        """First chunk: causal SDPA over the chunk's own post-RoPE q/k/v, in fp32
+        (decode.py:363-389)."""
+        G = self.num_heads // self.num_kv_heads
+        k = as_kv_heads(k, self.num_kv_heads, self.head_size, "key").float()
+        v = as_kv_heads(v, self.num_kv_heads, self.head_size, "value").float()
+        T = q.shape[0]
+        kk = k[:, :, None, :].expand(T, self.num_kv_heads, G, self.head_size).reshape(
+            T, self.num_heads, self.head_size)
+        vv = v[:, :, None, :].expand(T, self.num_kv_heads, G, self.head_size).reshape(
+            T, self.num_heads, self.head_size)
+        o = torch.nn.functional.scaled_dot_product_attention(
+            q.float().transpose(0, 1).unsqueeze(0), kk.transpose(0, 1).unsqueeze(0),
+            vv.transpose(0, 1).unsqueeze(0), is_causal=True, scale=self.scale)
+        return o.squeeze(0).transpose(0, 1)
+
+    # ------------------------------------------------------------------ resolution / guards
+    def _layout(self, layer) -> TTKLayout:
+        lay = getattr(layer, "ttkv_layout", None)
+        if lay is None:
+            lay = layout_for_layer(getattr(layer, "layer_name", None))
+        if lay is None:
+            raise RuntimeError(f"no TT-KV layout for layer {getattr(layer, 'layer_name', None)!r}"
+                               f"; load a calibration table (VLLM_TTKV_CALIBRATION)")
+        if lay.d != self.head_size:
+            raise RuntimeError(f"the layout was built for head_dim={lay.d} but this layer has "
+                               f"head_size={self.head_size}")
+        return lay
+
+    @staticmethod
+    def _cache_tensor(kv_cache):
+        if isinstance(kv_cache, (tuple, list)):
+            raise RuntimeError(f"expected ONE cache tensor but got {len(kv_cache)}: K and V "
+                               f"share one region per token")
+        return kv_cache
+
+    @staticmethod
+    def _block_size(cache) -> int:
+        if cache.dim() == 4:
+            return int(cache.shape[2])
+        if cache.dim() == 3:
+            return int(cache.shape[1])
+        raise ValueError(f"expected an LBNHC page [num_blocks, head_slots, block_size, C], got "
+                         f"{tuple(cache.shape)}")
+
+    @staticmethod
+    def _cos_sin_cache(layer, stash):
+        csc = stash.get("cos_sin_cache")
+        if csc is None:
+            csc = getattr(getattr(layer, "rotary_emb", None), "cos_sin_cache", None)
+        if csc is None:
+            raise RuntimeError(f"layer {getattr(layer, 'layer_name', None)!r} has no RoPE table "
+                               f"(the rotary stash and layer.rotary_emb both lack one)")
+        return csc

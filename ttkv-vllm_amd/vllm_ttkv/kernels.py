@@ -165,3 +165,125 @@ def write_paged(lay: TTKLayout, key: torch.Tensor, value: torch.Tensor,
         _hip.ptr(coeff_out), _hip.ptr(resid_out), error_word.data_ptr(),
         _hip.stream_ptr(key.device))
     _hip.check(rc, "ttkv_write_paged")
+
+
+def _read_checks(lay: TTKLayout, query, page, block_table, seq_lens, query_start_loc,
+                 dec_slot_of_block, dec_pool, cos_sin_cache):
+    """Host-visible checks shared by the read kernels (K1, K2)."""
+    _need_device(query, page, block_table, seq_lens, query_start_loc, dec_slot_of_block,
+                 dec_pool, cos_sin_cache)
+    if query.dim() != 3 or query.shape[2] != lay.d:
+        raise ValueError(f"query must be [N, num_heads, {lay.d}], got {tuple(query.shape)}")
+    if query.stride(2) != 1 or query.stride(1) != lay.d:
+        raise ValueError("query must be contiguous within a token ([HQ, d] rows)")
+    if query.dtype not in _hip.DTYPE_CODE:
+        raise ValueError("query dtype must be fp32, fp16 or bf16")
+    flat = page_bytes(page, lay.compressed_bytes_per_token())
+    _i32(block_table, "block_table")
+    _i32(seq_lens, "seq_lens")
+    _i32(query_start_loc, "query_start_loc")
+    _i32(dec_slot_of_block, "dec_slot_of_block")
+    if (dec_pool.dtype != torch.float32 or not dec_pool.is_contiguous() or dec_pool.dim() != 3
+            or tuple(dec_pool.shape[1:]) != (lay.r1, lay.H * lay.d)):
+        raise ValueError(f"dec_pool must be contiguous fp32 [slots, {lay.r1}, {lay.H * lay.d}], "
+                         f"got {tuple(dec_pool.shape)} {dec_pool.dtype}")
+    if cos_sin_cache.dtype != torch.float32 or not cos_sin_cache.is_contiguous():
+        raise ValueError("cos_sin_cache must be contiguous fp32 [max_pos, d]")
+    if cos_sin_cache.shape[-1] != lay.d:
+        raise NotImplementedError(
+            f"rotary_dim={cos_sin_cache.shape[-1]} != head_dim={lay.d} (partial rotary) is not "
+            f"supported: the kernels pair (j, j+d/2) across the whole row")
+    return flat
+
+
+def prefill_workspace(lay: TTKLayout, num_heads: int, num_reqs: int, max_q_len: int,
+                      max_seq_len: int, device) -> torch.Tensor:
+    n = _hip.lib().ttkv_prefill_workspace_bytes(_hip.Layout.of(lay), num_heads, num_reqs,
+                                                max_q_len, max_seq_len)
+    if n < 0:
+        raise ValueError("invalid layout / head count for the prefill workspace")
+    return torch.zeros(max(int(n), 256), dtype=torch.uint8, device=device)
+
+
+def prefill_paged(lay: TTKLayout, query: torch.Tensor, page: torch.Tensor, block_size: int,
+                  block_table: torch.Tensor, seq_lens: torch.Tensor,
+                  query_start_loc: torch.Tensor, max_q_len: int, max_seq_len: int,
+                  dec_slot_of_block: torch.Tensor, dec_pool: torch.Tensor,
+                  cos_sin_cache: torch.Tensor, scale: float,
+                  req_index: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                  workspace: torch.Tensor | None = None,
+                  error_word: torch.Tensor | None = None) -> torch.Tensor:
+    """K2: continuation attention for a batch of chunked-prefill requests, one launch.
+
+    Rows `query_start_loc[r] .. [r+1]` of `query` [N, HQ, d] (post-RoPE) attend causally over the
+    `seq_lens[r]` stored keys of request r (p0 = seq_len - q_len). `req_index` picks the batch
+    rows to process (default: all `seq_lens.numel()`). See `ttkv_prefill_paged`."""
+    flat = _read_checks(lay, query, page, block_table, seq_lens, query_start_loc,
+                        dec_slot_of_block, dec_pool, cos_sin_cache)
+    if req_index is not None:
+        _i32(req_index, "req_index")
+        num_reqs = int(req_index.numel())
+    else:
+        num_reqs = int(seq_lens.numel())
+    N, HQ, d = query.shape
+    if out is None:
+        out = torch.empty_like(query)
+    if out.shape != query.shape or out.stride(2) != 1 or out.stride(1) != d:
+        raise ValueError("out must match query's shape with contiguous [HQ, d] rows")
+    if out.dtype not in _hip.DTYPE_CODE:
+        raise ValueError("out dtype must be fp32, fp16 or bf16")
+    if workspace is None:
+        workspace = prefill_workspace(lay, HQ, num_reqs, max_q_len, max_seq_len, query.device)
+    if error_word is None:
+        error_word = torch.zeros(1, dtype=torch.int32, device=query.device)
+    rc = _hip.lib().ttkv_prefill_paged(
+        _hip.Layout.of(lay), HQ, float(scale),
+        query.data_ptr(), _hip.DTYPE_CODE[query.dtype], query.stride(0),
+        flat.data_ptr(), flat.shape[0], flat.stride(0),
+        int(block_size), block_table.data_ptr(), block_table.stride(0), block_table.shape[1],
+        seq_lens.data_ptr(), query_start_loc.data_ptr(), _hip.ptr(req_index), num_reqs,
+        int(max_q_len), int(max_seq_len),
+        dec_slot_of_block.data_ptr(), dec_slot_of_block.numel(), dec_pool.data_ptr(),
+        dec_pool.shape[0], cos_sin_cache.data_ptr(), cos_sin_cache.shape[0],
+        out.data_ptr(), _hip.DTYPE_CODE[out.dtype], out.stride(0),
+        workspace.data_ptr(), workspace.numel(), error_word.data_ptr(),
+        _hip.stream_ptr(query.device))
+    _hip.check(rc, "ttkv_prefill_paged")
+    return out
+
+
+def multi_scores_paged(lay: TTKLayout, query: torch.Tensor, page: torch.Tensor,
+                       block_size: int, block_table: torch.Tensor, seq_lens: torch.Tensor,
+                       query_start_loc: torch.Tensor, max_q_len: int, max_seq_len: int,
+                       dec_slot_of_block: torch.Tensor, dec_pool: torch.Tensor,
+                       cos_sin_cache: torch.Tensor, scale: float,
+                       scores: torch.Tensor | None = None,
+                       error_word: torch.Tensor | None = None) -> torch.Tensor:
+    """K2 scores mode for ONE request (row 0 of block_table / seq_lens / query_start_loc):
+    returns `scores` [HQ, Q, n] fp32 with -inf where key t > p0 + j (`krt_multi_from_slots`).
+    Q and n are `max_q_len` / `max_seq_len`, which must equal the request's own lengths."""
+    flat = _read_checks(lay, query, page, block_table, seq_lens, query_start_loc,
+                        dec_slot_of_block, dec_pool, cos_sin_cache)
+    HQ = query.shape[1]
+    if scores is None:
+        scores = torch.empty(HQ, max_q_len, max_seq_len, dtype=torch.float32,
+                             device=query.device)
+    if (scores.dtype != torch.float32 or scores.dim() != 3 or scores.shape[0] != HQ
+            or scores.shape[1] < max_q_len or scores.shape[2] < max_seq_len
+            or scores.stride(2) != 1):
+        raise ValueError(f"scores must be fp32 [{HQ}, >= {max_q_len}, >= {max_seq_len}] with "
+                         f"contiguous key rows")
+    if error_word is None:
+        error_word = torch.zeros(1, dtype=torch.int32, device=query.device)
+    rc = _hip.lib().ttkv_multi_scores_paged(
+        _hip.Layout.of(lay), HQ, float(scale),
+        query.data_ptr(), _hip.DTYPE_CODE[query.dtype], query.stride(0),
+        flat.data_ptr(), flat.shape[0], flat.stride(0),
+        int(block_size), block_table.data_ptr(), block_table.stride(0), block_table.shape[1],
+        seq_lens.data_ptr(), query_start_loc.data_ptr(), int(max_q_len), int(max_seq_len),
+        dec_slot_of_block.data_ptr(), dec_slot_of_block.numel(), dec_pool.data_ptr(),
+        dec_pool.shape[0], cos_sin_cache.data_ptr(), cos_sin_cache.shape[0],
+        scores.data_ptr(), scores.stride(0), scores.stride(1), error_word.data_ptr(),
+        _hip.stream_ptr(query.device))
+    _hip.check(rc, "ttkv_multi_scores_paged")
+    return scores
