@@ -282,6 +282,8 @@ def main():
     ap.add_argument("--layers", type=int, default=L_LAYERS)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
+    ap.add_argument("--config4-only", action="store_true",
+                    help="only the continuation workload (BASELINE config 4, K2); prints its line")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 1 GiB device copy (HBM-counter calibration for rocprofv3)")
     args = ap.parse_args()
@@ -300,6 +302,14 @@ def main():
     lay = layout_for_config(cfg, r1=R1)
     cache = rope.cos_sin_cache(16384, D, device=dev)
     extra = {}
+
+    if args.config4_only:
+        c4 = bench_config4(torch, lay, cfg, cache, dev, args.steps, args.warmup)
+        print(json.dumps(dict(metric="continuation chunk us/layer (K2, BASELINE config 4)",
+                              value=c4["us_per_chunk_layer"], unit="us", n_gpus=1,
+                              higher_is_better=False, dtype="f16 MFMA, fp32 accumulate",
+                              data="synthetic", **c4)))
+        return
 
     if args.calib_copy:
         src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
