@@ -227,6 +227,45 @@ def bench_config4(torch, lay, cfg, cache, dev, steps=10, warmup=3):
                 scores_mode_gbps_written=HQ * Q * n * 4 / (ms_s * 1e-3) / 1e9)
 
 
+def bench_dense(torch, lens, q, dev, steps=10, warmup=3):
+    """Dense fp16 paged attention of the same shapes (the per-cached-token comparison): this
+    build's dense HIP comparator over a shuffled paged cache, and torch SDPA over contiguous
+    per-request K/V (no paging)."""
+    from vllm_ttkv import kernels, synth
+    B = len(lens)
+    bt, nblk = synth.shuffled_block_table(lens, BS, seed=11, extra_blocks=2)
+    g = torch.Generator(device=dev).manual_seed(12)
+    kc = torch.randn(nblk * BS, H, D, generator=g, device=dev).to(torch.float16)
+    vc = torch.randn(nblk * BS, H, D, generator=g, device=dev).to(torch.float16)
+    bt_d = bt.to(dev)
+    sl = torch.tensor(lens, dtype=torch.int32, device=dev)
+    qsl = torch.arange(B + 1, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    n = kernels._hip.lib().ttkv_dense_workspace_bytes(H, HQ, B, max(lens), BS)
+    ws = torch.zeros(max(int(n), 256), dtype=torch.uint8, device=dev)
+
+    def run():
+        kernels.dense_decode_paged(q, kc, vc, BS, bt_d, sl, qsl, max(lens), D ** -0.5, out=out,
+                                   workspace=ws)
+
+    ms = time_launches(torch, run, steps, warmup)
+    del kc, vc
+    res = dict(us_per_layer=ms * 1e3, hbm_gbps=sum(lens) * H * D * 2 * 2 / (ms * 1e-3) / 1e9,
+               ns_per_cached_token=ms * 1e6 / sum(lens))
+    try:
+        import torch.nn.functional as F
+        kd = torch.randn(B, H, max(lens), D, generator=g, device=dev).to(torch.float16)
+        vd = torch.randn(B, H, max(lens), D, generator=g, device=dev).to(torch.float16)
+        q4 = q.reshape(B, HQ, 1, D)
+        ms_s = time_launches(torch, lambda: F.scaled_dot_product_attention(
+            q4, kd, vd, scale=D ** -0.5, enable_gqa=True), steps, warmup)
+        res["torch_sdpa_contiguous_us_per_layer"] = ms_s * 1e3
+        del kd, vd
+    except Exception as e:  # noqa: BLE001 - report, do not fail the bench line
+        res["torch_sdpa_contiguous_us_per_layer"] = f"unavailable: {type(e).__name__}"
+    return res
+
+
 def cpu_baseline(torch, lay, store, q, cache, n, budget_s=12.0):
     """The torch-CPU oracle (reference.py:149-163 restated, float32, the reference's request
     loop) on a bounded sample: request-layers of the headline workload, timed until `budget_s`."""
@@ -355,7 +394,17 @@ def main():
         extra["config3_b8_random"] = dict(contexts=lens3, us_per_layer=ml * 1e3,
                                           hbm_gbps=b / (ml * 1e-3) / 1e9,
                                           tokens_per_s=8 / (ml * 1e-3 * L_LAYERS))
+        dn = bench_dense(torch, lens3, q, dev)
+        dn["compressed_ns_per_cached_token"] = ml * 1e6 / sum(lens3)
+        extra["config3_dense_fp16_comparator"] = dn
+        log(f"dense fp16 comparator (config 3 shapes): {dn['us_per_layer']:.1f} us/layer, "
+            f"{dn['hbm_gbps']:.0f} GB/s")
         del st
+        dh = bench_dense(torch, lens, q, dev)
+        dh["compressed_ns_per_cached_token"] = ms_launch * 1e6 / sum(lens)
+        extra["headline_dense_fp16_comparator"] = dh
+        log(f"dense fp16 comparator (8x14402): {dh['us_per_layer']:.1f} us/layer, "
+            f"{dh['hbm_gbps']:.0f} GB/s")
         extra["config4_continuation"] = bench_config4(torch, lay, cfg, cache, dev)
 
     cpu = None

@@ -171,6 +171,22 @@ int ttkv_multi_scores_paged(const ttkv_layout* lay, int32_t num_heads, float sca
                             int64_t s_head_stride, int64_t s_q_stride, int32_t* error_word,
                             ttkv_stream_t stream);
 
+/* Benchmark comparator (no counterpart in the compressed path): dense paged decode attention over
+ * an uncompressed fp16/bf16 KV cache of the same shapes and launch structure as
+ * ttkv_decode_paged, for the "per-cached-token cost vs dense" comparison the reference's bench
+ * makes (bench_decode_read.py:132-151).
+ * k_cache / v_cache [n_slots, H, d] (dtype = TTKV_DTYPE_F16 or _BF16 for q, caches and out). */
+int64_t ttkv_dense_workspace_bytes(int32_t H, int32_t num_heads, int32_t num_reqs,
+                                   int32_t max_seq_len, int32_t block_size);
+int ttkv_dense_decode_paged(int32_t H, int32_t num_heads, int32_t d, float scale,
+                            const void* query, int64_t q_row_stride, const void* k_cache,
+                            const void* v_cache, int32_t dtype, int64_t n_slots,
+                            int32_t block_size, const int32_t* block_table,
+                            int64_t bt_row_stride, int32_t max_blocks, const int32_t* seq_lens,
+                            const int32_t* query_start_loc, int32_t num_reqs,
+                            int32_t max_seq_len, void* out, int64_t out_row_stride,
+                            void* workspace, int64_t workspace_bytes, ttkv_stream_t stream);
+
 /* Message for the last nonzero return on this thread. */
 const char* ttkv_last_error(void);
 

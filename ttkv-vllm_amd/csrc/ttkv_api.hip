@@ -139,4 +139,24 @@ int ttkv_multi_scores_paged(const ttkv_layout* lay, int32_t num_heads, float sca
                        (hipStream_t)stream);
 }
 
+int64_t ttkv_dense_workspace_bytes(int32_t H, int32_t num_heads, int32_t num_reqs,
+                                   int32_t max_seq_len, int32_t block_size) {
+  if (H <= 0 || num_heads <= 0 || num_heads % H || num_reqs < 0 || block_size <= 0) return -1;
+  return dense_workspace_bytes(H, num_heads / H, num_reqs, max_seq_len, block_size);
+}
+
+int ttkv_dense_decode_paged(int32_t H, int32_t num_heads, int32_t d, float scale,
+                            const void* query, int64_t q_row_stride, const void* k_cache,
+                            const void* v_cache, int32_t dtype, int64_t n_slots,
+                            int32_t block_size, const int32_t* block_table,
+                            int64_t bt_row_stride, int32_t max_blocks, const int32_t* seq_lens,
+                            const int32_t* query_start_loc, int32_t num_reqs,
+                            int32_t max_seq_len, void* out, int64_t out_row_stride,
+                            void* workspace, int64_t workspace_bytes, ttkv_stream_t stream) {
+  return dense_decode_paged(H, num_heads, d, scale, query, q_row_stride, k_cache, v_cache, dtype,
+                            n_slots, block_size, block_table, bt_row_stride, max_blocks, seq_lens,
+                            query_start_loc, num_reqs, max_seq_len, out, out_row_stride,
+                            workspace, workspace_bytes, (hipStream_t)stream);
+}
+
 }  // extern "C"

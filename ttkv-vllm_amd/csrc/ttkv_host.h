@@ -49,3 +49,13 @@ int prefill_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype
                   int64_t out_row_stride, float* s_out, int64_t s_head_stride, int64_t s_q_stride,
                   void* ws, int64_t ws_bytes, int32_t* err, hipStream_t st);
 }  // namespace ttkv
+
+namespace ttkv {
+int64_t dense_workspace_bytes(int H, int G, int num_reqs, int max_seq_len, int block_size);
+int dense_decode_paged(int H, int HQ, int d, float scale, const void* q, int64_t q_row_stride,
+                       const void* k_cache, const void* v_cache, int dtype, int64_t n_slots,
+                       int block_size, const int32_t* bt, int64_t bt_row_stride, int max_blocks,
+                       const int32_t* seq_lens, const int32_t* qsl, int num_reqs, int max_seq_len,
+                       void* out, int64_t out_row_stride, void* ws, int64_t ws_bytes,
+                       hipStream_t st);
+}  // namespace ttkv

@@ -112,6 +112,16 @@ def lib():
         P, I64, I64,                  # scores, s_head_stride, s_q_stride
         P, P,                         # error_word, stream
     ]
+    L.ttkv_dense_workspace_bytes.restype = I64
+    L.ttkv_dense_workspace_bytes.argtypes = [I32, I32, I32, I32, I32]
+    L.ttkv_dense_decode_paged.restype = ctypes.c_int
+    L.ttkv_dense_decode_paged.argtypes = [
+        I32, I32, I32, F32,           # H, num_heads, d, scale
+        P, I64, P, P, I32, I64,       # query, q_row_stride, k_cache, v_cache, dtype, n_slots
+        I32, P, I64, I32,             # block_size, block_table, bt_row_stride, max_blocks
+        P, P, I32, I32,               # seq_lens, query_start_loc, num_reqs, max_seq_len
+        P, I64, P, I64, P,            # out, out_row_stride, workspace, workspace_bytes, stream
+    ]
     for name in EXPORTS:
         getattr(L, name)  # every declared symbol must resolve
     _LIB = L
@@ -121,7 +131,8 @@ def lib():
 # Every symbol include/ttkv_hip.h declares (checked by tests/test_abi.py).
 EXPORTS = ("ttkv_last_error", "ttkv_blob_bytes", "ttkv_decode_workspace_bytes",
            "ttkv_decode_paged", "ttkv_write_paged", "ttkv_prefill_workspace_bytes",
-           "ttkv_prefill_paged", "ttkv_multi_scores_paged")
+           "ttkv_prefill_paged", "ttkv_multi_scores_paged", "ttkv_dense_workspace_bytes",
+           "ttkv_dense_decode_paged")
 
 
 def check(rc: int, what: str) -> None:

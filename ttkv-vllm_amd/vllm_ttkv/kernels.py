@@ -287,3 +287,40 @@ def multi_scores_paged(lay: TTKLayout, query: torch.Tensor, page: torch.Tensor,
         _hip.stream_ptr(query.device))
     _hip.check(rc, "ttkv_multi_scores_paged")
     return scores
+
+
+def dense_decode_paged(query: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                       block_size: int, block_table: torch.Tensor, seq_lens: torch.Tensor,
+                       query_start_loc: torch.Tensor, max_seq_len: int, scale: float,
+                       out: torch.Tensor | None = None,
+                       workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Benchmark comparator: dense paged decode attention over uncompressed caches
+    k_cache / v_cache [n_slots, H, d] (fp16 or bf16, same dtype as query). One launch."""
+    _need_device(query, k_cache, v_cache, block_table, seq_lens, query_start_loc)
+    N, HQ, d = query.shape
+    n_slots, H, d2 = k_cache.shape
+    if d2 != d or v_cache.shape != k_cache.shape:
+        raise ValueError("k_cache / v_cache must be [n_slots, H, d] with the query's d")
+    if query.dtype not in (torch.float16, torch.bfloat16) or k_cache.dtype != query.dtype \
+            or v_cache.dtype != query.dtype:
+        raise ValueError("dense comparator: query and caches must share fp16 or bf16")
+    for t in (query, k_cache, v_cache):
+        if not t.is_contiguous():
+            raise ValueError("dense comparator tensors must be contiguous")
+    _i32(block_table, "block_table")
+    _i32(seq_lens, "seq_lens")
+    _i32(query_start_loc, "query_start_loc")
+    B = int(seq_lens.numel())
+    if out is None:
+        out = torch.empty_like(query)
+    if workspace is None:
+        n = _hip.lib().ttkv_dense_workspace_bytes(H, HQ, B, int(max_seq_len), int(block_size))
+        workspace = torch.zeros(max(int(n), 256), dtype=torch.uint8, device=query.device)
+    rc = _hip.lib().ttkv_dense_decode_paged(
+        H, HQ, d, float(scale), query.data_ptr(), query.stride(0), k_cache.data_ptr(),
+        v_cache.data_ptr(), _hip.DTYPE_CODE[query.dtype], n_slots, int(block_size),
+        block_table.data_ptr(), block_table.stride(0), block_table.shape[1], seq_lens.data_ptr(),
+        query_start_loc.data_ptr(), B, int(max_seq_len), out.data_ptr(), out.stride(0),
+        workspace.data_ptr(), workspace.numel(), _hip.stream_ptr(query.device))
+    _hip.check(rc, "ttkv_dense_decode_paged")
+    return out
