@@ -60,7 +60,8 @@ def build_store(torch, lay, cfg, lens, n_layers, seed, dev, fit_on=FIT_ON, disti
         if li >= distinct:
             # replicate a built layer into this layer's own pages (distinct HBM addresses)
             src = layers[li % distinct]
-            layers.append(dict(page=src["page"].clone(), dec_pool=src["dec_pool"].clone()))
+            layers.append(dict(page=src["page"].clone(), dec_pool=src["dec_pool"].clone(),
+                               pinv_pool=src["pinv_pool"].clone()))
             continue
         page = torch.zeros(nblk * BS, C, dtype=torch.uint8, device=dev)
         dec_pool = torch.zeros(B, lay.r1, H * D, dtype=torch.float32, device=dev)
@@ -100,7 +101,7 @@ def build_store(torch, lay, cfg, lens, n_layers, seed, dev, fit_on=FIT_ON, disti
         torch.cuda.synchronize()
         t_write += time.perf_counter() - t0
         del first_k, first_v, rest
-        layers.append(dict(page=page, dec_pool=dec_pool))
+        layers.append(dict(page=page, dec_pool=dec_pool, pinv_pool=pinv_pool))
     if int(err.item()):
         raise RuntimeError(f"store build: device error word {int(err.item())}")
     return dict(layers=layers, bt=bt_d, dec_map=dec_map_d, nblk=nblk, B=B,
@@ -266,6 +267,82 @@ def bench_dense(torch, lens, q, dev, steps=10, warmup=3):
     return res
 
 
+def bench_config5(torch, cache, dev, steps=10, warmup=3, n_layers=L_LAYERS):
+    """the reference's 4-bit store (`campaign4x`: 64 lanes of 4-bit codes for
+    K residual and V, int8 coefficients, fp16 rulers), 8 requests at 16k context, 28 layers. Each
+    step writes one new key/value per request per layer (K3: projection onto the decoder, bitmap
+    select, quantise, pack, slot write) and then reads the layer (K1) -- both timed together."""
+    from vllm_ttkv import kernels, synth
+    from vllm_ttkv.layout import CONFIGS, layout_for_config
+    cfg5 = CONFIGS["campaign4x"]
+    lay5 = layout_for_config(cfg5, r1=R1)
+    ctx, B, spare = 16384, 8, 16
+    st = build_store(torch, lay5, cfg5, [ctx + spare] * B, n_layers, seed=6, dev=dev)
+    bt_cpu = st["bt"].cpu()
+    qsl_w = torch.arange(B + 1, dtype=torch.int32, device=dev)
+    newk = [synth.keys(spare, seed=900 + r, device=dev).permute(1, 0, 2) for r in range(B)]
+    newv = [synth.values(spare, seed=900 + r, device=dev).permute(1, 0, 2) for r in range(B)]
+    q = synth.queries(B, seed=9, device=dev)
+    out = torch.empty_like(q)
+    ws = kernels.decode_workspace(lay5, HQ, B, ctx + spare, dev, BS)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    plans = []
+    for j in range(spare):  # step j writes position ctx + j and reads ctx + j + 1 tokens
+        pos = ctx + j
+        slots = torch.tensor([int(bt_cpu[r, pos // BS]) * BS + pos % BS for r in range(B)],
+                             dtype=torch.int64, device=dev)
+        k_new = torch.stack([newk[r][j] for r in range(B)]).contiguous()
+        v_new = torch.stack([newv[r][j] for r in range(B)]).contiguous()
+        plans.append((slots, k_new, v_new, torch.full((B,), pos + 1, dtype=torch.int32,
+                                                      device=dev)))
+    ev = {"k3": [], "k1": []}
+    wws = kernels.write_workspace(lay5, B, dev)
+
+    def step(j, timed):
+        slots, k_new, v_new, sl = plans[j % spare]
+        for li in range(n_layers):
+            L = st["layers"][li]
+            e = [torch.cuda.Event(enable_timing=True) for _ in range(3)] if timed else None
+            if timed:
+                e[0].record()
+            kernels.write_paged(lay5, k_new, v_new, slots, qsl_w, st["bt"], st["dec_map"],
+                                L["dec_pool"], L["pinv_pool"], L["page"], error_word=err,
+                                workspace=wws)
+            if timed:
+                e[1].record()
+            kernels.decode_paged(lay5, q, L["page"], BS, st["bt"], sl, qsl_w, ctx + spare,
+                                 st["dec_map"], L["dec_pool"], cache, D ** -0.5, out=out,
+                                 workspace=ws, error_word=err)
+            if timed:
+                e[2].record()
+                ev["k3"].append((e[0], e[1]))
+                ev["k1"].append((e[1], e[2]))
+
+    for j in range(warmup):
+        step(j, False)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for j in range(steps):
+        step(warmup + j, True)
+    t1.record()
+    torch.cuda.synchronize()
+    if int(err.item()):
+        raise RuntimeError(f"config 5: device error word {int(err.item())}")
+    ms_step = t0.elapsed_time(t1) / steps
+    k3 = sum(a.elapsed_time(b) for a, b in ev["k3"]) / len(ev["k3"])
+    k1 = sum(a.elapsed_time(b) for a, b in ev["k1"]) / len(ev["k1"])
+    nbytes = k1_bytes(lay5, [ctx + 8] * B, R1, ctx + 8)
+    log(f"config5 campaign4x 8x16k: {ms_step * 1e3 / n_layers:.1f} us/layer (K3 {k3 * 1e3:.1f} "
+        f"+ K1 {k1 * 1e3:.1f})")
+    return dict(allocation="campaign4x (4-bit residual/V codes, int8 coefficients)",
+                requests=B, context=ctx, layers=n_layers, ms_per_step=ms_step,
+                us_per_layer=ms_step * 1e3 / n_layers, k3_us_per_launch=k3 * 1e3,
+                k1_us_per_launch=k1 * 1e3, tokens_per_s=B / (ms_step * 1e-3),
+                k1_hbm_gbps=nbytes / (k1 * 1e-3) / 1e9)
+
+
 def cpu_baseline(torch, lay, store, q, cache, n, budget_s=12.0):
     """The torch-CPU oracle (reference.py:149-163 restated, float32, the reference's request
     loop) on a bounded sample: request-layers of the headline workload, timed until `budget_s`."""
@@ -321,6 +398,8 @@ def main():
     ap.add_argument("--layers", type=int, default=L_LAYERS)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
+    ap.add_argument("--config5-only", action="store_true",
+                    help="only the 4-bit read+write workload (BASELINE config 5); prints its line")
     ap.add_argument("--config4-only", action="store_true",
                     help="only the continuation workload (BASELINE config 4, K2); prints its line")
     ap.add_argument("--calib-copy", action="store_true",
@@ -339,7 +418,7 @@ def main():
     dev = torch.device("cuda:0")
     cfg = CONFIGS["safe"]
     lay = layout_for_config(cfg, r1=R1)
-    cache = rope.cos_sin_cache(16384, D, device=dev)
+    cache = rope.cos_sin_cache(32768, D, device=dev)
     extra = {}
 
     if args.config4_only:
@@ -348,6 +427,14 @@ def main():
                               value=c4["us_per_chunk_layer"], unit="us", n_gpus=1,
                               higher_is_better=False, dtype="f16 MFMA, fp32 accumulate",
                               data="synthetic", **c4)))
+        return
+
+    if args.config5_only:
+        c5 = bench_config5(torch, cache, dev, args.steps, args.warmup)
+        print(json.dumps(dict(metric="4-bit decode step us/layer, K3 write + K1 read (BASELINE "
+                                     "config 5)", value=c5["us_per_layer"], unit="us",
+                              n_gpus=1, higher_is_better=False, dtype="f32", data="synthetic",
+                              **c5)))
         return
 
     if args.calib_copy:
@@ -406,6 +493,7 @@ def main():
         log(f"dense fp16 comparator (8x14402): {dh['us_per_layer']:.1f} us/layer, "
             f"{dh['hbm_gbps']:.0f} GB/s")
         extra["config4_continuation"] = bench_config4(torch, lay, cfg, cache, dev)
+        extra["config5_4bit_read_write"] = bench_config5(torch, cache, dev)
 
     cpu = None
     if not args.no_cpu:

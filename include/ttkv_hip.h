@@ -108,7 +108,10 @@ int ttkv_decode_paged(const ttkv_layout* lay, int32_t num_heads, float scale,
  * Bytes are bit-exact functions of R and value (select_triton.py:24-91): exact top-k by magnitude
  * (ties -> lowest lane), ruler = rowmax * fp32(1/(2^(b-1)-1)), q = rint(x / ruler) (IEEE div).
  * coeff_out [N, r1] and resid_out [N, H*d] (optional, fp32) receive c and R.
- * key/value: [N, H, d] rows with the given element stride between tokens. */
+ * key/value: [N, H, d] rows with the given element stride between tokens.
+ * Work is spread over (token, KV head) workgroups in two launches: per-head partial projections
+ * (the token's last workgroup sums them in head order and quantises) and, per head, the residual
+ * and the K and V rows. The partials live in `workspace` (ttkv_write_workspace_bytes). */
 int ttkv_write_paged(const ttkv_layout* lay, const void* key, int32_t k_dtype, int64_t k_row_stride,
                      const void* value, int32_t v_dtype, int64_t v_row_stride,
                      const int64_t* slot_mapping, int32_t num_tokens,
@@ -117,7 +120,12 @@ int ttkv_write_paged(const ttkv_layout* lay, const void* key, int32_t k_dtype, i
                      const float* dec_pool, const float* pinv_pool, int64_t n_dec_slots,
                      const int8_t* coeff_q_in, const float* coeff_scale_in, uint8_t* page,
                      int64_t n_slots, int64_t slot_stride, float* coeff_out, float* resid_out,
-                     int32_t* error_word, ttkv_stream_t stream);
+                     void* workspace, int64_t workspace_bytes, int32_t* error_word,
+                     ttkv_stream_t stream);
+
+/* Workspace bytes `ttkv_write_paged` needs for `num_tokens` projected tokens (none when the
+ * coefficients come from coeff_q_in). Zero-filled before first use; calls leave it reusable. */
+int64_t ttkv_write_workspace_bytes(const ttkv_layout* lay, int32_t num_tokens);
 
 /* Workspace bytes `ttkv_prefill_paged` needs for this batch shape (0 when one key split covers
  * every query block). Zero-filled before first use; every call leaves the counters zero. */

@@ -79,14 +79,21 @@ int ttkv_write_paged(const ttkv_layout* lay, const void* key, int32_t k_dtype, i
                      const float* dec_pool, const float* pinv_pool, int64_t n_dec_slots,
                      const int8_t* coeff_q_in, const float* coeff_scale_in, uint8_t* page,
                      int64_t n_slots, int64_t slot_stride, float* coeff_out, float* resid_out,
-                     int32_t* error_word, ttkv_stream_t stream) {
+                     void* workspace, int64_t workspace_bytes, int32_t* error_word,
+                     ttkv_stream_t stream) {
   Geom g;
   if (!make_geom(lay, &g)) return host_fail(TTKV_E_INVALID, "invalid layout");
   return write_paged(g, key, k_dtype, k_row_stride, value, v_dtype, v_row_stride, slot_mapping,
                      num_tokens, query_start_loc, num_reqs, block_table, bt_row_stride,
                      dec_slot_of_block, num_blocks, dec_pool, pinv_pool, n_dec_slots, coeff_q_in,
-                     coeff_scale_in, page, n_slots, slot_stride, coeff_out, resid_out, error_word,
-                     (hipStream_t)stream);
+                     coeff_scale_in, page, n_slots, slot_stride, coeff_out, resid_out, workspace,
+                     workspace_bytes, error_word, (hipStream_t)stream);
+}
+
+int64_t ttkv_write_workspace_bytes(const ttkv_layout* lay, int32_t num_tokens) {
+  Geom g;
+  if (!make_geom(lay, &g) || num_tokens < 0) return -1;
+  return write_workspace_bytes(g, num_tokens);
 }
 
 int64_t ttkv_prefill_workspace_bytes(const ttkv_layout* lay, int32_t num_heads, int32_t num_reqs,

@@ -38,7 +38,8 @@ namespace ttkv {
 constexpr int kTile = 64;
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
-constexpr int kRawDw = 16;      // dwords per staged head row (49-50 B rows + window slack)
+constexpr int kRawDw = 17;      // dwords per staged head row (49-50 B rows + window slack); odd so
+                                // threads reading the same offset of different rows hit distinct banks
 constexpr int kCodeStride = 144;  // bytes per code row (128 + bank stagger)
 constexpr int kSegMax = 260;    // block ids staged per chunk
 
@@ -81,7 +82,7 @@ struct DecodeSmem {
   uint32_t rawv[kTile][kRawDw];
   uint8_t kcode[kTile][kCodeStride];
   uint8_t vcode[kTile][kCodeStride];
-  float spart[kWaves][kTile][8];  // per wave partial scores (G <= 8)
+  float spart[kWaves][8][kTile];  // per wave partial scores [wave][head][token] (G <= 8)
   uint2 lut[256];
   int32_t seg[kSegMax];
   float cs[kTile];
@@ -135,14 +136,15 @@ __device__ __forceinline__ void prefetch(Prefetch<KSTEPS>& P, const uint8_t* bas
     const uint32_t* src = (const uint32_t*)(A & ~(uintptr_t)3);
     const int nsrc = (int)((A & 3) + g.k_row + 3) >> 2;
 #pragma unroll
-    for (int i = 0; i < 5; ++i) P.krow[i] = (part * 4 + i < nsrc) ? src[part * 4 + i] : 0u;
+    // clamped index: every load stays inside the row's dwords (the extra ones are never decoded)
+    for (int i = 0; i < 5; ++i) P.krow[i] = src[min(part * 4 + i, nsrc - 1)];
   }
   {
     const uintptr_t A = (uintptr_t)(base + v_row_off);
     const uint32_t* src = (const uint32_t*)(A & ~(uintptr_t)3);
     const int nsrc = (int)((A & 3) + g.v_row + 3) >> 2;
 #pragma unroll
-    for (int i = 0; i < 5; ++i) P.vrow[i] = (part * 4 + i < nsrc) ? src[part * 4 + i] : 0u;
+    for (int i = 0; i < 5; ++i) P.vrow[i] = src[min(part * 4 + i, nsrc - 1)];
   }
   P.rul = 0u;
   if (part == 0 && g.coeff_bytes + 2 > KSTEPS * 32)
@@ -387,7 +389,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
           sp = fmaf(qh[i], yh[i], sp);
         }
         sp = cross_row_sum(sp);
-        if (gq == (p & 3)) S.spart[wv][tok][p] = sp;
+        if (gq == (p & 3)) S.spart[wv][p][tok] = sp;
       }
     }
     // next tile's angles: issued after this tile's raw-byte prefetch, needed one tile later
@@ -402,8 +404,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
       const float vr = S.vrul[tok];
 #pragma unroll
       for (int p = 0; p < G; ++p) {
-        float s = S.spart[0][tok][p] + S.spart[1][tok][p] + S.spart[2][tok][p] +
-                  S.spart[3][tok][p];
+        float s = S.spart[0][p][tok] + S.spart[1][p][tok] + S.spart[2][p][tok] +
+                  S.spart[3][p][tok];
         s = valid ? s : -INFINITY;
         const float mt = wave_max(s);
         const float mn = fmaxf(m_run[p], mt);

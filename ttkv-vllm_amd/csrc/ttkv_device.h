@@ -59,25 +59,38 @@ __device__ __forceinline__ void decode_half_row(const uint32_t* row, int half, c
   // code c becomes c ^ 2^(b-1), so after the zero-filling scatter a final XOR restores c and
   // turns the zero bytes into the zero code 2^(b-1).
   constexpr uint32_t FLIP = BITS == 4 ? 0x88888888u : 0x92492400u;
-  int rank = 0;
-  if (half) rank = __builtin_popcount(row[0]) + __builtin_popcount(row[1]);
   const uint32_t bm0 = row[2 * half], bm1 = row[2 * half + 1];
+  int rank = half ? __builtin_popcount(row[0]) + __builtin_popcount(row[1]) : 0;
   const uint32_t* st = row + 4;
+  // All stream offsets follow from the bitmap alone, so every LDS read of the half row (8
+  // selector pairs, 16 window words) is issued before any of them is consumed.
+  uint32_t B[8];
+  int bp[8];
 #pragma unroll
   for (int m = 0; m < 8; ++m) {
-    const uint32_t B = __builtin_amdgcn_ubfe(m < 4 ? bm0 : bm1, 8 * (m & 3), 8);
-    const int bp = rank * BITS;
-    const int wi = bp >> 5;
-    const uint64_t pair = ((uint64_t)bswap32(st[wi]) << 32) | (uint64_t)bswap32(st[wi + 1]);
-    const uint32_t w = (uint32_t)((pair << (bp & 31)) >> 32) ^ FLIP;
+    B[m] = __builtin_amdgcn_ubfe(m < 4 ? bm0 : bm1, 8 * (m & 3), 8);
+    bp[m] = rank * BITS;
+    rank += __builtin_popcount(B[m]);
+  }
+  uint2 sel[8];
+  uint32_t w0[8], w1[8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    sel[m] = lut[B[m]];
+    const int wi = bp[m] >> 5;
+    w0[m] = st[wi];
+    w1[m] = st[wi + 1];
+  }
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    const uint64_t pair = ((uint64_t)bswap32(w0[m]) << 32) | (uint64_t)bswap32(w1[m]);
+    const uint32_t w = (uint32_t)((pair << (bp[m] & 31)) >> 32) ^ FLIP;
     uint32_t e0, e1;
     spread8<BITS>(w, e0, e1);
-    const uint2 sel = lut[B];
     uint2 out;
-    out.x = __builtin_amdgcn_perm(e1, e0, sel.x) ^ OFFB;
-    out.y = __builtin_amdgcn_perm(e1, e0, sel.y) ^ OFFB;
+    out.x = __builtin_amdgcn_perm(e1, e0, sel[m].x) ^ OFFB;
+    out.y = __builtin_amdgcn_perm(e1, e0, sel[m].y) ^ OFFB;
     *(uint2*)(dst + 8 * m) = out;
-    rank += __builtin_popcount(B);
   }
 }
 

@@ -33,7 +33,9 @@ int write_paged(const Geom& g, const void* key, int k_dtype, int64_t k_row_strid
                 const int32_t* dec_map, int64_t num_blocks, const float* dec_pool,
                 const float* pinv_pool, int64_t n_dec_slots, const int8_t* cq_in,
                 const float* cs_in, uint8_t* page, int64_t n_slots, int64_t slot_stride,
-                float* c_out, float* r_out, int32_t* err, hipStream_t st);
+                float* c_out, float* r_out, void* ws, int64_t ws_bytes, int32_t* err,
+                hipStream_t st);
+int64_t write_workspace_bytes(const Geom& g, int num_tokens);
 }  // namespace ttkv
 
 namespace ttkv {

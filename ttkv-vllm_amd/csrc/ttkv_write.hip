@@ -1,7 +1,12 @@
 // K3: write/encode of new tokens into compressed slots, one launch for all tokens of a layer.
 // gfx950 / CDNA4.
 //
-// One 256-thread workgroup per token:
+// Two launches, each with one 256-thread workgroup per (token, KV head), so a decode batch of B
+// tokens spreads its 2 x B x 450 KB of pinv / decoder reads over B x H CUs:
+//   K3a project  partial c_h[a] = sum_j M[h*d+j] * pinv[h*d+j][a] per head; the last workgroup of
+//             the token sums the H partials in head order (fixed, deterministic), quantises, and
+//             leaves (cq, cs) in the workspace                    -- skipped when a fit gives them
+//   K3b pack     the rest, per (token, head):
 //   project   c[a] = sum_m M[m] * pinv[m][a], M = the token's raw key flattened m = h*d + j
 //             (encode.py:322-324), fp32 in a fixed order          -- or take (cq, cs) from a fit
 //   quantise  cs = max|c| * fp32(1/127) (1 if 0); cq = clamp(rint(c / cs), -128, 127)
@@ -53,20 +58,31 @@ struct WriteArgs {
   float* c_out;
   float* r_out;
   int* err;
+  int* ws_cnt;      // [num_tokens] arrival counters (zero between calls)
+  float* ws_part;   // [num_tokens][H][r1] per-head partial projections
+  float* ws_q;      // [num_tokens][r1 + 1] cq (as floats) then cs
   float inv127, inv_rk, inv_rv;
 };
 
-struct WriteSmem {
-  float kraw[8 * kD];   // the token's raw key, flattened m = h*d + j (H <= 8)
-  float resid[8 * kD];  // R
-  float c[256];         // projection / coefficients (r1 <= 256)
-  float cpart[256];
-  float cqs[256];       // cq * cs (fp32)
-  float red[kWThreads / 64];
-  uint8_t codes[4][kD];  // per-wave code bytes by rank
-  int req;
-  int dslot;
-};
+// Request of token i (qsl[r] <= i < qsl[r+1]) and its decoder slot, or -1.
+__device__ int token_decoder(const WriteArgs& a, int i) {
+  int lo = 0, hi = a.num_reqs - 1, r = -1;
+  while (lo <= hi) {
+    const int mid = (lo + hi) >> 1;
+    if (a.qsl[mid] <= i) {
+      r = mid;
+      lo = mid + 1;
+    } else {
+      hi = mid - 1;
+    }
+  }
+  int ds = -1;
+  if (r >= 0 && i < a.qsl[r + 1]) {
+    const int blk0 = a.bt[(int64_t)r * a.bt_row_stride];
+    if (blk0 >= 0 && blk0 < a.num_blocks) ds = a.dec_map[blk0];
+  }
+  return (ds < 0 || ds >= a.n_dec_slots) ? -1 : ds;
+}
 
 // Exact top-k select + quantise + pack of one 128-lane row held as lane l: x0 = dim l,
 // x1 = dim l+64. Writes bitmap, codes and fp16 ruler at dst (any alignment). `codes` is this
@@ -144,129 +160,149 @@ __device__ void pack_row(float x0, float x1, int k, float inv_ruler, uint8_t* ds
   }
 }
 
-template <int RB, int VB>
-__global__ __launch_bounds__(kWThreads) void write_paged_kernel(WriteArgs a) {
-  __shared__ WriteSmem S;
+// K3a: per-head partial projections; the token's last workgroup combines and quantises.
+__global__ __launch_bounds__(kWThreads) void write_project_kernel(WriteArgs a) {
+  __shared__ float mk[kD];
+  __shared__ float part[2][256];
+  __shared__ float red[kWThreads / 64];
+  __shared__ int is_last;
   const Geom& g = a.g;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wv = tid >> 6;
-  const int i = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int i = blockIdx.x / g.H;
+  const int h = blockIdx.x % g.H;
   const int HD = g.H * kD;
-
-  if (tid == 0) {
-    // request of token i: qsl[r] <= i < qsl[r+1]
-    int lo = 0, hi = a.num_reqs - 1, r = -1;
-    while (lo <= hi) {
-      const int mid = (lo + hi) >> 1;
-      if (a.qsl[mid] <= i) {
-        r = mid;
-        lo = mid + 1;
-      } else {
-        hi = mid - 1;
-      }
+  const int64_t slot = a.slot_mapping[i];
+  const int ds = token_decoder(a, i);
+  if (ds < 0 || slot < 0 || slot >= a.n_slots) return;  // K3b reports it
+  if (tid < kD) mk[tid] = load_act(a.key, a.k_dtype, (int64_t)i * a.k_row_stride + h * kD + tid);
+  __syncthreads();
+  const float* pinv = a.pinv_pool + (int64_t)ds * HD * g.r1 + (int64_t)h * kD * g.r1;
+  float* pp = a.ws_part + ((int64_t)i * g.H + h) * g.r1;
+  const int half = tid >> 7, ar = tid & 127;
+  for (int a0 = 0; a0 < g.r1; a0 += 128) {
+    const int aa = a0 + ar;
+    float acc = 0.f;
+    if (aa < g.r1) {
+#pragma unroll 8
+      for (int j = 64 * half; j < 64 * half + 64; ++j)
+        acc = fmaf(mk[j], pinv[(int64_t)j * g.r1 + aa], acc);
     }
-    int ds = -1;
-    if (r >= 0 && i < a.qsl[r + 1]) {
-      const int blk0 = a.bt[(int64_t)r * a.bt_row_stride];
-      if (blk0 >= 0 && blk0 < a.num_blocks) ds = a.dec_map[blk0];
-    }
-    if (ds < 0 || ds >= a.n_dec_slots) {
-      atomicOr(a.err, TTKV_ERR_NO_DECODER);
-      ds = -1;
-    }
-    S.req = r;
-    S.dslot = ds;
+    part[half][ar] = acc;
+    __syncthreads();
+    if (half == 0 && aa < g.r1)
+      __hip_atomic_store(&pp[aa], part[0][ar] + part[1][ar], __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
   }
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0)
+    is_last = __hip_atomic_fetch_add(&a.ws_cnt[i], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+              g.H - 1;
+  __syncthreads();
+  if (!is_last) return;
+  // c[a] = sum over heads in head order
+  float* cq = a.ws_q + (int64_t)i * (g.r1 + 1);
+  float mx = 0.f;
+  float cv = 0.f;
+  const bool mine = tid < g.r1;
+  if (mine) {
+    const float* base = a.ws_part + (int64_t)i * g.H * g.r1;
+    for (int hh = 0; hh < g.H; ++hh)
+      cv += __hip_atomic_load(&base[hh * g.r1 + tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    mx = fabsf(cv);
+    if (a.c_out) a.c_out[(int64_t)i * g.r1 + tid] = cv;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if (lane == 0) red[wv] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float cs = mx * a.inv127;
+  if (cs == 0.f) cs = 1.f;
+  if (mine) cq[tid] = fminf(fmaxf(rintf(__fdiv_rn(cv, cs)), -128.f), 127.f);
+  if (tid == 0) {
+    cq[g.r1] = cs;
+    __hip_atomic_store(&a.ws_cnt[i], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// K3b: residual of head h, then its K row and V row; head 0 also writes the coefficients.
+template <int RB, int VB>
+__global__ __launch_bounds__(kWThreads) void write_pack_kernel(WriteArgs a) {
+  __shared__ float cqs[256];
+  __shared__ float rp[4][kD];
+  __shared__ uint8_t codes[2][kD];
+  const Geom& g = a.g;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int i = blockIdx.x / g.H;
+  const int h = blockIdx.x % g.H;
+  const int HD = g.H * kD;
   const int64_t slot = a.slot_mapping[i];
   const bool slot_ok = slot >= 0 && slot < a.n_slots;
-  if (!slot_ok && tid == 0) atomicOr(a.err, TTKV_ERR_BAD_SLOT);
-  for (int m = tid; m < HD; m += kWThreads)
-    S.kraw[m] = load_act(a.key, a.k_dtype, (int64_t)i * a.k_row_stride + m);
-  __syncthreads();
-  const int ds = S.dslot;
+  const int ds = token_decoder(a, i);
+  if (h == 0 && tid == 0) {
+    if (!slot_ok) atomicOr(a.err, TTKV_ERR_BAD_SLOT);
+    if (ds < 0) atomicOr(a.err, TTKV_ERR_NO_DECODER);
+  }
   if (ds < 0 || !slot_ok) return;
-  const float* dec = a.dec_pool + (int64_t)ds * g.r1 * HD;
-
-  // ---- coefficients
-  if (a.cq_in) {
-    for (int ar = tid; ar < g.r1; ar += kWThreads) S.c[ar] = (float)a.cq_in[(int64_t)i * g.r1 + ar];
-    __syncthreads();
-  } else {
-    const float* pinv = a.pinv_pool + (int64_t)ds * HD * g.r1;
-    // thread (ar, half): half of the 1024-long dot product, fixed order, then combined.
-    const int nh = kWThreads / 128 > 0 ? 2 : 1;
-    const int ar = tid & 127;
-    const int part = tid >> 7;
-    for (int a0 = 0; a0 < g.r1; a0 += 128) {
-      const int aa = a0 + ar;
-      float acc = 0.f;
-      if (aa < g.r1) {
-        const int m0 = part * (HD / nh), m1 = m0 + HD / nh;
-        for (int m = m0; m < m1; ++m) acc = fmaf(S.kraw[m], pinv[(int64_t)m * g.r1 + aa], acc);
-      }
-      if (part == 1 && aa < g.r1) S.cpart[aa] = acc;
-      __syncthreads();
-      if (part == 0 && aa < g.r1) S.c[aa] = acc + S.cpart[aa];
-      __syncthreads();
-    }
-    // max |c|
-    float mx = 0.f;
-    for (int ar2 = tid; ar2 < g.r1; ar2 += kWThreads) mx = fmaxf(mx, fabsf(S.c[ar2]));
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    if (lane == 0) S.red[wv] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(S.red[0], S.red[1]), fmaxf(S.red[2], S.red[3]));
-    float cs = mx * a.inv127;
-    if (cs == 0.f) cs = 1.f;
-    if (a.c_out)
-      for (int ar2 = tid; ar2 < g.r1; ar2 += kWThreads) a.c_out[(int64_t)i * g.r1 + ar2] = S.c[ar2];
-    __syncthreads();
-    for (int ar2 = tid; ar2 < g.r1; ar2 += kWThreads)
-      S.c[ar2] = fminf(fmaxf(rintf(__fdiv_rn(S.c[ar2], cs)), -128.f), 127.f);
-    if (tid == 0) S.red[0] = cs;
-    __syncthreads();
-  }
-  const float cs = a.cq_in ? a.cs_in[i] : S.red[0];
-  uint8_t* base = a.page + slot * a.slot_stride;
+  const float cs = a.cq_in ? a.cs_in[i] : a.ws_q[(int64_t)i * (g.r1 + 1) + g.r1];
   for (int ar = tid; ar < g.r1; ar += kWThreads) {
-    S.cqs[ar] = S.c[ar] * cs;
-    base[ar] = (uint8_t)(int8_t)(int)S.c[ar];
+    const float q = a.cq_in ? (float)a.cq_in[(int64_t)i * g.r1 + ar]
+                            : a.ws_q[(int64_t)i * (g.r1 + 1) + ar];
+    cqs[ar] = q * cs;
   }
-  if (tid == 0) {
-    const uint16_t hb = __builtin_bit_cast(uint16_t, (_Float16)cs);
-    base[g.coeff_bytes] = (uint8_t)(hb & 0xff);
-    base[g.coeff_bytes + 1] = (uint8_t)(hb >> 8);
-  }
-  // zero padding after the last K row and after the last V row
-  for (int b = g.k_field + g.H * g.k_row + tid; b < g.k_slot; b += kWThreads) base[b] = 0;
-  for (int b = g.k_slot + g.H * g.v_row + tid; b < g.blob; b += kWThreads) base[b] = 0;
-  __syncthreads();
-
-  // ---- residual R = K - (cq*cs) @ decoder_f
-  for (int m = tid; m < HD; m += kWThreads) {
-    float acc = 0.f;
-    for (int ar = 0; ar < g.r1; ++ar) acc = fmaf(S.cqs[ar], dec[(int64_t)ar * HD + m], acc);
-    const float R = S.kraw[m] - acc;
-    S.resid[m] = R;
-    if (a.r_out) a.r_out[(int64_t)i * HD + m] = R;
+  uint8_t* base = a.page + slot * a.slot_stride;
+  if (h == 0) {
+    for (int ar = tid; ar < g.r1; ar += kWThreads) {
+      const float q = a.cq_in ? (float)a.cq_in[(int64_t)i * g.r1 + ar]
+                              : a.ws_q[(int64_t)i * (g.r1 + 1) + ar];
+      base[ar] = (uint8_t)(int8_t)(int)q;
+    }
+    if (tid == 0) {
+      const uint16_t hb = __builtin_bit_cast(uint16_t, (_Float16)cs);
+      base[g.coeff_bytes] = (uint8_t)(hb & 0xff);
+      base[g.coeff_bytes + 1] = (uint8_t)(hb >> 8);
+    }
+    for (int b = g.k_field + g.H * g.k_row + tid; b < g.k_slot; b += kWThreads) base[b] = 0;
+    for (int b = g.k_slot + g.H * g.v_row + tid; b < g.blob; b += kWThreads) base[b] = 0;
   }
   __syncthreads();
-
-  // ---- rows: wave wv packs heads wv, wv+4 (K residual, then V)
-  for (int h = wv; h < g.H; h += 4) {
-    pack_row<RB>(S.resid[h * kD + lane], S.resid[h * kD + 64 + lane], g.res_k, a.inv_rk,
-                 base + g.k_field + h * g.k_row, S.codes[wv]);
-    __builtin_amdgcn_wave_barrier();
+  // R[j] = K[h*d+j] - sum_a cqs[a] * dec[a][h*d+j]: wave w sums a = w, w+4, ...; lanes own j, j+64
+  const float* dec = a.dec_pool + (int64_t)ds * g.r1 * HD + h * kD;
+  float acc0 = 0.f, acc1 = 0.f;
+  for (int ar = wv; ar < g.r1; ar += 4) {
+    const float c = cqs[ar];
+    acc0 = fmaf(c, dec[(int64_t)ar * HD + lane], acc0);
+    acc1 = fmaf(c, dec[(int64_t)ar * HD + 64 + lane], acc1);
+  }
+  rp[wv][lane] = acc0;
+  rp[wv][64 + lane] = acc1;
+  __syncthreads();
+  if (wv == 0) {
+    const int64_t kb = (int64_t)i * a.k_row_stride + h * kD;
+    float r0 = load_act(a.key, a.k_dtype, kb + lane) -
+               (((rp[0][lane] + rp[1][lane]) + rp[2][lane]) + rp[3][lane]);
+    float r1v = load_act(a.key, a.k_dtype, kb + 64 + lane) -
+                (((rp[0][64 + lane] + rp[1][64 + lane]) + rp[2][64 + lane]) + rp[3][64 + lane]);
+    if (a.r_out) {
+      a.r_out[(int64_t)i * HD + h * kD + lane] = r0;
+      a.r_out[(int64_t)i * HD + h * kD + 64 + lane] = r1v;
+    }
+    pack_row<RB>(r0, r1v, g.res_k, a.inv_rk, base + g.k_field + h * g.k_row, codes[0]);
+  } else if (wv == 1) {
     const int64_t vb = (int64_t)i * a.v_row_stride + h * kD;
     pack_row<VB>(load_act(a.val, a.v_dtype, vb + lane), load_act(a.val, a.v_dtype, vb + 64 + lane),
-                 g.v_lanes, a.inv_rv, base + g.k_slot + h * g.v_row, S.codes[wv]);
-    __builtin_amdgcn_wave_barrier();
+                 g.v_lanes, a.inv_rv, base + g.k_slot + h * g.v_row, codes[1]);
   }
 }
 
 static float inv_ruler_f32(int bits) { return (float)(1.0 / (double)((1 << (bits - 1)) - 1)); }
+
+int64_t write_workspace_bytes(const Geom& g, int num_tokens) {
+  const int64_t cnt = ((int64_t)std::max(num_tokens, 0) * 4 + 255) / 256 * 256;
+  return cnt + (int64_t)std::max(num_tokens, 0) * (g.H * g.r1 + g.r1 + 1) * 4;
+}
 
 int write_paged(const Geom& g, const void* key, int k_dtype, int64_t k_row_stride, const void* val,
                 int v_dtype, int64_t v_row_stride, const int64_t* slot_mapping, int num_tokens,
@@ -274,7 +310,8 @@ int write_paged(const Geom& g, const void* key, int k_dtype, int64_t k_row_strid
                 const int32_t* dec_map, int64_t num_blocks, const float* dec_pool,
                 const float* pinv_pool, int64_t n_dec_slots, const int8_t* cq_in,
                 const float* cs_in, uint8_t* page, int64_t n_slots, int64_t slot_stride,
-                float* c_out, float* r_out, int32_t* err, hipStream_t st) {
+                float* c_out, float* r_out, void* ws, int64_t ws_bytes, int32_t* err,
+                hipStream_t st) {
   if (g.d != kD) return host_fail(TTKV_E_UNSUPPORTED, "head dim must be 128");
   if (g.H > 8) return host_fail(TTKV_E_UNSUPPORTED, "H > 8 KV heads is not built");
   if (g.qbits != 8) return host_fail(TTKV_E_UNSUPPORTED, "coefficient width must be 8 bits");
@@ -291,6 +328,13 @@ int write_paged(const Geom& g, const void* key, int k_dtype, int64_t k_row_strid
     return host_fail(TTKV_E_INVALID, "dtype code");
   if (num_tokens < 0 || num_reqs < 0) return host_fail(TTKV_E_INVALID, "negative size");
   if (num_tokens == 0) return TTKV_OK;
+  if (!cq_in) {
+    const int64_t need = write_workspace_bytes(g, num_tokens);
+    if (!ws || ws_bytes < need || (uintptr_t)ws % 256)
+      return host_fail(TTKV_E_WORKSPACE, "write workspace needs " + std::to_string(need) +
+                                             " bytes (256-aligned), got " +
+                                             std::to_string(ws_bytes));
+  }
   WriteArgs a{};
   a.g = g;
   a.key = key;
@@ -318,13 +362,21 @@ int write_paged(const Geom& g, const void* key, int k_dtype, int64_t k_row_strid
   a.c_out = c_out;
   a.r_out = r_out;
   a.err = err;
+  if (!cq_in) {
+    const int64_t cnt = ((int64_t)num_tokens * 4 + 255) / 256 * 256;
+    a.ws_cnt = (int*)ws;
+    a.ws_part = (float*)((char*)ws + cnt);
+    a.ws_q = a.ws_part + (int64_t)num_tokens * g.H * g.r1;
+  }
   a.inv127 = inv_ruler_f32(8);
   a.inv_rk = inv_ruler_f32(g.res_bits);
   a.inv_rv = inv_ruler_f32(g.v_bits);
+  const int grid = num_tokens * g.H;
+  if (!cq_in) hipLaunchKernelGGL(write_project_kernel, dim3(grid), dim3(kWThreads), 0, st, a);
   if (g.res_bits == 3)
-    hipLaunchKernelGGL((write_paged_kernel<3, 3>), dim3(num_tokens), dim3(kWThreads), 0, st, a);
+    hipLaunchKernelGGL((write_pack_kernel<3, 3>), dim3(grid), dim3(kWThreads), 0, st, a);
   else
-    hipLaunchKernelGGL((write_paged_kernel<4, 4>), dim3(num_tokens), dim3(kWThreads), 0, st, a);
+    hipLaunchKernelGGL((write_pack_kernel<4, 4>), dim3(grid), dim3(kWThreads), 0, st, a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return host_fail(TTKV_E_LAUNCH, std::string("write launch: ") +
                                                           hipGetErrorString(e));

@@ -82,8 +82,11 @@ def lib():
         P, P, I64,                    # dec_pool, pinv_pool, n_dec_slots
         P, P,                         # coeff_q_in, coeff_scale_in
         P, I64, I64,                  # page, n_slots, slot_stride
-        P, P, P, P,                   # coeff_out, resid_out, error_word, stream
+        P, P,                         # coeff_out, resid_out
+        P, I64, P, P,                 # workspace, workspace_bytes, error_word, stream
     ]
+    L.ttkv_write_workspace_bytes.restype = I64
+    L.ttkv_write_workspace_bytes.argtypes = [LP, I32]
     L.ttkv_prefill_workspace_bytes.restype = I64
     L.ttkv_prefill_workspace_bytes.argtypes = [LP, I32, I32, I32, I32]
     L.ttkv_prefill_paged.restype = ctypes.c_int
@@ -132,7 +135,7 @@ def lib():
 EXPORTS = ("ttkv_last_error", "ttkv_blob_bytes", "ttkv_decode_workspace_bytes",
            "ttkv_decode_paged", "ttkv_write_paged", "ttkv_prefill_workspace_bytes",
            "ttkv_prefill_paged", "ttkv_multi_scores_paged", "ttkv_dense_workspace_bytes",
-           "ttkv_dense_decode_paged")
+           "ttkv_dense_decode_paged", "ttkv_write_workspace_bytes")
 
 
 def check(rc: int, what: str) -> None:

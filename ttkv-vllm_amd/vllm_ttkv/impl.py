@@ -118,6 +118,7 @@ class TTKVAttentionImpl(_ImplBase):
         self.error_word = None
         self._ws = None
         self._pws = None
+        self._wws = None
 
     # ------------------------------------------------------------------ entry point
     def forward(self, layer, query, key, value, kv_cache, attn_metadata, output=None,
@@ -191,7 +192,8 @@ class TTKVAttentionImpl(_ImplBase):
         if not plan.prefills:
             # decode-only step: every request has a decoder; one launch, no host reads
             kernels.write_paged(lay, K, V, slots, qsl_d, bt, store.dec_map, store.dec_pool,
-                                store.pinv_pool, cache, error_word=self.error_word)
+                                store.pinv_pool, cache, error_word=self.error_word,
+                                workspace=self._write_workspace(lay, N, K.device))
             return
         # A step with prefill chunks: a request without a decoder is on its first chunk and is
         # fitted (encode.py:257-298); one host read of the first block ids and lengths decides.
@@ -226,7 +228,9 @@ class TTKVAttentionImpl(_ImplBase):
             kernels.write_paged(lay, K[idx].contiguous(), V[idx].contiguous(), slots[idx], sub_qsl,
                                 bt[rows].contiguous(), store.dec_map, store.dec_pool,
                                 store.pinv_pool, cache, coeff_q_in=cq, coeff_scale_in=cs,
-                                error_word=self.error_word)
+                                error_word=self.error_word,
+                                workspace=None if cq is not None else
+                                self._write_workspace(lay, len(idx), dev))
 
         if frozen:
             launch(frozen)
@@ -241,6 +245,12 @@ class TTKVAttentionImpl(_ImplBase):
         if self._ws is None or self._ws.numel() < need or self._ws.device != device:
             self._ws = torch.zeros(max(int(need), 256), dtype=torch.uint8, device=device)
         return self._ws
+
+    def _write_workspace(self, lay, num_tokens, device):
+        need = _hip.lib().ttkv_write_workspace_bytes(_hip.Layout.of(lay), num_tokens)
+        if self._wws is None or self._wws.numel() < need or self._wws.device != device:
+            self._wws = torch.zeros(max(int(need), 256), dtype=torch.uint8, device=device)
+        return self._wws
 
     def _prefill_workspace(self, lay, num_reqs, max_q, max_seq, device):
         need = _hip.lib().ttkv_prefill_workspace_bytes(_hip.Layout.of(lay), self.num_heads,

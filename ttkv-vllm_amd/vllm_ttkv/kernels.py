@@ -120,7 +120,8 @@ def write_paged(lay: TTKLayout, key: torch.Tensor, value: torch.Tensor,
                 coeff_q_in: torch.Tensor | None = None,
                 coeff_scale_in: torch.Tensor | None = None,
                 coeff_out: torch.Tensor | None = None, resid_out: torch.Tensor | None = None,
-                error_word: torch.Tensor | None = None) -> None:
+                error_word: torch.Tensor | None = None,
+                workspace: torch.Tensor | None = None) -> None:
     """K3: encode + pack `key`/`value` ([N, H, d], raw pre-RoPE keys) into their slots.
 
     See `ttkv_write_paged` in include/ttkv_hip.h. `pinv_pool` [slots, H*d, r1] fp32 drives the
@@ -155,6 +156,8 @@ def write_paged(lay: TTKLayout, key: torch.Tensor, value: torch.Tensor,
         if coeff_scale_in is None:
             raise ValueError("coeff_q_in needs coeff_scale_in (fp32)")
         coeff_scale_in = coeff_scale_in.to(torch.float32).contiguous()
+    if workspace is None and cq is None:
+        workspace = write_workspace(lay, N, key.device)
     rc = _hip.lib().ttkv_write_paged(
         _hip.Layout.of(lay), key.data_ptr(), _hip.DTYPE_CODE[key.dtype], key.stride(0),
         value.data_ptr(), _hip.DTYPE_CODE[value.dtype], value.stride(0),
@@ -162,9 +165,18 @@ def write_paged(lay: TTKLayout, key: torch.Tensor, value: torch.Tensor,
         block_table.data_ptr(), block_table.stride(0), dec_slot_of_block.data_ptr(),
         dec_slot_of_block.numel(), dec_pool.data_ptr(), _hip.ptr(pinv_pool), dec_pool.shape[0],
         _hip.ptr(cq), _hip.ptr(coeff_scale_in), flat.data_ptr(), flat.shape[0], flat.stride(0),
-        _hip.ptr(coeff_out), _hip.ptr(resid_out), error_word.data_ptr(),
+        _hip.ptr(coeff_out), _hip.ptr(resid_out), _hip.ptr(workspace),
+        0 if workspace is None else workspace.numel(), error_word.data_ptr(),
         _hip.stream_ptr(key.device))
     _hip.check(rc, "ttkv_write_paged")
+
+
+def write_workspace(lay: TTKLayout, num_tokens: int, device) -> torch.Tensor:
+    """A zero-filled workspace for `write_paged` over `num_tokens` projected tokens."""
+    n = _hip.lib().ttkv_write_workspace_bytes(_hip.Layout.of(lay), int(num_tokens))
+    if n < 0:
+        raise ValueError("invalid layout for the write workspace")
+    return torch.zeros(max(int(n), 256), dtype=torch.uint8, device=device)
 
 
 def _read_checks(lay: TTKLayout, query, page, block_table, seq_lens, query_start_loc,
