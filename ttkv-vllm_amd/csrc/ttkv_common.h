@@ -19,6 +19,7 @@ namespace ttkv {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kD = 128;           // head dim the kernels are built for
 constexpr int kBitmapBytes = kD / 8;
@@ -52,6 +53,14 @@ __host__ inline bool make_geom(const ttkv_layout* l, Geom* g) {
   g->v_slot = align_up16(g->H * g->v_row);
   g->blob = g->k_slot + g->v_slot;
   return true;
+}
+
+// A pointer known to be in global memory, so loads through it are global_load_* (vector memory
+// counter only). Loads through a generic pointer become flat_load_*, which also count against the
+// LDS counter, so every later LDS wait would also wait for them.
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* gbl(const T* p) {
+  return (const __attribute__((address_space(1))) T*)p;
 }
 
 __device__ __forceinline__ float f16_bits_to_float(uint32_t bits16) {

@@ -19,7 +19,8 @@
 //   rope+qk : k = cs * acc + ruler * (code - 2^(b-1)); rotate by the row's absolute position; fp32
 //             dot with the G query heads (pre-scaled by scale * log2 e); partial dots reduced
 //             across the 4 lane groups and the 4 waves.
-//   softmax : online, base 2, evaluated redundantly by every wave (no extra barrier).
+//   softmax : online, base 2, evaluated redundantly by every wave (no extra barrier), with the
+//             rescale skipped unless the running max grows by more than 2^8.
 //   P.V     : o[p] += P[p,t] * ruler_v[t] * code; the 2^(b-1) offset is removed once at the end
 //             through the running sum of P * ruler_v.
 // Chunks of one (r, h) are combined in the same launch by the last workgroup to finish
@@ -84,6 +85,7 @@ struct DecodeSmem {
   uint8_t vcode[kTile][kCodeStride];
   float spart[kWaves][8][kTile];  // per wave partial scores [wave][head][token] (G <= 8)
   uint2 lut[256];
+  uint32_t lut3[4096];
   int32_t seg[kSegMax];
   float cs[kTile];
   float krul[kTile];
@@ -147,8 +149,7 @@ __device__ __forceinline__ void prefetch(Prefetch<KSTEPS>& P, const uint8_t* bas
     for (int i = 0; i < 5; ++i) P.vrow[i] = src[min(part * 4 + i, nsrc - 1)];
   }
   P.rul = 0u;
-  if (part == 0 && g.coeff_bytes + 2 > KSTEPS * 32)
-    P.rul = (uint32_t)base[g.coeff_bytes] | ((uint32_t)base[g.coeff_bytes + 1] << 8);
+  if (part == 0) P.rul = *(const uint16_t*)(base + g.coeff_bytes);  // 2-aligned (r1 even)
 }
 
 template <int G, int RB, int VB, int KSTEPS>
@@ -208,6 +209,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
 
   // ---- selector table for the code scatter, and this chunk's block ids
   S.lut[tid] = scatter_lut_entry((uint32_t)tid);
+  if (RB == 3 || VB == 3)
+    for (int i = tid; i < 4096; i += kThreads) S.lut3[i] = spread4_entry3((uint32_t)i);
   const int bfirst = t0 / a.block_size;
   const int nseg = (t1 - 1) / a.block_size - bfirst + 1;
   for (int i = tid; i < nseg; i += kThreads) {
@@ -286,34 +289,16 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
       uint32_t* cdst = (uint32_t*)&S.coef[ptok][part * kCPP];
 #pragma unroll
       for (int dw = 0; dw < KSTEPS * 2; ++dw) {
-        const int b0 = part * kCPP + dw * 4;
-        uint32_t x = P.coef[dw];
-        const int keep = g.r1 - b0;  // bytes of this dword that are coefficients
-        if (keep <= 0) x = 0;
-        else if (keep < 4) x &= (1u << (8 * keep)) - 1u;
+        // bytes past r1 (the ruler, head 0's row) are converted too: they are finite, and the
+        // decoder fragments are zero for k >= r1, so they contribute exactly 0
+        const uint32_t x = P.coef[dw];
         uint32_t p01, p23;
         i8x4_to_f16(x, p01, p23);
         cdst[2 * dw] = p01;
         cdst[2 * dw + 1] = p23;
       }
-      // coefficient ruler (fp16 LE at byte coeff_bytes)
-      const int rb = g.coeff_bytes;
-      if (rb + 2 <= KSTEPS * 32) {
-        if (part == rb / kCPP) {
-          const int off = rb - part * kCPP;
-          const int dw = off >> 2, sh = off & 3;
-          uint32_t lo = 0u, hi = 0u;  // select without dynamic register indexing
-#pragma unroll
-          for (int i = 0; i < KSTEPS * 2; ++i) {
-            lo = (i == dw) ? P.coef[i] : lo;
-            hi = (i == dw + 1) ? P.coef[i] : hi;
-          }
-          const uint32_t v = sh ? __builtin_amdgcn_alignbyte(hi, lo, sh) : lo;
-          S.cs[ptok] = f16_bits_to_float(v & 0xffffu);
-        }
-      } else if (part == 0) {
-        S.cs[ptok] = f16_bits_to_float(P.rul);
-      }
+      // coefficient ruler (fp16 LE at byte coeff_bytes), fetched by part 0
+      if (part == 0) S.cs[ptok] = f16_bits_to_float(P.rul);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         S.rawk[ptok][part * 4 + i] =
@@ -332,7 +317,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
       const int half = tid & 1;
       if (kind == 0) {
         const uint32_t* row = S.rawk[tok];
-        decode_half_row<RB>(row, half, S.lut, &S.kcode[tok][64 * half]);
+        decode_half_row<RB>(row, half, S.lut, S.lut3, &S.kcode[tok][64 * half]);
         if (half == 0) {
           const int rb = 16 + g.k_pb;
           const uint32_t bits = __builtin_amdgcn_alignbyte(row[(rb >> 2) + 1], row[rb >> 2], rb & 3);
@@ -340,7 +325,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
         }
       } else {
         const uint32_t* row = S.rawv[tok];
-        decode_half_row<VB>(row, half, S.lut, &S.vcode[tok][64 * half]);
+        decode_half_row<VB>(row, half, S.lut, S.lut3, &S.vcode[tok][64 * half]);
         if (half == 0) {
           const int rb = 16 + g.v_pb;
           const uint32_t bits = __builtin_amdgcn_alignbyte(row[(rb >> 2) + 1], row[rb >> 2], rb & 3);
@@ -407,16 +392,21 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
         float s = S.spart[0][p][tok] + S.spart[1][p][tok] + S.spart[2][p][tok] +
                   S.spart[3][p][tok];
         s = valid ? s : -INFINITY;
+        // Lazy rescaling: the reference point m_run only moves when the tile max exceeds it by
+        // more than 2^8, so most tiles skip the rescale (p stays <= 256; fp32 has the range).
+        // m_run is the same in every lane and wave (same inputs), so the branch is uniform.
         const float mt = wave_max(s);
-        const float mn = fmaxf(m_run[p], mt);
-        const float alpha = exp2f(m_run[p] - mn);
-        const float pr = valid ? exp2f(s - mn) : 0.f;
-        l_run[p] = l_run[p] * alpha + wave_sum(pr);
-        m_run[p] = mn;
-        pv[p] = pr * vr;
+        if (mt > m_run[p] + 8.f) {
+          const float alpha = exp2f(m_run[p] - mt);
+          m_run[p] = mt;
+          l_run[p] *= alpha;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) o[p][i] *= alpha;
-        psum[p] *= alpha;
+          for (int i = 0; i < 8; ++i) o[p][i] *= alpha;
+          psum[p] *= alpha;
+        }
+        const float pr = valid ? exp2f(s - m_run[p]) : 0.f;
+        l_run[p] += wave_sum(pr);
+        pv[p] = pr * vr;
       }
     }
     // ---------------------------------------------------------------- P.V

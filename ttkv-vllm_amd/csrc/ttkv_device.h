@@ -51,14 +51,25 @@ __device__ __forceinline__ void spread8(uint32_t w, uint32_t& e0, uint32_t& e1) 
 // stream from dword 4) into one code byte per lane at dst[0..63]; lanes outside the bitmap get
 // 2^(BITS-1). `lut[B]` holds the v_perm selectors that move the byte-spread codes of bitmap
 // byte B onto its set lanes (0x0c -> zero byte for the others).
+// 3-bit spread table: entry x (12 bits = 4 codes, first code in the top 3 bits) holds the 4 codes
+// one per byte, each with its top bit flipped (c ^ 4), first code in byte 0.
+__device__ __forceinline__ uint32_t spread4_entry3(uint32_t x) {
+  return ((x >> 9) ^ 4u) | ((((x >> 6) & 7u) ^ 4u) << 8) | ((((x >> 3) & 7u) ^ 4u) << 16) |
+         (((x & 7u) ^ 4u) << 24);
+}
+
+// Decode dims [64*half, 64*half+64) of one staged head row (bitmap dwords 0..3, MSB-first code
+// stream from dword 4) into one code byte per lane at dst[0..63]; lanes outside the bitmap get
+// 2^(BITS-1). `lut[B]` holds the v_perm selectors that move the byte-spread codes of bitmap
+// byte B onto its set lanes (0x0c -> zero byte for the others); for 3-bit codes `lut3` spreads
+// 4 codes per lookup (spread4_entry3).
 template <int BITS>
 __device__ __forceinline__ void decode_half_row(const uint32_t* row, int half, const uint2* lut,
-                                                uint8_t* dst) {
+                                                const uint32_t* lut3, uint8_t* dst) {
   constexpr uint32_t OFFB = (1u << (BITS - 1)) * 0x01010101u;
-  // XOR pattern that flips the top bit of each of 8 codes at the top of the window: a kept
-  // code c becomes c ^ 2^(b-1), so after the zero-filling scatter a final XOR restores c and
-  // turns the zero bytes into the zero code 2^(b-1).
-  constexpr uint32_t FLIP = BITS == 4 ? 0x88888888u : 0x92492400u;
+  // A kept code c is carried as c ^ 2^(b-1), so after the zero-filling scatter a final XOR
+  // restores c and turns the zero bytes into the zero code 2^(b-1).
+  constexpr uint32_t FLIP = 0x88888888u;  // 4-bit: top bit of each nibble
   const uint32_t bm0 = row[2 * half], bm1 = row[2 * half + 1];
   int rank = half ? __builtin_popcount(row[0]) + __builtin_popcount(row[1]) : 0;
   const uint32_t* st = row + 4;
@@ -81,15 +92,23 @@ __device__ __forceinline__ void decode_half_row(const uint32_t* row, int half, c
     w0[m] = st[wi];
     w1[m] = st[wi + 1];
   }
+  uint32_t e0[8], e1[8];
 #pragma unroll
   for (int m = 0; m < 8; ++m) {
     const uint64_t pair = ((uint64_t)bswap32(w0[m]) << 32) | (uint64_t)bswap32(w1[m]);
-    const uint32_t w = (uint32_t)((pair << (bp[m] & 31)) >> 32) ^ FLIP;
-    uint32_t e0, e1;
-    spread8<BITS>(w, e0, e1);
+    const uint32_t w = (uint32_t)((pair << (bp[m] & 31)) >> 32);
+    if constexpr (BITS == 3) {
+      e0[m] = lut3[w >> 20];
+      e1[m] = lut3[(w >> 8) & 0xfffu];
+    } else {
+      spread8<BITS>(w ^ FLIP, e0[m], e1[m]);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
     uint2 out;
-    out.x = __builtin_amdgcn_perm(e1, e0, sel[m].x) ^ OFFB;
-    out.y = __builtin_amdgcn_perm(e1, e0, sel[m].y) ^ OFFB;
+    out.x = __builtin_amdgcn_perm(e1[m], e0[m], sel[m].x) ^ OFFB;
+    out.y = __builtin_amdgcn_perm(e1[m], e0[m], sel[m].y) ^ OFFB;
     *(uint2*)(dst + 8 * m) = out;
   }
 }

@@ -94,6 +94,7 @@ struct PrefillSmem {
   uint8_t vcode[kPTile][kPCode];  // decode -> transpose
   _Float16 vt[kD][kVtStride];     // transpose -> P.V
   uint2 lut[256];
+  uint32_t lut3[4096];
   float cs[kPTile], krul[kPTile], vrul[kPTile];
   int is_last;
 };
@@ -185,6 +186,8 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
   }
 
   S.lut[tid] = scatter_lut_entry((uint32_t)tid);
+  if (RB == 3 || VB == 3)
+    for (int i = tid; i < 4096; i += kPThreads) S.lut3[i] = spread4_entry3((uint32_t)i);
 
   // ---- query fragments (B operand of S^T = Kp Q^T): column = query 16*wv + n of the block
   const int qj = qa + 16 * wv + n;
@@ -299,7 +302,7 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
       const int half = tid & 1;
       if (kind == 0) {
         const uint32_t* row = S.u.raw.k[key];
-        decode_half_row<RB>(row, half, S.lut, &S.kcode[key][64 * half]);
+        decode_half_row<RB>(row, half, S.lut, S.lut3, &S.kcode[key][64 * half]);
         if (half == 0) {
           const int rb = 16 + g.k_pb;
           const uint32_t bits =
@@ -308,7 +311,7 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
         }
       } else {
         const uint32_t* row = S.u.raw.v[key];
-        decode_half_row<VB>(row, half, S.lut, &S.vcode[key][64 * half]);
+        decode_half_row<VB>(row, half, S.lut, S.lut3, &S.vcode[key][64 * half]);
         if (half == 0) {
           const int rb = 16 + g.v_pb;
           const uint32_t bits =
