@@ -197,7 +197,7 @@ def bench_config4(torch, lay, cfg, cache, dev, steps=10, warmup=3):
     q = synth.queries(4 * Q, seed=8, device=dev)
     qsl = torch.arange(0, 4 * Q + 1, Q, dtype=torch.int32, device=dev)
     out = torch.empty_like(q)
-    ws = kernels.prefill_workspace(lay, HQ, 4, Q, n, dev)
+    ws = kernels.prefill_workspace(lay, HQ, 4, Q, n, dev, BS)
     err = torch.zeros(1, dtype=torch.int32, device=dev)
 
     def attend():

@@ -130,7 +130,7 @@ int64_t ttkv_write_workspace_bytes(const ttkv_layout* lay, int32_t num_tokens);
 /* Workspace bytes `ttkv_prefill_paged` needs for this batch shape (0 when one key split covers
  * every query block). Zero-filled before first use; every call leaves the counters zero. */
 int64_t ttkv_prefill_workspace_bytes(const ttkv_layout* lay, int32_t num_heads, int32_t num_reqs,
-                                     int32_t max_q_len, int32_t max_seq_len);
+                                     int32_t max_q_len, int32_t max_seq_len, int32_t block_size);
 
 /* K2 -- multi-query read for chunked-prefill continuations, ONE launch over the batch.
  *

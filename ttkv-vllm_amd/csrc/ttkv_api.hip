@@ -97,10 +97,11 @@ int64_t ttkv_write_workspace_bytes(const ttkv_layout* lay, int32_t num_tokens) {
 }
 
 int64_t ttkv_prefill_workspace_bytes(const ttkv_layout* lay, int32_t num_heads, int32_t num_reqs,
-                                     int32_t max_q_len, int32_t max_seq_len) {
+                                     int32_t max_q_len, int32_t max_seq_len, int32_t block_size) {
   Geom g;
-  if (!make_geom(lay, &g) || num_heads <= 0 || num_heads % g.H || num_reqs < 0) return -1;
-  return prefill_workspace_bytes(g, num_heads / g.H, num_reqs, max_q_len, max_seq_len);
+  if (!make_geom(lay, &g) || num_heads <= 0 || num_heads % g.H || num_reqs < 0 || block_size <= 0)
+    return -1;
+  return prefill_workspace_bytes(g, num_heads / g.H, num_reqs, max_q_len, max_seq_len, block_size);
 }
 
 int ttkv_prefill_paged(const ttkv_layout* lay, int32_t num_heads, float scale, const void* query,

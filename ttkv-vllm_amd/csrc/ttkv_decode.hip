@@ -404,7 +404,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
           for (int i = 0; i < 8; ++i) o[p][i] *= alpha;
           psum[p] *= alpha;
         }
-        const float pr = valid ? exp2f(s - m_run[p]) : 0.f;
+        const float pr = valid ? fast_exp2(s - m_run[p]) : 0.f;
         l_run[p] += wave_sum(pr);
         pv[p] = pr * vr;
       }

@@ -159,7 +159,7 @@ __global__ __launch_bounds__(kDThreads) void dense_decode_kernel(DenseArgs a) {
       float ls = 0.f;
 #pragma unroll
       for (int u = 0; u < kDUnroll; ++u) {
-        s[p][u] = exp2f(s[p][u] - mref);
+        s[p][u] = fast_exp2(s[p][u] - mref);
         ls += s[p][u];
       }
       l[p] = l[p] * alpha + cross_row_sum(ls);

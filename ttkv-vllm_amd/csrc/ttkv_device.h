@@ -51,6 +51,50 @@ __device__ __forceinline__ void spread8(uint32_t w, uint32_t& e0, uint32_t& e1) 
 // stream from dword 4) into one code byte per lane at dst[0..63]; lanes outside the bitmap get
 // 2^(BITS-1). `lut[B]` holds the v_perm selectors that move the byte-spread codes of bitmap
 // byte B onto its set lanes (0x0c -> zero byte for the others).
+// The slot bytes one of a token's 4 loader threads needs for one KV head: its quarter of the
+// coefficient window (KSTEPS*8 bytes), source dwords part*4 .. part*4+4 of the head's K and V
+// rows (4 output dwords + the funnel for realignment), and the fp16 coefficient ruler (part 0).
+template <int KSTEPS>
+struct RawSlot {
+  uint32_t coef[KSTEPS * 2];
+  uint32_t krow[5], vrow[5];
+  uint32_t rul;
+};
+
+template <int KSTEPS>
+__device__ __forceinline__ void fetch_raw_slot(RawSlot<KSTEPS>& P, const uint8_t* base, int part,
+                                               const Geom& g, int k_row_off, int v_row_off) {
+  constexpr int kCPP = KSTEPS * 8;
+  if (!base) {
+#pragma unroll
+    for (int i = 0; i < KSTEPS * 2; ++i) P.coef[i] = 0u;
+#pragma unroll
+    for (int i = 0; i < 5; ++i) P.krow[i] = P.vrow[i] = 0u;
+    P.rul = 0u;
+    return;
+  }
+  const uint32_t* cs = (const uint32_t*)(base + part * kCPP);
+#pragma unroll
+  for (int i = 0; i < KSTEPS * 2; ++i) P.coef[i] = cs[i];
+  {
+    const uintptr_t A = (uintptr_t)(base + k_row_off);
+    const uint32_t* src = (const uint32_t*)(A & ~(uintptr_t)3);
+    const int nsrc = (int)((A & 3) + g.k_row + 3) >> 2;
+    // clamped index: every load stays inside the row's dwords (the extra ones are never decoded)
+#pragma unroll
+    for (int i = 0; i < 5; ++i) P.krow[i] = src[min(part * 4 + i, nsrc - 1)];
+  }
+  {
+    const uintptr_t A = (uintptr_t)(base + v_row_off);
+    const uint32_t* src = (const uint32_t*)(A & ~(uintptr_t)3);
+    const int nsrc = (int)((A & 3) + g.v_row + 3) >> 2;
+#pragma unroll
+    for (int i = 0; i < 5; ++i) P.vrow[i] = src[min(part * 4 + i, nsrc - 1)];
+  }
+  P.rul = 0u;
+  if (part == 0) P.rul = *(const uint16_t*)(base + g.coeff_bytes);  // 2-aligned (r1 even)
+}
+
 // 3-bit spread table: entry x (12 bits = 4 codes, first code in the top 3 bits) holds the 4 codes
 // one per byte, each with its top bit flipped (c ^ 4), first code in byte 0.
 __device__ __forceinline__ uint32_t spread4_entry3(uint32_t x) {
@@ -112,6 +156,10 @@ __device__ __forceinline__ void decode_half_row(const uint32_t* row, int half, c
     *(uint2*)(dst + 8 * m) = out;
   }
 }
+
+// 2^x on the hardware exp unit (one v_exp_f32). Softmax weights below 2^-126 flush to zero,
+// which is far below fp32 resolution of the sums they join; -inf gives 0.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Cross-lane helpers on DPP and the gfx950 permlane swaps (VALU ops, no LDS round trip).
 __device__ __forceinline__ float dpp_f(float v, int ctrl_sel) {

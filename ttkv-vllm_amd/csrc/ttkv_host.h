@@ -40,7 +40,7 @@ int64_t write_workspace_bytes(const Geom& g, int num_tokens);
 
 namespace ttkv {
 int64_t prefill_workspace_bytes(const Geom& g, int G, int num_reqs, int max_q_len,
-                                int max_seq_len);
+                                int max_seq_len, int block_size);
 int prefill_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype,
                   int64_t q_row_stride, const uint8_t* page, int64_t n_slots, int64_t slot_stride,
                   int block_size, const int32_t* bt, int64_t bt_row_stride, int max_blocks,

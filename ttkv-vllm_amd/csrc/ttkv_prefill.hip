@@ -46,6 +46,7 @@ constexpr int kPRawDw = 16;     // dwords per staged head row
 constexpr int kPCode = 144;     // bytes per code row
 constexpr int kKpStride = 136;  // halves per reconstructed key row (128 + 8)
 constexpr int kVtStride = 72;   // halves per transposed V row (64 keys + 8)
+constexpr int kPSeg = 516;      // block ids of one key range staged in LDS
 
 struct PrefillArgs {
   Geom g;
@@ -95,6 +96,7 @@ struct PrefillSmem {
   _Float16 vt[kD][kVtStride];     // transpose -> P.V
   uint2 lut[256];
   uint32_t lut3[4096];
+  int32_t seg[kPSeg];
   float cs[kPTile], krul[kPTile], vrul[kPTile];
   int is_last;
 };
@@ -241,50 +243,55 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
   const int part = tid & 3;
   const int dl = 16 * wv + 4 * gq;
   const float voff = (float)(1 << (VB - 1));
+  // this key range's block ids, staged once (no global read on the per-tile address path)
+  const int bfirst = k0 / a.block_size;
+  const int nseg = (k1 - 1) / a.block_size - bfirst + 1;
+  for (int i = tid; i < nseg; i += kPThreads) {
+    int blk = a.bt[(int64_t)r * a.bt_row_stride + bfirst + i];
+    if (blk < 0 || blk >= a.num_blocks) {
+      atomicOr(a.err, TTKV_ERR_BAD_BLOCK);
+      blk = -1;
+    }
+    S.seg[i] = blk;
+  }
+  __syncthreads();
+  auto slot_base = [&](int tt) -> const uint8_t* {
+    if (ptok >= min(kPTile, k1 - tt)) return nullptr;
+    const int pos = tt + ptok;
+    const int bi = pos / a.block_size;
+    const int blk = S.seg[bi - bfirst];
+    if (blk < 0) return nullptr;
+    const int64_t slot = (int64_t)blk * a.block_size + (pos - bi * a.block_size);
+    return slot < a.n_slots ? a.page + slot * a.slot_stride : nullptr;
+  };
+  RawSlot<KSTEPS> P;
+  fetch_raw_slot<KSTEPS>(P, slot_base(k0), part, g, k_row_off, v_row_off);
 
   for (int tt = k0; tt < k1; tt += kPTile) {
     const int ntile = min(kPTile, k1 - tt);
     // ------------------------------------------------------------ commit this tile's bytes
     {
-      const uint8_t* base = nullptr;
-      if (ptok < ntile) {
-        const int pos = tt + ptok;
-        const int bi = pos / a.block_size;
-        const int blk = a.bt[(int64_t)r * a.bt_row_stride + bi];
-        if (blk < 0 || blk >= a.num_blocks) {
-          if (part == 0) atomicOr(a.err, TTKV_ERR_BAD_BLOCK);
-        } else {
-          const int64_t slot = (int64_t)blk * a.block_size + (pos - bi * a.block_size);
-          if (slot < a.n_slots) base = a.page + slot * a.slot_stride;
-        }
-      }
       uint32_t* cdst = (uint32_t*)&S.coef[ptok][part * kCPP];
-      if (base) {
-        const uint32_t* src = (const uint32_t*)(base + part * kCPP);
 #pragma unroll
-        for (int dw = 0; dw < KSTEPS * 2; ++dw) {
-          const int b0 = part * kCPP + dw * 4;
-          uint32_t x = src[dw];
-          const int keep = g.r1 - b0;
-          if (keep <= 0) x = 0;
-          else if (keep < 4) x &= (1u << (8 * keep)) - 1u;
-          uint32_t p01, p23;
-          i8x4_to_f16(x, p01, p23);
-          cdst[2 * dw] = p01;
-          cdst[2 * dw + 1] = p23;
-        }
-        if (part == 0)
-          S.cs[ptok] = f16_bits_to_float((uint32_t)base[g.coeff_bytes] |
-                                         ((uint32_t)base[g.coeff_bytes + 1] << 8));
-        copy_row_realign(base + k_row_off, g.k_row, S.u.raw.k[ptok], part, 4);
-        copy_row_realign(base + v_row_off, g.v_row, S.u.raw.v[ptok], part, 4);
-      } else {
+      for (int dw = 0; dw < KSTEPS * 2; ++dw) {
+        // bytes past r1 are finite int8 values and meet zero decoder rows: they contribute 0
+        uint32_t p01, p23;
+        i8x4_to_f16(P.coef[dw], p01, p23);
+        cdst[2 * dw] = p01;
+        cdst[2 * dw + 1] = p23;
+      }
+      if (part == 0) S.cs[ptok] = f16_bits_to_float(P.rul);
+      const int k_sh = k_row_off & 3, v_sh = v_row_off & 3;  // slot bases are 16-aligned
 #pragma unroll
-        for (int dw = 0; dw < KSTEPS * 4; ++dw) cdst[dw] = 0u;
-        if (part == 0) S.cs[ptok] = 0.f;
-        for (int dw = part; dw < kPRawDw; dw += 4) S.u.raw.k[ptok][dw] = S.u.raw.v[ptok][dw] = 0u;
+      for (int i = 0; i < 4; ++i) {
+        S.u.raw.k[ptok][part * 4 + i] =
+            k_sh ? __builtin_amdgcn_alignbyte(P.krow[i + 1], P.krow[i], k_sh) : P.krow[i];
+        S.u.raw.v[ptok][part * 4 + i] =
+            v_sh ? __builtin_amdgcn_alignbyte(P.vrow[i + 1], P.vrow[i], v_sh) : P.vrow[i];
       }
     }
+    // the next tile's bytes are in flight while this tile is computed
+    if (tt + kPTile < k1) fetch_raw_slot<KSTEPS>(P, slot_base(tt + kPTile), part, g, k_row_off, v_row_off);
     // this lane's RoPE angles for the tile: keys 16*nb + n, dims dl..dl+3 (cos) / 64+dl.. (sin)
     float4v cosv[4], sinv[4];
 #pragma unroll
@@ -452,22 +459,26 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
             mt = fmaxf(mt, tv);
           }
         mt = cross_row_max(mt);
-        const float mn = fmaxf(m_run[gg], mt);
-        const float mref = mn == -INFINITY ? 0.f : mn;
-        const float alpha = exp2f(m_run[gg] - mref);
+        // lazy rescaling: the reference point moves only when the column max grows by more
+        // than 2^8 (p <= 256 otherwise); a fully masked tile leaves it at -inf
+        if (mt > m_run[gg] + 8.f) {
+          const float alpha = exp2f(m_run[gg] - mt);
+          m_run[gg] = mt;
+          l_run[gg] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < 8; ++dt) o[dt][gg] *= alpha;
+        }
+        const float mref = m_run[gg] == -INFINITY ? 0.f : m_run[gg];
         float ps = 0.f;
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
           for (int jj = 0; jj < 4; ++jj) {
-            const float p = exp2f(sacc[kt][gg][jj] - mref);
+            const float p = fast_exp2(sacc[kt][gg][jj] - mref);
             ps += p;
             pb[gg][kt >> 1][4 * (kt & 1) + jj] = (_Float16)(p * vr[kt][jj]);
           }
-        l_run[gg] = l_run[gg] * alpha + cross_row_sum(ps);
-        m_run[gg] = mn;
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) o[dt][gg] *= alpha;
+        l_run[gg] += cross_row_sum(ps);
       }
       // ---------------------------------------------------------- O^T += Vt (P ruler_v)^T
 #pragma unroll
@@ -610,20 +621,23 @@ static int prefill_dispatch_k(const PrefillArgs& a, int ksteps, int grid, hipStr
 
 // Key range per split: enough splits that the grid fills the chip about once at two resident
 // workgroups per CU, each split at least 256 keys.
-static int prefill_kchunk(int items, int max_seq_len) {
+static int prefill_kchunk(int items, int max_seq_len, int block_size) {
   const int64_t target = 2LL * device_cu_count();
   const int64_t want = std::max<int64_t>(1, (target + items - 1) / std::max(items, 1));
   int64_t kc = (std::max(max_seq_len, 1) + want - 1) / want;
   kc = (kc + kPTile - 1) / kPTile * kPTile;
-  return (int)std::max<int64_t>(kc, 4 * kPTile);
+  kc = std::max<int64_t>(kc, 4 * kPTile);
+  // the block ids of one key range are staged in LDS: at most kPSeg of them
+  const int64_t seg_cap = (int64_t)(kPSeg - 2) * std::max(block_size, 1) / kPTile * kPTile;
+  return (int)std::max<int64_t>(std::min(kc, seg_cap), kPTile);
 }
 
 int64_t prefill_workspace_bytes(const Geom& g, int G, int num_reqs, int max_q_len,
-                                int max_seq_len) {
+                                int max_seq_len, int block_size) {
   if (num_reqs <= 0 || max_q_len <= 0) return 0;
   const int n_qb = (max_q_len + kPQ - 1) / kPQ;
   const int items = num_reqs * g.H * n_qb;
-  const int kc = prefill_kchunk(items, max_seq_len);
+  const int kc = prefill_kchunk(items, max_seq_len, block_size);
   const int nsplit = std::max(1, (max_seq_len + kc - 1) / kc);
   if (nsplit == 1) return 0;
   const int64_t cnt = ((int64_t)items * 4 + 255) / 256 * 256;
@@ -710,10 +724,10 @@ int prefill_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype
   a.max_q = max_q_len;
   a.n_qb = (max_q_len + kPQ - 1) / kPQ;
   const int items = num_reqs * g.H * a.n_qb;
-  a.kchunk = prefill_kchunk(items, max_seq_len);
+  a.kchunk = prefill_kchunk(items, max_seq_len, block_size);
   a.nsplit = std::max(1, (max_seq_len + a.kchunk - 1) / a.kchunk);
   if (!scores && a.nsplit > 1) {
-    const int64_t need = prefill_workspace_bytes(g, G, num_reqs, max_q_len, max_seq_len);
+    const int64_t need = prefill_workspace_bytes(g, G, num_reqs, max_q_len, max_seq_len, block_size);
     if (!ws || ws_bytes < need)
       return host_fail(TTKV_E_WORKSPACE, "prefill workspace needs " + std::to_string(need) +
                                              " bytes, got " + std::to_string(ws_bytes));

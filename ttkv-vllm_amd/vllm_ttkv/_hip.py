@@ -88,7 +88,7 @@ def lib():
     L.ttkv_write_workspace_bytes.restype = I64
     L.ttkv_write_workspace_bytes.argtypes = [LP, I32]
     L.ttkv_prefill_workspace_bytes.restype = I64
-    L.ttkv_prefill_workspace_bytes.argtypes = [LP, I32, I32, I32, I32]
+    L.ttkv_prefill_workspace_bytes.argtypes = [LP, I32, I32, I32, I32, I32]
     L.ttkv_prefill_paged.restype = ctypes.c_int
     L.ttkv_prefill_paged.argtypes = [
         LP, I32, F32,                 # layout, num_heads, scale

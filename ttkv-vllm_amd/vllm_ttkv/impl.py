@@ -252,9 +252,9 @@ class TTKVAttentionImpl(_ImplBase):
             self._wws = torch.zeros(max(int(need), 256), dtype=torch.uint8, device=device)
         return self._wws
 
-    def _prefill_workspace(self, lay, num_reqs, max_q, max_seq, device):
+    def _prefill_workspace(self, lay, num_reqs, max_q, max_seq, device, block_size):
         need = _hip.lib().ttkv_prefill_workspace_bytes(_hip.Layout.of(lay), self.num_heads,
-                                                       num_reqs, max_q, max_seq)
+                                                       num_reqs, max_q, max_seq, block_size)
         if self._pws is None or self._pws.numel() < need or self._pws.device != device:
             self._pws = torch.zeros(max(int(need), 256), dtype=torch.uint8, device=device)
         return self._pws
@@ -291,7 +291,8 @@ class TTKVAttentionImpl(_ImplBase):
                 md.seq_lens.to(torch.int32), md.query_start_loc.to(torch.int32), max_q, max_seq,
                 store.dec_map, store.dec_pool, store.cos_sin_cache, self.scale,
                 req_index=torch.tensor(cont, dtype=torch.int32, device=dev), out=output,
-                workspace=self._prefill_workspace(lay, len(cont), max_q, max_seq, dev),
+                workspace=self._prefill_workspace(lay, len(cont), max_q, max_seq, dev,
+                                                  self._block_size(cache)),
                 error_word=self.error_word)
 
     def _sdpa(self, q, k, v):

@@ -209,9 +209,9 @@ def _read_checks(lay: TTKLayout, query, page, block_table, seq_lens, query_start
 
 
 def prefill_workspace(lay: TTKLayout, num_heads: int, num_reqs: int, max_q_len: int,
-                      max_seq_len: int, device) -> torch.Tensor:
+                      max_seq_len: int, device, block_size: int = 16) -> torch.Tensor:
     n = _hip.lib().ttkv_prefill_workspace_bytes(_hip.Layout.of(lay), num_heads, num_reqs,
-                                                max_q_len, max_seq_len)
+                                                max_q_len, max_seq_len, block_size)
     if n < 0:
         raise ValueError("invalid layout / head count for the prefill workspace")
     return torch.zeros(max(int(n), 256), dtype=torch.uint8, device=device)
@@ -245,7 +245,8 @@ def prefill_paged(lay: TTKLayout, query: torch.Tensor, page: torch.Tensor, block
     if out.dtype not in _hip.DTYPE_CODE:
         raise ValueError("out dtype must be fp32, fp16 or bf16")
     if workspace is None:
-        workspace = prefill_workspace(lay, HQ, num_reqs, max_q_len, max_seq_len, query.device)
+        workspace = prefill_workspace(lay, HQ, num_reqs, max_q_len, max_seq_len, query.device,
+                                      block_size)
     if error_word is None:
         error_word = torch.zeros(1, dtype=torch.int32, device=query.device)
     rc = _hip.lib().ttkv_prefill_paged(
