@@ -75,7 +75,7 @@ struct DecodeArgs {
   int chunk, max_chunks, nwork, max_seq;
 };
 
-template <int KSTEPS>
+template <int KSTEPS, int G>
 struct DecodeSmem {
   static constexpr int kCoefStride = KSTEPS * 32 + 8;  // fp16 per token row
   _Float16 coef[kTile][kCoefStride];
@@ -83,15 +83,14 @@ struct DecodeSmem {
   uint32_t rawv[kTile][kRawDw];
   uint8_t kcode[kTile][kCodeStride];
   uint8_t vcode[kTile][kCodeStride];
-  float spart[kWaves][8][kTile];  // per wave partial scores [wave][head][token] (G <= 8)
+  float spart[kWaves][G][kTile];  // per wave partial scores [wave][head][token]
   uint2 lut[256];
-  uint32_t lut3[4096];
   int32_t seg[kSegMax];
   float cs[kTile];
   float krul[kTile];
   float vrul[kTile];
-  float qs[8][kD];  // this KV head's query rows, pre-scaled by scale * log2(e)
-  float m[8], l[8];
+  float qs[G][kD];  // this KV head's query rows, pre-scaled by scale * log2(e)
+  float m[G], l[G];
   int is_last;
 };
 
@@ -100,23 +99,10 @@ struct DecodeSmem {
 // prefetch and its use (vmcnt retires in order).
 template <int KSTEPS>
 struct Prefetch {
-  float4v cosv[4], sinv[4];
   uint32_t coef[KSTEPS * 2];  // KSTEPS*8 coefficient bytes
   uint32_t krow[5], vrow[5];  // 5 source dwords (4 output dwords + funnel)
   uint32_t rul;               // coefficient ruler bits when outside the coefficient window
 };
-
-template <int KSTEPS>
-__device__ __forceinline__ void prefetch_angles(Prefetch<KSTEPS>& P, const float* cs_cache, int tt,
-                                                int ntile, int n, int dl) {
-#pragma unroll
-  for (int nb = 0; nb < 4; ++nb) {
-    const int tok = 16 * nb + n;
-    const int pos = tok < ntile ? tt + tok : tt;
-    P.cosv[nb] = *(const float4v*)&cs_cache[(int64_t)pos * kD + dl];
-    P.sinv[nb] = *(const float4v*)&cs_cache[(int64_t)pos * kD + 64 + dl];
-  }
-}
 
 template <int KSTEPS>
 __device__ __forceinline__ void prefetch(Prefetch<KSTEPS>& P, const uint8_t* base, int part,
@@ -155,7 +141,7 @@ __device__ __forceinline__ void prefetch(Prefetch<KSTEPS>& P, const uint8_t* bas
 template <int G, int RB, int VB, int KSTEPS>
 __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  DecodeSmem<KSTEPS>& S = *reinterpret_cast<DecodeSmem<KSTEPS>*>(smem_raw);
+  DecodeSmem<KSTEPS, G>& S = *reinterpret_cast<DecodeSmem<KSTEPS, G>*>(smem_raw);
   constexpr int kCPP = KSTEPS * 8;
   const Geom& g = a.g;
   const int tid = threadIdx.x;
@@ -209,8 +195,6 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
 
   // ---- selector table for the code scatter, and this chunk's block ids
   S.lut[tid] = scatter_lut_entry((uint32_t)tid);
-  if (RB == 3 || VB == 3)
-    for (int i = tid; i < 4096; i += kThreads) S.lut3[i] = spread4_entry3((uint32_t)i);
   const int bfirst = t0 / a.block_size;
   const int nseg = (t1 - 1) / a.block_size - bfirst + 1;
   for (int i = tid; i < nseg; i += kThreads) {
@@ -244,7 +228,6 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   // first tile's bytes in flight while the decoder is loaded
   Prefetch<KSTEPS> P;
   prefetch<KSTEPS>(P, slot_base(t0), part, g, k_row_off, v_row_off);
-  prefetch_angles<KSTEPS>(P, a.cs_cache, t0, min(kTile, t1 - t0), n, dl);
 
   // ---- decoder fragments (A operand, M = dims, K = r1), hi/lo fp16, resident in registers.
   const int HD = g.H * kD;
@@ -317,7 +300,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
       const int half = tid & 1;
       if (kind == 0) {
         const uint32_t* row = S.rawk[tok];
-        decode_half_row<RB>(row, half, S.lut, S.lut3, &S.kcode[tok][64 * half]);
+        decode_half_row<RB>(row, half, S.lut, nullptr, &S.kcode[tok][64 * half]);
         if (half == 0) {
           const int rb = 16 + g.k_pb;
           const uint32_t bits = __builtin_amdgcn_alignbyte(row[(rb >> 2) + 1], row[rb >> 2], rb & 3);
@@ -325,7 +308,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
         }
       } else {
         const uint32_t* row = S.rawv[tok];
-        decode_half_row<VB>(row, half, S.lut, S.lut3, &S.vcode[tok][64 * half]);
+        decode_half_row<VB>(row, half, S.lut, nullptr, &S.vcode[tok][64 * half]);
         if (half == 0) {
           const int rb = 16 + g.v_pb;
           const uint32_t bits = __builtin_amdgcn_alignbyte(row[(rb >> 2) + 1], row[rb >> 2], rb & 3);
@@ -335,10 +318,20 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
     }
     __syncthreads();
     // ---------------------------------------------------------------- recon + rope + q.k
+    // RoPE angles (shared by every request and head, L2-resident), fetched one block ahead
+    auto angle_row = [&](int nb, float4v& cv, float4v& sv) {
+      const int tok = 16 * nb + n;
+      const int64_t pos = tok < ntile ? tt + tok : tt;
+      cv = *gbl((const float4v*)&a.cs_cache[pos * kD + dl]);
+      sv = *gbl((const float4v*)&a.cs_cache[pos * kD + 64 + dl]);
+    };
+    float4v cvn, svn;
+    angle_row(0, cvn, svn);
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
       const int tok = 16 * nb + n;
-      const float4v cv = P.cosv[nb], sv = P.sinv[nb];
+      const float4v cv = cvn, sv = svn;
+      if (nb < 3) angle_row(nb + 1, cvn, svn);
       float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < KSTEPS; ++s) {
@@ -378,8 +371,6 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
       }
     }
     // next tile's angles: issued after this tile's raw-byte prefetch, needed one tile later
-    if (tt + kTile < t1)
-      prefetch_angles<KSTEPS>(P, a.cs_cache, tt + kTile, min(kTile, t1 - tt - kTile), n, dl);
     __syncthreads();
     // ---------------------------------------------------------------- online softmax (every wave)
     float pv[G];
@@ -529,7 +520,7 @@ namespace ttkv {
 
 template <int G, int RB, int VB, int KSTEPS>
 static int launch_decode_t(const DecodeArgs& a, int grid, hipStream_t st) {
-  const size_t smem = sizeof(DecodeSmem<KSTEPS>);
+  const size_t smem = sizeof(DecodeSmem<KSTEPS, G>);
   auto kfn = decode_paged_kernel<G, RB, VB, KSTEPS>;
   static bool attr_set = false;  // per instantiation; benign race (idempotent)
   if (!attr_set) {

@@ -105,8 +105,8 @@ __device__ __forceinline__ uint32_t spread4_entry3(uint32_t x) {
 // Decode dims [64*half, 64*half+64) of one staged head row (bitmap dwords 0..3, MSB-first code
 // stream from dword 4) into one code byte per lane at dst[0..63]; lanes outside the bitmap get
 // 2^(BITS-1). `lut[B]` holds the v_perm selectors that move the byte-spread codes of bitmap
-// byte B onto its set lanes (0x0c -> zero byte for the others); for 3-bit codes `lut3` spreads
-// 4 codes per lookup (spread4_entry3).
+// byte B onto its set lanes (0x0c -> zero byte for the others); for 3-bit codes `lut3`, when
+// given, spreads 4 codes per lookup (spread4_entry3), else the codes are cut with bit ops.
 template <int BITS>
 __device__ __forceinline__ void decode_half_row(const uint32_t* row, int half, const uint2* lut,
                                                 const uint32_t* lut3, uint8_t* dst) {
@@ -141,11 +141,11 @@ __device__ __forceinline__ void decode_half_row(const uint32_t* row, int half, c
   for (int m = 0; m < 8; ++m) {
     const uint64_t pair = ((uint64_t)bswap32(w0[m]) << 32) | (uint64_t)bswap32(w1[m]);
     const uint32_t w = (uint32_t)((pair << (bp[m] & 31)) >> 32);
-    if constexpr (BITS == 3) {
+    if (BITS == 3 && lut3) {
       e0[m] = lut3[w >> 20];
       e1[m] = lut3[(w >> 8) & 0xfffu];
     } else {
-      spread8<BITS>(w ^ FLIP, e0[m], e1[m]);
+      spread8<BITS>(w ^ (BITS == 3 ? 0x92492400u : FLIP), e0[m], e1[m]);
     }
   }
 #pragma unroll
