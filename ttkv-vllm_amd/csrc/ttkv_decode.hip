@@ -325,33 +325,22 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
       cv = *gbl((const float4v*)&a.cs_cache[pos * kD + dl]);
       sv = *gbl((const float4v*)&a.cs_cache[pos * kD + 64 + dl]);
     };
-    // Reconstruction of block nb+1 is issued before the epilogue of block nb, so the MFMA
-    // pipeline runs under the epilogue's VALU work. hi and lo accumulate separately (4
-    // independent chains) and are summed in the epilogue.
-    auto recon_block = [&](int nb, float4v acc[4]) {
-      const int tok = 16 * nb + n;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = float4v{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < KSTEPS; ++s) {
-        const half8 b = *(const half8*)&S.coef[tok][32 * s + 8 * gq];
-        acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[0][s], b, acc[0], 0, 0, 0);
-        acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[0][s], b, acc[1], 0, 0, 0);
-        acc[2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[1][s], b, acc[2], 0, 0, 0);
-        acc[3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[1][s], b, acc[3], 0, 0, 0);
-      }
-    };
     float4v cvn, svn;
     angle_row(0, cvn, svn);
-    float4v accn[4];
-    recon_block(0, accn);
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
       const int tok = 16 * nb + n;
       const float4v cv = cvn, sv = svn;
       if (nb < 3) angle_row(nb + 1, cvn, svn);
-      const float4v acc0 = accn[0] + accn[1], acc1 = accn[2] + accn[3];
-      if (nb < 3) recon_block(nb + 1, accn);
+      float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) {
+        const half8 b = *(const half8*)&S.coef[tok][32 * s + 8 * gq];
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[0][s], b, acc0, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[0][s], b, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[1][s], b, acc1, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[1][s], b, acc1, 0, 0, 0);
+      }
       const float cs = S.cs[tok];
       const float kr = S.krul[tok];
       const float kb = -(float)(1 << (RB - 1)) * kr;

@@ -117,43 +117,46 @@ __device__ __forceinline__ void decode_half_row(const uint32_t* row, int half, c
   const uint32_t bm0 = row[2 * half], bm1 = row[2 * half + 1];
   int rank = half ? __builtin_popcount(row[0]) + __builtin_popcount(row[1]) : 0;
   const uint32_t* st = row + 4;
-  // All stream offsets follow from the bitmap alone, so every LDS read of the half row (8
-  // selector pairs, 16 window words) is issued before any of them is consumed.
-  uint32_t B[8];
-  int bp[8];
+  // All stream offsets follow from the bitmap alone, so the LDS reads of a batch of 4 bitmap
+  // bytes (selector pairs and window words) are issued before any of them is consumed.
 #pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    B[m] = __builtin_amdgcn_ubfe(m < 4 ? bm0 : bm1, 8 * (m & 3), 8);
-    bp[m] = rank * BITS;
-    rank += __builtin_popcount(B[m]);
-  }
-  uint2 sel[8];
-  uint32_t w0[8], w1[8];
+  for (int m0 = 0; m0 < 8; m0 += 4) {
+    uint32_t B[4];
+    int bp[4];
 #pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    sel[m] = lut[B[m]];
-    const int wi = bp[m] >> 5;
-    w0[m] = st[wi];
-    w1[m] = st[wi + 1];
-  }
-  uint32_t e0[8], e1[8];
-#pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    const uint64_t pair = ((uint64_t)bswap32(w0[m]) << 32) | (uint64_t)bswap32(w1[m]);
-    const uint32_t w = (uint32_t)((pair << (bp[m] & 31)) >> 32);
-    if (BITS == 3 && lut3) {
-      e0[m] = lut3[w >> 20];
-      e1[m] = lut3[(w >> 8) & 0xfffu];
-    } else {
-      spread8<BITS>(w ^ (BITS == 3 ? 0x92492400u : FLIP), e0[m], e1[m]);
+    for (int m = 0; m < 4; ++m) {
+      B[m] = __builtin_amdgcn_ubfe(m0 < 4 ? bm0 : bm1, 8 * m, 8);
+      bp[m] = rank * BITS;
+      rank += __builtin_popcount(B[m]);
     }
-  }
+    uint2 sel[4];
+    uint32_t w0[4], w1[4];
 #pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    uint2 out;
-    out.x = __builtin_amdgcn_perm(e1[m], e0[m], sel[m].x) ^ OFFB;
-    out.y = __builtin_amdgcn_perm(e1[m], e0[m], sel[m].y) ^ OFFB;
-    *(uint2*)(dst + 8 * m) = out;
+    for (int m = 0; m < 4; ++m) {
+      sel[m] = lut[B[m]];
+      const int wi = bp[m] >> 5;
+      w0[m] = st[wi];
+      w1[m] = st[wi + 1];
+    }
+    uint32_t e0[4], e1[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const uint64_t pair = ((uint64_t)bswap32(w0[m]) << 32) | (uint64_t)bswap32(w1[m]);
+      const uint32_t w = (uint32_t)((pair << (bp[m] & 31)) >> 32);
+      if (BITS == 3 && lut3) {
+        e0[m] = lut3[w >> 20];
+        e1[m] = lut3[(w >> 8) & 0xfffu];
+      } else {
+        spread8<BITS>(w ^ (BITS == 3 ? 0x92492400u : FLIP), e0[m], e1[m]);
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      uint2 out;
+      out.x = __builtin_amdgcn_perm(e1[m], e0[m], sel[m].x) ^ OFFB;
+      out.y = __builtin_amdgcn_perm(e1[m], e0[m], sel[m].y) ^ OFFB;
+      *(uint2*)(dst + 8 * (m0 + m)) = out;
+    }
   }
 }
 
