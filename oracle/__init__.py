@@ -25,6 +25,9 @@ Pinning (what each part is checked against; see `tests/test_oracle_*.py`):
     and a planted-mistake control.
   * scores / attention: two index orders (`attend_raw_store` vs `oracle_attend`), negative
     controls on rotation, one-hot readout, causal pattern, brute-force float64 loops.
-  * TT-SVD fit and pinv projection: invariants only (rank rule, exact zero padding, least
-    squares) -- their bits depend on LAPACK, so they are "parity unpinned" bit-wise.
+  * TT-SVD fit and pinv projection: invariants (rank rule, exact zero padding, least squares),
+    and vectors written by the reference implementation itself on the CPU
+    (`tests/golden/ref_encode_*.npz`, `tests/test_golden.py`): the fit, the frozen encode and the
+    V encode reproduce the reference's bytes exactly, on a capped and on a padded rank. A
+    different LAPACK may still change the fit's bits; the invariants hold there.
 """

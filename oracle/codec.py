@@ -135,9 +135,10 @@ def quant_rows(M: torch.Tensor, qbits: int, ruler_mode: str = "gpu"):
     return q, sc.to(torch.float16).reshape(-1)
 
 
-# ------------------------------------------------------------------ the fit (parity unpinned)
+# ------------------------------------------------------------------ the fit (LAPACK-dependent)
 def tt_svd(X: torch.Tensor, tol: float, max_rank=None):
-    """ttkv_codec.py:78-109. Energy-truncated TT-SVD. Bits depend on LAPACK: parity unpinned."""
+    """ttkv_codec.py:78-109. Energy-truncated TT-SVD. Bits depend on LAPACK; with the CPU torch
+    the reference ran on they match its output exactly (tests/test_golden.py)."""
     dims = list(X.shape)
     rest = X.reshape(dims[0], -1).contiguous()
     cores, ranks, r_prev = [], [], 1

@@ -22,7 +22,8 @@ from .layout import Layout, pack_k_slots, pack_v_slots
 
 def fit_into_budget(K: torch.Tensor, lay: Layout, cfg: dict, ruler_mode: str = "gpu"):
     """encode.py:257-298. K [H,n,d] raw -> fitted store zero-padded to lay.r1. The TT-SVD makes
-    the result LAPACK-dependent: parity unpinned bit-wise, pinned by invariants."""
+    the result LAPACK-dependent; pinned by invariants and, on the CPU, bit-exactly against vectors
+    the reference wrote (tests/golden/ref_encode_*.npz)."""
     H, n, d = K.shape
     kl = codec.build_k_layer(K, cfg["tols"], cfg["qbits"], cfg["res_frac"], cfg["res_bits"],
                              max_rank=lay.r1, ruler_mode=ruler_mode)

@@ -134,3 +134,36 @@ def test_slot_refusals_set_the_error_word_and_write_nothing():
         ok_rows = [j for j in range(3) if j != bad_i]
         assert int(page.abs().sum()) > 0
         assert all(int(page[bad[j]].abs().sum()) > 0 for j in ok_rows)
+
+
+@pytest.mark.parametrize("case", ["ref_encode_safe_r16", "ref_encode_campaign4x_r64"])
+def test_frozen_write_against_reference_vectors(case):
+    """K3 on the reference's own inputs (tests/golden/, written by the reference's
+    `encode_frozen` / `encode_v` on the CPU). The reference's CPU rulers are divisions and its
+    CPU lane selection on a magnitude tie is `torch.topk`'s, so bytes may differ in a few places;
+    the stores must agree byte-for-byte almost everywhere. Decoded K agrees within a coefficient
+    step; decoded V within a residual step, or a tied lane's own magnitude where the two
+    selections keep different lanes."""
+    import pathlib
+    import numpy as np
+    z = np.load(pathlib.Path(__file__).parent / "golden" / f"{case}.npz")
+    name = str(z["config"])
+    lay = layout_for_config(codec.CONFIGS[name], r1=int(z["r1"]))
+    dec = torch.from_numpy(z["fit_decoder_f"])
+    pinv = torch.from_numpy(z["pinv"])
+    K1 = torch.from_numpy(z["K1"]).float()
+    n = K1.shape[1]
+    V = torch.from_numpy(z["V0"]).float()[:, :n].contiguous()
+    slots = torch.arange(n, dtype=torch.int64)
+    page, _, _, err = _run(lay, dec, pinv, K1, V, slots, n)
+    assert err == 0
+    want = torch.cat([torch.from_numpy(z["frozen_k_slots"]),
+                      torch.from_numpy(z["v_slots"])[:n]], dim=1)
+    frac = float((page != want).float().mean())
+    assert frac < 0.01, f"{case}: {frac:.4f} of bytes differ"
+    kg = attend.dense_k_from_slots(lay, page[:, :lay.k_slot_bytes], dec)
+    kr = attend.dense_k_from_slots(lay, want[:, :lay.k_slot_bytes], dec)
+    assert float((kg - kr).abs().max()) <= 0.05 * float(K1.abs().max())
+    vg = attend.dense_v_from_slots(lay, page[:, lay.v_offset:])
+    vr = attend.dense_v_from_slots(lay, want[:, lay.v_offset:])
+    assert float((vg - vr).abs().max()) <= 0.3 * float(V.abs().max())
