@@ -3,26 +3,31 @@
 //
 // Work item = (request r, KV head h, token chunk c). A 256-thread workgroup (4 waves) walks its
 // chunk in 64-token tiles with the next tile's raw bytes prefetched into registers while the
-// current one is computed (global loads in flight across the whole tile):
+// current one is computed:
 //   commit  : prefetched bytes -> LDS: coefficients as fp16 MFMA B-fragments (int8 is exact in
-//             fp16), this head's K and V rows realigned to 4 bytes.
-//   decode  : one thread per half row. Per bitmap byte, the next 8 codes are cut from the MSB-first
-//             stream, spread one per byte and scattered to their lanes with one v_perm driven by a
-//             256-entry selector table; lanes outside the bitmap get the zero code 2^(b-1).
-//             Output: one code byte per (token, lane) for K and for V.
+//             fp16); this head's K and V rows realigned, the code streams byte-reversed per dword
+//             (one v_perm each) so that a code window is one v_alignbit.
+//   decode  : one thread per half row. Per bitmap byte, the next 8 codes are spread one per byte
+//             through a 4096-entry table (3-bit) or nibble perms (4-bit) and scattered onto their
+//             lanes with one v_perm driven by a 256-entry selector table. 3-bit codes come out as
+//             fp8 bytes of the signed value c - 4 (0 outside the bitmap), which the arithmetic
+//             reads two at a time with v_cvt_pk_f32_fp8.
 //   recon   : K_pre^T[128 x 16 tokens] = Dec^T[128 x r1] * coeff^T[r1 x 16] on MFMA 16x16x32 f16.
 //             The decoder is split hi + lo in fp16 and both halves are applied; decoder_f values
 //             are int8 * fp16 row rulers (<= 19 significant bits), so hi + lo is exact and the
 //             products are exact in the fp32 accumulator. Wave w owns dims {16w..16w+15} and
 //             {64+16w..64+16w+15}, so each RoPE pair (j, j+64) sits in one lane and the decoder
 //             fragments stay in registers for the whole chunk.
-//   rope+qk : k = cs * acc + ruler * (code - 2^(b-1)); rotate by the row's absolute position; fp32
-//             dot with the G query heads (pre-scaled by scale * log2 e); partial dots reduced
-//             across the 4 lane groups and the 4 waves.
-//   softmax : online, base 2, evaluated redundantly by every wave (no extra barrier), with the
-//             rescale skipped unless the running max grows by more than 2^8.
-//   P.V     : o[p] += P[p,t] * ruler_v[t] * code; the 2^(b-1) offset is removed once at the end
-//             through the running sum of P * ruler_v.
+//   rope    : k / cs = acc + (ruler / cs) * (code - 2^(b-1)), rotated by the row's absolute
+//             position. The coefficient ruler cs is a per-token factor of the key, so it is
+//             applied to the score instead (with scale * log2 e).
+//   q.k     : on MFMA: S[p, token] = Q[p, dims] * Y[dims, token] over the wave's 32 dims, with the
+//             rotated keys split hi + lo in fp16 (22 significant bits) and the query split the
+//             same way; partial scores of the 4 waves are summed through LDS.
+//   softmax : online, base 2, evaluated redundantly by every wave (lane = token, no barrier). The
+//             reference point moves only when some score exceeds it by more than 2^8 (a ballot),
+//             so the wave-wide max is rarely computed; sums stay per lane until the end.
+//   P.V     : o[p] += P[p,t] * (ruler_v[t] / unit) * code on VALU, codes converted two per op.
 // Chunks of one (r, h) are combined in the same launch by the last workgroup to finish
 // (device-scope fence + counter), which also resets the counter to zero.
 //
@@ -53,7 +58,7 @@ struct DecodeArgs {
   int64_t q_row_stride;
   const uint8_t* page;
   int64_t n_slots, slot_stride;
-  int block_size;
+  int block_size, bs_shift;
   const int32_t* bt;
   int64_t bt_row_stride;
   int max_blocks;
@@ -78,30 +83,30 @@ struct DecodeArgs {
 template <int KSTEPS, int G>
 struct DecodeSmem {
   static constexpr int kCoefStride = KSTEPS * 32 + 8;  // fp16 per token row
+  static constexpr int kSP = G <= 4 ? 4 : 8;           // score slots per token
   _Float16 coef[kTile][kCoefStride];
   uint32_t rawk[kTile][kRawDw];
   uint32_t rawv[kTile][kRawDw];
   uint8_t kcode[kTile][kCodeStride];
   uint8_t vcode[kTile][kCodeStride];
-  float spart[kWaves][G][kTile];  // per wave partial scores [wave][head][token]
+  float spart[kWaves][kTile][kSP];  // per wave partial q.k [wave][token][head]
   uint2 lut[256];
+  uint32_t lut3[4096];
   int32_t seg[kSegMax];
-  float cs[kTile];
-  float krul[kTile];
-  float vrul[kTile];
-  float qs[G][kD];  // this KV head's query rows, pre-scaled by scale * log2(e)
+  float cs[kTile];  // coefficient ruler
+  float kr[kTile];  // K residual ruler / (cs * unit)
+  float vr[kTile];  // V ruler / unit
+  float f[kTile];   // cs * scale * log2(e)
   float m[G], l[G];
   int is_last;
 };
 
-// Raw bytes of one token prefetched by one of its 4 threads, plus this lane's RoPE angles for
-// the tile (4 tokens x 4 dims of cos and of sin), so that no global load is issued between the
-// prefetch and its use (vmcnt retires in order).
+// Raw bytes of one token prefetched by one of its 4 threads.
 template <int KSTEPS>
 struct Prefetch {
   uint32_t coef[KSTEPS * 2];  // KSTEPS*8 coefficient bytes
   uint32_t krow[5], vrow[5];  // 5 source dwords (4 output dwords + funnel)
-  uint32_t rul;               // coefficient ruler bits when outside the coefficient window
+  uint32_t rul;               // coefficient ruler bits (part 0)
 };
 
 template <int KSTEPS>
@@ -138,11 +143,27 @@ __device__ __forceinline__ void prefetch(Prefetch<KSTEPS>& P, const uint8_t* bas
   if (part == 0) P.rul = *(const uint16_t*)(base + g.coeff_bytes);  // 2-aligned (r1 even)
 }
 
+// hi + lo fp16 split of 8 fp32 values (22 significant bits): hi truncated, lo the exact
+// remainder rounded toward zero.
+__device__ __forceinline__ void split8(const float y[8], half8& hi, half8& lo) {
+#pragma unroll
+  for (int i = 0; i < 8; i += 2) {
+    const auto h = __builtin_amdgcn_cvt_pkrtz(y[i], y[i + 1]);
+    const auto l = __builtin_amdgcn_cvt_pkrtz(y[i] - (float)h[0], y[i + 1] - (float)h[1]);
+    hi[i] = (_Float16)h[0];
+    hi[i + 1] = (_Float16)h[1];
+    lo[i] = (_Float16)l[0];
+    lo[i + 1] = (_Float16)l[1];
+  }
+}
+
 template <int G, int RB, int VB, int KSTEPS>
 __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  DecodeSmem<KSTEPS, G>& S = *reinterpret_cast<DecodeSmem<KSTEPS, G>*>(smem_raw);
+  using Smem = DecodeSmem<KSTEPS, G>;
+  Smem& S = *reinterpret_cast<Smem*>(smem_raw);
   constexpr int kCPP = KSTEPS * 8;
+  constexpr int kSP = Smem::kSP;
   const Geom& g = a.g;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -193,8 +214,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
     return;
   }
 
-  // ---- selector table for the code scatter, and this chunk's block ids
-  S.lut[tid] = scatter_lut_entry((uint32_t)tid);
+  // ---- code tables, and this chunk's block ids
+  stage_luts(S.lut, (RB == 3 || VB == 3) ? S.lut3 : nullptr, tid, kThreads);
   const int bfirst = t0 / a.block_size;
   const int nseg = (t1 - 1) / a.block_size - bfirst + 1;
   for (int i = tid; i < nseg; i += kThreads) {
@@ -210,14 +231,22 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   const int v_row_off = g.k_slot + h * g.v_row;
   const int ptok = tid >> 2;  // token / part handled by this thread in prefetch + commit
   const int part = tid & 3;
-  const int k_sh = (k_row_off & 3), v_sh = (v_row_off & 3);  // slot bases are 16-aligned
+  // slot bases are 16-aligned, so a row's byte misalignment is fixed per head
+  const uint32_t ksel = stage_selector(k_row_off & 3, part != 0);
+  const uint32_t vsel = stage_selector(v_row_off & 3, part != 0);
   const int dl = 16 * wv + 4 * gq;
+  // fp8 code unit of the hardware conversion (2^-9 for OCP e4m3, 2^-10 for FNUZ); codes of 4
+  // bits are converted as plain bytes
+  const float inv_unit_k =
+      RB == 3 ? 1.0f / __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0] : 1.0f;
+  const float inv_unit_v =
+      VB == 3 ? 1.0f / __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0] : 1.0f;
   __syncthreads();  // seg
 
   auto slot_base = [&](int tt) -> const uint8_t* {
     if (ptok >= min(kTile, t1 - tt)) return nullptr;
     const int pos = tt + ptok;
-    const int bi = pos / a.block_size;
+    const int bi = a.bs_shift >= 0 ? pos >> a.bs_shift : pos / a.block_size;
     const int blk = S.seg[bi - bfirst];
     if (blk < 0) return nullptr;
     const int64_t slot = (int64_t)blk * a.block_size + (pos - bi * a.block_size);
@@ -249,21 +278,30 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
     }
   }
 
-  // ---- query rows of the G heads of KV head h, pre-scaled by scale * log2(e), into LDS.
-  for (int i = tid; i < G * kD; i += kThreads)
-    S.qs[i / kD][i % kD] =
-        load_act(a.q, a.q_dtype, qrow * a.q_row_stride + (int64_t)(h * G) * kD + i) * a.scale_log2;
+  // ---- query fragments (A operand of q.k, M = heads, K = this wave's 32 dims in the order of
+  // the rotated-key fragments: 8*gq + i <-> dim dl + i, 8*gq + 4 + i <-> dim 64 + dl + i),
+  // split hi + lo in fp16; rows >= G are zero.
+  half8 qhi, qlo;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int dim = (j < 4 ? dl + j : 64 + dl + j - 4);
+    const float f =
+        n < G ? load_act(a.q, a.q_dtype, qrow * a.q_row_stride + (int64_t)(h * G + n) * kD + dim)
+              : 0.f;
+    const _Float16 hi = (_Float16)f;
+    qhi[j] = hi;
+    qlo[j] = (_Float16)(f - (float)hi);
+  }
 
-  float o[G][8], psum[G], m_run[G], l_run[G];
+  float o[G][8], m_run[G], l_lane[G], psum[G];
 #pragma unroll
   for (int p = 0; p < G; ++p) {
-    psum[p] = 0.f;
     m_run[p] = -INFINITY;
-    l_run[p] = 0.f;
+    l_lane[p] = 0.f;
+    psum[p] = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[p][i] = 0.f;
   }
-
 
   for (int tt = t0; tt < t1; tt += kTile) {
     const int ntile = min(kTile, t1 - tt);
@@ -274,20 +312,16 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
       for (int dw = 0; dw < KSTEPS * 2; ++dw) {
         // bytes past r1 (the ruler, head 0's row) are converted too: they are finite, and the
         // decoder fragments are zero for k >= r1, so they contribute exactly 0
-        const uint32_t x = P.coef[dw];
         uint32_t p01, p23;
-        i8x4_to_f16(x, p01, p23);
+        i8x4_to_f16(P.coef[dw], p01, p23);
         cdst[2 * dw] = p01;
         cdst[2 * dw + 1] = p23;
       }
-      // coefficient ruler (fp16 LE at byte coeff_bytes), fetched by part 0
       if (part == 0) S.cs[ptok] = f16_bits_to_float(P.rul);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        S.rawk[ptok][part * 4 + i] =
-            k_sh ? __builtin_amdgcn_alignbyte(P.krow[i + 1], P.krow[i], k_sh) : P.krow[i];
-        S.rawv[ptok][part * 4 + i] =
-            v_sh ? __builtin_amdgcn_alignbyte(P.vrow[i + 1], P.vrow[i], v_sh) : P.vrow[i];
+        S.rawk[ptok][part * 4 + i] = __builtin_amdgcn_perm(P.krow[i + 1], P.krow[i], ksel);
+        S.rawv[ptok][part * 4 + i] = __builtin_amdgcn_perm(P.vrow[i + 1], P.vrow[i], vsel);
       }
     }
     // ---------------------------------------------------------------- prefetch the next tile
@@ -300,20 +334,18 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
       const int half = tid & 1;
       if (kind == 0) {
         const uint32_t* row = S.rawk[tok];
-        decode_half_row<RB>(row, half, S.lut, nullptr, &S.kcode[tok][64 * half]);
+        decode_half_row_be<RB>(row, half, S.lut, S.lut3, &S.kcode[tok][64 * half]);
         if (half == 0) {
-          const int rb = 16 + g.k_pb;
-          const uint32_t bits = __builtin_amdgcn_alignbyte(row[(rb >> 2) + 1], row[rb >> 2], rb & 3);
-          S.krul[tok] = f16_bits_to_float(bits & 0xffffu);
+          const float kr = f16_bits_to_float(staged_u16(row, kBitmapBytes + g.k_pb));
+          const float cs = S.cs[tok];
+          S.kr[tok] = cs != 0.f ? kr * inv_unit_k / cs : 0.f;
+          S.f[tok] = cs * a.scale_log2;
         }
       } else {
         const uint32_t* row = S.rawv[tok];
-        decode_half_row<VB>(row, half, S.lut, nullptr, &S.vcode[tok][64 * half]);
-        if (half == 0) {
-          const int rb = 16 + g.v_pb;
-          const uint32_t bits = __builtin_amdgcn_alignbyte(row[(rb >> 2) + 1], row[rb >> 2], rb & 3);
-          S.vrul[tok] = f16_bits_to_float(bits & 0xffffu);
-        }
+        decode_half_row_be<VB>(row, half, S.lut, S.lut3, &S.vcode[tok][64 * half]);
+        if (half == 0)
+          S.vr[tok] = f16_bits_to_float(staged_u16(row, kBitmapBytes + g.v_pb)) * inv_unit_v;
       }
     }
     __syncthreads();
@@ -332,7 +364,10 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
       const int tok = 16 * nb + n;
       const float4v cv = cvn, sv = svn;
       if (nb < 3) angle_row(nb + 1, cvn, svn);
-      float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+      const float krp = S.kr[tok];
+      // 4-bit codes arrive as c: the -8 * ruler offset enters as the accumulator's start
+      const float kb = RB == 4 ? -8.f * krp : 0.f;
+      float4v acc0 = {kb, kb, kb, kb}, acc1 = {kb, kb, kb, kb};
 #pragma unroll
       for (int s = 0; s < KSTEPS; ++s) {
         const half8 b = *(const half8*)&S.coef[tok][32 * s + 8 * gq];
@@ -341,63 +376,66 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
         acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[1][s], b, acc1, 0, 0, 0);
         acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[1][s], b, acc1, 0, 0, 0);
       }
-      const float cs = S.cs[tok];
-      const float kr = S.krul[tok];
-      const float kb = -(float)(1 << (RB - 1)) * kr;
-      const uint32_t cl = *(const uint32_t*)&S.kcode[tok][dl];
-      const uint32_t ch = *(const uint32_t*)&S.kcode[tok][64 + dl];
-      float yl[4], yh[4];
+      float vl[4], vh[4];
+      codes4<RB>(*(const uint32_t*)&S.kcode[tok][dl], vl);
+      codes4<RB>(*(const uint32_t*)&S.kcode[tok][64 + dl], vh);
+      float y[8];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float rl = fmaf((float)((cl >> (8 * i)) & 0xffu), kr, kb);
-        const float rh = fmaf((float)((ch >> (8 * i)) & 0xffu), kr, kb);
-        const float kl = fmaf(cs, acc0[i], rl);
-        const float kh = fmaf(cs, acc1[i], rh);
-        yl[i] = kl * cv[i] - kh * sv[i];
-        yh[i] = kh * cv[i] + kl * sv[i];
+        const float kl = fmaf(krp, vl[i], acc0[i]);
+        const float kh = fmaf(krp, vh[i], acc1[i]);
+        y[i] = kl * cv[i] - kh * sv[i];
+        y[4 + i] = kh * cv[i] + kl * sv[i];
       }
-#pragma unroll
-      for (int p = 0; p < G; ++p) {
-        const float4v ql = *(const float4v*)&S.qs[p][dl];
-        const float4v qh = *(const float4v*)&S.qs[p][64 + dl];
-        float sp = 0.f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          sp = fmaf(ql[i], yl[i], sp);
-          sp = fmaf(qh[i], yh[i], sp);
-        }
-        sp = cross_row_sum(sp);
-        if (gq == (p & 3)) S.spart[wv][p][tok] = sp;
-      }
+      half8 yhi, ylo;
+      split8(y, yhi, ylo);
+      float4v sacc = {0.f, 0.f, 0.f, 0.f};
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qhi, yhi, sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qhi, ylo, sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qlo, yhi, sacc, 0, 0, 0);
+      // lane (n, gq) holds heads 4*gq .. 4*gq+3 of token n
+      if (4 * gq < G) *(float4v*)&S.spart[wv][tok][4 * gq] = sacc;
     }
-    // next tile's angles: issued after this tile's raw-byte prefetch, needed one tile later
     __syncthreads();
     // ---------------------------------------------------------------- online softmax (every wave)
     float pv[G];
     {
-      const int tok = lane;
-      const bool valid = tok < ntile;
-      const float vr = S.vrul[tok];
+      const bool valid = lane < ntile;
+      const float ft = S.f[lane];
+      const float vrt = S.vr[lane];
+      float sum[kSP];
+#pragma unroll
+      for (int i = 0; i < kSP; ++i) sum[i] = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < kWaves; ++ww) {
+#pragma unroll
+        for (int i = 0; i < kSP; i += 4) {
+          const float4v x = *(const float4v*)&S.spart[ww][lane][i];
+          sum[i] += x[0];
+          sum[i + 1] += x[1];
+          sum[i + 2] += x[2];
+          sum[i + 3] += x[3];
+        }
+      }
 #pragma unroll
       for (int p = 0; p < G; ++p) {
-        float s = S.spart[0][p][tok] + S.spart[1][p][tok] + S.spart[2][p][tok] +
-                  S.spart[3][p][tok];
-        s = valid ? s : -INFINITY;
-        // Lazy rescaling: the reference point m_run only moves when the tile max exceeds it by
-        // more than 2^8, so most tiles skip the rescale (p stays <= 256; fp32 has the range).
-        // m_run is the same in every lane and wave (same inputs), so the branch is uniform.
-        const float mt = wave_max(s);
-        if (mt > m_run[p] + 8.f) {
+        const float s = valid ? sum[p] * ft : -INFINITY;
+        // Lazy rescaling: the reference point m_run only moves when some score exceeds it by
+        // more than 2^8, so most tiles skip the wave-wide max (p stays <= 256; fp32 has the
+        // range). m_run is the same in every lane and wave (same inputs), so the branch is
+        // uniform.
+        if (__builtin_amdgcn_ballot_w64(s > m_run[p] + 8.f) != 0) {
+          const float mt = wave_max(s);
           const float alpha = exp2f(m_run[p] - mt);
           m_run[p] = mt;
-          l_run[p] *= alpha;
+          l_lane[p] *= alpha;
+          psum[p] *= alpha;
 #pragma unroll
           for (int i = 0; i < 8; ++i) o[p][i] *= alpha;
-          psum[p] *= alpha;
         }
-        const float pr = valid ? fast_exp2(s - m_run[p]) : 0.f;
-        l_run[p] += wave_sum(pr);
-        pv[p] = pr * vr;
+        const float pr = fast_exp2(s - m_run[p]);
+        l_lane[p] += pr;
+        pv[p] = pr * vrt;
       }
     }
     // ---------------------------------------------------------------- P.V
@@ -407,36 +445,32 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
       const int tok = 16 * nb + n;
-      const uint32_t cl = *(const uint32_t*)&S.vcode[tok][dl];
-      const uint32_t ch = *(const uint32_t*)&S.vcode[tok][64 + dl];
       float v[8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v[i] = (float)((cl >> (8 * i)) & 0xffu);
-        v[4 + i] = (float)((ch >> (8 * i)) & 0xffu);
-      }
+      codes4<VB>(*(const uint32_t*)&S.vcode[tok][dl], v);
+      codes4<VB>(*(const uint32_t*)&S.vcode[tok][64 + dl], v + 4);
 #pragma unroll
       for (int p = 0; p < G; ++p) {
         const float pw = pwb[p][nb];
-        psum[p] += pw;
+        if (VB == 4) psum[p] += pw;
 #pragma unroll
         for (int i = 0; i < 8; ++i) o[p][i] = fmaf(pw, v[i], o[p][i]);
       }
     }
   }
 
-  // ---- reduce o over the 16 token lanes of each lane group; remove the 2^(b-1) code offset
+  // ---- reduce o over the 16 token lanes of each lane group (4-bit: remove the code offset)
 #pragma unroll
   for (int p = 0; p < G; ++p) {
-    const float off = (float)(1 << (VB - 1)) * row_sum(psum[p]);
+    const float off = VB == 4 ? 8.f * row_sum(psum[p]) : 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[p][i] = row_sum(o[p][i]) - off;
+    l_lane[p] = wave_sum(l_lane[p]);
   }
   if (tid == 0) {
 #pragma unroll
     for (int p = 0; p < G; ++p) {
       S.m[p] = m_run[p];
-      S.l[p] = l_run[p];
+      S.l[p] = l_lane[p];
     }
   }
   __syncthreads();
@@ -627,6 +661,7 @@ int decode_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype,
   a.n_slots = n_slots;
   a.slot_stride = slot_stride;
   a.block_size = block_size;
+  a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
   a.bt = bt;
   a.bt_row_stride = bt_row_stride;
   a.max_blocks = max_blocks;

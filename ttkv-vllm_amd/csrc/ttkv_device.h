@@ -234,6 +234,152 @@ __device__ __forceinline__ void bcast_rows(float v, float out[4]) {
 }
 
 
+// ------------------------------------------------------------------ big-endian staged rows
+// The read kernels stage a head row in LDS as dwords 0..3 = bitmap (as stored) and dwords 4.. =
+// code stream with each dword byte-reversed, so that the MSB-first stream reads as big-endian
+// words: stream bit b is bit 31 - (b & 31) of word b >> 5. One v_perm per dword does the
+// realignment (the row starts at any byte) and the reversal together.
+//
+// v_perm_b32(S0, S1, sel): byte k of the result is byte sel.k of the 8 bytes {S1 (0..3), S0
+// (4..7)}; selector 0x0c gives 0x00.
+__device__ __forceinline__ uint32_t stage_selector(int sh, bool reverse) {
+  const uint32_t s = (uint32_t)sh;
+  return reverse ? ((s + 3u) | ((s + 2u) << 8) | ((s + 1u) << 16) | (s << 24))
+                 : (s | ((s + 1u) << 8) | ((s + 2u) << 16) | ((s + 3u) << 24));
+}
+
+// The 16-bit ruler at row byte `rb` (little-endian), read back from a staged row whose bytes
+// from 16 on are reversed within their dwords.
+__device__ __forceinline__ uint32_t staged_u16(const uint32_t* row, int rb) {
+  const uint32_t lo = (row[rb >> 2] >> (8 * (3 - (rb & 3)))) & 0xffu;
+  const int rb1 = rb + 1;
+  const uint32_t hi = (row[rb1 >> 2] >> (8 * (3 - (rb1 & 3)))) & 0xffu;
+  return lo | (hi << 8);
+}
+
+// Codes are handed to the arithmetic as fp8 (e4m3) bytes holding the signed value c - 2^(b-1)
+// in sign-magnitude: magnitude k <= 15 is byte k in both e4m3 variants (k * 2^-9 in OCP e4m3,
+// k * 2^-10 in the FNUZ one; the kernels read the unit back from the hardware conversion).
+// Lanes outside the bitmap get byte 0 (+0), i.e. residual 0, with no fix-up pass.
+__host__ __device__ constexpr uint32_t fp8_signed_byte(int d) {
+  return d >= 0 ? (uint32_t)d : (0x80u | (uint32_t)(-d));
+}
+
+// 3-bit spread table: entry x (12 bits = 4 codes, first code in the top 3 bits) -> the 4 codes
+// as fp8 signed bytes (c - 4), first code in byte 0.
+struct SpreadLut3 {
+  uint32_t v[4096];
+  constexpr SpreadLut3() : v() {
+    for (uint32_t x = 0; x < 4096; ++x) {
+      uint32_t r = 0;
+      for (int i = 0; i < 4; ++i) r |= fp8_signed_byte((int)((x >> (9 - 3 * i)) & 7u) - 4) << (8 * i);
+      v[x] = r;
+    }
+  }
+};
+// Scatter table: entry B holds the v_perm selectors that move the byte-spread codes of bitmap
+// byte B (MSB = first lane) onto its set lanes, 0x0c (zero byte) on the others.
+struct ScatterLut {
+  uint32_t v[512];
+  constexpr ScatterLut() : v() {
+    for (uint32_t B = 0; B < 256; ++B) {
+      uint32_t s0 = 0, s1 = 0, idx = 0;
+      for (int k = 0; k < 8; ++k) {
+        const bool present = (B >> (7 - k)) & 1u;
+        const uint32_t sel = present ? idx : 0x0cu;
+        idx += present ? 1u : 0u;
+        if (k < 4) s0 |= sel << (8 * k);
+        else s1 |= sel << (8 * (k - 4));
+      }
+      v[2 * B] = s0;
+      v[2 * B + 1] = s1;
+    }
+  }
+};
+static __constant__ SpreadLut3 kSpreadLut3 = SpreadLut3();
+static __constant__ ScatterLut kScatterLut = ScatterLut();
+
+// Copy the tables into LDS with 16-byte loads (256-thread blocks).
+__device__ __forceinline__ void stage_luts(uint2* lut, uint32_t* lut3, int tid, int nthreads) {
+  const u32x4* s = (const u32x4*)kScatterLut.v;
+  for (int i = tid; i < 128; i += nthreads) ((u32x4*)lut)[i] = s[i];
+  if (lut3) {
+    const u32x4* s3 = (const u32x4*)kSpreadLut3.v;
+    for (int i = tid; i < 1024; i += nthreads) ((u32x4*)lut3)[i] = s3[i];
+  }
+}
+
+// Decode dims [64*half, 64*half+64) of one big-endian staged head row into one byte per lane at
+// dst[0..63].
+//   BITS == 3: fp8 signed bytes (c - 4), 0 outside the bitmap; needs lut3 (SpreadLut3).
+//   BITS == 4: offset-binary code bytes c, 8 outside the bitmap.
+// Per bitmap byte: the code window at bit offset bp is one v_alignbit of the words holding bits
+// bp-1 and bp+31 (shift (-bp) mod 32; word -1 is the last bitmap dword, read but unused).
+template <int BITS>
+__device__ __forceinline__ void decode_half_row_be(const uint32_t* row, int half, const uint2* lut,
+                                                   const uint32_t* lut3, uint8_t* dst) {
+  const uint32_t bm0 = row[2 * half], bm1 = row[2 * half + 1];
+  int rank = half ? __builtin_popcount(row[0]) + __builtin_popcount(row[1]) : 0;
+  const uint32_t* st = row + 4;
+#pragma unroll
+  for (int m0 = 0; m0 < 8; m0 += 4) {
+    uint32_t B[4];
+    int bp[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      B[m] = __builtin_amdgcn_ubfe(m0 < 4 ? bm0 : bm1, 8 * m, 8);
+      bp[m] = rank * BITS;
+      rank += __builtin_popcount(B[m]);
+    }
+    uint2 sel[4];
+    uint32_t w[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      sel[m] = lut[B[m]];
+      const uint32_t* wp = st + ((bp[m] - 1) >> 5);
+      w[m] = __builtin_amdgcn_alignbit(wp[0], wp[1], (uint32_t)(-bp[m]));
+    }
+    uint32_t e0[4], e1[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      if constexpr (BITS == 3) {
+        e0[m] = lut3[w[m] >> 20];
+        e1[m] = lut3[(w[m] >> 8) & 0xfffu];
+      } else {
+        spread8<4>(w[m] ^ 0x88888888u, e0[m], e1[m]);
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      uint2 out;
+      out.x = __builtin_amdgcn_perm(e1[m], e0[m], sel[m].x);
+      out.y = __builtin_amdgcn_perm(e1[m], e0[m], sel[m].y);
+      if constexpr (BITS == 4) {
+        out.x ^= 0x08080808u;
+        out.y ^= 0x08080808u;
+      }
+      *(uint2*)(dst + 8 * (m0 + m)) = out;
+    }
+  }
+}
+
+// Four decoded code bytes -> floats. BITS == 3: fp8 signed bytes -> (c - 4) * unit, two per
+// v_cvt_pk_f32_fp8. BITS == 4: offset-binary bytes -> c (the caller removes the offset).
+template <int BITS>
+__device__ __forceinline__ void codes4(uint32_t x, float v[4]) {
+  if constexpr (BITS == 3) {
+    const auto a = __builtin_amdgcn_cvt_pk_f32_fp8((int)x, false);
+    const auto b = __builtin_amdgcn_cvt_pk_f32_fp8((int)x, true);
+    v[0] = a[0];
+    v[1] = a[1];
+    v[2] = b[0];
+    v[3] = b[1];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = (float)((x >> (8 * i)) & 0xffu);
+  }
+}
+
 // Selector table for decode_half_row: entry B holds the v_perm selectors that move the
 // byte-spread codes of bitmap byte B onto its set lanes (0x0c -> zero byte elsewhere). One entry
 // per thread of a 256-thread block.
