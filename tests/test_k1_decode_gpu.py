@@ -23,7 +23,7 @@ def _run_k1(stores, q, cache, block_size=16, seed=0, out_dtype=torch.float16):
     for r in range(B):
         dec_map[pg["block_table"][r, 0]] = r
     qsl = torch.arange(B + 1, dtype=torch.int32)
-    out = torch.zeros(B, HQ, 128, dtype=out_dtype, device=dev)
+    out = torch.zeros(B, q.shape[1], 128, dtype=out_dtype, device=dev)
     err = torch.zeros(1, dtype=torch.int32, device=dev)
     kernels.decode_paged(lay, q.to(dev), pg["page"].to(dev), block_size,
                          pg["block_table"].to(dev), pg["seq_lens"].to(dev), qsl.to(dev),
@@ -152,3 +152,47 @@ def test_write_then_read_loop():
     cosim = torch.nn.functional.cosine_similarity(out.float().cpu().double().reshape(1, -1),
                                                    ref.reshape(1, -1)).item()
     assert cosim > 0.95, cosim
+
+
+@pytest.mark.parametrize("hq,r1,bs", [(8, 64, 16), (16, 110, 32), (32, 160, 24), (64, 110, 16)])
+def test_head_groups_ranks_and_block_sizes(hq, r1, bs):
+    """Every built instantiation family: 1/2/4/8 query heads per KV head, rank budgets that take
+    2, 4 and 5 MFMA k-steps, and block sizes including one that is not a power of two."""
+    lens = [37, 300, 1025]
+    stores = [fitted_store("safe", n, seed=40 + i, r1=r1) for i, n in enumerate(lens)]
+    q = synth.queries(len(lens), HQ=hq, seed=7)
+    cache = llama3_cache(2048)
+    got, pg = _run_k1(stores, q, cache, block_size=bs, seed=9)
+    _check(got, _oracle(stores, q, cache, pg, block_size=bs), f"hq={hq} r1={r1} bs={bs}")
+
+
+def test_empty_context_and_missing_decoder():
+    """A request with no cached tokens reads as zeros (the reference's einsum over zero rows); a
+    request whose first block has no registered decoder sets error bit 1 and reads as NaN, and
+    neither disturbs the other requests of the launch."""
+    stores = [fitted_store("safe", n, seed=60 + i) for i, n in enumerate([200, 1, 500])]
+    q = synth.queries(3, seed=8)
+    cache = llama3_cache(1024)
+    pg = paged(stores, 16, 3)
+    dev = "cuda"
+    lay = stores[0]["lay"]
+    seq_lens = pg["seq_lens"].clone()
+    seq_lens[1] = 0                                      # request 1: empty
+    dec_pool = torch.stack([s["decoder"] for s in stores]).to(dev)
+    dec_map = torch.full((pg["num_blocks"],), -1, dtype=torch.int32)
+    dec_map[pg["block_table"][0, 0]] = 0                 # request 2 left unregistered
+    dec_map[pg["block_table"][1, 0]] = 1
+    out = torch.full((3, HQ, 128), 7.0, dtype=torch.float16, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    kernels.decode_paged(lay, q.to(dev), pg["page"].to(dev), 16, pg["block_table"].to(dev),
+                         seq_lens.to(dev), torch.arange(4, dtype=torch.int32).to(dev),
+                         int(seq_lens.max()), dec_map.to(dev), dec_pool, cache.to(dev),
+                         128 ** -0.5, out=out, error_word=err)
+    torch.cuda.synchronize()
+    got = out.float().cpu()
+    assert int(err.item()) == 1
+    assert torch.all(got[1] == 0)
+    assert torch.isnan(got[2]).all()
+    want = _oracle(stores[:1], q[:1], cache, dict(pg, block_table=pg["block_table"][:1],
+                                                  seq_lens=pg["seq_lens"][:1]))
+    _check(got[:1], want, "request 0 beside an empty and an undecodable request")

@@ -80,9 +80,11 @@ struct DecodeArgs {
   int chunk, max_chunks, nwork, max_seq;
 };
 
-template <int KSTEPS, int G>
+// KU = coefficient window in 16-wide k units: r1 is padded to 16 * KU; the reconstruction runs
+// KU / 2 MFMA steps of k = 32 and, for odd KU, one of k = 16.
+template <int KU, int G>
 struct DecodeSmem {
-  static constexpr int kCoefStride = KSTEPS * 32 + 8;  // fp16 per token row
+  static constexpr int kCoefStride = KU * 16 + 8;  // fp16 per token row
   static constexpr int kSP = G <= 4 ? 4 : 8;           // score slots per token
   _Float16 coef[kTile][kCoefStride];
   uint32_t rawk[kTile][kRawDw];
@@ -102,20 +104,20 @@ struct DecodeSmem {
 };
 
 // Raw bytes of one token prefetched by one of its 4 threads.
-template <int KSTEPS>
+template <int KU>
 struct Prefetch {
-  uint32_t coef[KSTEPS * 2];  // KSTEPS*8 coefficient bytes
+  uint32_t coef[KU];  // this part's quarter of the 16*KU coefficient bytes
   uint32_t krow[5], vrow[5];  // 5 source dwords (4 output dwords + funnel)
   uint32_t rul;               // coefficient ruler bits (part 0)
 };
 
-template <int KSTEPS>
-__device__ __forceinline__ void prefetch(Prefetch<KSTEPS>& P, const uint8_t* base, int part,
+template <int KU>
+__device__ __forceinline__ void prefetch(Prefetch<KU>& P, const uint8_t* base, int part,
                                          const Geom& g, int k_row_off, int v_row_off) {
-  constexpr int kCPP = KSTEPS * 8;
+  constexpr int kCPP = KU * 4;
   if (!base) {
 #pragma unroll
-    for (int i = 0; i < KSTEPS * 2; ++i) P.coef[i] = 0u;
+    for (int i = 0; i < KU; ++i) P.coef[i] = 0u;
 #pragma unroll
     for (int i = 0; i < 5; ++i) P.krow[i] = P.vrow[i] = 0u;
     P.rul = 0u;
@@ -123,7 +125,7 @@ __device__ __forceinline__ void prefetch(Prefetch<KSTEPS>& P, const uint8_t* bas
   }
   const uint32_t* cs = (const uint32_t*)(base + part * kCPP);
 #pragma unroll
-  for (int i = 0; i < KSTEPS * 2; ++i) P.coef[i] = cs[i];
+  for (int i = 0; i < KU; ++i) P.coef[i] = cs[i];
   {
     const uintptr_t A = (uintptr_t)(base + k_row_off);
     const uint32_t* src = (const uint32_t*)(A & ~(uintptr_t)3);
@@ -157,12 +159,14 @@ __device__ __forceinline__ void split8(const float y[8], half8& hi, half8& lo) {
   }
 }
 
-template <int G, int RB, int VB, int KSTEPS>
+template <int G, int RB, int VB, int KU>
 __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  using Smem = DecodeSmem<KSTEPS, G>;
+  using Smem = DecodeSmem<KU, G>;
   Smem& S = *reinterpret_cast<Smem*>(smem_raw);
-  constexpr int kCPP = KSTEPS * 8;
+  constexpr int kCPP = KU * 4;
+  constexpr int KSTEPS = KU / 2;  // k = 32 steps
+  constexpr bool KTAIL = KU & 1;  // one more k = 16 step
   constexpr int kSP = Smem::kSP;
   const Geom& g = a.g;
   const int tid = threadIdx.x;
@@ -255,13 +259,14 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   };
 
   // first tile's bytes in flight while the decoder is loaded
-  Prefetch<KSTEPS> P;
-  prefetch<KSTEPS>(P, slot_base(t0), part, g, k_row_off, v_row_off);
+  Prefetch<KU> P;
+  prefetch<KU>(P, slot_base(t0), part, g, k_row_off, v_row_off);
 
   // ---- decoder fragments (A operand, M = dims, K = r1), hi/lo fp16, resident in registers.
   const int HD = g.H * kD;
   const float* dec = a.dec_pool + (int64_t)dslot * g.r1 * HD + h * kD;
   half8 ahi[2][KSTEPS], alo[2][KSTEPS];
+  half4 thi[2], tlo[2];  // k = 16 tail step (odd KU)
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi) {
     const int dim = 16 * (wv + 4 * mi) + n;
@@ -275,6 +280,14 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
         ahi[mi][s][j] = hi;
         alo[mi][s][j] = (_Float16)(f - (float)hi);
       }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int ar = 32 * KSTEPS + 4 * gq + j;
+      const float f = KTAIL && ar < g.r1 ? dec[(int64_t)ar * HD + dim] : 0.f;
+      const _Float16 hi = (_Float16)f;
+      thi[mi][j] = hi;
+      tlo[mi][j] = (_Float16)(f - (float)hi);
     }
   }
 
@@ -309,7 +322,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
     {
       uint32_t* cdst = (uint32_t*)&S.coef[ptok][part * kCPP];
 #pragma unroll
-      for (int dw = 0; dw < KSTEPS * 2; ++dw) {
+      for (int dw = 0; dw < KU; ++dw) {
         // bytes past r1 (the ruler, head 0's row) are converted too: they are finite, and the
         // decoder fragments are zero for k >= r1, so they contribute exactly 0
         uint32_t p01, p23;
@@ -325,7 +338,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
       }
     }
     // ---------------------------------------------------------------- prefetch the next tile
-    if (tt + kTile < t1) prefetch<KSTEPS>(P, slot_base(tt + kTile), part, g, k_row_off, v_row_off);
+    if (tt + kTile < t1) prefetch<KU>(P, slot_base(tt + kTile), part, g, k_row_off, v_row_off);
     __syncthreads();
     // ---------------------------------------------------------------- decode (thread = half row)
     {
@@ -375,6 +388,13 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
         acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[0][s], b, acc0, 0, 0, 0);
         acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[1][s], b, acc1, 0, 0, 0);
         acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[1][s], b, acc1, 0, 0, 0);
+      }
+      if constexpr (KTAIL) {
+        const half4 b = *(const half4*)&S.coef[tok][32 * KSTEPS + 4 * gq];
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x16f16(thi[0], b, acc0, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x16f16(tlo[0], b, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x16f16(thi[1], b, acc1, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x16f16(tlo[1], b, acc1, 0, 0, 0);
       }
       float vl[4], vh[4];
       codes4<RB>(*(const uint32_t*)&S.kcode[tok][dl], vl);
@@ -552,10 +572,10 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
 
 namespace ttkv {
 
-template <int G, int RB, int VB, int KSTEPS>
+template <int G, int RB, int VB, int KU>
 static int launch_decode_t(const DecodeArgs& a, int grid, hipStream_t st) {
-  const size_t smem = sizeof(DecodeSmem<KSTEPS, G>);
-  auto kfn = decode_paged_kernel<G, RB, VB, KSTEPS>;
+  const size_t smem = sizeof(DecodeSmem<KU, G>);
+  auto kfn = decode_paged_kernel<G, RB, VB, KU>;
   static bool attr_set = false;  // per instantiation; benign race (idempotent)
   if (!attr_set) {
     if (hipFuncSetAttribute((const void*)kfn, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -570,25 +590,26 @@ static int launch_decode_t(const DecodeArgs& a, int grid, hipStream_t st) {
   return TTKV_OK;
 }
 
-template <int RB, int VB, int KSTEPS>
+template <int RB, int VB, int KU>
 static int dispatch_g(const DecodeArgs& a, int grid, hipStream_t st) {
   switch (a.G) {
-    case 1: return launch_decode_t<1, RB, VB, KSTEPS>(a, grid, st);
-    case 2: return launch_decode_t<2, RB, VB, KSTEPS>(a, grid, st);
-    case 3: return launch_decode_t<3, RB, VB, KSTEPS>(a, grid, st);
-    case 4: return launch_decode_t<4, RB, VB, KSTEPS>(a, grid, st);
-    case 8: return launch_decode_t<8, RB, VB, KSTEPS>(a, grid, st);
+    case 1: return launch_decode_t<1, RB, VB, KU>(a, grid, st);
+    case 2: return launch_decode_t<2, RB, VB, KU>(a, grid, st);
+    case 3: return launch_decode_t<3, RB, VB, KU>(a, grid, st);
+    case 4: return launch_decode_t<4, RB, VB, KU>(a, grid, st);
+    case 8: return launch_decode_t<8, RB, VB, KU>(a, grid, st);
   }
   return host_fail(TTKV_E_UNSUPPORTED, "num_heads / H = " + std::to_string(a.G) +
                                            " query heads per KV head is not built (1,2,3,4,8)");
 }
 
 template <int RB, int VB>
-static int dispatch_k(const DecodeArgs& a, int ksteps, int grid, hipStream_t st) {
-  switch (ksteps) {
-    case 2: return dispatch_g<RB, VB, 2>(a, grid, st);
+static int dispatch_k(const DecodeArgs& a, int ku, int grid, hipStream_t st) {
+  switch (ku) {
     case 4: return dispatch_g<RB, VB, 4>(a, grid, st);
-    case 5: return dispatch_g<RB, VB, 5>(a, grid, st);
+    case 7: return dispatch_g<RB, VB, 7>(a, grid, st);
+    case 8: return dispatch_g<RB, VB, 8>(a, grid, st);
+    case 10: return dispatch_g<RB, VB, 10>(a, grid, st);
   }
   return host_fail(TTKV_E_UNSUPPORTED, "r1 > 160 is not built");
 }
@@ -626,9 +647,10 @@ int decode_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype,
     return host_fail(TTKV_E_UNSUPPORTED, "res_bits/v_bits must be 3/3 or 4/4");
   if (HQ <= 0 || HQ % g.H) return host_fail(TTKV_E_INVALID, "num_heads is not a multiple of H");
   const int G = HQ / g.H;
-  const int ksteps = g.r1 <= 64 ? 2 : g.r1 <= 128 ? 4 : g.r1 <= 160 ? 5 : 0;
-  if (!ksteps) return host_fail(TTKV_E_UNSUPPORTED, "r1 > 160 is not built");
-  if (ksteps * 32 > g.k_slot)
+  // coefficient window in 16-wide k units (r1 padded to 16 * ku)
+  const int ku = g.r1 <= 64 ? 4 : g.r1 <= 112 ? 7 : g.r1 <= 128 ? 8 : g.r1 <= 160 ? 10 : 0;
+  if (!ku) return host_fail(TTKV_E_UNSUPPORTED, "r1 > 160 is not built");
+  if (ku * 16 > g.k_slot)
     return host_fail(TTKV_E_UNSUPPORTED, "padded coefficient block exceeds the K slot");
   if (!q || !page || !bt || !seq_lens || !qsl || !dec_map || !dec_pool || !cs_cache || !out || !err)
     return host_fail(TTKV_E_INVALID, "null pointer argument");
@@ -693,8 +715,8 @@ int decode_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype,
   a.max_seq = max_seq_len;
   a.nwork = num_reqs * a.max_chunks * g.H;
   const int grid = (a.nwork + 7) / 8 * 8;
-  if (g.res_bits == 3) return dispatch_k<3, 3>(a, ksteps, grid, st);
-  return dispatch_k<4, 4>(a, ksteps, grid, st);
+  if (g.res_bits == 3) return dispatch_k<3, 3>(a, ku, grid, st);
+  return dispatch_k<4, 4>(a, ku, grid, st);
 }
 
 }  // namespace ttkv
