@@ -27,7 +27,9 @@
 //   softmax : online, base 2, evaluated redundantly by every wave (lane = token, no barrier). The
 //             reference point moves only when some score exceeds it by more than 2^8 (a ballot),
 //             so the wave-wide max is rarely computed; sums stay per lane until the end.
-//   P.V     : o[p] += P[p,t] * (ruler_v[t] / unit) * code on VALU, codes converted two per op.
+//   P.V     : o[p] += P'[p,t] * (code - 2^(b-1)) with P' = P * ruler_v. 3-bit codes: packed fp16
+//             dot products over token pairs (codes as exact fp16 integers, P' * 2^-8 rounded
+//             to nearest fp16); 4-bit codes: fp32.
 // Chunks of one (r, h) are combined in the same launch by the last workgroup to finish
 // (device-scope fence + counter), which also resets the counter to zero.
 //
@@ -241,10 +243,11 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   const int dl = 16 * wv + 4 * gq;
   // fp8 code unit of the hardware conversion (2^-9 for OCP e4m3, 2^-10 for FNUZ); codes of 4
   // bits are converted as plain bytes
-  const float inv_unit_k =
-      RB == 3 ? 1.0f / __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0] : 1.0f;
-  const float inv_unit_v =
-      VB == 3 ? 1.0f / __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0] : 1.0f;
+  const float inv_unit = 1.0f / __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0];
+  const float inv_unit_k = RB == 3 ? inv_unit : 1.0f;
+  // 3-bit V codes are read as exact integers (c - 4) and P' carries ruler_v * 2^-8; 4-bit codes
+  // are read as c with ruler_v
+  const float vr_scale = VB == 3 ? 1.0f / 256.f : 1.0f;
   __syncthreads();  // seg
 
   auto slot_base = [&](int tt) -> const uint8_t* {
@@ -358,7 +361,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
         const uint32_t* row = S.rawv[tok];
         decode_half_row_be<VB>(row, half, S.lut, S.lut3, &S.vcode[tok][64 * half]);
         if (half == 0)
-          S.vr[tok] = f16_bits_to_float(staged_u16(row, kBitmapBytes + g.v_pb)) * inv_unit_v;
+          S.vr[tok] = f16_bits_to_float(staged_u16(row, kBitmapBytes + g.v_pb)) * vr_scale;
       }
     }
     __syncthreads();
@@ -462,18 +465,49 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
     float pwb[G][4];
 #pragma unroll
     for (int p = 0; p < G; ++p) bcast_rows(pv[p], pwb[p]);
+    if constexpr (VB == 3) {
+      // Packed fp16 dot products over token pairs (16nb + n, 16nb + 16 + n): the two tokens'
+      // fp8 codes of one dim are interleaved by v_perm and converted to an exact fp16 integer
+      // pair; P' = P * ruler_v * 2^-8 is rounded to nearest fp16 (<= ruler_v, so in range).
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-      const int tok = 16 * nb + n;
-      float v[8];
-      codes4<VB>(*(const uint32_t*)&S.vcode[tok][dl], v);
-      codes4<VB>(*(const uint32_t*)&S.vcode[tok][64 + dl], v + 4);
+      for (int pp = 0; pp < 2; ++pp) {
+        const int ta = 32 * pp + n, tb = ta + 16;
+        const uint32_t al = *(const uint32_t*)&S.vcode[ta][dl];
+        const uint32_t bl = *(const uint32_t*)&S.vcode[tb][dl];
+        const uint32_t ah = *(const uint32_t*)&S.vcode[ta][64 + dl];
+        const uint32_t bh = *(const uint32_t*)&S.vcode[tb][64 + dl];
+        const uint32_t il[4] = {__builtin_amdgcn_perm(bl, al, 0x05010400u),
+                                __builtin_amdgcn_perm(bl, al, 0x07030602u),
+                                __builtin_amdgcn_perm(bh, ah, 0x05010400u),
+                                __builtin_amdgcn_perm(bh, ah, 0x07030602u)};
+        half2v cp[8];
 #pragma unroll
-      for (int p = 0; p < G; ++p) {
-        const float pw = pwb[p][nb];
-        if (VB == 4) psum[p] += pw;
+        for (int m = 0; m < 4; ++m) {
+          cp[2 * m] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(il[m], inv_unit, false);
+          cp[2 * m + 1] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(il[m], inv_unit, true);
+        }
 #pragma unroll
-        for (int i = 0; i < 8; ++i) o[p][i] = fmaf(pw, v[i], o[p][i]);
+        for (int p = 0; p < G; ++p) {
+          const half2v pp2 =
+              __builtin_convertvector(float2v{pwb[p][2 * pp], pwb[p][2 * pp + 1]}, half2v);
+#pragma unroll
+          for (int k = 0; k < 8; ++k) o[p][k] = __builtin_amdgcn_fdot2(cp[k], pp2, o[p][k], false);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) {
+        const int tok = 16 * nb + n;
+        float v[8];
+        codes4<VB>(*(const uint32_t*)&S.vcode[tok][dl], v);
+        codes4<VB>(*(const uint32_t*)&S.vcode[tok][64 + dl], v + 4);
+#pragma unroll
+        for (int p = 0; p < G; ++p) {
+          const float pw = pwb[p][nb];
+          psum[p] += pw;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[p][i] = fmaf(pw, v[i], o[p][i]);
+        }
       }
     }
   }
@@ -482,8 +516,9 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
 #pragma unroll
   for (int p = 0; p < G; ++p) {
     const float off = VB == 4 ? 8.f * row_sum(psum[p]) : 0.f;
+    const float osc = VB == 3 ? 256.f : 1.f;  // undo the 2^-8 of P'
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o[p][i] = row_sum(o[p][i]) - off;
+    for (int i = 0; i < 8; ++i) o[p][i] = row_sum(o[p][i]) * osc - off;
     l_lane[p] = wave_sum(l_lane[p]);
   }
   if (tid == 0) {
