@@ -220,6 +220,37 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
     return;
   }
 
+  // ---- decoder and query values for the MFMA fragments: loaded now, so that their latency
+  // overlaps the table and block-id staging; converted after the first prefetch is issued
+  const int dl = 16 * wv + 4 * gq;
+  const int HD = g.H * kD;
+  const float* dec = a.dec_pool + (int64_t)dslot * g.r1 * HD + h * kD;
+  float draw[2][KSTEPS * 8 + 4];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi) {
+    const int dim = 16 * (wv + 4 * mi) + n;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int ar = 32 * s + 8 * gq + j;
+        draw[mi][8 * s + j] = ar < g.r1 ? dec[(int64_t)ar * HD + dim] : 0.f;
+      }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int ar = 32 * KSTEPS + 4 * gq + j;
+      draw[mi][8 * KSTEPS + j] = KTAIL && ar < g.r1 ? dec[(int64_t)ar * HD + dim] : 0.f;
+    }
+  }
+  float qraw[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int dim = (j < 4 ? dl + j : 64 + dl + j - 4);
+    qraw[j] = n < G ? load_act(a.q, a.q_dtype,
+                               qrow * a.q_row_stride + (int64_t)(h * G + n) * kD + dim)
+                    : 0.f;
+  }
+
   // ---- code tables, and this chunk's block ids
   stage_luts(S.lut, (RB == 3 || VB == 3) ? S.lut3 : nullptr, tid, kThreads);
   const int bfirst = t0 / a.block_size;
@@ -240,7 +271,6 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   // slot bases are 16-aligned, so a row's byte misalignment is fixed per head
   const uint32_t ksel = stage_selector(k_row_off & 3, part != 0);
   const uint32_t vsel = stage_selector(v_row_off & 3, part != 0);
-  const int dl = 16 * wv + 4 * gq;
   // fp8 code unit of the hardware conversion (2^-9 for OCP e4m3, 2^-10 for FNUZ); codes of 4
   // bits are converted as plain bytes
   const float inv_unit = 1.0f / __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0];
@@ -266,28 +296,22 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   prefetch<KU>(P, slot_base(t0), part, g, k_row_off, v_row_off);
 
   // ---- decoder fragments (A operand, M = dims, K = r1), hi/lo fp16, resident in registers.
-  const int HD = g.H * kD;
-  const float* dec = a.dec_pool + (int64_t)dslot * g.r1 * HD + h * kD;
   half8 ahi[2][KSTEPS], alo[2][KSTEPS];
   half4 thi[2], tlo[2];  // k = 16 tail step (odd KU)
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi) {
-    const int dim = 16 * (wv + 4 * mi) + n;
 #pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) {
+    for (int s = 0; s < KSTEPS; ++s)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int ar = 32 * s + 8 * gq + j;
-        const float f = ar < g.r1 ? dec[(int64_t)ar * HD + dim] : 0.f;
+        const float f = draw[mi][8 * s + j];
         const _Float16 hi = (_Float16)f;
         ahi[mi][s][j] = hi;
         alo[mi][s][j] = (_Float16)(f - (float)hi);
       }
-    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int ar = 32 * KSTEPS + 4 * gq + j;
-      const float f = KTAIL && ar < g.r1 ? dec[(int64_t)ar * HD + dim] : 0.f;
+      const float f = draw[mi][8 * KSTEPS + j];
       const _Float16 hi = (_Float16)f;
       thi[mi][j] = hi;
       tlo[mi][j] = (_Float16)(f - (float)hi);
@@ -300,13 +324,9 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   half8 qhi, qlo;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const int dim = (j < 4 ? dl + j : 64 + dl + j - 4);
-    const float f =
-        n < G ? load_act(a.q, a.q_dtype, qrow * a.q_row_stride + (int64_t)(h * G + n) * kD + dim)
-              : 0.f;
-    const _Float16 hi = (_Float16)f;
+    const _Float16 hi = (_Float16)qraw[j];
     qhi[j] = hi;
-    qlo[j] = (_Float16)(f - (float)hi);
+    qlo[j] = (_Float16)(qraw[j] - (float)hi);
   }
 
   float o[G][8], m_run[G], l_lane[G], psum[G];
