@@ -8,7 +8,8 @@
 // Work item = (request, KV head h, block of 64 queries, key split). A 256-thread workgroup walks
 // its key range in 64-key tiles:
 //   commit    : the tile's slot bytes -> LDS (coefficients as exact fp16, this head's K and V rows)
-//   decode    : bitmap + MSB-first code stream -> one code byte per (key, lane), as in K1
+//   decode    : bitmap + MSB-first code stream -> one code byte per (key, lane), as in K1 (3-bit
+//               codes as fp8 signed bytes, 4-bit as offset-binary bytes)
 //   transpose : V codes -> Vt[dim][key] = code - 2^(b-1) in fp16 (small integers, exact)
 //   recon     : K_pre^T[dims x 16 keys] = Dec^T * coeff^T on MFMA 16x16x32 f16 (decoder fragments
 //               resident in registers), + cs * acc + residual, RoPE in registers -> Kp[key][dim]
@@ -187,9 +188,7 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
     return;
   }
 
-  S.lut[tid] = scatter_lut_entry((uint32_t)tid);
-  if (RB == 3 || VB == 3)
-    for (int i = tid; i < 4096; i += kPThreads) S.lut3[i] = spread4_entry3((uint32_t)i);
+  stage_luts(S.lut, (RB == 3 || VB == 3) ? S.lut3 : nullptr, tid, kPThreads);
 
   // ---- query fragments (B operand of S^T = Kp Q^T): column = query 16*wv + n of the block
   const int qj = qa + 16 * wv + n;
@@ -243,6 +242,11 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
   const int part = tid & 3;
   const int dl = 16 * wv + 4 * gq;
   const float voff = (float)(1 << (VB - 1));
+  // staged rows: realigned, code streams byte-reversed per dword (slot bases are 16-aligned)
+  const uint32_t ksel = stage_selector(k_row_off & 3, part != 0);
+  const uint32_t vsel = stage_selector(v_row_off & 3, part != 0);
+  // fp8 code unit of the hardware conversion (3-bit codes are decoded as fp8 signed bytes)
+  const float inv_unit = 1.0f / __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0];
   // this key range's block ids, staged once (no global read on the per-tile address path)
   const int bfirst = k0 / a.block_size;
   const int nseg = (k1 - 1) / a.block_size - bfirst + 1;
@@ -281,13 +285,10 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
         cdst[2 * dw + 1] = p23;
       }
       if (part == 0) S.cs[ptok] = f16_bits_to_float(P.rul);
-      const int k_sh = k_row_off & 3, v_sh = v_row_off & 3;  // slot bases are 16-aligned
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        S.u.raw.k[ptok][part * 4 + i] =
-            k_sh ? __builtin_amdgcn_alignbyte(P.krow[i + 1], P.krow[i], k_sh) : P.krow[i];
-        S.u.raw.v[ptok][part * 4 + i] =
-            v_sh ? __builtin_amdgcn_alignbyte(P.vrow[i + 1], P.vrow[i], v_sh) : P.vrow[i];
+        S.u.raw.k[ptok][part * 4 + i] = __builtin_amdgcn_perm(P.krow[i + 1], P.krow[i], ksel);
+        S.u.raw.v[ptok][part * 4 + i] = __builtin_amdgcn_perm(P.vrow[i + 1], P.vrow[i], vsel);
       }
     }
     // the next tile's bytes are in flight while this tile is computed
@@ -309,22 +310,18 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
       const int half = tid & 1;
       if (kind == 0) {
         const uint32_t* row = S.u.raw.k[key];
-        decode_half_row<RB>(row, half, S.lut, S.lut3, &S.kcode[key][64 * half]);
+        decode_half_row_be<RB>(row, half, S.lut, S.lut3, &S.kcode[key][64 * half]);
         if (half == 0) {
-          const int rb = 16 + g.k_pb;
-          const uint32_t bits =
-              __builtin_amdgcn_alignbyte(row[(rb >> 2) + 1], row[rb >> 2], rb & 3);
-          S.krul[key] = f16_bits_to_float(bits & 0xffffu);
+          // 3-bit codes come out as fp8 (c - 4) * unit: the ruler takes the 1 / unit
+          const float kr = f16_bits_to_float(staged_u16(row, kBitmapBytes + g.k_pb));
+          S.krul[key] = RB == 3 ? kr * inv_unit : kr;
         }
       } else {
         const uint32_t* row = S.u.raw.v[key];
-        decode_half_row<VB>(row, half, S.lut, S.lut3, &S.vcode[key][64 * half]);
-        if (half == 0) {
-          const int rb = 16 + g.v_pb;
-          const uint32_t bits =
-              __builtin_amdgcn_alignbyte(row[(rb >> 2) + 1], row[rb >> 2], rb & 3);
-          S.vrul[key] = key < ntile ? f16_bits_to_float(bits & 0xffffu) : 0.f;
-        }
+        decode_half_row_be<VB>(row, half, S.lut, S.lut3, &S.vcode[key][64 * half]);
+        if (half == 0)
+          S.vrul[key] =
+              key < ntile ? f16_bits_to_float(staged_u16(row, kBitmapBytes + g.v_pb)) : 0.f;
       }
     }
     __syncthreads();
@@ -351,7 +348,14 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           uint32_t p01, p23;
-          u8x4_to_f16_minus(y[i], voff, p01, p23);
+          if constexpr (VB == 3) {  // fp8 signed codes -> exact fp16 integers c - 4
+            p01 = __builtin_bit_cast(uint32_t,
+                                     __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(y[i], inv_unit, false));
+            p23 = __builtin_bit_cast(uint32_t,
+                                     __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(y[i], inv_unit, true));
+          } else {
+            u8x4_to_f16_minus(y[i], voff, p01, p23);
+          }
           *(uint2*)&S.vt[4 * dg + i][4 * kg] = make_uint2(p01, p23);
         }
       }
@@ -373,15 +377,17 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
       }
       const float cs = S.cs[key];
       const float kr = S.krul[key];
-      const float kb = -(float)(1 << (RB - 1)) * kr;
-      const uint32_t cl = *(const uint32_t*)&S.kcode[key][dl];
-      const uint32_t ch = *(const uint32_t*)&S.kcode[key][64 + dl];
+      // 3-bit: codes read as (c - 4) * unit (ruler carries 1 / unit); 4-bit: as c
+      const float kb = RB == 3 ? 0.f : -8.f * kr;
+      float vcl[4], vch[4];
+      codes4<RB>(*(const uint32_t*)&S.kcode[key][dl], vcl);
+      codes4<RB>(*(const uint32_t*)&S.kcode[key][64 + dl], vch);
       const float4v cv = cosv[nb], sv = sinv[nb];
       half2v yl[2], yh[2], zl[2], zh[2];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float kl = fmaf(cs, acc0[i], fmaf((float)((cl >> (8 * i)) & 0xffu), kr, kb));
-        const float kh = fmaf(cs, acc1[i], fmaf((float)((ch >> (8 * i)) & 0xffu), kr, kb));
+        const float kl = fmaf(cs, acc0[i], fmaf(vcl[i], kr, kb));
+        const float kh = fmaf(cs, acc1[i], fmaf(vch[i], kr, kb));
         const float y1 = kl * cv[i] - kh * sv[i];
         const float y2 = kh * cv[i] + kl * sv[i];
         const _Float16 h1 = (_Float16)y1, h2 = (_Float16)y2;
