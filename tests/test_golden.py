@@ -121,3 +121,49 @@ def test_product_fit_matches_reference(path):
     assert float((dq != 0).float().mean()) < 0.02
     torch.testing.assert_close(fit.coeff_scale.to(torch.float16), t(f["fit_coeff_scale"]),
                                rtol=1e-3, atol=0)
+
+
+PACKED = GOLDEN / "ref_packed_rows.npz"
+ATTEND = GOLDEN / "ref_attend_safe.npz"
+
+
+def _packed_keys():
+    z = np.load(PACKED)
+    return sorted({k.rsplit("_", 1)[0] for k in z.files if k.endswith("_X")})
+
+
+@pytest.mark.parametrize("key", _packed_keys())
+def test_packed_rows_build_matches_reference(key):
+    """PackedRows.build on the reference's own (X, mask) pairs: bitmap, MSB-first code stream and
+    fp16 ruler bytes identical (CPU rulers: correctly rounded division)."""
+    z = np.load(PACKED)
+    X, mask = t(z[f"{key}_X"]), t(z[f"{key}_mask"])
+    bits, k = int(z[f"{key}_bits"]), int(z[f"{key}_k"])
+    bm, pk, sc = oc.packed_rows_build(X, mask, bits, k, ruler_mode="cpu")
+    assert torch.equal(bm, t(z[f"{key}_bitmap"]))
+    assert torch.equal(pk, t(z[f"{key}_packed"]))
+    assert torch.equal(sc, t(z[f"{key}_scale"]))
+
+
+def test_attention_oracle_matches_reference():
+    """Scores, causal multi-query scores and both attention orders against the reference's
+    reference.py on the same fitted store (fp32 CPU; summation order may differ, so 1e-5)."""
+    from oracle import attend
+    z = np.load(ATTEND)
+    lay = layout_for_config(oc.CONFIGS[str(z["config"])], int(z["r1"]), H=int(z["H"]),
+                            d=int(z["d"]))
+    ks, vs, dec = t(z["k_slots"]), t(z["v_slots"]), t(z["decoder_f"])
+    cos, sin, q, qm = t(z["cos"]), t(z["sin"]), t(z["q"]), t(z["qm"])
+    p0 = int(z["p0"])
+
+    def close(got, want):
+        torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5)
+
+    close(attend.raw_scores(lay, ks, dec, q, cos, sin), t(z["raw_scores"]))
+    close(attend.raw_scores_multi(lay, ks, dec, qm, cos, sin), t(z["raw_scores_multi"]))
+    causal = attend.raw_scores_multi(lay, ks, dec, qm, cos, sin, p0=p0)
+    want = t(z["raw_scores_multi_causal"])
+    assert torch.equal(torch.isinf(causal), torch.isinf(want))
+    close(causal[~torch.isinf(want)], want[~torch.isinf(want)])
+    close(attend.attend_raw_store(lay, ks, vs, dec, q, cos, sin), t(z["attend_raw_store"]))
+    close(attend.oracle_attend(lay, ks, vs, dec, q, cos, sin), t(z["oracle_attend"]))
