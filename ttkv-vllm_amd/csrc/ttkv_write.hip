@@ -64,18 +64,18 @@ struct WriteArgs {
   float inv127, inv_rk, inv_rv;
 };
 
-// Request of token i (qsl[r] <= i < qsl[r+1]) and its decoder slot, or -1.
+// Request of token i (qsl[r] <= i < qsl[r+1]; qsl is non-decreasing) and its decoder slot, or
+// -1: r + 1 = the number of qsl[0..num_reqs) <= i, counted 64 at a time with one load per lane
+// (one memory round trip for a decode batch instead of a dependent binary search). Every lane of
+// the wave must call it; all get the same answer.
 __device__ int token_decoder(const WriteArgs& a, int i) {
-  int lo = 0, hi = a.num_reqs - 1, r = -1;
-  while (lo <= hi) {
-    const int mid = (lo + hi) >> 1;
-    if (a.qsl[mid] <= i) {
-      r = mid;
-      lo = mid + 1;
-    } else {
-      hi = mid - 1;
-    }
+  const int lane = threadIdx.x & 63;
+  int cnt = 0;
+  for (int j0 = 0; j0 < a.num_reqs; j0 += 64) {
+    const int j = j0 + lane;
+    cnt += __builtin_popcountll(__ballot(j < a.num_reqs && a.qsl[j] <= i));
   }
+  const int r = cnt - 1;
   int ds = -1;
   if (r >= 0 && i < a.qsl[r + 1]) {
     const int blk0 = a.bt[(int64_t)r * a.bt_row_stride];
@@ -172,9 +172,12 @@ __global__ __launch_bounds__(kWThreads) void write_project_kernel(WriteArgs a) {
   const int h = blockIdx.x % g.H;
   const int HD = g.H * kD;
   const int64_t slot = a.slot_mapping[i];
+  // the key does not depend on the decoder lookup: its load overlaps the lookup's round trips
+  const float kv = tid < kD ? load_act(a.key, a.k_dtype, (int64_t)i * a.k_row_stride + h * kD + tid)
+                            : 0.f;
   const int ds = token_decoder(a, i);
   if (ds < 0 || slot < 0 || slot >= a.n_slots) return;  // K3b reports it
-  if (tid < kD) mk[tid] = load_act(a.key, a.k_dtype, (int64_t)i * a.k_row_stride + h * kD + tid);
+  if (tid < kD) mk[tid] = kv;
   __syncthreads();
   const float* pinv = a.pinv_pool + (int64_t)ds * HD * g.r1 + (int64_t)h * kD * g.r1;
   float* pp = a.ws_part + ((int64_t)i * g.H + h) * g.r1;
@@ -183,9 +186,12 @@ __global__ __launch_bounds__(kWThreads) void write_project_kernel(WriteArgs a) {
     const int aa = a0 + ar;
     float acc = 0.f;
     if (aa < g.r1) {
-#pragma unroll 8
-      for (int j = 64 * half; j < 64 * half + 64; ++j)
-        acc = fmaf(mk[j], pinv[(int64_t)j * g.r1 + aa], acc);
+      // all 64 loads issued before the dependent sum (one memory round trip)
+      float pv[64];
+#pragma unroll
+      for (int j = 0; j < 64; ++j) pv[j] = pinv[(int64_t)(64 * half + j) * g.r1 + aa];
+#pragma unroll
+      for (int j = 0; j < 64; ++j) acc = fmaf(mk[64 * half + j], pv[j], acc);
     }
     part[half][ar] = acc;
     __syncthreads();
@@ -246,6 +252,20 @@ __global__ __launch_bounds__(kWThreads) void write_pack_kernel(WriteArgs a) {
     if (ds < 0) atomicOr(a.err, TTKV_ERR_NO_DECODER);
   }
   if (ds < 0 || !slot_ok) return;
+  // this head's decoder columns (rows a = wv, wv + 4, ...) do not depend on the coefficients:
+  // their loads are issued before the coefficients' round trip (r1 <= kDecRows * 4 here)
+  const float* dec = a.dec_pool + (int64_t)ds * g.r1 * HD + h * kD;
+  constexpr int kDecRows = 32;
+  float d0[kDecRows], d1[kDecRows];
+  const bool dec_regs = g.r1 <= 4 * kDecRows;
+  if (dec_regs) {
+#pragma unroll
+    for (int u = 0; u < kDecRows; ++u) {
+      const int ar = wv + 4 * u;
+      d0[u] = ar < g.r1 ? dec[(int64_t)ar * HD + lane] : 0.f;
+      d1[u] = ar < g.r1 ? dec[(int64_t)ar * HD + 64 + lane] : 0.f;
+    }
+  }
   const float cs = a.cq_in ? a.cs_in[i] : a.ws_q[(int64_t)i * (g.r1 + 1) + g.r1];
   for (int ar = tid; ar < g.r1; ar += kWThreads) {
     const float q = a.cq_in ? (float)a.cq_in[(int64_t)i * g.r1 + ar]
@@ -269,12 +289,32 @@ __global__ __launch_bounds__(kWThreads) void write_pack_kernel(WriteArgs a) {
   }
   __syncthreads();
   // R[j] = K[h*d+j] - sum_a cqs[a] * dec[a][h*d+j]: wave w sums a = w, w+4, ...; lanes own j, j+64
-  const float* dec = a.dec_pool + (int64_t)ds * g.r1 * HD + h * kD;
   float acc0 = 0.f, acc1 = 0.f;
-  for (int ar = wv; ar < g.r1; ar += 4) {
-    const float c = cqs[ar];
-    acc0 = fmaf(c, dec[(int64_t)ar * HD + lane], acc0);
-    acc1 = fmaf(c, dec[(int64_t)ar * HD + 64 + lane], acc1);
+  if (dec_regs) {
+#pragma unroll
+    for (int u = 0; u < kDecRows; ++u) {
+      const int ar = wv + 4 * u;
+      const float c = ar < g.r1 ? cqs[ar] : 0.f;
+      acc0 = fmaf(c, d0[u], acc0);
+      acc1 = fmaf(c, d1[u], acc1);
+    }
+  }
+  // larger ranks: rows in batches of 16 whose loads are all issued before their sums
+  for (int a0 = wv; !dec_regs && a0 < g.r1; a0 += 64) {
+    float d0[16], d1[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int ar = a0 + 4 * u;
+      d0[u] = ar < g.r1 ? dec[(int64_t)ar * HD + lane] : 0.f;
+      d1[u] = ar < g.r1 ? dec[(int64_t)ar * HD + 64 + lane] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int ar = a0 + 4 * u;
+      const float c = ar < g.r1 ? cqs[ar] : 0.f;
+      acc0 = fmaf(c, d0[u], acc0);
+      acc1 = fmaf(c, d1[u], acc1);
+    }
   }
   rp[wv][lane] = acc0;
   rp[wv][64 + lane] = acc1;
