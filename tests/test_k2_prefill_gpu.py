@@ -153,3 +153,30 @@ def test_missing_decoder_sets_error_and_nan():
     torch.cuda.synchronize()
     assert int(err.item()) & 1
     assert torch.isnan(out).all()
+
+
+@pytest.mark.parametrize("cfg", ["campaign4x", "tight"])
+def test_attend_mode_other_allocations(cfg):
+    """Attention mode on the 4-bit (campaign4x) and the narrow 3-bit (tight) allocations, two
+    requests with key splits, fp16 in and out."""
+    shapes = [(700, 64), (1500, 130)]
+    stores = [fitted_store(cfg, n, seed=50 + i) for i, (n, _) in enumerate(shapes)]
+    cache = llama3_cache(2048)
+    pg, dec_pool, dec_map = _dev_inputs(stores, seed=6)
+    q = torch.cat([synth.queries(Q, seed=300 + i).reshape(Q, HQ, 128)
+                   for i, (_, Q) in enumerate(shapes)])
+    qsl = torch.tensor([0, 64, 194], dtype=torch.int32)
+    out = torch.zeros_like(q, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    kernels.prefill_paged(stores[0]["lay"], q.cuda(), pg["page"].cuda(), 16,
+                          pg["block_table"].cuda(), pg["seq_lens"].cuda(), qsl.cuda(), 130, 1500,
+                          dec_map, dec_pool, cache.cuda(), SCALE, out=out, error_word=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    want = attend.paged_continuation(stores[0]["lay"], pg["page"], pg["block_table"],
+                                     pg["seq_lens"], qsl, q.double(),
+                                     [s["decoder"] for s in stores], cache, 16, SCALE,
+                                     dtype=torch.float64)
+    for r in range(2):
+        s, e = int(qsl[r]), int(qsl[r + 1])
+        _check(out[s:e].float(), want[r], f"attend {cfg} req {r}", exact_inf=False)

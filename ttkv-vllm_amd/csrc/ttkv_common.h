@@ -99,23 +99,4 @@ __device__ __forceinline__ void store_act(void* p, int dt, int64_t i, float v) {
   }
 }
 
-// Copy `nbytes` bytes starting at an arbitrary global byte address `src` into LDS at a 4-byte
-// aligned `dst`, realigned so dst[0] == src[0]. Uses only aligned dword loads that stay inside
-// [floor4(src), ceil4(src + nbytes)), so it never reads past a 16-byte-aligned blob end.
-// `part`/`nparts` split the dwords of one row between cooperating threads.
-__device__ __forceinline__ void copy_row_realign(const uint8_t* src, int nbytes, uint32_t* dst,
-                                                 int part, int nparts) {
-  const uintptr_t a = (uintptr_t)src;
-  const uint32_t* base = (const uint32_t*)(a & ~(uintptr_t)3);
-  const int sh = (int)(a & 3);
-  const int nsrc = (sh + nbytes + 3) >> 2;           // source dwords that hold the row
-  const int ndst = (nbytes + 3) >> 2;
-  for (int dw = part; dw < ndst; dw += nparts) {
-    uint32_t lo = base[dw];
-    uint32_t hi = (dw + 1 < nsrc) ? base[dw + 1] : 0u;
-    // bytes [sh, sh+4) of the 8-byte little-endian pair (hi:lo)
-    dst[dw] = sh ? __builtin_amdgcn_alignbyte(hi, lo, sh) : lo;
-  }
-}
-
 }  // namespace ttkv

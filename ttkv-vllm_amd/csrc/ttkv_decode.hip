@@ -105,48 +105,6 @@ struct DecodeSmem {
   int is_last;
 };
 
-// Raw bytes of one token prefetched by one of its 4 threads.
-template <int KU>
-struct Prefetch {
-  uint32_t coef[KU];  // this part's quarter of the 16*KU coefficient bytes
-  uint32_t krow[5], vrow[5];  // 5 source dwords (4 output dwords + funnel)
-  uint32_t rul;               // coefficient ruler bits (part 0)
-};
-
-template <int KU>
-__device__ __forceinline__ void prefetch(Prefetch<KU>& P, const uint8_t* base, int part,
-                                         const Geom& g, int k_row_off, int v_row_off) {
-  constexpr int kCPP = KU * 4;
-  if (!base) {
-#pragma unroll
-    for (int i = 0; i < KU; ++i) P.coef[i] = 0u;
-#pragma unroll
-    for (int i = 0; i < 5; ++i) P.krow[i] = P.vrow[i] = 0u;
-    P.rul = 0u;
-    return;
-  }
-  const uint32_t* cs = (const uint32_t*)(base + part * kCPP);
-#pragma unroll
-  for (int i = 0; i < KU; ++i) P.coef[i] = cs[i];
-  {
-    const uintptr_t A = (uintptr_t)(base + k_row_off);
-    const uint32_t* src = (const uint32_t*)(A & ~(uintptr_t)3);
-    const int nsrc = (int)((A & 3) + g.k_row + 3) >> 2;
-#pragma unroll
-    // clamped index: every load stays inside the row's dwords (the extra ones are never decoded)
-    for (int i = 0; i < 5; ++i) P.krow[i] = src[min(part * 4 + i, nsrc - 1)];
-  }
-  {
-    const uintptr_t A = (uintptr_t)(base + v_row_off);
-    const uint32_t* src = (const uint32_t*)(A & ~(uintptr_t)3);
-    const int nsrc = (int)((A & 3) + g.v_row + 3) >> 2;
-#pragma unroll
-    for (int i = 0; i < 5; ++i) P.vrow[i] = src[min(part * 4 + i, nsrc - 1)];
-  }
-  P.rul = 0u;
-  if (part == 0) P.rul = *(const uint16_t*)(base + g.coeff_bytes);  // 2-aligned (r1 even)
-}
-
 // y - h for h the low / high fp16 half of a packed pair, in one v_fma_mix_f32 (the fp16 operand is
 // widened exactly; the difference of a value and its fp16 truncation is exact in fp32).
 __device__ __forceinline__ float minus_lo16(float y, half2v h) {
@@ -308,8 +266,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   };
 
   // first tile's bytes in flight while the decoder is loaded
-  Prefetch<KU> P;
-  prefetch<KU>(P, slot_base(t0), part, g, k_row_off, v_row_off);
+  RawSlot<KU> P;
+  fetch_raw_slot<KU>(P, slot_base(t0), part, g, k_row_off, v_row_off);
 
   // ---- decoder fragments (A operand, M = dims, K = r1), hi/lo fp16, resident in registers.
   half8 ahi[2][KSTEPS], alo[2][KSTEPS];
@@ -377,7 +335,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
       }
     }
     // ---------------------------------------------------------------- prefetch the next tile
-    if (tt + kTile < t1) prefetch<KU>(P, slot_base(tt + kTile), part, g, k_row_off, v_row_off);
+    if (tt + kTile < t1) fetch_raw_slot<KU>(P, slot_base(tt + kTile), part, g, k_row_off, v_row_off);
     __syncthreads();
     // ---------------------------------------------------------------- decode (thread = half row)
     {

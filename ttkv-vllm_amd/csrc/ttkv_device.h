@@ -18,10 +18,6 @@ __device__ __forceinline__ void i8x4_to_f16(uint32_t x, uint32_t& p01, uint32_t&
   p23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, hi) - bias);
 }
 
-__device__ __forceinline__ uint32_t bswap32(uint32_t x) {
-  return __builtin_amdgcn_perm(0u, x, 0x00010203u);
-}
-
 // Spread the 8 codes at the top of a 32-bit MSB-first window (code k at bits 31-B*k-B+1 ..
 // 31-B*k) into bytes: e0 = codes 0..3, e1 = codes 4..7 (byte i of e0 = code i).
 template <int BITS>
@@ -47,27 +43,24 @@ __device__ __forceinline__ void spread8(uint32_t w, uint32_t& e0, uint32_t& e1) 
   }
 }
 
-// Decode dims [64*half, 64*half+64) of one staged head row (bitmap dwords 0..3, MSB-first code
-// stream from dword 4) into one code byte per lane at dst[0..63]; lanes outside the bitmap get
-// 2^(BITS-1). `lut[B]` holds the v_perm selectors that move the byte-spread codes of bitmap
-// byte B onto its set lanes (0x0c -> zero byte for the others).
 // The slot bytes one of a token's 4 loader threads needs for one KV head: its quarter of the
-// coefficient window (KSTEPS*8 bytes), source dwords part*4 .. part*4+4 of the head's K and V
-// rows (4 output dwords + the funnel for realignment), and the fp16 coefficient ruler (part 0).
-template <int KSTEPS>
+// coefficient window (NCW dwords), source dwords part*4 .. part*4+4 of the head's K and V rows
+// (4 output dwords + the funnel for realignment), and the fp16 coefficient ruler (part 0).
+template <int NCW>
 struct RawSlot {
-  uint32_t coef[KSTEPS * 2];
+  uint32_t coef[NCW];
   uint32_t krow[5], vrow[5];
   uint32_t rul;
 };
 
-template <int KSTEPS>
-__device__ __forceinline__ void fetch_raw_slot(RawSlot<KSTEPS>& P, const uint8_t* base, int part,
+// Fetch a token's RawSlot (all zero for a null slot base).
+template <int NCW>
+__device__ __forceinline__ void fetch_raw_slot(RawSlot<NCW>& P, const uint8_t* base, int part,
                                                const Geom& g, int k_row_off, int v_row_off) {
-  constexpr int kCPP = KSTEPS * 8;
+  constexpr int kCPP = NCW * 4;
   if (!base) {
 #pragma unroll
-    for (int i = 0; i < KSTEPS * 2; ++i) P.coef[i] = 0u;
+    for (int i = 0; i < NCW; ++i) P.coef[i] = 0u;
 #pragma unroll
     for (int i = 0; i < 5; ++i) P.krow[i] = P.vrow[i] = 0u;
     P.rul = 0u;
@@ -75,7 +68,7 @@ __device__ __forceinline__ void fetch_raw_slot(RawSlot<KSTEPS>& P, const uint8_t
   }
   const uint32_t* cs = (const uint32_t*)(base + part * kCPP);
 #pragma unroll
-  for (int i = 0; i < KSTEPS * 2; ++i) P.coef[i] = cs[i];
+  for (int i = 0; i < NCW; ++i) P.coef[i] = cs[i];
   {
     const uintptr_t A = (uintptr_t)(base + k_row_off);
     const uint32_t* src = (const uint32_t*)(A & ~(uintptr_t)3);
@@ -93,71 +86,6 @@ __device__ __forceinline__ void fetch_raw_slot(RawSlot<KSTEPS>& P, const uint8_t
   }
   P.rul = 0u;
   if (part == 0) P.rul = *(const uint16_t*)(base + g.coeff_bytes);  // 2-aligned (r1 even)
-}
-
-// 3-bit spread table: entry x (12 bits = 4 codes, first code in the top 3 bits) holds the 4 codes
-// one per byte, each with its top bit flipped (c ^ 4), first code in byte 0.
-__device__ __forceinline__ uint32_t spread4_entry3(uint32_t x) {
-  return ((x >> 9) ^ 4u) | ((((x >> 6) & 7u) ^ 4u) << 8) | ((((x >> 3) & 7u) ^ 4u) << 16) |
-         (((x & 7u) ^ 4u) << 24);
-}
-
-// Decode dims [64*half, 64*half+64) of one staged head row (bitmap dwords 0..3, MSB-first code
-// stream from dword 4) into one code byte per lane at dst[0..63]; lanes outside the bitmap get
-// 2^(BITS-1). `lut[B]` holds the v_perm selectors that move the byte-spread codes of bitmap
-// byte B onto its set lanes (0x0c -> zero byte for the others); for 3-bit codes `lut3`, when
-// given, spreads 4 codes per lookup (spread4_entry3), else the codes are cut with bit ops.
-template <int BITS>
-__device__ __forceinline__ void decode_half_row(const uint32_t* row, int half, const uint2* lut,
-                                                const uint32_t* lut3, uint8_t* dst) {
-  constexpr uint32_t OFFB = (1u << (BITS - 1)) * 0x01010101u;
-  // A kept code c is carried as c ^ 2^(b-1), so after the zero-filling scatter a final XOR
-  // restores c and turns the zero bytes into the zero code 2^(b-1).
-  constexpr uint32_t FLIP = 0x88888888u;  // 4-bit: top bit of each nibble
-  const uint32_t bm0 = row[2 * half], bm1 = row[2 * half + 1];
-  int rank = half ? __builtin_popcount(row[0]) + __builtin_popcount(row[1]) : 0;
-  const uint32_t* st = row + 4;
-  // All stream offsets follow from the bitmap alone, so the LDS reads of a batch of 4 bitmap
-  // bytes (selector pairs and window words) are issued before any of them is consumed.
-#pragma unroll
-  for (int m0 = 0; m0 < 8; m0 += 4) {
-    uint32_t B[4];
-    int bp[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      B[m] = __builtin_amdgcn_ubfe(m0 < 4 ? bm0 : bm1, 8 * m, 8);
-      bp[m] = rank * BITS;
-      rank += __builtin_popcount(B[m]);
-    }
-    uint2 sel[4];
-    uint32_t w0[4], w1[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      sel[m] = lut[B[m]];
-      const int wi = bp[m] >> 5;
-      w0[m] = st[wi];
-      w1[m] = st[wi + 1];
-    }
-    uint32_t e0[4], e1[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const uint64_t pair = ((uint64_t)bswap32(w0[m]) << 32) | (uint64_t)bswap32(w1[m]);
-      const uint32_t w = (uint32_t)((pair << (bp[m] & 31)) >> 32);
-      if (BITS == 3 && lut3) {
-        e0[m] = lut3[w >> 20];
-        e1[m] = lut3[(w >> 8) & 0xfffu];
-      } else {
-        spread8<BITS>(w ^ (BITS == 3 ? 0x92492400u : FLIP), e0[m], e1[m]);
-      }
-    }
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      uint2 out;
-      out.x = __builtin_amdgcn_perm(e1[m], e0[m], sel[m].x) ^ OFFB;
-      out.y = __builtin_amdgcn_perm(e1[m], e0[m], sel[m].y) ^ OFFB;
-      *(uint2*)(dst + 8 * (m0 + m)) = out;
-    }
-  }
 }
 
 // 2^x on the hardware exp unit (one v_exp_f32). Softmax weights below 2^-126 flush to zero,
@@ -378,22 +306,6 @@ __device__ __forceinline__ void codes4(uint32_t x, float v[4]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = (float)((x >> (8 * i)) & 0xffu);
   }
-}
-
-// Selector table for decode_half_row: entry B holds the v_perm selectors that move the
-// byte-spread codes of bitmap byte B onto its set lanes (0x0c -> zero byte elsewhere). One entry
-// per thread of a 256-thread block.
-__device__ __forceinline__ uint2 scatter_lut_entry(uint32_t B) {
-  uint32_t s0 = 0, s1 = 0, idx = 0;
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const bool present = (B >> (7 - k)) & 1u;
-    const uint32_t sel = present ? idx : 0x0cu;
-    idx += present;
-    if (k < 4) s0 |= sel << (8 * k);
-    else s1 |= sel << (8 * (k - 4));
-  }
-  return make_uint2(s0, s1);
 }
 
 }  // namespace ttkv

@@ -268,8 +268,8 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
     const int64_t slot = (int64_t)blk * a.block_size + (pos - bi * a.block_size);
     return slot < a.n_slots ? a.page + slot * a.slot_stride : nullptr;
   };
-  RawSlot<KSTEPS> P;
-  fetch_raw_slot<KSTEPS>(P, slot_base(k0), part, g, k_row_off, v_row_off);
+  RawSlot<2 * KSTEPS> P;
+  fetch_raw_slot<2 * KSTEPS>(P, slot_base(k0), part, g, k_row_off, v_row_off);
 
   for (int tt = k0; tt < k1; tt += kPTile) {
     const int ntile = min(kPTile, k1 - tt);
@@ -292,7 +292,7 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
       }
     }
     // the next tile's bytes are in flight while this tile is computed
-    if (tt + kPTile < k1) fetch_raw_slot<KSTEPS>(P, slot_base(tt + kPTile), part, g, k_row_off, v_row_off);
+    if (tt + kPTile < k1) fetch_raw_slot<2 * KSTEPS>(P, slot_base(tt + kPTile), part, g, k_row_off, v_row_off);
     // this lane's RoPE angles for the tile: keys 16*nb + n, dims dl..dl+3 (cos) / 64+dl.. (sin)
     float4v cosv[4], sinv[4];
 #pragma unroll
