@@ -565,22 +565,26 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (tid == 0) {
-    const int prev = __hip_atomic_fetch_add(&a.ws_cnt[r * g.H + h], 1, __ATOMIC_RELAXED,
+    const int prev = __hip_atomic_fetch_add(&a.ws_cnt[r * g.H + h], 1, __ATOMIC_ACQ_REL,
                                             __HIP_MEMORY_SCOPE_AGENT);
     S.is_last = (prev == n_chunks - 1);
   }
   __syncthreads();
   if (!S.is_last) return;
-  auto ld_agent = [](const float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  };
+  // Every partial is complete in L2 (write-through stores, waited on before their counter
+  // update). An agent-scope acquire drops this CU's L1 copies, after which plain loads see the
+  // partials -- and, unlike atomic loads, the loads of all chunks can be in flight together.
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  auto ld_agent = [](const float* p) { return *p; };
   const float* pbase = a.ws_part + (int64_t)(r * g.H + h) * a.max_chunks * pstride;
   for (int it = tid; it < G * kD; it += kThreads) {
     const int p = it / kD;
     const int dim = it - p * kD;
     float M = -INFINITY;
+#pragma unroll 8
     for (int cc = 0; cc < n_chunks; ++cc) M = fmaxf(M, ld_agent(&pbase[cc * pstride + p * (kD + 2) + kD]));
     float L = 0.f, O = 0.f;
+#pragma unroll 8
     for (int cc = 0; cc < n_chunks; ++cc) {
       const float* pc = pbase + cc * pstride + p * (kD + 2);
       const float f = exp2f(ld_agent(&pc[kD]) - M);

@@ -543,15 +543,17 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (tid == 0) {
-    const int prev = __hip_atomic_fetch_add(&a.ws_cnt[item], 1, __ATOMIC_RELAXED,
+    const int prev = __hip_atomic_fetch_add(&a.ws_cnt[item], 1, __ATOMIC_ACQ_REL,
                                             __HIP_MEMORY_SCOPE_AGENT);
     S.is_last = (prev == nparts - 1);
   }
   __syncthreads();
   if (!S.is_last) return;
-  auto ld_agent = [](const float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  };
+  // Every partial is complete in L2 (write-through stores, waited on before their counter
+  // update). An agent-scope acquire drops this CU's L1 copies, after which plain loads see the
+  // partials -- and, unlike atomic loads, the loads of all chunks can be in flight together.
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  auto ld_agent = [](const float* p) { return *p; };
   const float* pbase = a.ws_part + (int64_t)item * a.nsplit * pstride;
   const int nq = qe - qa;
   for (int it = tid; it < G * nq * kD; it += kPThreads) {
@@ -561,8 +563,10 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
     const int qq = row - gg * nq;
     const int64_t ro = (int64_t)(gg * kPQ + qq) * kRowF;
     float M = -INFINITY;
+#pragma unroll 8
     for (int c = 0; c < nparts; ++c) M = fmaxf(M, ld_agent(&pbase[c * pstride + ro + kD]));
     float L = 0.f, O = 0.f;
+#pragma unroll 8
     for (int c = 0; c < nparts; ++c) {
       const float* pc = pbase + c * pstride + ro;
       const float mc = ld_agent(&pc[kD]);
