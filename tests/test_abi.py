@@ -77,3 +77,75 @@ def test_host_refusals_before_launch():
     assert _decode_call(big) == 2 and b"r1" in L.ttkv_last_error()
     mixed = TTKLayout(H=8, d=128, r1=110, qbits=8, res_k=81, res_bits=3, v_lanes=64, v_bits=4)
     assert _decode_call(mixed) == 2
+
+
+def _prefill_call(lay, **kw):
+    L = _hip.lib()
+    a = dict(num_heads=24, scale=0.088, query=1, q_dtype=1, q_row_stride=3072, page=4096,
+             n_slots=64, slot_stride=912, block_size=16, block_table=1, bt_row_stride=4,
+             max_blocks=4, seq_lens=1, qsl=1, req_index=0, num_reqs=1, max_q_len=8,
+             max_seq_len=64, dec_map=1, num_blocks=4, dec_pool=1, n_dec=1, cs=16, max_pos=64,
+             out=1, out_dtype=1, out_row_stride=3072, ws=256, ws_bytes=1 << 24, err=1)
+    a.update(kw)
+    return L.ttkv_prefill_paged(_hip.Layout.of(lay), a["num_heads"], a["scale"], a["query"],
+                                a["q_dtype"], a["q_row_stride"], a["page"], a["n_slots"],
+                                a["slot_stride"], a["block_size"], a["block_table"],
+                                a["bt_row_stride"], a["max_blocks"], a["seq_lens"], a["qsl"],
+                                a["req_index"], a["num_reqs"], a["max_q_len"], a["max_seq_len"],
+                                a["dec_map"], a["num_blocks"], a["dec_pool"], a["n_dec"], a["cs"],
+                                a["max_pos"], a["out"], a["out_dtype"], a["out_row_stride"],
+                                a["ws"], a["ws_bytes"], a["err"], None)
+
+
+def _write_call(lay, **kw):
+    L = _hip.lib()
+    a = dict(key=1, k_dtype=1, k_row_stride=1024, value=1, v_dtype=1, v_row_stride=1024,
+             slot_mapping=1, num_tokens=4, qsl=1, num_reqs=1, block_table=1, bt_row_stride=1,
+             dec_map=1, num_blocks=1, dec_pool=1, pinv_pool=1, n_dec=1, cq_in=0, cs_in=0,
+             page=4096, n_slots=16, slot_stride=912, c_out=0, r_out=0, ws=256, ws_bytes=1 << 20,
+             err=1)
+    a.update(kw)
+    return L.ttkv_write_paged(_hip.Layout.of(lay), a["key"], a["k_dtype"], a["k_row_stride"],
+                              a["value"], a["v_dtype"], a["v_row_stride"], a["slot_mapping"],
+                              a["num_tokens"], a["qsl"], a["num_reqs"], a["block_table"],
+                              a["bt_row_stride"], a["dec_map"], a["num_blocks"], a["dec_pool"],
+                              a["pinv_pool"], a["n_dec"], a["cq_in"], a["cs_in"], a["page"],
+                              a["n_slots"], a["slot_stride"], a["c_out"], a["r_out"], a["ws"],
+                              a["ws_bytes"], a["err"], None)
+
+
+def test_prefill_host_refusals_before_launch():
+    """K2's host refusals (the continuation read, impl.py:725-778): geometry it is not built for,
+    a causal chunk longer than the store, positions past the angle table, a block table too
+    short for the context, and missing outputs. Dummy pointers only: nothing is launched."""
+    L = _hip.lib()
+    safe = layout_for_config(CONFIGS["safe"], 110)
+    d64 = TTKLayout(H=8, d=64, r1=110, qbits=8, res_k=40, res_bits=3, v_lanes=40, v_bits=3)
+    assert _prefill_call(d64) == 2 and b"head dim" in L.ttkv_last_error()
+    assert _prefill_call(safe, num_heads=20) == 1
+    assert _prefill_call(safe, max_q_len=65) == 1 and b"max_q_len" in L.ttkv_last_error()
+    assert _prefill_call(safe, max_pos=10) == 1 and b"cos_sin_cache" in L.ttkv_last_error()
+    assert _prefill_call(safe, max_blocks=2) == 1 and b"blocks" in L.ttkv_last_error()
+    assert _prefill_call(safe, out=0) == 1 and b"out" in L.ttkv_last_error()
+    assert _prefill_call(safe, cs=17) == 1 and b"16-aligned" in L.ttkv_last_error()
+    assert _prefill_call(layout_for_config(CONFIGS["safe"], 200)) == 2
+    assert _prefill_call(safe, q_dtype=7) == 1 and b"dtype" in L.ttkv_last_error()
+
+
+def test_write_host_refusals_before_launch():
+    """K3's host refusals (encode.py:446-468 slot checks stay on the device; these are the
+    geometry and argument checks): nothing is launched."""
+    L = _hip.lib()
+    safe = layout_for_config(CONFIGS["safe"], 110)
+    d64 = TTKLayout(H=8, d=64, r1=110, qbits=8, res_k=40, res_bits=3, v_lanes=40, v_bits=3)
+    assert _write_call(d64) == 2 and b"head dim" in L.ttkv_last_error()
+    h16 = TTKLayout(H=16, d=128, r1=110, qbits=8, res_k=81, res_bits=3, v_lanes=81, v_bits=3)
+    assert _write_call(h16) == 2 and b"H > 8" in L.ttkv_last_error()
+    assert _write_call(layout_for_config(CONFIGS["safe"], 300)) == 2
+    assert _write_call(safe, pinv_pool=0) == 1 and b"pinv_pool" in L.ttkv_last_error()
+    assert _write_call(safe, pinv_pool=0, cq_in=1) == 1 and b"coeff_scale_in" in L.ttkv_last_error()
+    assert _write_call(safe, slot_stride=800) == 1 and b"slot stride" in L.ttkv_last_error()
+    assert _write_call(safe, key=0) == 1 and b"null" in L.ttkv_last_error()
+    assert _write_call(safe, v_dtype=5) == 1 and b"dtype" in L.ttkv_last_error()
+    assert _write_call(safe, ws=0) == 4 and b"workspace" in L.ttkv_last_error()
+    assert _write_call(safe, num_tokens=0) == 0                          # nothing to do
