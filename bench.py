@@ -478,6 +478,7 @@ def main():
         st = build_store(torch, lay, cfg, lens3, 2, seed=3, dev=dev)
         _, ml = time_k1(torch, lay, st, q, cache, 20, 3, 2)
         b = k1_bytes(lay, lens3, R1, max(lens3))
+        log(f"K1 config3 ({sum(lens3)} tokens, longest {max(lens3)}): {ml * 1e3:.1f} us/layer")
         extra["config3_b8_random"] = dict(contexts=lens3, us_per_layer=ml * 1e3,
                                           hbm_gbps=b / (ml * 1e-3) / 1e9,
                                           tokens_per_s=8 / (ml * 1e-3 * L_LAYERS))

@@ -55,8 +55,13 @@ typedef struct ttkv_layout {
  * Replaces TTKLayout.compressed_bytes_per_token (vllm_ttkv/layout.py:152-154). */
 int64_t ttkv_blob_bytes(const ttkv_layout* lay);
 
-/* Workspace bytes `ttkv_decode_paged` needs for this batch shape. The workspace must be
- * zero-filled before its first use; every call leaves its counter region zero again. */
+/* Workspaces (all four `*_workspace_bytes`): the first 64 KiB of a workspace are arrival
+ * counters at a fixed place, followed by per-call partial results. A workspace must be
+ * zero-filled before its first use; every call leaves the counters zero again, and no call writes
+ * partials into them, so one buffer, once large enough, serves calls of any shape in turn.
+ * Calls that share a workspace must not overlap in time (run them on one stream).
+ *
+ * Workspace bytes `ttkv_decode_paged` needs for this batch shape. */
 int64_t ttkv_decode_workspace_bytes(const ttkv_layout* lay, int32_t num_heads,
                                     int32_t num_reqs, int32_t max_seq_len, int32_t block_size);
 
@@ -124,11 +129,11 @@ int ttkv_write_paged(const ttkv_layout* lay, const void* key, int32_t k_dtype, i
                      ttkv_stream_t stream);
 
 /* Workspace bytes `ttkv_write_paged` needs for `num_tokens` projected tokens (none when the
- * coefficients come from coeff_q_in). Zero-filled before first use; calls leave it reusable. */
+ * coefficients come from coeff_q_in); see the workspace note above ttkv_decode_workspace_bytes. */
 int64_t ttkv_write_workspace_bytes(const ttkv_layout* lay, int32_t num_tokens);
 
 /* Workspace bytes `ttkv_prefill_paged` needs for this batch shape (0 when one key split covers
- * every query block). Zero-filled before first use; every call leaves the counters zero. */
+ * every query block); see the workspace note above ttkv_decode_workspace_bytes. */
 int64_t ttkv_prefill_workspace_bytes(const ttkv_layout* lay, int32_t num_heads, int32_t num_reqs,
                                      int32_t max_q_len, int32_t max_seq_len, int32_t block_size);
 

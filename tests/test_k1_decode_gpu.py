@@ -13,7 +13,7 @@ pytestmark = pytest.mark.gpu
 MAX_ABS, MEAN_ABS = 2e-3, 1e-3
 
 
-def _run_k1(stores, q, cache, block_size=16, seed=0, out_dtype=torch.float16):
+def _run_k1(stores, q, cache, block_size=16, seed=0, out_dtype=torch.float16, workspace=None):
     pg = paged(stores, block_size, seed)
     dev = "cuda"
     lay = stores[0]["lay"]
@@ -28,7 +28,8 @@ def _run_k1(stores, q, cache, block_size=16, seed=0, out_dtype=torch.float16):
     kernels.decode_paged(lay, q.to(dev), pg["page"].to(dev), block_size,
                          pg["block_table"].to(dev), pg["seq_lens"].to(dev), qsl.to(dev),
                          int(pg["seq_lens"].max()), dec_map.to(dev), dec_pool,
-                         cache.to(dev), 128 ** -0.5, out=out, error_word=err)
+                         cache.to(dev), 128 ** -0.5, out=out, error_word=err,
+                         workspace=workspace)
     torch.cuda.synchronize()
     assert int(err.item()) == 0, f"device error word {int(err.item())}"
     return out.float().cpu(), pg
@@ -196,3 +197,71 @@ def test_empty_context_and_missing_decoder():
     want = _oracle(stores[:1], q[:1], cache, dict(pg, block_table=pg["block_table"][:1],
                                                   seq_lens=pg["seq_lens"][:1]))
     _check(got[:1], want, "request 0 beside an empty and an undecodable request")
+
+
+def test_one_long_request_among_short_ones():
+    """The work plan splits by the batch's total length, not by its longest request: one long
+    context beside sub-tile ones is cut into many chunks, the short ones into one each."""
+    lens = [6000, 1, 2, 3, 64, 65, 127, 128]
+    stores = [fitted_store("safe", n, seed=70 + i) for i, n in enumerate(lens)]
+    q = synth.queries(len(lens), seed=11)
+    cache = llama3_cache(6144)
+    got, pg = _run_k1(stores, q, cache, seed=12)
+    _check(got, _oracle(stores, q, cache, pg), "one long among short")
+
+
+def test_more_requests_than_one_launch_plans():
+    """300 requests: past the 256 a launch's work plan holds, so the call runs as two launches
+    over consecutive request ranges sharing one workspace."""
+    base = [fitted_store("safe", n, seed=80 + i) for i, n in enumerate([1, 17, 64, 65, 130, 257])]
+    stores = [base[i % len(base)] for i in range(300)]
+    q = synth.queries(len(stores), seed=13)
+    cache = llama3_cache(512)
+    got, pg = _run_k1(stores, q, cache, seed=14)
+    _check(got, _oracle(stores, q, cache, pg), "300 requests")
+
+
+def test_workspace_shared_across_batch_shapes():
+    """One workspace serves decode calls of different batch shapes in turn (a serving loop's
+    batch changes every step); each call's output equals the same call with a fresh workspace,
+    bit for bit (same work plan, same combine order)."""
+    from vllm_ttkv import kernels as K
+    batches = [[3000, 40, 900], [5000], [200] * 6 + [64], [3000, 40, 900], [70, 2000]]
+    stores = {n: fitted_store("safe", n, seed=90 + i)
+              for i, n in enumerate(sorted({n for b in batches for n in b}))}
+    cache = llama3_cache(5120)
+    lay = stores[5000]["lay"]
+    need = max(K.decode_workspace(lay, HQ, len(b), max(b), "cuda").numel() for b in batches)
+    shared = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    for i, b in enumerate(batches):
+        st = [stores[n] for n in b]
+        q = synth.queries(len(b), seed=20 + i)
+        got, _ = _run_k1(st, q, cache, seed=30 + i, workspace=shared)
+        want, _ = _run_k1(st, q, cache, seed=30 + i)
+        assert torch.equal(got, want), f"batch {b} with a shared workspace"
+    assert int(shared[:65536].abs().sum()) == 0, "counters left non-zero"
+
+
+def test_length_past_max_seq_len_is_flagged_and_clamped():
+    """A seq_lens entry beyond the max_seq_len the call was sized with sets error bit 8 and is
+    read over its first max_seq_len tokens; the other requests are unaffected."""
+    stores = [fitted_store("safe", n, seed=100 + i) for i, n in enumerate([300, 500])]
+    q = synth.queries(2, seed=15)
+    cache = llama3_cache(1024)
+    pg = paged(stores, 16, 4)
+    dev = "cuda"
+    lay = stores[0]["lay"]
+    dec_pool = torch.stack([s["decoder"] for s in stores]).to(dev)
+    dec_map = torch.full((pg["num_blocks"],), -1, dtype=torch.int32)
+    for r in range(2):
+        dec_map[pg["block_table"][r, 0]] = r
+    out = torch.zeros(2, HQ, 128, dtype=torch.float16, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    kernels.decode_paged(lay, q.to(dev), pg["page"].to(dev), 16, pg["block_table"].to(dev),
+                         pg["seq_lens"].to(dev), torch.arange(3, dtype=torch.int32).to(dev), 400,
+                         dec_map.to(dev), dec_pool, cache.to(dev), 128 ** -0.5, out=out,
+                         error_word=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 8
+    want = _oracle(stores, q, cache, dict(pg, seq_lens=torch.tensor([300, 400])))
+    _check(out.float().cpu(), want, "clamped at max_seq_len")

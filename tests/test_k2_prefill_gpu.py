@@ -180,3 +180,37 @@ def test_attend_mode_other_allocations(cfg):
     for r in range(2):
         s, e = int(qsl[r]), int(qsl[r + 1])
         _check(out[s:e].float(), want[r], f"attend {cfg} req {r}", exact_inf=False)
+
+
+def test_workspace_shared_across_batch_shapes():
+    """One workspace serves continuation calls of different shapes in turn; each call's output
+    equals the same call with a fresh workspace, bit for bit."""
+    calls = [[(1000, 128), (300, 40)], [(2100, 257)], [(700, 64), (1000, 128), (300, 40)],
+             [(1000, 128), (300, 40)]]
+    stores = {n: fitted_store("safe", n, seed=200 + n) for n in {n for c in calls for n, _ in c}}
+    cache = llama3_cache(4096)
+    lay = stores[1000]["lay"]
+    need = max(kernels.prefill_workspace(lay, HQ, len(c), max(Q for _, Q in c),
+                                         max(n for n, _ in c), "cuda").numel() for c in calls)
+    shared = torch.zeros(need, dtype=torch.uint8, device="cuda")
+
+    def run(shapes, ws, i):
+        st = [stores[n] for n, _ in shapes]
+        pg, dec_pool, dec_map = _dev_inputs(st, seed=40 + i)
+        q = torch.cat([synth.queries(Q, seed=300 + i + j).reshape(Q, HQ, 128)
+                       for j, (_, Q) in enumerate(shapes)])
+        qsl = torch.tensor([0] + list(torch.tensor([Q for _, Q in shapes]).cumsum(0)),
+                           dtype=torch.int32)
+        out = torch.zeros_like(q, device="cuda")
+        err = torch.zeros(1, dtype=torch.int32, device="cuda")
+        kernels.prefill_paged(lay, q.cuda(), pg["page"].cuda(), 16, pg["block_table"].cuda(),
+                              pg["seq_lens"].cuda(), qsl.cuda(), max(Q for _, Q in shapes),
+                              max(n for n, _ in shapes), dec_map, dec_pool, cache.cuda(), SCALE,
+                              out=out, error_word=err, workspace=ws)
+        torch.cuda.synchronize()
+        assert int(err.item()) == 0
+        return out.cpu()
+
+    for i, shapes in enumerate(calls):
+        assert torch.equal(run(shapes, shared, i), run(shapes, None, i)), f"call {shapes}"
+    assert int(shared[:65536].abs().sum()) == 0, "counters left non-zero"

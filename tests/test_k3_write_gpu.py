@@ -167,3 +167,34 @@ def test_frozen_write_against_reference_vectors(case):
     vg = attend.dense_v_from_slots(lay, page[:, lay.v_offset:])
     vr = attend.dense_v_from_slots(lay, want[:, lay.v_offset:])
     assert float((vg - vr).abs().max()) <= 0.3 * float(V.abs().max())
+
+
+def test_workspace_shared_across_token_counts():
+    """One workspace serves writes of different sizes in turn (a serving loop's token count
+    changes every step): each write's bytes equal those of the same write with a fresh
+    workspace. The arrival counters sit at a fixed place that no call's partials overlap."""
+    lay, dec, pinv, Knew, V = _setup("safe", 120, seed=51)
+    C = lay.compressed_bytes_per_token()
+    Kt = Knew.permute(1, 0, 2).contiguous().to(DEV)
+    Vt = V.permute(1, 0, 2).contiguous().to(DEV)
+    bt = torch.zeros(1, 1, dtype=torch.int32, device=DEV)
+    dec_map = torch.zeros(1, dtype=torch.int32, device=DEV)
+    shared = kernels.write_workspace(lay, 120, DEV)
+
+    def write(lo, hi, ws):
+        n = hi - lo
+        page = torch.zeros(128, C, dtype=torch.uint8, device=DEV)
+        err = torch.zeros(1, dtype=torch.int32, device=DEV)
+        kernels.write_paged(lay, Kt[lo:hi], Vt[lo:hi], torch.arange(n, dtype=torch.int64, device=DEV),
+                            torch.tensor([0, n], dtype=torch.int32, device=DEV), bt, dec_map,
+                            dec.unsqueeze(0).to(DEV), pinv.unsqueeze(0).to(DEV), page,
+                            error_word=err, workspace=ws)
+        torch.cuda.synchronize()
+        assert int(err.item()) == 0
+        return page.cpu()
+
+    for lo, hi in [(0, 50), (0, 100), (30, 50), (0, 120), (7, 8), (0, 100)]:
+        got = write(lo, hi, shared)
+        want = write(lo, hi, None)
+        assert torch.equal(got, want), f"tokens {lo}:{hi} with a shared workspace"
+    assert int(shared[:65536].abs().sum()) == 0, "counters left non-zero"

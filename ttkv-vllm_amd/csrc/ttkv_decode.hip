@@ -50,6 +50,8 @@ constexpr int kRawDw = 17;      // dwords per staged head row (49-50 B rows + wi
                                 // threads reading the same offset of different rows hit distinct banks
 constexpr int kCodeStride = 144;  // bytes per code row (128 + bank stagger)
 constexpr int kSegMax = 260;    // block ids staged per chunk
+constexpr int kPlanLanes = 4;   // requests per lane in the work plan
+constexpr int kPlanReqs = 64 * kPlanLanes;  // requests per launch (larger batches: several)
 
 struct DecodeArgs {
   Geom g;
@@ -79,7 +81,7 @@ struct DecodeArgs {
   float* ws_part;
   int* ws_cnt;
   int* err;
-  int chunk, max_chunks, nwork, max_seq;
+  int chunk_cap, target, max_seq;  // chunk length cap, work items aimed at, longest context
 };
 
 // KU = coefficient window in 16-wide k units: r1 is padded to 16 * KU; the reconstruction runs
@@ -151,41 +153,186 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   const int n = lane & 15;
   const int gq = lane >> 4;
 
-  // XCD-aware work order: blocks are dealt round-robin to the 8 XCDs, so consecutive work items
-  // go to one XCD. Items are chunk-major: the H heads of one (request, chunk) read the same
-  // coefficient bytes, and every request's chunk c reads the same rows of the angle table
-  // (positions are absolute), so both are fetched from HBM about once per XCD.
-  const int per_xcd = gridDim.x >> 3;
-  const int w = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-  if (w >= a.nwork) return;
-  const int h = w % g.H;
-  const int rc = w / g.H;
-  const int r = rc % a.num_reqs;
-  const int c = rc / a.num_reqs;
-  if (c >= a.max_chunks) return;
-  // independent per-request loads issued together (each is a full memory round trip)
-  const int seq_raw = a.seq_lens[r];
-  const int64_t qrow = a.qsl[r];
-  const int blk0 = a.bt[(int64_t)r * a.bt_row_stride];
-  int seq = seq_raw;
-  if (seq > a.max_seq) {  // the host sized the grid, workspace and table checks from max_seq
-    if (tid == 0 && c == 0) atomicOr(a.err, TTKV_ERR_SEQ_LEN);
-    seq = a.max_seq;
-  }
-  const int n_chunks = (seq + a.chunk - 1) / a.chunk;
-  if (c >= n_chunks) {
-    if (seq <= 0 && c == 0) {  // empty context: the reference's einsum over zero rows is 0
-      for (int i = tid; i < G * kD; i += kThreads)
-        store_act(a.out, a.out_dtype, qrow * a.out_row_stride + (int64_t)(h * G) * kD + i, 0.f);
+  // ---- work plan, from the batch's own lengths (no host round trip). Every wave computes it
+  // alike: the lengths of requests lane + 64 i; the shortest chunk (a multiple of the tile) whose
+  // (request, chunk, head) items fit `rounds` full rounds of resident blocks, each request
+  // having at least one chunk; and then this block's item. Items are enumerated chunk-major --
+  // (chunk c, request r, head h) over the requests that have a chunk c -- so the H heads of one
+  // (request, chunk) read the same coefficient bytes and every request's chunk c the same rows
+  // of the angle table (positions are absolute). Blocks are dealt round-robin to the 8 XCDs, so
+  // each XCD takes a contiguous range of items and both are fetched from HBM about once per XCD.
+  // Each request's query row and first block id are loaded with its length (one round trip).
+  const int nper = (a.num_reqs + 63) >> 6;  // groups of 64 requests in use (uniform)
+  int seql[kPlanLanes], nchl[kPlanLanes], qsll[kPlanLanes], blk0l[kPlanLanes];
+  int tot = 0, over = 0;
+#pragma unroll
+  for (int i = 0; i < kPlanLanes; ++i) {
+    const int rr = lane + 64 * i;
+    seql[i] = 0;
+    qsll[i] = 0;
+    blk0l[i] = -1;
+    if (i < nper && rr < a.num_reqs) {
+      const int sr = a.seq_lens[rr];
+      qsll[i] = a.qsl[rr];
+      blk0l[i] = a.max_blocks > 0 ? a.bt[(int64_t)rr * a.bt_row_stride] : -1;
+      over |= sr > a.max_seq;
+      seql[i] = min(max(sr, 0), a.max_seq);  // the host sized the launch from max_seq
+      tot += seql[i];                         // host: num_reqs * max_seq < 2^31
     }
+  }
+  tot = wave_sum_i(tot);
+  const bool any_over = __builtin_amdgcn_ballot_w64(over) != 0;
+  if (blockIdx.x == 0 && tid == 0 && any_over) atomicOr(a.err, TTKV_ERR_SEQ_LEN);
+  int chunk;
+  {
+    int tl[kPlanLanes];  // tiles per request
+#pragma unroll
+    for (int i = 0; i < kPlanLanes; ++i) tl[i] = (seql[i] + kTile - 1) / kTile;
+    // items at chunk = m tiles: ceil(ceil(n / 64) / m) = ceil(n / (64 m)) chunks per request
+    auto items_at = [&](int m) {
+      int sum = 0;
+#pragma unroll
+      for (int i = 0; i < kPlanLanes; ++i)
+        if (i < nper && lane + 64 * i < a.num_reqs) sum += max(1, (tl[i] + m - 1) / m);
+      return wave_sum_i(sum) * g.H;
+    };
+    const int rounds = max(1, (a.num_reqs * g.H + a.target - 1) / a.target);
+    const int64_t budget = (int64_t)rounds * a.target;
+    const int m_cap = a.chunk_cap / kTile;
+    // no chunk below tot * H / budget tiles can fit (items fall as the chunk grows): start there,
+    // gallop up to a chunk that fits, then bisect; the cap is taken when nothing fits
+    int m = (int)min<int64_t>(m_cap, max<int64_t>(1, ((int64_t)tot * g.H + budget * kTile - 1) /
+                                                         (budget * kTile)));
+    if (items_at(m) > budget) {
+      int bad = m, good = -1, step = 1;
+      while (good < 0 && bad < m_cap) {
+        const int t = min(m_cap, bad + step);
+        if (items_at(t) <= budget) good = t;
+        else bad = t;
+        step <<= 1;
+      }
+      if (good < 0) {
+        m = m_cap;
+      } else {
+        while (good - bad > 1) {
+          const int mid = (bad + good) >> 1;
+          if (items_at(mid) <= budget) good = mid;
+          else bad = mid;
+        }
+        m = good;
+      }
+    }
+    chunk = m * kTile;
+  }
+  int nreq_items = 0, maxc = 0;
+#pragma unroll
+  for (int i = 0; i < kPlanLanes; ++i) {
+    nchl[i] = 0;
+    if (i < nper && lane + 64 * i < a.num_reqs) nchl[i] = max(1, (seql[i] + chunk - 1) / chunk);
+    nreq_items += nchl[i];
+    maxc = max(maxc, nchl[i]);
+  }
+  // items: <= rounds * target < target + num_reqs * H, or, when nothing fits, the host's count
+  // with every request at max_seq and the capped chunk -- the grid is sized for the larger
+  const int n_pairs = wave_sum_i(nreq_items);
+  const int n_items = n_pairs * g.H;
+  maxc = wave_max_i(maxc);
+  const int per_xcd = (n_items + 7) >> 3;
+  if ((int)(blockIdx.x >> 3) >= per_xcd) return;
+  const int w = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  if (w >= n_items) return;
+  const int h = w % g.H;
+  const int j = w / g.H;
+  // (chunk c, request r) of pair j: c is the largest with P(c) <= j, P(c) = sum_r min(nch_r, c);
+  // r is the (j - P(c))-th request with more than c chunks; base = chunks of the requests before
+  // r (its partials follow theirs). When every request has the same count this is a division.
+  int c = 0, r = 0, base = 0;
+  if (n_pairs == maxc * a.num_reqs) {
+    c = j / a.num_reqs;
+    r = j - c * a.num_reqs;
+    base = r * maxc;
+  } else {
+    int pc = 0, hi = maxc;
+    while (hi - c > 1) {
+      const int mid = (c + hi) >> 1;
+      int pm = 0;
+#pragma unroll
+      for (int i = 0; i < kPlanLanes; ++i)
+        if (i < nper) pm += min(nchl[i], mid);
+      pm = wave_sum_i(pm);
+      if (pm <= j) {
+        c = mid;
+        pc = pm;
+      } else {
+        hi = mid;
+      }
+    }
+    int k = j - pc;
+    bool found = false;
+#pragma unroll
+    for (int i = 0; i < kPlanLanes; ++i) {
+      if (i < nper && !found) {
+        const uint64_t msk = __builtin_amdgcn_ballot_w64(nchl[i] > c);
+        const int cnt = __builtin_popcountll(msk);
+        if (k < cnt) {
+          const uint64_t below = lane ? msk & (~0ull >> (64 - lane)) : 0ull;
+          const bool hit = ((msk >> lane) & 1ull) && __builtin_popcountll(below) == k;
+          r = 64 * i + __builtin_ctzll(__builtin_amdgcn_ballot_w64(hit));
+          found = true;
+        } else {
+          k -= cnt;
+        }
+      }
+    }
+    int bl = 0;
+#pragma unroll
+    for (int i = 0; i < kPlanLanes; ++i)
+      if (i < nper) bl += lane + 64 * i < r ? nchl[i] : 0;
+    base = wave_sum_i(bl);
+  }
+  int n_chunks = 0, seq = 0, qrow_r = 0, blk0 = -1;
+#pragma unroll
+  for (int i = 0; i < kPlanLanes; ++i) {
+    if ((r >> 6) == i) {
+      n_chunks = __builtin_amdgcn_readlane(nchl[i], r & 63);
+      seq = __builtin_amdgcn_readlane(seql[i], r & 63);
+      qrow_r = __builtin_amdgcn_readlane(qsll[i], r & 63);
+      blk0 = __builtin_amdgcn_readlane(blk0l[i], r & 63);
+    }
+  }
+
+  const int t0 = c * chunk;
+  const int ptok = tid >> 2;  // token / part handled by this thread in prefetch + commit
+  const int part = tid & 3;
+  // block id of this thread's token in the first tile (position clamped into the context)
+  const int64_t bt_row = (int64_t)r * a.bt_row_stride;
+  const int pos0 = min(t0 + ptok, seq - 1);
+  const int bi0 = a.bs_shift >= 0 ? pos0 >> a.bs_shift : pos0 / a.block_size;
+  const int64_t qrow = qrow_r;
+  const int blk_t0 = seq > 0 ? a.bt[bt_row + bi0] : -1;
+  if (seq <= 0) {  // empty context: the reference's einsum over zero rows is 0
+    for (int i = tid; i < G * kD; i += kThreads)
+      store_act(a.out, a.out_dtype, qrow * a.out_row_stride + (int64_t)(h * G) * kD + i, 0.f);
     return;
   }
-  const int t0 = c * a.chunk;
-  const int t1 = min(seq, t0 + a.chunk);
+  const int t1 = min(seq, t0 + chunk);
 
-  // Decoder slot via the device registry keyed by the request's first block.
+  // Decoder slot via the device registry keyed by the request's first block, requested together
+  // with the first tile's block ids; the first tile's bytes follow with the decoder (bad block ids
+  // are flagged when the chunk's ids are staged)
   int dslot = -1;
   if (blk0 >= 0 && blk0 < a.num_blocks) dslot = a.dec_map[blk0];
+  const int k_row_off = g.k_field + h * g.k_row;
+  const int v_row_off = g.k_slot + h * g.v_row;
+  RawSlot<KU> P;
+  {
+    const uint8_t* base = nullptr;
+    if (ptok < min(kTile, t1 - t0) && blk_t0 >= 0 && blk_t0 < a.num_blocks) {
+      const int64_t slot = (int64_t)blk_t0 * a.block_size + (pos0 - bi0 * a.block_size);
+      if (slot < a.n_slots) base = a.page + slot * a.slot_stride;
+    }
+    fetch_raw_slot<KU>(P, base, part, g, k_row_off, v_row_off);
+  }
   if (dslot < 0 || dslot >= a.n_dec_slots) {
     if (tid == 0) atomicOr(a.err, TTKV_ERR_NO_DECODER);
     if (c == 0)
@@ -195,7 +342,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   }
 
   // ---- decoder and query values for the MFMA fragments: loaded now, so that their latency
-  // overlaps the table and block-id staging; converted after the first prefetch is issued
+  // overlaps the table and block-id staging
   const int dl = 16 * wv + 4 * gq;
   const int HD = g.H * kD;
   const float* dec = a.dec_pool + (int64_t)dslot * g.r1 * HD + h * kD;
@@ -226,7 +373,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   }
 
   // ---- code tables, and this chunk's block ids
-  stage_luts(S.lut, (RB == 3 || VB == 3) ? S.lut3 : nullptr, tid, kThreads);
+  build_luts(S.lut, (RB == 3 || VB == 3) ? S.lut3 : nullptr, tid, kThreads);
   const int bfirst = t0 / a.block_size;
   const int nseg = (t1 - 1) / a.block_size - bfirst + 1;
   for (int i = tid; i < nseg; i += kThreads) {
@@ -238,10 +385,6 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
     S.seg[i] = blk;
   }
 
-  const int k_row_off = g.k_field + h * g.k_row;
-  const int v_row_off = g.k_slot + h * g.v_row;
-  const int ptok = tid >> 2;  // token / part handled by this thread in prefetch + commit
-  const int part = tid & 3;
   // slot bases are 16-aligned, so a row's byte misalignment is fixed per head
   const uint32_t ksel = stage_selector(k_row_off & 3, part != 0);
   const uint32_t vsel = stage_selector(v_row_off & 3, part != 0);
@@ -264,10 +407,6 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
     if (slot >= a.n_slots) return nullptr;
     return a.page + slot * a.slot_stride;
   };
-
-  // first tile's bytes in flight while the decoder is loaded
-  RawSlot<KU> P;
-  fetch_raw_slot<KU>(P, slot_base(t0), part, g, k_row_off, v_row_off);
 
   // ---- decoder fragments (A operand, M = dims, K = r1), hi/lo fp16, resident in registers.
   half8 ahi[2][KSTEPS], alo[2][KSTEPS];
@@ -542,7 +681,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
 
   // ---- split-K partial: [G][kD + 2] per (r, h, c): unnormalised o, running max, running sum
   const int64_t pstride = (int64_t)G * (kD + 2);
-  float* partp = a.ws_part + ((int64_t)(r * g.H + h) * a.max_chunks + c) * pstride;
+  float* partp = a.ws_part + ((int64_t)(base + c) * g.H + h) * pstride;
   // The partial is written with agent-scope (write-through) atomic stores and waited on before
   // the counter update, so no cache-wide release fence is needed; the combining block reads the
   // partials with agent-scope atomic loads.
@@ -576,17 +715,18 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   // partials -- and, unlike atomic loads, the loads of all chunks can be in flight together.
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   auto ld_agent = [](const float* p) { return *p; };
-  const float* pbase = a.ws_part + (int64_t)(r * g.H + h) * a.max_chunks * pstride;
+  const float* pbase = a.ws_part + ((int64_t)base * g.H + h) * pstride;
+  const int64_t cstride = (int64_t)g.H * pstride;  // between chunks of one request and head
   for (int it = tid; it < G * kD; it += kThreads) {
     const int p = it / kD;
     const int dim = it - p * kD;
     float M = -INFINITY;
 #pragma unroll 8
-    for (int cc = 0; cc < n_chunks; ++cc) M = fmaxf(M, ld_agent(&pbase[cc * pstride + p * (kD + 2) + kD]));
+    for (int cc = 0; cc < n_chunks; ++cc) M = fmaxf(M, ld_agent(&pbase[cc * cstride + p * (kD + 2) + kD]));
     float L = 0.f, O = 0.f;
 #pragma unroll 8
     for (int cc = 0; cc < n_chunks; ++cc) {
-      const float* pc = pbase + cc * pstride + p * (kD + 2);
+      const float* pc = pbase + cc * cstride + p * (kD + 2);
       const float f = exp2f(ld_agent(&pc[kD]) - M);
       L = fmaf(ld_agent(&pc[kD + 1]), f, L);
       O = fmaf(ld_agent(&pc[dim]), f, O);
@@ -647,23 +787,42 @@ static int dispatch_k(const DecodeArgs& a, int ku, int grid, hipStream_t st) {
   return host_fail(TTKV_E_UNSUPPORTED, "r1 > 160 is not built");
 }
 
-int decode_chunk_for(int num_reqs, int H, int max_seq_len, int block_size) {
-  const int64_t work = (int64_t)num_reqs * H * std::max(max_seq_len, 1);
-  const int64_t target = 2LL * device_cu_count();  // one round at 2 resident blocks per CU
-  int64_t chunk = (work + target - 1) / target;
-  chunk = (chunk + kTile - 1) / kTile * kTile;
-  chunk = std::min<int64_t>(std::max<int64_t>(chunk, kTile), 4096);
+// Requests per launch: the work plan holds kPlanReqs of them, and a launch's token total must fit
+// an int. Larger batches run as several launches over consecutive request ranges.
+static int decode_slice_reqs(int num_reqs, int max_seq_len) {
+  const int64_t by_total = std::max<int64_t>(1, (int64_t)INT32_MAX / std::max(max_seq_len, 1));
+  return (int)std::min<int64_t>(std::min<int64_t>(num_reqs, kPlanReqs), by_total);
+}
+
+struct DecodeShape {
+  int chunk_cap, target;
+  int64_t items_cap;  // (request, chunk, head) items any batch of this shape can need
+};
+
+// The kernel picks its chunk length from the batch's token total T: 64 * ceil(T * H / target / 64),
+// clamped to [64, chunk_cap]. The batch with every request at max_seq_len gives the longest
+// chunk and bounds the item count when the cap binds; otherwise the items are at most
+// sum_r (seq_r / chunk + 1) * H <= target + num_reqs * H.
+static DecodeShape decode_shape(int num_reqs, int H, int max_seq_len, int block_size) {
+  DecodeShape s;
+  s.target = 2 * device_cu_count();  // one round at 2 resident blocks per CU
   // the block ids of one chunk are staged in LDS: at most kSegMax of them
   const int64_t seg_cap = (int64_t)(kSegMax - 2) * std::max(block_size, 1) / kTile * kTile;
-  return (int)std::max<int64_t>(std::min<int64_t>(chunk, seg_cap), kTile);
+  s.chunk_cap = (int)std::max<int64_t>(std::min<int64_t>(seg_cap, 4096), kTile);
+  const int64_t work = (int64_t)num_reqs * H * std::max(max_seq_len, 1);
+  int64_t chunk = (work + s.target - 1) / s.target;
+  chunk = std::min<int64_t>(std::max<int64_t>((chunk + kTile - 1) / kTile * kTile, kTile),
+                            s.chunk_cap);
+  const int64_t uniform = (int64_t)num_reqs * H * std::max<int64_t>(1, (max_seq_len + chunk - 1) / chunk);
+  s.items_cap = std::max<int64_t>((int64_t)s.target + (int64_t)num_reqs * H, uniform);
+  return s;
 }
 
 int64_t decode_workspace_bytes(const Geom& g, int G, int num_reqs, int max_seq_len,
                                int block_size) {
-  const int chunk = decode_chunk_for(num_reqs, g.H, max_seq_len, block_size);
-  const int max_chunks = std::max(1, (max_seq_len + chunk - 1) / chunk);
-  const int64_t cnt = ((int64_t)num_reqs * g.H * 4 + 255) / 256 * 256;
-  return cnt + (int64_t)num_reqs * g.H * max_chunks * G * (kD + 2) * 4;
+  const int nr = decode_slice_reqs(num_reqs, max_seq_len);
+  const DecodeShape s = decode_shape(nr, g.H, max_seq_len, block_size);
+  return kCounterBytes + s.items_cap * G * (kD + 2) * 4;
 }
 
 int decode_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype,
@@ -679,6 +838,7 @@ int decode_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype,
   if (!((g.res_bits == 3 && g.v_bits == 3) || (g.res_bits == 4 && g.v_bits == 4)))
     return host_fail(TTKV_E_UNSUPPORTED, "res_bits/v_bits must be 3/3 or 4/4");
   if (HQ <= 0 || HQ % g.H) return host_fail(TTKV_E_INVALID, "num_heads is not a multiple of H");
+  if (g.H * kPlanReqs > kMaxCounters) return host_fail(TTKV_E_UNSUPPORTED, "H > 64 KV heads");
   const int G = HQ / g.H;
   // coefficient window in 16-wide k units (r1 padded to 16 * ku)
   const int ku = g.r1 <= 64 ? 4 : g.r1 <= 112 ? 7 : g.r1 <= 128 ? 8 : g.r1 <= 160 ? 10 : 0;
@@ -733,23 +893,34 @@ int decode_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype,
   a.out_dtype = out_dtype;
   a.out_row_stride = out_row_stride;
   a.err = err;
-  a.chunk = decode_chunk_for(num_reqs, g.H, max_seq_len, block_size);
-  a.max_chunks = std::max(1, (max_seq_len + a.chunk - 1) / a.chunk);
-  if (a.max_chunks > 1) {
+  a.max_seq = max_seq_len;
+  if (max_seq_len > kTile) {  // a request may be split into chunks: partials + counters
     const int64_t need = decode_workspace_bytes(g, G, num_reqs, max_seq_len, block_size);
     if (!ws || ws_bytes < need)
       return host_fail(TTKV_E_WORKSPACE, "decode workspace needs " + std::to_string(need) +
                                              " bytes, got " + std::to_string(ws_bytes));
     if ((uintptr_t)ws % 256) return host_fail(TTKV_E_INVALID, "workspace not 256-byte aligned");
-    const int64_t cnt = ((int64_t)num_reqs * g.H * 4 + 255) / 256 * 256;
-    a.ws_cnt = (int*)ws;
-    a.ws_part = (float*)((char*)ws + cnt);
   }
-  a.max_seq = max_seq_len;
-  a.nwork = num_reqs * a.max_chunks * g.H;
-  const int grid = (a.nwork + 7) / 8 * 8;
-  if (g.res_bits == 3) return dispatch_k<3, 3>(a, ku, grid, st);
-  return dispatch_k<4, 4>(a, ku, grid, st);
+  const int slice = decode_slice_reqs(num_reqs, max_seq_len);
+  for (int r0 = 0; r0 < num_reqs; r0 += slice) {
+    DecodeArgs b = a;
+    b.num_reqs = std::min(slice, num_reqs - r0);
+    b.seq_lens = seq_lens + r0;
+    b.qsl = qsl + r0;
+    b.bt = bt + (int64_t)r0 * bt_row_stride;
+    const DecodeShape sh = decode_shape(b.num_reqs, g.H, max_seq_len, block_size);
+    b.chunk_cap = sh.chunk_cap;
+    b.target = sh.target;
+    if (max_seq_len > kTile) {  // counters [r * H + h]: kPlanReqs * H <= kMaxCounters
+      b.ws_cnt = (int*)ws;
+      b.ws_part = (float*)((char*)ws + kCounterBytes);
+    }
+    const int grid = (int)((sh.items_cap + 7) / 8 * 8);
+    const int rc = g.res_bits == 3 ? dispatch_k<3, 3>(b, ku, grid, st)
+                                   : dispatch_k<4, 4>(b, ku, grid, st);
+    if (rc != TTKV_OK) return rc;
+  }
+  return TTKV_OK;
 }
 
 }  // namespace ttkv

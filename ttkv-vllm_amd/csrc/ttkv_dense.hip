@@ -280,11 +280,23 @@ int dense_chunk_for(int num_reqs, int H, int max_seq_len, int block_size) {
   return (int)std::max<int64_t>(std::min(chunk, seg_cap), 256);
 }
 
-int64_t dense_workspace_bytes(int H, int G, int num_reqs, int max_seq_len, int block_size) {
-  const int chunk = dense_chunk_for(num_reqs, H, max_seq_len, block_size);
+// Requests per launch: one arrival counter per (request, head).
+static int dense_slice_reqs(int H, int num_reqs) {
+  return std::min(num_reqs, std::max(1, kMaxCounters / std::max(H, 1)));
+}
+
+static int64_t dense_part_bytes(int H, int G, int nr, int max_seq_len, int block_size) {
+  const int chunk = dense_chunk_for(nr, H, max_seq_len, block_size);
   const int max_chunks = std::max(1, (max_seq_len + chunk - 1) / chunk);
-  const int64_t cnt = ((int64_t)num_reqs * H * 4 + 255) / 256 * 256;
-  return cnt + (int64_t)num_reqs * H * max_chunks * G * (kD + 2) * 4;
+  return (int64_t)nr * H * max_chunks * G * (kD + 2) * 4;
+}
+
+int64_t dense_workspace_bytes(int H, int G, int num_reqs, int max_seq_len, int block_size) {
+  if (num_reqs <= 0) return kCounterBytes;
+  const int slice = dense_slice_reqs(H, num_reqs);
+  return kCounterBytes +
+         std::max(dense_part_bytes(H, G, slice, max_seq_len, block_size),
+                  dense_part_bytes(H, G, (num_reqs - 1) % slice + 1, max_seq_len, block_size));
 }
 
 template <int G, int DT>
@@ -333,27 +345,42 @@ int dense_decode_paged(int H, int HQ, int d, float scale, const void* q, int64_t
   a.out = out;
   a.out_row_stride = out_row_stride;
   a.max_seq = max_seq_len;
-  a.chunk = dense_chunk_for(num_reqs, H, max_seq_len, block_size);
-  a.max_chunks = std::max(1, (max_seq_len + a.chunk - 1) / a.chunk);
-  if (a.max_chunks > 1) {
+  if (a.G < 1 || a.G > 4) return host_fail(TTKV_E_UNSUPPORTED, "G must be 1..4 for the dense comparator");
+  if (H > kMaxCounters) return host_fail(TTKV_E_UNSUPPORTED, "H");
+  const bool multi = dense_chunk_for(dense_slice_reqs(H, num_reqs), H, max_seq_len, block_size) <
+                     max_seq_len;
+  if (multi) {
     const int64_t need = dense_workspace_bytes(H, a.G, num_reqs, max_seq_len, block_size);
     if (!ws || ws_bytes < need || (uintptr_t)ws % 256)
       return host_fail(TTKV_E_WORKSPACE, "dense workspace needs " + std::to_string(need) +
                                              " bytes, 256-aligned");
-    const int64_t cnt = ((int64_t)num_reqs * H * 4 + 255) / 256 * 256;
-    a.ws_cnt = (int*)ws;
-    a.ws_part = (float*)((char*)ws + cnt);
   }
-  a.nwork = num_reqs * a.max_chunks * H;
-  const int grid = (a.nwork + 7) / 8 * 8;
-  const bool f16 = dtype == TTKV_DTYPE_F16;
-  switch (a.G) {
-    case 1: return f16 ? launch_dense_t<1, TTKV_DTYPE_F16>(a, grid, st) : launch_dense_t<1, TTKV_DTYPE_BF16>(a, grid, st);
-    case 2: return f16 ? launch_dense_t<2, TTKV_DTYPE_F16>(a, grid, st) : launch_dense_t<2, TTKV_DTYPE_BF16>(a, grid, st);
-    case 3: return f16 ? launch_dense_t<3, TTKV_DTYPE_F16>(a, grid, st) : launch_dense_t<3, TTKV_DTYPE_BF16>(a, grid, st);
-    case 4: return f16 ? launch_dense_t<4, TTKV_DTYPE_F16>(a, grid, st) : launch_dense_t<4, TTKV_DTYPE_BF16>(a, grid, st);
+  const int slice = dense_slice_reqs(H, num_reqs);
+  for (int r0 = 0; r0 < num_reqs; r0 += slice) {
+    DenseArgs b = a;
+    b.num_reqs = std::min(slice, num_reqs - r0);
+    b.seq_lens = seq_lens + r0;
+    b.qsl = qsl + r0;
+    b.bt = bt + (int64_t)r0 * bt_row_stride;
+    b.chunk = dense_chunk_for(b.num_reqs, H, max_seq_len, block_size);
+    b.max_chunks = std::max(1, (max_seq_len + b.chunk - 1) / b.chunk);
+    if (b.max_chunks > 1) {  // counters [r * H + h] <= kMaxCounters
+      b.ws_cnt = (int*)ws;
+      b.ws_part = (float*)((char*)ws + kCounterBytes);
+    }
+    b.nwork = b.num_reqs * b.max_chunks * H;
+    const int grid = (b.nwork + 7) / 8 * 8;
+    const bool f16 = dtype == TTKV_DTYPE_F16;
+    int rc = TTKV_OK;
+    switch (a.G) {
+      case 1: rc = f16 ? launch_dense_t<1, TTKV_DTYPE_F16>(b, grid, st) : launch_dense_t<1, TTKV_DTYPE_BF16>(b, grid, st); break;
+      case 2: rc = f16 ? launch_dense_t<2, TTKV_DTYPE_F16>(b, grid, st) : launch_dense_t<2, TTKV_DTYPE_BF16>(b, grid, st); break;
+      case 3: rc = f16 ? launch_dense_t<3, TTKV_DTYPE_F16>(b, grid, st) : launch_dense_t<3, TTKV_DTYPE_BF16>(b, grid, st); break;
+      case 4: rc = f16 ? launch_dense_t<4, TTKV_DTYPE_F16>(b, grid, st) : launch_dense_t<4, TTKV_DTYPE_BF16>(b, grid, st); break;
+    }
+    if (rc != TTKV_OK) return rc;
   }
-  return host_fail(TTKV_E_UNSUPPORTED, "G must be 1..4 for the dense comparator");
+  return TTKV_OK;
 }
 
 }  // namespace ttkv

@@ -93,16 +93,38 @@ __device__ __forceinline__ void fetch_raw_slot(RawSlot<NCW>& P, const uint8_t* b
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Cross-lane helpers on DPP and the gfx950 permlane swaps (VALU ops, no LDS round trip).
-__device__ __forceinline__ float dpp_f(float v, int ctrl_sel) {
-  const int iv = __builtin_bit_cast(int, v);
-  int r = 0;
+__device__ __forceinline__ int dpp_i(int iv, int ctrl_sel) {
   switch (ctrl_sel) {  // dpp control must be a constant
-    case 0: r = __builtin_amdgcn_update_dpp(0, iv, 0xB1, 0xF, 0xF, false); break;   // xor 1
-    case 1: r = __builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xF, 0xF, false); break;   // xor 2
-    case 2: r = __builtin_amdgcn_update_dpp(0, iv, 0x124, 0xF, 0xF, false); break;  // row_ror 4
-    default: r = __builtin_amdgcn_update_dpp(0, iv, 0x128, 0xF, 0xF, false); break; // row_ror 8
+    case 0: return __builtin_amdgcn_update_dpp(0, iv, 0xB1, 0xF, 0xF, false);   // xor 1
+    case 1: return __builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xF, 0xF, false);   // xor 2
+    case 2: return __builtin_amdgcn_update_dpp(0, iv, 0x124, 0xF, 0xF, false);  // row_ror 4
+    default: return __builtin_amdgcn_update_dpp(0, iv, 0x128, 0xF, 0xF, false); // row_ror 8
   }
-  return __builtin_bit_cast(float, r);
+}
+__device__ __forceinline__ float dpp_f(float v, int ctrl_sel) {
+  return __builtin_bit_cast(float, dpp_i(__builtin_bit_cast(int, v), ctrl_sel));
+}
+// Integer sum / max over the whole wave, returned as a wave-uniform (scalar) value; all lanes
+// must be active.
+__device__ __forceinline__ int wave_sum_i(int v) {
+  v += dpp_i(v, 0);
+  v += dpp_i(v, 1);
+  v += dpp_i(v, 2);
+  v += dpp_i(v, 3);
+  auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = (int)r[0] + (int)r[1];
+  r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return __builtin_amdgcn_readfirstlane((int)r[0] + (int)r[1]);
+}
+__device__ __forceinline__ int wave_max_i(int v) {
+  v = max(v, dpp_i(v, 0));
+  v = max(v, dpp_i(v, 1));
+  v = max(v, dpp_i(v, 2));
+  v = max(v, dpp_i(v, 3));
+  auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = max((int)r[0], (int)r[1]);
+  r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return __builtin_amdgcn_readfirstlane(max((int)r[0], (int)r[1]));
 }
 // Sum / max over the 16 lanes of each row (every lane gets its row's result).
 __device__ __forceinline__ float row_sum(float v) {
@@ -189,57 +211,45 @@ __device__ __forceinline__ uint32_t staged_u16(const uint32_t* row, int rb) {
 // in sign-magnitude: magnitude k <= 15 is byte k in both e4m3 variants (k * 2^-9 in OCP e4m3,
 // k * 2^-10 in the FNUZ one; the kernels read the unit back from the hardware conversion).
 // Lanes outside the bitmap get byte 0 (+0), i.e. residual 0, with no fix-up pass.
-__host__ __device__ constexpr uint32_t fp8_signed_byte(int d) {
-  return d >= 0 ? (uint32_t)d : (0x80u | (uint32_t)(-d));
+
+// The decode tables, built in LDS by the workgroup itself (a few hundred VALU operations per
+// thread, no memory traffic at kernel start):
+//   lut3[x]  (3-bit codes): x = 12 bits holding 4 codes, the first in the top 3 bits -> the 4
+//            codes as fp8 signed bytes (c - 4), first code in byte 0. The byte map c -> fp8(c - 4)
+//            is one v_perm over the 8-byte table {84 83 82 81 00 01 02 03}.
+//   lut[B]   selectors that move the byte-spread codes of bitmap byte B (MSB = first lane) onto its
+//            set lanes: lane k gets the rank of its bit among B's set bits, 0x0c (zero) if unset.
+__device__ __forceinline__ uint32_t lut3_entry(uint32_t x) {
+  const uint32_t c = (x >> 9) | (((x >> 6) & 7u) << 8) | (((x >> 3) & 7u) << 16) | ((x & 7u) << 24);
+  return __builtin_amdgcn_perm(0x03020100u, 0x81828384u, c);
 }
-
-// 3-bit spread table: entry x (12 bits = 4 codes, first code in the top 3 bits) -> the 4 codes
-// as fp8 signed bytes (c - 4), first code in byte 0.
-struct SpreadLut3 {
-  uint32_t v[4096];
-  constexpr SpreadLut3() : v() {
-    for (uint32_t x = 0; x < 4096; ++x) {
-      uint32_t r = 0;
-      for (int i = 0; i < 4; ++i) r |= fp8_signed_byte((int)((x >> (9 - 3 * i)) & 7u) - 4) << (8 * i);
-      v[x] = r;
-    }
+__device__ __forceinline__ uint2 scatter_entry(uint32_t B) {
+  uint32_t s0 = 0, s1 = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t present = (B >> (7 - k)) & 1u;
+    const uint32_t idx = __builtin_popcount(B >> (8 - k));  // set bits before lane k
+    const uint32_t sel = present ? idx : 0x0cu;
+    if (k < 4) s0 |= sel << (8 * k);
+    else s1 |= sel << (8 * (k - 4));
   }
-};
-// Scatter table: entry B holds the v_perm selectors that move the byte-spread codes of bitmap
-// byte B (MSB = first lane) onto its set lanes, 0x0c (zero byte) on the others.
-struct ScatterLut {
-  uint32_t v[512];
-  constexpr ScatterLut() : v() {
-    for (uint32_t B = 0; B < 256; ++B) {
-      uint32_t s0 = 0, s1 = 0, idx = 0;
-      for (int k = 0; k < 8; ++k) {
-        const bool present = (B >> (7 - k)) & 1u;
-        const uint32_t sel = present ? idx : 0x0cu;
-        idx += present ? 1u : 0u;
-        if (k < 4) s0 |= sel << (8 * k);
-        else s1 |= sel << (8 * (k - 4));
-      }
-      v[2 * B] = s0;
-      v[2 * B + 1] = s1;
-    }
-  }
-};
-static __constant__ SpreadLut3 kSpreadLut3 = SpreadLut3();
-static __constant__ ScatterLut kScatterLut = ScatterLut();
-
-// Copy the tables into LDS with 16-byte loads (256-thread blocks).
-__device__ __forceinline__ void stage_luts(uint2* lut, uint32_t* lut3, int tid, int nthreads) {
-  const u32x4* s = (const u32x4*)kScatterLut.v;
-  for (int i = tid; i < 128; i += nthreads) ((u32x4*)lut)[i] = s[i];
+  return make_uint2(s0, s1);
+}
+__device__ __forceinline__ void build_luts(uint2* lut, uint32_t* lut3, int tid, int nthreads) {
+  for (int i = tid; i < 256; i += nthreads) lut[i] = scatter_entry((uint32_t)i);
   if (lut3) {
-    const u32x4* s3 = (const u32x4*)kSpreadLut3.v;
-    for (int i = tid; i < 1024; i += nthreads) ((u32x4*)lut3)[i] = s3[i];
+    for (int i = tid; i < 1024; i += nthreads) {
+      u32x4 e;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) e[k] = lut3_entry((uint32_t)(4 * i + k));
+      ((u32x4*)lut3)[i] = e;
+    }
   }
 }
 
 // Decode dims [64*half, 64*half+64) of one big-endian staged head row into one byte per lane at
 // dst[0..63].
-//   BITS == 3: fp8 signed bytes (c - 4), 0 outside the bitmap; needs lut3 (SpreadLut3).
+//   BITS == 3: fp8 signed bytes (c - 4), 0 outside the bitmap; needs lut3 (build_luts).
 //   BITS == 4: offset-binary code bytes c, 8 outside the bitmap.
 // Per bitmap byte: the code window at bit offset bp is one v_alignbit of the words holding bits
 // bp-1 and bp+31 (shift (-bp) mod 32; word -1 is the last bitmap dword, read but unused).

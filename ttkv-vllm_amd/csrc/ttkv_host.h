@@ -12,7 +12,14 @@ namespace ttkv {
 int host_fail(int code, const std::string& msg);
 int device_cu_count();
 
-int decode_chunk_for(int num_reqs, int H, int max_seq_len, int block_size);
+// Every workspace starts with a fixed region of arrival counters: zero before first use (a fresh
+// zero-filled buffer), left zero by every call. It sits at the same offset with the same size
+// whatever the call's shape, so one buffer can serve calls of any shape in turn: a call's data
+// never lands where a later call expects zeroed counters. A launch uses at most kMaxCounters of
+// them; larger batches run as several launches.
+constexpr int64_t kCounterBytes = 65536;
+constexpr int kMaxCounters = (int)(kCounterBytes / 4);
+
 int64_t decode_workspace_bytes(const Geom& g, int G, int num_reqs, int max_seq_len,
                                int block_size);
 int decode_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype,

@@ -79,6 +79,7 @@ struct PrefillArgs {
   int* ws_cnt;
   int* err;
   int n_qb, kchunk, nsplit, nwork, max_seq, max_q;
+  int ri0;  // first batch row of this launch (rows ri0 .. ri0 + num_reqs - 1)
 };
 
 template <int KSTEPS, bool EXACT>
@@ -138,7 +139,7 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
   const int sp = t % a.nsplit;
   const int ri = t / a.nsplit;
   if (ri >= a.num_reqs) return;
-  const int r = a.req_index ? a.req_index[ri] : ri;
+  const int r = a.req_index ? a.req_index[a.ri0 + ri] : a.ri0 + ri;
   const int q0 = a.qsl[r];
   int qlen = a.qsl[r + 1] - q0;
   int seq = a.seq_lens[r];
@@ -188,7 +189,7 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
     return;
   }
 
-  stage_luts(S.lut, (RB == 3 || VB == 3) ? S.lut3 : nullptr, tid, kPThreads);
+  build_luts(S.lut, (RB == 3 || VB == 3) ? S.lut3 : nullptr, tid, kPThreads);
 
   // ---- query fragments (B operand of S^T = Kp Q^T): column = query 16*wv + n of the block
   const int qj = qa + 16 * wv + n;
@@ -642,16 +643,31 @@ static int prefill_kchunk(int items, int max_seq_len, int block_size) {
   return (int)std::max<int64_t>(std::min(kc, seg_cap), kPTile);
 }
 
-int64_t prefill_workspace_bytes(const Geom& g, int G, int num_reqs, int max_q_len,
-                                int max_seq_len, int block_size) {
-  if (num_reqs <= 0 || max_q_len <= 0) return 0;
+// Batch rows per launch: one arrival counter per (row, head, query block).
+static int prefill_slice_reqs(const Geom& g, int num_reqs, int max_q_len) {
   const int n_qb = (max_q_len + kPQ - 1) / kPQ;
-  const int items = num_reqs * g.H * n_qb;
+  return std::min(num_reqs, std::max(1, kMaxCounters / (g.H * n_qb)));
+}
+
+// Partials of a launch over nr rows (0 when its keys are not split).
+static int64_t prefill_part_bytes(const Geom& g, int G, int nr, int max_q_len, int max_seq_len,
+                                  int block_size) {
+  const int n_qb = (max_q_len + kPQ - 1) / kPQ;
+  const int items = nr * g.H * n_qb;
   const int kc = prefill_kchunk(items, max_seq_len, block_size);
   const int nsplit = std::max(1, (max_seq_len + kc - 1) / kc);
   if (nsplit == 1) return 0;
-  const int64_t cnt = ((int64_t)items * 4 + 255) / 256 * 256;
-  return cnt + (int64_t)items * nsplit * G * kPQ * (kD + 2) * 4;
+  return (int64_t)items * nsplit * G * kPQ * (kD + 2) * 4;
+}
+
+int64_t prefill_workspace_bytes(const Geom& g, int G, int num_reqs, int max_q_len,
+                                int max_seq_len, int block_size) {
+  if (num_reqs <= 0 || max_q_len <= 0) return 0;
+  const int slice = prefill_slice_reqs(g, num_reqs, max_q_len);
+  const int64_t part = std::max(
+      prefill_part_bytes(g, G, slice, max_q_len, max_seq_len, block_size),
+      prefill_part_bytes(g, G, (num_reqs - 1) % slice + 1, max_q_len, max_seq_len, block_size));
+  return part ? kCounterBytes + part : 0;
 }
 
 int prefill_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype,
@@ -733,27 +749,41 @@ int prefill_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype
   a.max_seq = max_seq_len;
   a.max_q = max_q_len;
   a.n_qb = (max_q_len + kPQ - 1) / kPQ;
-  const int items = num_reqs * g.H * a.n_qb;
-  a.kchunk = prefill_kchunk(items, max_seq_len, block_size);
-  a.nsplit = std::max(1, (max_seq_len + a.kchunk - 1) / a.kchunk);
-  if (!scores && a.nsplit > 1) {
+  if ((int64_t)g.H * a.n_qb > kMaxCounters)
+    return host_fail(TTKV_E_UNSUPPORTED, "max_q_len=" + std::to_string(max_q_len) +
+                                             " is past the longest query chunk built");
+  if (!scores) {
     const int64_t need = prefill_workspace_bytes(g, G, num_reqs, max_q_len, max_seq_len, block_size);
-    if (!ws || ws_bytes < need)
+    if (need && (!ws || ws_bytes < need))
       return host_fail(TTKV_E_WORKSPACE, "prefill workspace needs " + std::to_string(need) +
                                              " bytes, got " + std::to_string(ws_bytes));
-    if ((uintptr_t)ws % 256) return host_fail(TTKV_E_INVALID, "workspace not 256-byte aligned");
-    const int64_t cnt = ((int64_t)items * 4 + 255) / 256 * 256;
-    a.ws_cnt = (int*)ws;
-    a.ws_part = (float*)((char*)ws + cnt);
+    if (need && (uintptr_t)ws % 256)
+      return host_fail(TTKV_E_INVALID, "workspace not 256-byte aligned");
   }
-  a.nwork = items * a.nsplit;
-  const int grid = (a.nwork + 7) / 8 * 8;
-  if (scores) {
-    if (g.res_bits == 3) return prefill_dispatch_k<3, 3, true>(a, ksteps, grid, st);
-    return prefill_dispatch_k<4, 4, true>(a, ksteps, grid, st);
+  const int slice = prefill_slice_reqs(g, num_reqs, max_q_len);
+  for (int ri0 = 0; ri0 < num_reqs; ri0 += slice) {
+    PrefillArgs b = a;
+    b.ri0 = ri0;
+    b.num_reqs = std::min(slice, num_reqs - ri0);
+    const int items = b.num_reqs * g.H * a.n_qb;
+    b.kchunk = prefill_kchunk(items, max_seq_len, block_size);
+    b.nsplit = std::max(1, (max_seq_len + b.kchunk - 1) / b.kchunk);
+    if (!scores && b.nsplit > 1) {  // counters [item]: items <= kMaxCounters
+      b.ws_cnt = (int*)ws;
+      b.ws_part = (float*)((char*)ws + kCounterBytes);
+    }
+    b.nwork = items * b.nsplit;
+    const int grid = (b.nwork + 7) / 8 * 8;
+    int rc;
+    if (scores)
+      rc = g.res_bits == 3 ? prefill_dispatch_k<3, 3, true>(b, ksteps, grid, st)
+                           : prefill_dispatch_k<4, 4, true>(b, ksteps, grid, st);
+    else
+      rc = g.res_bits == 3 ? prefill_dispatch_k<3, 3, false>(b, ksteps, grid, st)
+                           : prefill_dispatch_k<4, 4, false>(b, ksteps, grid, st);
+    if (rc != TTKV_OK) return rc;
   }
-  if (g.res_bits == 3) return prefill_dispatch_k<3, 3, false>(a, ksteps, grid, st);
-  return prefill_dispatch_k<4, 4, false>(a, ksteps, grid, st);
+  return TTKV_OK;
 }
 
 }  // namespace ttkv

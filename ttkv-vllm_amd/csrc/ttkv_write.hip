@@ -58,6 +58,7 @@ struct WriteArgs {
   float* c_out;
   float* r_out;
   int* err;
+  int tok0;         // first token of this launch (tokens tok0 .. tok0 + num_tokens - 1)
   int* ws_cnt;      // [num_tokens] arrival counters (zero between calls)
   float* ws_part;   // [num_tokens][H][r1] per-head partial projections
   float* ws_q;      // [num_tokens][r1 + 1] cq (as floats) then cs
@@ -168,7 +169,8 @@ __global__ __launch_bounds__(kWThreads) void write_project_kernel(WriteArgs a) {
   __shared__ int is_last;
   const Geom& g = a.g;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int i = blockIdx.x / g.H;
+  const int il = blockIdx.x / g.H;  // token within this launch: its workspace rows
+  const int i = a.tok0 + il;
   const int h = blockIdx.x % g.H;
   const int HD = g.H * kD;
   const int64_t slot = a.slot_mapping[i];
@@ -180,7 +182,7 @@ __global__ __launch_bounds__(kWThreads) void write_project_kernel(WriteArgs a) {
   if (tid < kD) mk[tid] = kv;
   __syncthreads();
   const float* pinv = a.pinv_pool + (int64_t)ds * HD * g.r1 + (int64_t)h * kD * g.r1;
-  float* pp = a.ws_part + ((int64_t)i * g.H + h) * g.r1;
+  float* pp = a.ws_part + ((int64_t)il * g.H + h) * g.r1;
   const int half = tid >> 7, ar = tid & 127;
   for (int a0 = 0; a0 < g.r1; a0 += 128) {
     const int aa = a0 + ar;
@@ -203,17 +205,17 @@ __global__ __launch_bounds__(kWThreads) void write_project_kernel(WriteArgs a) {
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (tid == 0)
-    is_last = __hip_atomic_fetch_add(&a.ws_cnt[i], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+    is_last = __hip_atomic_fetch_add(&a.ws_cnt[il], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
               g.H - 1;
   __syncthreads();
   if (!is_last) return;
   // c[a] = sum over heads in head order
-  float* cq = a.ws_q + (int64_t)i * (g.r1 + 1);
+  float* cq = a.ws_q + (int64_t)il * (g.r1 + 1);
   float mx = 0.f;
   float cv = 0.f;
   const bool mine = tid < g.r1;
   if (mine) {
-    const float* base = a.ws_part + (int64_t)i * g.H * g.r1;
+    const float* base = a.ws_part + (int64_t)il * g.H * g.r1;
     for (int hh = 0; hh < g.H; ++hh)
       cv += __hip_atomic_load(&base[hh * g.r1 + tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     mx = fabsf(cv);
@@ -229,7 +231,7 @@ __global__ __launch_bounds__(kWThreads) void write_project_kernel(WriteArgs a) {
   if (mine) cq[tid] = fminf(fmaxf(rintf(__fdiv_rn(cv, cs)), -128.f), 127.f);
   if (tid == 0) {
     cq[g.r1] = cs;
-    __hip_atomic_store(&a.ws_cnt[i], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&a.ws_cnt[il], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -241,7 +243,8 @@ __global__ __launch_bounds__(kWThreads) void write_pack_kernel(WriteArgs a) {
   __shared__ uint8_t codes[2][kD];
   const Geom& g = a.g;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int i = blockIdx.x / g.H;
+  const int il = blockIdx.x / g.H;  // token within this launch: its workspace rows
+  const int i = a.tok0 + il;
   const int h = blockIdx.x % g.H;
   const int HD = g.H * kD;
   const int64_t slot = a.slot_mapping[i];
@@ -266,17 +269,16 @@ __global__ __launch_bounds__(kWThreads) void write_pack_kernel(WriteArgs a) {
       d1[u] = ar < g.r1 ? dec[(int64_t)ar * HD + 64 + lane] : 0.f;
     }
   }
-  const float cs = a.cq_in ? a.cs_in[i] : a.ws_q[(int64_t)i * (g.r1 + 1) + g.r1];
+  const float* wq = a.ws_q + (int64_t)il * (g.r1 + 1);
+  const float cs = a.cq_in ? a.cs_in[i] : wq[g.r1];
   for (int ar = tid; ar < g.r1; ar += kWThreads) {
-    const float q = a.cq_in ? (float)a.cq_in[(int64_t)i * g.r1 + ar]
-                            : a.ws_q[(int64_t)i * (g.r1 + 1) + ar];
+    const float q = a.cq_in ? (float)a.cq_in[(int64_t)i * g.r1 + ar] : wq[ar];
     cqs[ar] = q * cs;
   }
   uint8_t* base = a.page + slot * a.slot_stride;
   if (h == 0) {
     for (int ar = tid; ar < g.r1; ar += kWThreads) {
-      const float q = a.cq_in ? (float)a.cq_in[(int64_t)i * g.r1 + ar]
-                              : a.ws_q[(int64_t)i * (g.r1 + 1) + ar];
+      const float q = a.cq_in ? (float)a.cq_in[(int64_t)i * g.r1 + ar] : wq[ar];
       base[ar] = (uint8_t)(int8_t)(int)q;
     }
     if (tid == 0) {
@@ -339,9 +341,10 @@ __global__ __launch_bounds__(kWThreads) void write_pack_kernel(WriteArgs a) {
 
 static float inv_ruler_f32(int bits) { return (float)(1.0 / (double)((1 << (bits - 1)) - 1)); }
 
+// Tokens per launch: one arrival counter each.
 int64_t write_workspace_bytes(const Geom& g, int num_tokens) {
-  const int64_t cnt = ((int64_t)std::max(num_tokens, 0) * 4 + 255) / 256 * 256;
-  return cnt + (int64_t)std::max(num_tokens, 0) * (g.H * g.r1 + g.r1 + 1) * 4;
+  const int64_t nt = std::min(std::max(num_tokens, 0), kMaxCounters);
+  return kCounterBytes + nt * (g.H * g.r1 + g.r1 + 1) * 4;
 }
 
 int write_paged(const Geom& g, const void* key, int k_dtype, int64_t k_row_stride, const void* val,
@@ -402,21 +405,25 @@ int write_paged(const Geom& g, const void* key, int k_dtype, int64_t k_row_strid
   a.c_out = c_out;
   a.r_out = r_out;
   a.err = err;
-  if (!cq_in) {
-    const int64_t cnt = ((int64_t)num_tokens * 4 + 255) / 256 * 256;
-    a.ws_cnt = (int*)ws;
-    a.ws_part = (float*)((char*)ws + cnt);
-    a.ws_q = a.ws_part + (int64_t)num_tokens * g.H * g.r1;
-  }
   a.inv127 = inv_ruler_f32(8);
   a.inv_rk = inv_ruler_f32(g.res_bits);
   a.inv_rv = inv_ruler_f32(g.v_bits);
-  const int grid = num_tokens * g.H;
-  if (!cq_in) hipLaunchKernelGGL(write_project_kernel, dim3(grid), dim3(kWThreads), 0, st, a);
-  if (g.res_bits == 3)
-    hipLaunchKernelGGL((write_pack_kernel<3, 3>), dim3(grid), dim3(kWThreads), 0, st, a);
-  else
-    hipLaunchKernelGGL((write_pack_kernel<4, 4>), dim3(grid), dim3(kWThreads), 0, st, a);
+  for (int t0 = 0; t0 < num_tokens; t0 += kMaxCounters) {
+    WriteArgs b = a;
+    b.tok0 = t0;
+    b.num_tokens = std::min(kMaxCounters, num_tokens - t0);
+    if (!cq_in) {
+      b.ws_cnt = (int*)ws;
+      b.ws_part = (float*)((char*)ws + kCounterBytes);
+      b.ws_q = b.ws_part + (int64_t)b.num_tokens * g.H * g.r1;
+    }
+    const int grid = b.num_tokens * g.H;
+    if (!cq_in) hipLaunchKernelGGL(write_project_kernel, dim3(grid), dim3(kWThreads), 0, st, b);
+    if (g.res_bits == 3)
+      hipLaunchKernelGGL((write_pack_kernel<3, 3>), dim3(grid), dim3(kWThreads), 0, st, b);
+    else
+      hipLaunchKernelGGL((write_pack_kernel<4, 4>), dim3(grid), dim3(kWThreads), 0, st, b);
+  }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return host_fail(TTKV_E_LAUNCH, std::string("write launch: ") +
                                                           hipGetErrorString(e));
