@@ -141,3 +141,77 @@ def test_forward_write_then_read_loop_and_mixed_batch():
     want_f = _sdpa_ref(q[qsl[2]:qsl[3]], k_post[qsl[2]:qsl[3]], seqs[2].V[0:300])
     _check(out[qsl[2]:qsl[3]], want_f, "mixed: first chunk rows")
     rope_store.clear_stores()
+
+
+def test_decode_steps_replayed_from_one_captured_graph(monkeypatch):
+    """A decode-only `forward` (K3 write, then one K1 launch) captured once in a HIP graph and
+    replayed for three steps, the inputs updated in place between replays (next token's q/k/v,
+    slot ids, lengths). Each replay matches the oracle over the cache bytes it wrote: the step
+    makes no host read-back and allocates nothing, and K1's work plan follows the new lengths on
+    the device. The graph is sized with max_seq_len above every length it will see."""
+    monkeypatch.delenv("VLLM_TTKV_CHECK", raising=False)
+    lay = layout_for_config(CONFIGS["safe"], 110)
+    olay = oracle_layout(CONFIGS["safe"], 110)
+    rope_store.clear_stores()
+    csc = cos_sin_cache(2048)
+    csc_d = csc.cuda()
+    seqs = [_Seq(900, 21), _Seq(600, 22)]
+    bt, nblk = synth.shuffled_block_table([900, 600], BS, seed=23, extra_blocks=2)
+    C = lay.compressed_bytes_per_token()
+    cache = torch.zeros(nblk, 1, BS, C // 2, dtype=torch.bfloat16, device="cuda")
+    im = TTKVAttentionImpl(HQ, D, SCALE, H)
+    layer = _Layer(NAME, lay)
+    _step(im, layer, cache, csc, bt, [(seqs[0], 0, 700), (seqs[1], 0, 400)])   # first chunks
+
+    dev = "cuda"
+    sq = torch.zeros(2, HQ, D, dtype=torch.float16, device=dev)
+    sk = torch.zeros(2, H * D, dtype=torch.float16, device=dev)
+    sv = torch.zeros(2, H * D, dtype=torch.float16, device=dev)
+    sraw = torch.zeros(2, H * D, dtype=torch.float32, device=dev)
+    out = torch.zeros(2, HQ, D, dtype=torch.float16, device=dev)
+    md = TTKVAttentionMetadata(
+        seq_lens=torch.zeros(2, dtype=torch.int32, device=dev),
+        slot_mapping=torch.zeros(2, dtype=torch.int64, device=dev),
+        block_table=bt[:2].to(dev), query_start_loc=torch.tensor([0, 1, 2], dtype=torch.int32,
+                                                                   device=dev),
+        query_start_loc_cpu=torch.tensor([0, 1, 2], dtype=torch.int32), num_actual_tokens=2,
+        max_query_len=1, max_seq_len=900)
+
+    def fill(t):
+        pos = [700 + t, 400 + t]
+        raw = torch.stack([seqs[r].K[p] for r, p in enumerate(pos)])            # [2, H, d]
+        c, s = cos_sin_from_cache(csc, torch.tensor(pos), D)
+        kp = rope_apply(raw, c.unsqueeze(1), s.unsqueeze(1))
+        sq.copy_(torch.stack([seqs[r].Q[p] for r, p in enumerate(pos)]).to(torch.float16))
+        sk.copy_(kp.reshape(2, H * D).to(torch.float16))
+        sv.copy_(torch.stack([seqs[r].V[p] for r, p in enumerate(pos)]).reshape(2, H * D)
+                 .to(torch.float16))
+        sraw.copy_(raw.reshape(2, H * D))
+        md.seq_lens.copy_(torch.tensor([p + 1 for p in pos], dtype=torch.int32))
+        md.slot_mapping.copy_(torch.stack([bt[r, p // BS].long() * BS + p % BS
+                                           for r, p in enumerate(pos)]))
+        return pos
+
+    # eager warm-up with the same static tensors (step 0), then capture
+    fill(0)
+    patch.stash_raw_k(NAME, sraw, cos_sin_cache=csc_d)
+    im.forward(layer, sq, sk, sv, cache, md, output=out)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    patch.stash_raw_k(NAME, sraw, cos_sin_cache=csc_d)
+    with torch.cuda.graph(graph):
+        im.forward(layer, sq, sk, sv, cache, md, output=out)
+    for t in range(3):
+        pos = fill(t)
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert int(im.error_word.item()) == 0
+        flat = cache.view(torch.uint8).reshape(-1, C).cpu()
+        st = rope_store.store_for_layer(NAME)
+        decs = [st.decoders[int(bt[r, 0])].decoder_f.cpu() for r in range(2)]
+        want = attend.paged_decode(olay, flat, bt[:2], torch.tensor([p + 1 for p in pos]),
+                                   torch.tensor([0, 1, 2]), sq.float().cpu(), decs, csc, BS,
+                                   SCALE, dtype=torch.float64)
+        _check(out.float().cpu(), want, f"graph replay {t}")
+    rope_store.clear_stores()
