@@ -267,6 +267,52 @@ def bench_dense(torch, lens, q, dev, steps=10, warmup=3):
     return res
 
 
+def bench_container(torch, dev, B=8, n=14402, r1=R1, steps=10, warmup=3):
+    """The container-layout reads (the codec's pooled container, not slots) at the headline shape:
+    B sequences of n tokens, safe rows (81 lanes at 3 bits). The container is synthetic and
+    structurally valid (every row has exactly k set lanes); timing does not depend on values."""
+    from vllm_ttkv import container
+    g = torch.Generator(device=dev).manual_seed(21)
+    k, bits, pb = 81, 3, (81 * 3 + 7) // 8
+    rows = B * H * n
+
+    def synth_rows():
+        bm = torch.empty(rows, 16, dtype=torch.uint8, device=dev)
+        w = (2 ** torch.arange(7, -1, -1, device=dev)).to(torch.int32)
+        for r0 in range(0, rows, 1 << 17):                       # bounded temporaries
+            r1_ = min(rows, r0 + (1 << 17))
+            idx = torch.rand(r1_ - r0, D, generator=g, device=dev).topk(k, dim=1).indices
+            mask = torch.zeros(r1_ - r0, D, dtype=torch.int32, device=dev).scatter_(1, idx, 1)
+            bm[r0:r1_] = (mask.view(-1, 16, 8) * w).sum(-1).to(torch.uint8)
+        pk = torch.randint(0, 256, (rows, pb), generator=g, device=dev, dtype=torch.uint8)
+        sc = torch.rand(rows, generator=g, device=dev) * 0.01
+        return container.PackedRows(bm, pk, sc, bits)
+
+    cq = torch.randint(-127, 128, (B * n, r1), generator=g, device=dev, dtype=torch.int8)
+    cs = torch.rand(B * n, generator=g, device=dev) * 0.01
+    dq = torch.randint(-127, 128, (B, r1, H * D), generator=g, device=dev, dtype=torch.int8)
+    ds = torch.rand(B, r1, generator=g, device=dev) * 0.01
+    kr, vr = synth_rows(), synth_rows()
+    from vllm_ttkv import rope
+    csc = rope.cos_sin_cache(n, D, device=dev)
+    cos = torch.cat([csc[:, :D // 2]] * 2, -1).contiguous()
+    sin = torch.cat([csc[:, D // 2:]] * 2, -1).contiguous()
+    q = torch.randn(B, HQ, D, generator=g, device=dev)
+    p = torch.softmax(torch.randn(B, HQ, n, generator=g, device=dev), -1)
+    ms_k = time_launches(torch, lambda: container.krt(cq, cs, dq, ds, kr, cos, sin, q, n, HQ,
+                                                      HQ // H, D), steps, warmup)
+    ms_v = time_launches(torch, lambda: container.v_out(p, vr, n, HQ, HQ // H, D), steps, warmup)
+    # algorithmic bytes: each array once (decoder as fp32 after the launcher's conversion)
+    kb = (B * n * (r1 + 4) + rows * (16 + pb + 4) + B * r1 * H * D * 4 + 2 * n * D * 4
+          + B * HQ * D * 4 + B * HQ * n * 4)
+    vb = rows * (16 + pb + 4) + B * HQ * n * 4 + B * HQ * D * 4
+    log(f"container krt B={B}x{n}: {ms_k * 1e3:.1f} us ({kb / (ms_k * 1e-3) / 1e9:.0f} GB/s); "
+        f"v_out {ms_v * 1e3:.1f} us ({vb / (ms_v * 1e-3) / 1e9:.0f} GB/s)")
+    return dict(B=B, n=n, r1=r1, krt_us=ms_k * 1e3, krt_bytes=kb,
+                krt_gbps=kb / (ms_k * 1e-3) / 1e9, v_out_us=ms_v * 1e3, v_out_bytes=vb,
+                v_out_gbps=vb / (ms_v * 1e-3) / 1e9)
+
+
 def bench_config5(torch, cache, dev, steps=10, warmup=3, n_layers=L_LAYERS):
     """the reference's 4-bit store (`campaign4x`: 64 lanes of 4-bit codes for
     K residual and V, int8 coefficients, fp16 rulers), 8 requests at 16k context, 28 layers. Each
@@ -402,6 +448,8 @@ def main():
                     help="only the 4-bit read+write workload (BASELINE config 5); prints its line")
     ap.add_argument("--config4-only", action="store_true",
                     help="only the continuation workload (BASELINE config 4, K2); prints its line")
+    ap.add_argument("--container-only", action="store_true",
+                    help="only the container-layout reads (krt + v_out at 8 x 14402); prints its line")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 1 GiB device copy (HBM-counter calibration for rocprofv3)")
     args = ap.parse_args()
@@ -427,6 +475,13 @@ def main():
                               value=c4["us_per_chunk_layer"], unit="us", n_gpus=1,
                               higher_is_better=False, dtype="f16 MFMA, fp32 accumulate",
                               data="synthetic", **c4)))
+        return
+
+    if args.container_only:
+        cr = bench_container(torch, dev, steps=args.steps, warmup=args.warmup)
+        print(json.dumps(dict(metric="container-layout reads us/launch (krt + v_out, 8 x 14402)",
+                              value=cr["krt_us"] + cr["v_out_us"], unit="us", n_gpus=1,
+                              higher_is_better=False, dtype="f32", data="synthetic", **cr)))
         return
 
     if args.config5_only:
@@ -495,6 +550,7 @@ def main():
             f"{dh['hbm_gbps']:.0f} GB/s")
         extra["config4_continuation"] = bench_config4(torch, lay, cfg, cache, dev)
         extra["config5_4bit_read_write"] = bench_config5(torch, cache, dev)
+        extra["container_reads_b8_ctx14402"] = bench_container(torch, dev)
 
     cpu = None
     if not args.no_cpu:

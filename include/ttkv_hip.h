@@ -200,6 +200,38 @@ int ttkv_dense_decode_paged(int32_t H, int32_t num_heads, int32_t d, float scale
                             int32_t max_seq_len, void* out, int64_t out_row_stride,
                             void* workspace, int64_t workspace_bytes, ttkv_stream_t stream);
 
+/* Container-layout reads (the codec's pooled container, not slots): drop-ins for the codec's
+ * fused container kernels `ttkv_krt` and `ttkv_v_out` (codec/ttkv_kernels.cu:208-277, 338-513),
+ * as launched by codec/ttkv_cuda.py:169-257 (`krt`) and :144-166 (`v_out`).
+ *
+ * Container of B equal-length sequences of n tokens (codec/ttkv_packed_cache.py:337-385):
+ *   coeff_q [B*n, r1] int8 and coeff_scale [B*n] fp32 (row b*n + i);
+ *   decoder_f fp32 = dec_q * dec_scale, [r1, H*d] shared by the batch (decoder_per_seq = 0) or
+ *     [B, r1, H*d] (decoder_per_seq = 1);
+ *   rows (K residual or V): bitmap [B*H*n, d/8] u8 (16-byte aligned), packed [B*H*n, PB] u8
+ *     (MSB-first codes of the set lanes in lane order), scale [B*H*n] fp32, row b*H*n + h*n + i.
+ *
+ * ttkv_container_krt: scores [B, num_heads, n] fp32, UNSCALED,
+ *   s[b, p, i] = q[b, p] . RoPE_i((cq[i] * cs[i]) @ decoder_f[:, h*d:(h+1)*d] + resid[h, i]),
+ *   h = p / (num_heads / H); cos / sin [n, d] fp32 in rope_apply's frame (absolute position i);
+ *   query [B, num_heads, d] fp32 post-RoPE. res_bitmap = NULL: no residual (mode without rows).
+ *   Carried at fp32 accuracy (hi + lo fp16 MFMA operands).
+ * ttkv_container_v_out: out [B, num_heads, d] fp32 += sum_i p[b, p, i] * V[b, h, i, :];
+ *   p[b, p, i] at p + b*p_batch_stride + p*p_head_stride + i. `out` must be zero-filled: the
+ *   launch accumulates tile partials with atomic adds (the codec kernel's contract).
+ * Built for d = 128, r1 <= 160, 3- or 4-bit rows of <= 48 packed bytes, num_heads / H in
+ * {1, 2, 3, 4, 8}. */
+int ttkv_container_krt(int32_t H, int32_t num_heads, int32_t d, int32_t B, int32_t n, int32_t r1,
+                       const int8_t* coeff_q, const float* coeff_scale, const float* decoder_f,
+                       int32_t decoder_per_seq, const uint8_t* res_bitmap,
+                       const uint8_t* res_packed, const float* res_scale, int32_t res_pb,
+                       int32_t res_bits, const float* cos, const float* sin, const float* query,
+                       float* scores, ttkv_stream_t stream);
+int ttkv_container_v_out(int32_t H, int32_t num_heads, int32_t d, int32_t B, int32_t n,
+                         const float* p, int64_t p_head_stride, int64_t p_batch_stride,
+                         const uint8_t* v_bitmap, const uint8_t* v_packed, const float* v_scale,
+                         int32_t v_pb, int32_t v_bits, float* out, ttkv_stream_t stream);
+
 /* Message for the last nonzero return on this thread. */
 const char* ttkv_last_error(void);
 

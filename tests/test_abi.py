@@ -149,3 +149,39 @@ def test_write_host_refusals_before_launch():
     assert _write_call(safe, v_dtype=5) == 1 and b"dtype" in L.ttkv_last_error()
     assert _write_call(safe, ws=0) == 4 and b"workspace" in L.ttkv_last_error()
     assert _write_call(safe, num_tokens=0) == 0                          # nothing to do
+
+
+def test_container_host_refusals_before_launch():
+    """The container reads' host refusals: geometry they are not built for, missing arrays and
+    weight strides smaller than [B, HQ, n]. Dummy pointers only: nothing is launched."""
+    L = _hip.lib()
+
+    def krt(**kw):
+        a = dict(H=8, HQ=24, d=128, B=1, n=64, r1=110, cq=16, cs=16, dec=16, per=0, bm=16,
+                 pk=16, rs=16, pb=31, bits=3, cos=16, sin=16, q=16, s=16)
+        a.update(kw)
+        return L.ttkv_container_krt(a["H"], a["HQ"], a["d"], a["B"], a["n"], a["r1"], a["cq"],
+                                    a["cs"], a["dec"], a["per"], a["bm"], a["pk"], a["rs"],
+                                    a["pb"], a["bits"], a["cos"], a["sin"], a["q"], a["s"], None)
+
+    def vout(**kw):
+        a = dict(H=8, HQ=24, d=128, B=1, n=64, p=16, ph=64, pbs=24 * 64, bm=16, pk=16, rs=16,
+                 pb=31, bits=3, o=16)
+        a.update(kw)
+        return L.ttkv_container_v_out(a["H"], a["HQ"], a["d"], a["B"], a["n"], a["p"], a["ph"],
+                                      a["pbs"], a["bm"], a["pk"], a["rs"], a["pb"], a["bits"],
+                                      a["o"], None)
+
+    assert krt(d=64) == 2 and b"head dim" in L.ttkv_last_error()
+    assert krt(HQ=20) == 1
+    assert krt(r1=161) == 2 and b"r1" in L.ttkv_last_error()
+    assert krt(pb=49) == 2 and b"packed row" in L.ttkv_last_error()
+    assert krt(bits=5) == 2
+    assert krt(q=0) == 1 and b"null" in L.ttkv_last_error()
+    assert krt(pk=0) == 1 and b"residual" in L.ttkv_last_error()
+    assert krt(cos=8) == 1 and b"aligned" in L.ttkv_last_error()
+    assert krt(HQ=40, H=8) == 2                                    # 5 heads per KV head
+    assert krt(n=0) == 0                                           # nothing to do
+    assert vout(ph=63) == 1 and b"strides" in L.ttkv_last_error()
+    assert vout(o=0) == 1
+    assert vout(bits=2) == 2

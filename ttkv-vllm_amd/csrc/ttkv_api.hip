@@ -167,4 +167,23 @@ int ttkv_dense_decode_paged(int32_t H, int32_t num_heads, int32_t d, float scale
                             workspace, workspace_bytes, (hipStream_t)stream);
 }
 
+int ttkv_container_krt(int32_t H, int32_t num_heads, int32_t d, int32_t B, int32_t n, int32_t r1,
+                       const int8_t* coeff_q, const float* coeff_scale, const float* decoder_f,
+                       int32_t decoder_per_seq, const uint8_t* res_bitmap,
+                       const uint8_t* res_packed, const float* res_scale, int32_t res_pb,
+                       int32_t res_bits, const float* cos, const float* sin, const float* query,
+                       float* scores, ttkv_stream_t stream) {
+  return container_krt(H, num_heads, d, B, n, r1, coeff_q, coeff_scale, decoder_f,
+                       decoder_per_seq, res_bitmap, res_packed, res_scale, res_pb, res_bits, cos,
+                       sin, query, scores, (hipStream_t)stream);
+}
+
+int ttkv_container_v_out(int32_t H, int32_t num_heads, int32_t d, int32_t B, int32_t n,
+                         const float* p, int64_t p_head_stride, int64_t p_batch_stride,
+                         const uint8_t* v_bitmap, const uint8_t* v_packed, const float* v_scale,
+                         int32_t v_pb, int32_t v_bits, float* out, ttkv_stream_t stream) {
+  return container_v_out(H, num_heads, d, B, n, p, p_head_stride, p_batch_stride, v_bitmap,
+                         v_packed, v_scale, v_pb, v_bits, out, (hipStream_t)stream);
+}
+
 }  // extern "C"

@@ -1,0 +1,471 @@
+// Reads of the codec's pooled CONTAINER layout (not slots): the drop-in for the codec's fused
+// container kernels `ttkv_krt` and `ttkv_v_out` (codec/ttkv_kernels.cu; launched by
+// codec/ttkv_cuda.py:144-257). gfx950 / CDNA4.
+//
+// Container (codec/ttkv_packed_cache.py:337-385, pooled over B sequences of n tokens each):
+//   coefficients  coeff_q [B*n, r1] int8, coeff_scale [B*n]           row = b*n + i
+//   decoder       decoder_f [r1, H*d] fp32 (shared) or [B, r1, H*d]    = dec_q * dec_scale
+//   residual rows bitmap [B*H*n, d/8], packed [B*H*n, PB], scale [B*H*n]  row = b*H*n + h*n + i
+//   V rows        the same three arrays for V.
+// Semantics (vllm_ttkv/reference.py:47-109, per row its own absolute position i):
+//   krt   : s[b, p, i] = q[b, p] . RoPE_i( (cq[i] * cs[i]) @ decoder_f[:, h(p)*d:(h(p)+1)*d]
+//                                          + residual[h(p), i] )            (unscaled, fp32)
+//   v_out : o[b, p, :] = sum_i p[b, p, i] * V[b, h(p), i, :]
+//
+// Both reuse the decode read's machinery. A 256-thread workgroup walks a run of token tiles of one
+// (KV head, sequence), building its decode tables and register fragments once. krt (64-token
+// tiles): coefficients become exact fp16 MFMA B-fragments in LDS, the residual rows are staged
+// big-endian and table-decoded (as the slot read does), the decoder is split hi + lo into resident
+// A-fragments, and the rotated key is split hi + lo against a hi + lo query, so every score is the
+// fp32 dot product up to fp32 rounding. v_out (128-token tiles): decodes its V rows, accumulates
+// in registers and adds its partial sums into `out` with fp32 atomic adds, as the codec kernel
+// does (its caller zero-fills `out`).
+#include <math.h>
+
+#include "ttkv_device.h"
+
+namespace ttkv {
+
+constexpr int kCTile = 64;       // tokens per krt tile
+constexpr int kCVTile = 128;     // tokens per v_out tile
+constexpr int kCThreads = 256;
+constexpr int kCRawDw = 17;      // staged row: bitmap (4 dwords) + code stream (<= 12) + slack
+constexpr int kCCode = 144;      // bytes per decoded code row
+
+struct ContainerArgs {
+  int n, r1, H, G, B, PB, dec_per_seq, has_res;
+  int tiles_per_wg;  // consecutive token tiles one workgroup walks
+  const int8_t* cq;
+  const float* cs;
+  const float* dec;
+  const uint8_t* bm;
+  const uint8_t* pk;
+  const float* rs;
+  const float* cosv;
+  const float* sinv;
+  const float* q;
+  float* s;
+  const float* p;
+  int64_t p_head_stride, p_batch_stride;
+  float* o;
+};
+
+// Stage source dwords [c0, c0 + 4] of a byte row at `src` (any alignment, `len` valid bytes) as 4
+// realigned dwords, byte-reversed when `reverse` (big-endian code words). Reads stay inside the
+// row's dwords (the bytes past `len` are never decoded).
+__device__ __forceinline__ void stage4(const uint8_t* src, int len, int c0, bool reverse,
+                                       uint32_t out[4]) {
+  const uintptr_t A = (uintptr_t)src;
+  const uint32_t* w = (const uint32_t*)(A & ~(uintptr_t)3);
+  const int sh = (int)(A & 3);
+  const int nsrc = (sh + len + 3) >> 2;
+  const uint32_t sel = stage_selector(sh, reverse);
+  uint32_t x[5];
+#pragma unroll
+  for (int i = 0; i < 5; ++i) x[i] = w[min(c0 + i, nsrc - 1)];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) out[i] = __builtin_amdgcn_perm(x[i + 1], x[i], sel);
+}
+
+// One token's residual / V row into the staged LDS format the table decoder reads: dwords 0..3
+// the bitmap as stored, dwords 4.. the code stream with each dword byte-reversed. `part` 0..3 of
+// the token's four stager threads writes dwords 4*part .. 4*part+3 (part 0: the bitmap).
+__device__ __forceinline__ void stage_row4(const ContainerArgs& a, int64_t row, bool valid,
+                                           int part, uint32_t* dst) {
+  uint32_t v[4] = {0u, 0u, 0u, 0u};
+  if (valid) {
+    if (part == 0) {
+      const uint4 b = *(const uint4*)(a.bm + row * kBitmapBytes);
+      v[0] = b.x;
+      v[1] = b.y;
+      v[2] = b.z;
+      v[3] = b.w;
+    } else {
+      stage4(a.pk + row * a.PB, a.PB, 4 * (part - 1), true, v);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) dst[4 * part + i] = v[i];
+  if (part == 3) dst[16] = 0u;
+}
+
+template <int KS>
+struct KrtSmem {
+  _Float16 coef[kCTile][KS * 32 + 8];
+  uint32_t raw[kCTile][kCRawDw];
+  uint8_t code[kCTile][kCCode];
+  float spart[4][kCTile][8];
+  uint2 lut[256];
+  uint32_t lut3[4096];
+  float cs[kCTile], kr[kCTile];
+};
+
+// ---------------------------------------------------------------------------- krt
+template <int G, int BITS, int KS>
+__global__ __launch_bounds__(kCThreads, 2) void container_krt_kernel(ContainerArgs a) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  KrtSmem<KS>& S = *reinterpret_cast<KrtSmem<KS>*>(smem_raw);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = tid >> 6;
+  const int n = lane & 15;
+  const int gq = lane >> 4;
+  const int dl = 16 * wv + 4 * gq;
+  const int hv = blockIdx.y;
+  const int bz = blockIdx.z;
+  const int HD = a.H * kD;
+  const int ntiles = (a.n + kCTile - 1) / kCTile;
+  const int tile0 = blockIdx.x * a.tiles_per_wg;
+  const int tile1 = min(ntiles, tile0 + a.tiles_per_wg);
+  if (tile0 >= tile1) return;
+
+  build_luts(S.lut, BITS == 3 ? S.lut3 : nullptr, tid, kCThreads);
+  // ---- decoder fragments (A operand, M = dims, K = r1), hi + lo fp16, resident in registers
+  const float* dec = a.dec + (a.dec_per_seq ? (int64_t)bz * a.r1 * HD : 0) + (int64_t)hv * kD;
+  half8 ahi[2][KS], alo[2][KS];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi) {
+    const int dim = 16 * (wv + 4 * mi) + n;
+#pragma unroll
+    for (int st = 0; st < KS; ++st)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int ar = 32 * st + 8 * gq + j;
+        const float f = ar < a.r1 ? dec[(int64_t)ar * HD + dim] : 0.f;
+        const _Float16 hi = (_Float16)f;
+        ahi[mi][st][j] = hi;
+        alo[mi][st][j] = (_Float16)(f - (float)hi);
+      }
+  }
+  // ---- query fragments (A operand of q.k, M = heads, K = this wave's 32 dims in the order of
+  // the rotated-key fragments), hi + lo fp16; rows >= G are zero
+  half8 qhi, qlo;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int dim = j < 4 ? dl + j : 64 + dl + j - 4;
+    const float x = n < G ? a.q[((int64_t)bz * a.H * G + hv * G + n) * kD + dim] : 0.f;
+    const _Float16 hi = (_Float16)x;
+    qhi[j] = hi;
+    qlo[j] = (_Float16)(x - (float)hi);
+  }
+
+  for (int tile = tile0; tile < tile1; ++tile) {
+    const int i0 = tile * kCTile;
+    // ---- stage: coefficients (exact fp16), coefficient ruler, residual row
+    const int ptok = tid >> 2, part = tid & 3;
+    const bool tvalid = i0 + ptok < a.n;
+    {
+      const int64_t crow = (int64_t)bz * a.n + i0 + ptok;
+      uint32_t* cdst = (uint32_t*)&S.coef[ptok][part * (8 * KS)];
+      // this part's 8*KS coefficient bytes: source dwords 2*KS*part .. in groups of 4
+#pragma unroll
+      for (int g4 = 0; g4 < KS; g4 += 2) {
+        uint32_t v[4] = {0u, 0u, 0u, 0u};
+        if (tvalid) stage4((const uint8_t*)(a.cq + crow * a.r1), a.r1, 2 * KS * part + 2 * g4, false, v);
+        const int nd = KS - g4 >= 2 ? 4 : 2;  // dwords of this group that belong to the part
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (i < nd) {
+            uint32_t p01, p23;
+            i8x4_to_f16(v[i], p01, p23);
+            cdst[2 * (2 * g4 + i)] = p01;
+            cdst[2 * (2 * g4 + i) + 1] = p23;
+          }
+        }
+      }
+      const int64_t rrow = ((int64_t)bz * a.H + hv) * a.n + i0 + ptok;
+      stage_row4(a, rrow, tvalid && a.has_res, part, S.raw[ptok]);
+      if (part == 0) {
+        S.cs[ptok] = tvalid ? a.cs[crow] : 0.f;
+        // 3-bit codes decode as fp8 (c - 4) * unit: the ruler takes the 1 / unit
+        const float unit = __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0];
+        S.kr[ptok] = tvalid && a.has_res ? a.rs[rrow] * (BITS == 3 ? 1.0f / unit : 1.0f) : 0.f;
+      }
+    }
+    __syncthreads();
+
+    // ---- decode the residual rows (threads 0..127: token tid/2, half tid&1)
+    if (tid < 2 * kCTile) {
+      const int tok = tid >> 1, half = tid & 1;
+      decode_half_row_be<BITS>(S.raw[tok], half, S.lut, S.lut3, &S.code[tok][64 * half]);
+    }
+    __syncthreads();
+
+    // ---- reconstruct + residual + RoPE + scores, 16 tokens at a time
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      const int tok = 16 * nb + n;
+      const int pos = min(i0 + tok, a.n - 1);
+      float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < KS; ++st) {
+        const half8 b = *(const half8*)&S.coef[tok][32 * st + 8 * gq];
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[0][st], b, acc0, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[0][st], b, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[1][st], b, acc1, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[1][st], b, acc1, 0, 0, 0);
+      }
+      const float cs = S.cs[tok], kr = S.kr[tok];
+      const float kb = BITS == 4 ? -8.f * kr : 0.f;  // 4-bit codes arrive as c
+      float vl[4], vh[4];
+      codes4<BITS>(*(const uint32_t*)&S.code[tok][dl], vl);
+      codes4<BITS>(*(const uint32_t*)&S.code[tok][64 + dl], vh);
+      const float4v cl = *(const float4v*)&a.cosv[(int64_t)pos * kD + dl];
+      const float4v ch = *(const float4v*)&a.cosv[(int64_t)pos * kD + 64 + dl];
+      const float4v sl = *(const float4v*)&a.sinv[(int64_t)pos * kD + dl];
+      const float4v sh = *(const float4v*)&a.sinv[(int64_t)pos * kD + 64 + dl];
+      float y[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float xl = fmaf(cs, acc0[i], fmaf(kr, vl[i], kb));
+        const float xh = fmaf(cs, acc1[i], fmaf(kr, vh[i], kb));
+        y[i] = xl * cl[i] - xh * sl[i];
+        y[4 + i] = xh * ch[i] + xl * sh[i];
+      }
+      half8 yhi, ylo;
+      split8(y, yhi, ylo);
+      float4v sacc = {0.f, 0.f, 0.f, 0.f};
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qhi, yhi, sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qhi, ylo, sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qlo, yhi, sacc, 0, 0, 0);
+      // lane (n, gq) holds heads 4*gq .. 4*gq+3 of token n, over this wave's 32 dims
+      if (4 * gq < G) *(float4v*)&S.spart[wv][tok][4 * gq] = sacc;
+    }
+    __syncthreads();
+    for (int idx = tid; idx < G * kCTile; idx += kCThreads) {
+      const int tok = idx & (kCTile - 1), p = idx / kCTile;
+      if (i0 + tok < a.n) {
+        const float v = (S.spart[0][tok][p] + S.spart[1][tok][p]) + (S.spart[2][tok][p] + S.spart[3][tok][p]);
+        a.s[((int64_t)bz * a.H * G + hv * G + p) * a.n + i0 + tok] = v;
+      }
+    }
+    __syncthreads();  // the next tile overwrites the staged rows, codes and partial scores
+  }
+}
+
+// ---------------------------------------------------------------------------- v_out
+struct VoutSmem {
+  uint32_t raw[kCVTile][kCRawDw];
+  uint8_t code[kCVTile][kCCode];
+  float pw[8][kCVTile];
+  float vr[kCVTile];
+  float part[8][kD];
+  uint2 lut[256];
+  uint32_t lut3[4096];
+};
+
+template <int G, int BITS>
+__global__ __launch_bounds__(kCThreads) void container_v_out_kernel(ContainerArgs a) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  VoutSmem& S = *reinterpret_cast<VoutSmem*>(smem_raw);
+  const int tid = threadIdx.x;
+  const int hv = blockIdx.y;
+  const int bz = blockIdx.z;
+  const int ntiles = (a.n + kCVTile - 1) / kCVTile;
+  const int tile0 = blockIdx.x * a.tiles_per_wg;
+  const int tile1 = min(ntiles, tile0 + a.tiles_per_wg);
+  if (tile0 >= tile1) return;
+  build_luts(S.lut, BITS == 3 ? S.lut3 : nullptr, tid, kCThreads);
+  const int dim = tid & (kD - 1), par = tid >> 7;
+  float acc[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) acc[g] = 0.f;
+
+  for (int tile = tile0; tile < tile1; ++tile) {
+    const int i0 = tile * kCVTile;
+    // ---- stage the tile's V rows (4 threads per token, two passes), rulers and weights
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+      const int tok = (tid >> 2) + 64 * pass, part = tid & 3;
+      const bool valid = i0 + tok < a.n;
+      const int64_t row = ((int64_t)bz * a.H + hv) * a.n + i0 + tok;
+      stage_row4(a, row, valid, part, S.raw[tok]);
+      if (part == 0) {
+        const float unit = __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0];
+        S.vr[tok] = valid ? a.rs[row] * (BITS == 3 ? 1.0f / unit : 1.0f) : 0.f;
+      }
+    }
+    for (int idx = tid; idx < G * kCVTile; idx += kCThreads) {
+      const int tok = idx & (kCVTile - 1), g = idx / kCVTile;
+      S.pw[g][tok] = i0 + tok < a.n
+                         ? a.p[(int64_t)bz * a.p_batch_stride + (int64_t)(hv * G + g) * a.p_head_stride + i0 + tok]
+                         : 0.f;
+    }
+    __syncthreads();
+    // ---- decode (thread = token tid/2, half tid&1)
+    decode_half_row_be<BITS>(S.raw[tid >> 1], tid & 1, S.lut, S.lut3, &S.code[tid >> 1][64 * (tid & 1)]);
+    __syncthreads();
+    // ---- o[g][dim] over this tile: thread = (dim, token parity)
+    for (int tok = par; tok < kCVTile; tok += 2) {
+      const uint32_t c = S.code[tok][dim];
+      float v;
+      if constexpr (BITS == 3) v = __builtin_amdgcn_cvt_f32_fp8((int)c, 0);
+      else v = (float)c - 8.f;
+      const float w = v * S.vr[tok];
+#pragma unroll
+      for (int g = 0; g < G; ++g) acc[g] = fmaf(S.pw[g][tok], w, acc[g]);
+    }
+    __syncthreads();  // the next tile overwrites the staged rows, codes and weights
+  }
+  if (par == 1) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) S.part[g][dim] = acc[g];
+  }
+  __syncthreads();
+  if (par == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+      atomicAdd(&a.o[((int64_t)bz * a.H * G + hv * G + g) * kD + dim], acc[g] + S.part[g][dim]);
+  }
+}
+
+}  // namespace ttkv
+
+// ------------------------------------------------------------------------------------ host side
+#include "ttkv_host.h"
+
+namespace ttkv {
+
+// Token tiles per workgroup: about one round of two resident workgroups per CU over the
+// (sequence, head) pairs, so each workgroup builds its tables and decoder fragments once.
+static int tiles_per_wg(int ntiles, int pairs) {
+  const int target = 2 * device_cu_count();
+  const int per_pair = std::max(1, target / std::max(pairs, 1));
+  return std::max(1, (ntiles + per_pair - 1) / per_pair);
+}
+
+template <typename K>
+static int launch_with_smem(K kfn, size_t smem, dim3 grid, hipStream_t st, const ContainerArgs& a,
+                            const char* what) {
+  if (hipFuncSetAttribute((const void*)kfn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)smem) != hipSuccess)
+    return host_fail(TTKV_E_LAUNCH, std::string(what) + ": hipFuncSetAttribute failed");
+  hipLaunchKernelGGL(kfn, grid, dim3(kCThreads), smem, st, a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return host_fail(TTKV_E_LAUNCH, std::string(what) + ": " + hipGetErrorString(e));
+  return TTKV_OK;
+}
+
+template <int G, int BITS>
+static int krt_ks(const ContainerArgs& a, int ks, dim3 grid, hipStream_t st) {
+  switch (ks) {
+    case 1: return launch_with_smem(container_krt_kernel<G, BITS, 1>, sizeof(KrtSmem<1>), grid, st, a, "container krt");
+    case 2: return launch_with_smem(container_krt_kernel<G, BITS, 2>, sizeof(KrtSmem<2>), grid, st, a, "container krt");
+    case 3: return launch_with_smem(container_krt_kernel<G, BITS, 3>, sizeof(KrtSmem<3>), grid, st, a, "container krt");
+    case 4: return launch_with_smem(container_krt_kernel<G, BITS, 4>, sizeof(KrtSmem<4>), grid, st, a, "container krt");
+    case 5: return launch_with_smem(container_krt_kernel<G, BITS, 5>, sizeof(KrtSmem<5>), grid, st, a, "container krt");
+  }
+  return host_fail(TTKV_E_UNSUPPORTED, "r1 > 160 is not built");
+}
+
+template <int BITS>
+static int krt_g(const ContainerArgs& a, int ks, dim3 grid, hipStream_t st) {
+  switch (a.G) {
+    case 1: return krt_ks<1, BITS>(a, ks, grid, st);
+    case 2: return krt_ks<2, BITS>(a, ks, grid, st);
+    case 3: return krt_ks<3, BITS>(a, ks, grid, st);
+    case 4: return krt_ks<4, BITS>(a, ks, grid, st);
+    case 8: return krt_ks<8, BITS>(a, ks, grid, st);
+  }
+  return host_fail(TTKV_E_UNSUPPORTED, "num_heads / H = " + std::to_string(a.G) +
+                                           " query heads per KV head is not built (1,2,3,4,8)");
+}
+
+static int container_common(int H, int HQ, int d, int B, int n, int pb, int bits, bool need_rows,
+                            int& G) {
+  if (d != kD) return host_fail(TTKV_E_UNSUPPORTED, "head dim must be 128");
+  if (H <= 0 || HQ <= 0 || HQ % H) return host_fail(TTKV_E_INVALID, "num_heads is not a multiple of H");
+  G = HQ / H;
+  if (B < 0 || n < 0) return host_fail(TTKV_E_INVALID, "negative size");
+  if (need_rows) {
+    if (bits != 3 && bits != 4) return host_fail(TTKV_E_UNSUPPORTED, "row code width must be 3 or 4 bits");
+    if (pb <= 0 || pb > 48)
+      return host_fail(TTKV_E_UNSUPPORTED, "packed row bytes must be in 1..48 (<= 96 lanes at 4 bits)");
+  }
+  return TTKV_OK;
+}
+
+int container_krt(int H, int HQ, int d, int B, int n, int r1, const int8_t* cq, const float* cs,
+                  const float* dec, int dec_per_seq, const uint8_t* bm, const uint8_t* pk,
+                  const float* rs, int pb, int bits, const float* cosv, const float* sinv,
+                  const float* q, float* s, hipStream_t st) {
+  const bool has_res = bm != nullptr;
+  int G = 0;
+  if (int rc = container_common(H, HQ, d, B, n, pb, has_res ? bits : 3, has_res, G)) return rc;
+  if (r1 <= 0) return host_fail(TTKV_E_INVALID, "r1 must be positive");
+  const int ks = (r1 + 31) / 32;
+  if (ks > 5) return host_fail(TTKV_E_UNSUPPORTED, "r1 > 160 is not built");
+  if (!cq || !cs || !dec || !cosv || !sinv || !q || !s)
+    return host_fail(TTKV_E_INVALID, "null pointer argument");
+  if (has_res && (!pk || !rs)) return host_fail(TTKV_E_INVALID, "residual arrays incomplete");
+  if (((uintptr_t)cosv | (uintptr_t)sinv | (uintptr_t)bm) % 16)
+    return host_fail(TTKV_E_INVALID, "cos / sin / bitmap must be 16-byte aligned");
+  if (B == 0 || n == 0) return TTKV_OK;
+  ContainerArgs a{};
+  a.n = n;
+  a.r1 = r1;
+  a.H = H;
+  a.G = G;
+  a.B = B;
+  a.PB = pb;
+  a.dec_per_seq = dec_per_seq;
+  a.has_res = has_res;
+  a.cq = cq;
+  a.cs = cs;
+  a.dec = dec;
+  a.bm = bm;
+  a.pk = pk;
+  a.rs = rs;
+  a.cosv = cosv;
+  a.sinv = sinv;
+  a.q = q;
+  a.s = s;
+  a.tiles_per_wg = tiles_per_wg((n + kCTile - 1) / kCTile, H * B);
+  const dim3 grid(((n + kCTile - 1) / kCTile + a.tiles_per_wg - 1) / a.tiles_per_wg, H, B);
+  // without residual rows the staged bitmaps are zero and the 3-bit decode contributes 0
+  return (has_res && bits == 4) ? krt_g<4>(a, ks, grid, st) : krt_g<3>(a, ks, grid, st);
+}
+
+template <int BITS>
+static int vout_g(const ContainerArgs& a, dim3 grid, hipStream_t st) {
+  switch (a.G) {
+    case 1: return launch_with_smem(container_v_out_kernel<1, BITS>, sizeof(VoutSmem), grid, st, a, "container v_out");
+    case 2: return launch_with_smem(container_v_out_kernel<2, BITS>, sizeof(VoutSmem), grid, st, a, "container v_out");
+    case 3: return launch_with_smem(container_v_out_kernel<3, BITS>, sizeof(VoutSmem), grid, st, a, "container v_out");
+    case 4: return launch_with_smem(container_v_out_kernel<4, BITS>, sizeof(VoutSmem), grid, st, a, "container v_out");
+    case 8: return launch_with_smem(container_v_out_kernel<8, BITS>, sizeof(VoutSmem), grid, st, a, "container v_out");
+  }
+  return host_fail(TTKV_E_UNSUPPORTED, "num_heads / H = " + std::to_string(a.G) +
+                                           " query heads per KV head is not built (1,2,3,4,8)");
+}
+
+int container_v_out(int H, int HQ, int d, int B, int n, const float* p, int64_t p_head_stride,
+                    int64_t p_batch_stride, const uint8_t* bm, const uint8_t* pk, const float* rs,
+                    int pb, int bits, float* o, hipStream_t st) {
+  int G = 0;
+  if (int rc = container_common(H, HQ, d, B, n, pb, bits, true, G)) return rc;
+  if (!p || !bm || !pk || !rs || !o) return host_fail(TTKV_E_INVALID, "null pointer argument");
+  if ((uintptr_t)bm % 16) return host_fail(TTKV_E_INVALID, "bitmap must be 16-byte aligned");
+  if (p_head_stride < n || p_batch_stride < (int64_t)HQ * p_head_stride)
+    return host_fail(TTKV_E_INVALID, "p strides are smaller than its [B, HQ, n] extent");
+  if (B == 0 || n == 0) return TTKV_OK;
+  ContainerArgs a{};
+  a.n = n;
+  a.H = H;
+  a.G = G;
+  a.B = B;
+  a.PB = pb;
+  a.bm = bm;
+  a.pk = pk;
+  a.rs = rs;
+  a.p = p;
+  a.p_head_stride = p_head_stride;
+  a.p_batch_stride = p_batch_stride;
+  a.o = o;
+  a.tiles_per_wg = tiles_per_wg((n + kCVTile - 1) / kCVTile, H * B);
+  const dim3 grid(((n + kCVTile - 1) / kCVTile + a.tiles_per_wg - 1) / a.tiles_per_wg, H, B);
+  return bits == 4 ? vout_g<4>(a, grid, st) : vout_g<3>(a, grid, st);
+}
+
+}  // namespace ttkv

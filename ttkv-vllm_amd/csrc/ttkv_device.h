@@ -184,6 +184,36 @@ __device__ __forceinline__ void bcast_rows(float v, float out[4]) {
 }
 
 
+// y - h for h the low / high fp16 half of a packed pair, in one v_fma_mix_f32 (the fp16 operand is
+// widened exactly; the difference of a value and its fp16 truncation is exact in fp32).
+__device__ __forceinline__ float minus_lo16(float y, half2v h) {
+  float r;
+  __asm__("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(y));
+  return r;
+}
+__device__ __forceinline__ float minus_hi16(float y, half2v h) {
+  float r;
+  __asm__("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+          : "=v"(r)
+          : "v"(h), "v"(y));
+  return r;
+}
+
+// hi + lo fp16 split of 8 fp32 values (22 significant bits): hi truncated, lo the exact
+// remainder rounded toward zero.
+__device__ __forceinline__ void split8(const float y[8], half8& hi, half8& lo) {
+#pragma unroll
+  for (int i = 0; i < 8; i += 2) {
+    const auto h = __builtin_amdgcn_cvt_pkrtz(y[i], y[i + 1]);
+    const half2v hh = {(_Float16)h[0], (_Float16)h[1]};
+    const auto l = __builtin_amdgcn_cvt_pkrtz(minus_lo16(y[i], hh), minus_hi16(y[i + 1], hh));
+    hi[i] = hh[0];
+    hi[i + 1] = hh[1];
+    lo[i] = (_Float16)l[0];
+    lo[i + 1] = (_Float16)l[1];
+  }
+}
+
 // ------------------------------------------------------------------ big-endian staged rows
 // The read kernels stage a head row in LDS as dwords 0..3 = bitmap (as stored) and dwords 4.. =
 // code stream with each dword byte-reversed, so that the MSB-first stream reads as big-endian

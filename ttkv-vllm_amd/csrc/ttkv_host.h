@@ -68,3 +68,13 @@ int dense_decode_paged(int H, int HQ, int d, float scale, const void* q, int64_t
                        void* out, int64_t out_row_stride, void* ws, int64_t ws_bytes,
                        hipStream_t st);
 }  // namespace ttkv
+
+namespace ttkv {
+int container_krt(int H, int HQ, int d, int B, int n, int r1, const int8_t* cq, const float* cs,
+                  const float* dec, int dec_per_seq, const uint8_t* bm, const uint8_t* pk,
+                  const float* rs, int pb, int bits, const float* cosv, const float* sinv,
+                  const float* q, float* s, hipStream_t st);
+int container_v_out(int H, int HQ, int d, int B, int n, const float* p, int64_t p_head_stride,
+                    int64_t p_batch_stride, const uint8_t* bm, const uint8_t* pk, const float* rs,
+                    int pb, int bits, float* o, hipStream_t st);
+}  // namespace ttkv

@@ -125,6 +125,20 @@ def lib():
         P, P, I32, I32,               # seq_lens, query_start_loc, num_reqs, max_seq_len
         P, I64, P, I64, P,            # out, out_row_stride, workspace, workspace_bytes, stream
     ]
+    L.ttkv_container_krt.restype = ctypes.c_int
+    L.ttkv_container_krt.argtypes = [
+        I32, I32, I32, I32, I32, I32,  # H, num_heads, d, B, n, r1
+        P, P, P, I32,                 # coeff_q, coeff_scale, decoder_f, decoder_per_seq
+        P, P, P, I32, I32,            # res_bitmap, res_packed, res_scale, res_pb, res_bits
+        P, P, P, P, P,                # cos, sin, query, scores, stream
+    ]
+    L.ttkv_container_v_out.restype = ctypes.c_int
+    L.ttkv_container_v_out.argtypes = [
+        I32, I32, I32, I32, I32,      # H, num_heads, d, B, n
+        P, I64, I64,                  # p, p_head_stride, p_batch_stride
+        P, P, P, I32, I32,            # v_bitmap, v_packed, v_scale, v_pb, v_bits
+        P, P,                         # out, stream
+    ]
     for name in EXPORTS:
         getattr(L, name)  # every declared symbol must resolve
     _LIB = L
@@ -135,7 +149,8 @@ def lib():
 EXPORTS = ("ttkv_last_error", "ttkv_blob_bytes", "ttkv_decode_workspace_bytes",
            "ttkv_decode_paged", "ttkv_write_paged", "ttkv_prefill_workspace_bytes",
            "ttkv_prefill_paged", "ttkv_multi_scores_paged", "ttkv_dense_workspace_bytes",
-           "ttkv_dense_decode_paged", "ttkv_write_workspace_bytes")
+           "ttkv_dense_decode_paged", "ttkv_write_workspace_bytes", "ttkv_container_krt",
+           "ttkv_container_v_out")
 
 
 def check(rc: int, what: str) -> None:
