@@ -185,7 +185,51 @@ def k2_flops(lens, qlens, r1):
     return f
 
 
-def bench_config4(torch, lay, cfg, cache, dev, steps=10, warmup=3):
+def _oracle_layout(lay):
+    sys.path.insert(0, str(ROOT))
+    from oracle.layout import Layout
+    return Layout(lay.H, lay.d, lay.r1, lay.qbits, lay.res_k, lay.res_bits, lay.v_lanes, lay.v_bits)
+
+
+def cpu_k2_sample(torch, lay, st, L, q_chunk, cache, n, Q):
+    """The torch-CPU oracle's continuation (impl.py:770-777 restated: scores, softmax, V readout)
+    for ONE request's chunk of config 4, all host threads: ms per chunk-layer."""
+    from oracle import attend, rope as orope
+    olay = _oracle_layout(lay)
+    torch.set_num_threads(os.cpu_count() or 1)
+    bt = st["bt"].cpu()
+    p = torch.arange(n)
+    slots = (bt[0, p // BS].long() * BS + p % BS)
+    blob = L["page"][slots.to(L["page"].device)].cpu()
+    k_s, v_s = blob[:, :olay.k_slot_bytes].contiguous(), blob[:, olay.k_slot_bytes:].contiguous()
+    dec = L["dec_pool"][0].cpu()
+    cos, sin = orope.cos_sin_from_cache(cache.cpu(), p, D)
+    qq = q_chunk.float().cpu().permute(1, 0, 2).contiguous()                # [HQ, Q, d]
+    t0 = time.perf_counter()
+    attend.attend_multi(olay, k_s, v_s, dec, qq, cos, sin, D ** -0.5, p0=n - Q)
+    return (time.perf_counter() - t0) * 1e3, torch.get_num_threads()
+
+
+def cpu_k3_sample(torch, lay, k_new, v_new, dec_pool, pinv_pool):
+    """The torch-CPU oracle's write (encode.py:301-443 restated: projection, quantisation,
+    residual, top-k select and pack of K and V rows) for the B new tokens of one config-5
+    step-layer, each against its own request's decoder as the reference's request loop does
+    (impl.py:543-653), all host threads: ms per step-layer write."""
+    from oracle import encode as oenc
+    olay = _oracle_layout(lay)
+    torch.set_num_threads(os.cpu_count() or 1)
+    K = k_new.float().cpu().permute(1, 0, 2).contiguous()                  # [H, B, d]
+    V = v_new.float().cpu().permute(1, 0, 2).contiguous()
+    dec, pinv = dec_pool.cpu(), pinv_pool.cpu()
+    t0 = time.perf_counter()
+    for r in range(K.shape[1]):
+        ef = oenc.encode_frozen(K[:, r:r + 1].contiguous(), dec[r], olay, pinv[r])
+        oenc.k_slots_from(olay, ef["coeff_q"], ef["coeff_scale"], ef["resid"])
+        oenc.v_slots_from(olay, oenc.encode_v(V[:, r:r + 1].contiguous(), olay))
+    return (time.perf_counter() - t0) * 1e3, torch.get_num_threads()
+
+
+def bench_config4(torch, lay, cfg, cache, dev, steps=10, warmup=3, cpu=False):
     """4 requests, 7400 cached tokens each plus a 256-query chunk whose keys
     are already written (n = 7656), causal over cached + chunk positions; one K2 launch per
     layer over the 4 chunks."""
@@ -221,11 +265,18 @@ def bench_config4(torch, lay, cfg, cache, dev, steps=10, warmup=3):
     tf = fl / (ms * 1e-3) / 1e12
     log(f"K2 config4: {ms * 1e3:.1f} us/launch (4 chunks), {tf:.1f} TFLOP/s; scores mode "
         f"{ms_s * 1e3:.1f} us per chunk")
-    return dict(requests=4, cached=7400, chunk=Q, us_per_launch=ms * 1e3,
-                us_per_chunk_layer=ms * 1e3 / 4, algorithmic_flop_per_launch=fl,
-                tflops=tf, mfma_peak_tflops=2500.0, mfma_frac=tf / 2500.0,
-                scores_mode_us_per_chunk_layer=ms_s * 1e3,
-                scores_mode_gbps_written=HQ * Q * n * 4 / (ms_s * 1e-3) / 1e9)
+    res = dict(requests=4, cached=7400, chunk=Q, us_per_launch=ms * 1e3,
+               us_per_chunk_layer=ms * 1e3 / 4, algorithmic_flop_per_launch=fl,
+               tflops=tf, mfma_peak_tflops=2500.0, mfma_frac=tf / 2500.0,
+               scores_mode_us_per_chunk_layer=ms_s * 1e3,
+               scores_mode_gbps_written=HQ * Q * n * 4 / (ms_s * 1e-3) / 1e9)
+    if cpu:
+        cms, cores = cpu_k2_sample(torch, lay, st, L, q[:Q], cache, n, Q)
+        res["cpu_baseline"] = dict(value=cms, unit="ms per chunk-layer", cores=cores, kind="port",
+                                   sample="one request's 256-query chunk over 7,656 keys through "
+                                          "the torch-CPU oracle attend_multi")
+        log(f"K2 config4 cpu baseline: {cms:.0f} ms per chunk-layer on {cores} threads")
+    return res
 
 
 def bench_dense(torch, lens, q, dev, steps=10, warmup=3):
@@ -313,7 +364,7 @@ def bench_container(torch, dev, B=8, n=14402, r1=R1, steps=10, warmup=3):
                 v_out_gbps=vb / (ms_v * 1e-3) / 1e9)
 
 
-def bench_config5(torch, cache, dev, steps=10, warmup=3, n_layers=L_LAYERS):
+def bench_config5(torch, cache, dev, steps=10, warmup=3, n_layers=L_LAYERS, cpu=False):
     """the reference's 4-bit store (`campaign4x`: 64 lanes of 4-bit codes for
     K residual and V, int8 coefficients, fp16 rulers), 8 requests at 16k context, 28 layers. Each
     step writes one new key/value per request per layer (K3: projection onto the decoder, bitmap
@@ -382,11 +433,21 @@ def bench_config5(torch, cache, dev, steps=10, warmup=3, n_layers=L_LAYERS):
     nbytes = k1_bytes(lay5, [ctx + 8] * B, R1, ctx + 8)
     log(f"config5 campaign4x 8x16k: {ms_step * 1e3 / n_layers:.1f} us/layer (K3 {k3 * 1e3:.1f} "
         f"+ K1 {k1 * 1e3:.1f})")
-    return dict(allocation="campaign4x (4-bit residual/V codes, int8 coefficients)",
-                requests=B, context=ctx, layers=n_layers, ms_per_step=ms_step,
-                us_per_layer=ms_step * 1e3 / n_layers, k3_us_per_launch=k3 * 1e3,
-                k1_us_per_launch=k1 * 1e3, tokens_per_s=B / (ms_step * 1e-3),
-                k1_hbm_gbps=nbytes / (k1 * 1e-3) / 1e9)
+    res = dict(allocation="campaign4x (4-bit residual/V codes, int8 coefficients)",
+               requests=B, context=ctx, layers=n_layers, ms_per_step=ms_step,
+               us_per_layer=ms_step * 1e3 / n_layers, k3_us_per_launch=k3 * 1e3,
+               k1_us_per_launch=k1 * 1e3, tokens_per_s=B / (ms_step * 1e-3),
+               k1_hbm_gbps=nbytes / (k1 * 1e-3) / 1e9)
+    if cpu:
+        L = st["layers"][0]
+        slots, k_new, v_new, _ = plans[0]
+        cms, cores = cpu_k3_sample(torch, lay5, k_new, v_new, L["dec_pool"], L["pinv_pool"])
+        res["k3_cpu_baseline"] = dict(value=cms, unit="ms per 8-token write", cores=cores,
+                                      kind="port",
+                                      sample="one step-layer's 8 new tokens through the "
+                                             "torch-CPU oracle encode_frozen + row packing")
+        log(f"config5 K3 cpu baseline: {cms:.1f} ms per 8-token write on {cores} threads")
+    return res
 
 
 def cpu_baseline(torch, lay, store, q, cache, n, budget_s=12.0):
@@ -548,8 +609,9 @@ def main():
         extra["headline_dense_fp16_comparator"] = dh
         log(f"dense fp16 comparator (8x14402): {dh['us_per_layer']:.1f} us/layer, "
             f"{dh['hbm_gbps']:.0f} GB/s")
-        extra["config4_continuation"] = bench_config4(torch, lay, cfg, cache, dev)
-        extra["config5_4bit_read_write"] = bench_config5(torch, cache, dev)
+        extra["config4_continuation"] = bench_config4(torch, lay, cfg, cache, dev,
+                                                      cpu=not args.no_cpu)
+        extra["config5_4bit_read_write"] = bench_config5(torch, cache, dev, cpu=not args.no_cpu)
         extra["container_reads_b8_ctx14402"] = bench_container(torch, dev)
 
     cpu = None
