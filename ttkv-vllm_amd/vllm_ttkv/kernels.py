@@ -40,7 +40,8 @@ def page_bytes(page: torch.Tensor, blob: int) -> torch.Tensor:
 
 def decode_workspace(lay: TTKLayout, num_heads: int, num_reqs: int, max_seq_len: int,
                      device, block_size: int = 16) -> torch.Tensor:
-    """A zero-filled workspace sized for this batch shape (the kernel keeps it zero)."""
+    """A zero-filled workspace sized for this batch shape. Its counter region (the first 64 KiB)
+    is left zero by every call, so a buffer this large serves later calls of any shape."""
     n = _hip.lib().ttkv_decode_workspace_bytes(_hip.Layout.of(lay), num_heads, num_reqs,
                                                max_seq_len, block_size)
     if n < 0:
