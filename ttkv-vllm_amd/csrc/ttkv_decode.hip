@@ -653,8 +653,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   const int64_t pstride = (int64_t)G * (kD + 2);
   float* partp = a.ws_part + ((int64_t)(base + c) * g.H + h) * pstride;
   // The partial is written with agent-scope (write-through) atomic stores and waited on before
-  // the counter update, so no cache-wide release fence is needed; the combining block reads the
-  // partials with agent-scope atomic loads.
+  // the counter update, so no cache-wide release fence is needed.
   auto st_agent = [](float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
@@ -687,22 +686,66 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   auto ld_agent = [](const float* p) { return *p; };
   const float* pbase = a.ws_part + ((int64_t)base * g.H + h) * pstride;
   const int64_t cstride = (int64_t)g.H * pstride;  // between chunks of one request and head
-  for (int it = tid; it < G * kD; it += kThreads) {
-    const int p = it / kD;
-    const int dim = it - p * kD;
-    float M = -INFINITY;
-#pragma unroll 8
-    for (int cc = 0; cc < n_chunks; ++cc) M = fmaxf(M, ld_agent(&pbase[cc * cstride + p * (kD + 2) + kD]));
-    float L = 0.f, O = 0.f;
-#pragma unroll 8
-    for (int cc = 0; cc < n_chunks; ++cc) {
+  // Many chunks: weights in LDS (the tile buffers are free now) -- every chunk's (max, sum) in
+  // one round of loads, the per-head max and normaliser by one wave per head, then each output's
+  // chunk loads issued together: a few memory round trips whatever the chunk count. Up to 8
+  // chunks, one pass per output (two round trips, no barriers) is shorter.
+  float* wsh = reinterpret_cast<float*>(&S.coef[0][0]);
+  constexpr int kWCap = (int)(sizeof(S.coef) / sizeof(float));
+  const int ncp = n_chunks * G;
+  if (n_chunks > 8 && 2 * ncp <= kWCap) {
+    for (int i = tid; i < ncp; i += kThreads) {
+      const int cc = i / G, p = i - cc * G;
       const float* pc = pbase + cc * cstride + p * (kD + 2);
-      const float f = exp2f(ld_agent(&pc[kD]) - M);
-      L = fmaf(ld_agent(&pc[kD + 1]), f, L);
-      O = fmaf(ld_agent(&pc[dim]), f, O);
+      wsh[i] = ld_agent(&pc[kD]);
+      wsh[ncp + i] = ld_agent(&pc[kD + 1]);
     }
-    store_act(a.out, a.out_dtype, qrow * a.out_row_stride + (int64_t)(h * G + p) * kD + dim,
-              O / L);
+    __syncthreads();
+    for (int p = wv; p < G; p += kWaves) {  // wave-uniform: whole waves take a head each
+      float mx = -INFINITY;
+      for (int cc = lane; cc < n_chunks; cc += 64) mx = fmaxf(mx, wsh[cc * G + p]);
+      mx = wave_max(mx);
+      float L = 0.f;
+      for (int cc = lane; cc < n_chunks; cc += 64)
+        L = fmaf(wsh[ncp + cc * G + p], exp2f(wsh[cc * G + p] - mx), L);
+      const float invL = 1.f / wave_sum(L);
+      for (int cc = lane; cc < n_chunks; cc += 64)
+        wsh[cc * G + p] = exp2f(wsh[cc * G + p] - mx) * invL;
+    }
+    __syncthreads();
+    for (int it = tid; it < G * kD; it += kThreads) {
+      const int p = it / kD;
+      const int dim = it - p * kD;
+      const float* po = pbase + p * (kD + 2) + dim;
+      float O = 0.f;
+      for (int c0 = 0; c0 < n_chunks; c0 += 32) {
+        float v[32];
+#pragma unroll
+        for (int j = 0; j < 32; ++j) v[j] = c0 + j < n_chunks ? ld_agent(&po[(c0 + j) * cstride]) : 0.f;
+#pragma unroll
+        for (int j = 0; j < 32; ++j)
+          if (c0 + j < n_chunks) O = fmaf(v[j], wsh[(c0 + j) * G + p], O);
+      }
+      store_act(a.out, a.out_dtype, qrow * a.out_row_stride + (int64_t)(h * G + p) * kD + dim, O);
+    }
+  } else {
+    for (int it = tid; it < G * kD; it += kThreads) {
+      const int p = it / kD;
+      const int dim = it - p * kD;
+      float M = -INFINITY;
+#pragma unroll 8
+      for (int cc = 0; cc < n_chunks; ++cc) M = fmaxf(M, ld_agent(&pbase[cc * cstride + p * (kD + 2) + kD]));
+      float L = 0.f, O = 0.f;
+#pragma unroll 8
+      for (int cc = 0; cc < n_chunks; ++cc) {
+        const float* pc = pbase + cc * cstride + p * (kD + 2);
+        const float f = exp2f(ld_agent(&pc[kD]) - M);
+        L = fmaf(ld_agent(&pc[kD + 1]), f, L);
+        O = fmaf(ld_agent(&pc[dim]), f, O);
+      }
+      store_act(a.out, a.out_dtype, qrow * a.out_row_stride + (int64_t)(h * G + p) * kD + dim,
+                O / L);
+    }
   }
   if (tid == 0) __hip_atomic_store(&a.ws_cnt[r * g.H + h], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
