@@ -294,15 +294,6 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
     }
     // the next tile's bytes are in flight while this tile is computed
     if (tt + kPTile < k1) fetch_raw_slot<2 * KSTEPS>(P, slot_base(tt + kPTile), part, g, k_row_off, v_row_off);
-    // this lane's RoPE angles for the tile: keys 16*nb + n, dims dl..dl+3 (cos) / 64+dl.. (sin)
-    float4v cosv[4], sinv[4];
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-      const int key = 16 * nb + n;
-      const int pos = key < ntile ? tt + key : tt;
-      cosv[nb] = *(const float4v*)&a.cs_cache[(int64_t)pos * kD + dl];
-      sinv[nb] = *(const float4v*)&a.cs_cache[(int64_t)pos * kD + 64 + dl];
-    }
     __syncthreads();
     // ------------------------------------------------------------ decode (thread = half row)
     {
@@ -362,9 +353,20 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
       }
     }
     // ------------------------------------------------------------ recon + residual + RoPE -> Kp
+    // RoPE angles of keys 16*nb + n, dims dl..dl+3 (cos) / 64+dl.. (sin), one block ahead
+    auto angle_row = [&](int nb, float4v& cv, float4v& sv) {
+      const int key = 16 * nb + n;
+      const int pos = key < ntile ? tt + key : tt;
+      cv = *(const float4v*)&a.cs_cache[(int64_t)pos * kD + dl];
+      sv = *(const float4v*)&a.cs_cache[(int64_t)pos * kD + 64 + dl];
+    };
+    float4v cvn, svn;
+    angle_row(0, cvn, svn);
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
       const int key = 16 * nb + n;
+      const float4v cv = cvn, sv = svn;
+      if (nb < 3) angle_row(nb + 1, cvn, svn);
       float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < KSTEPS; ++s) {
@@ -383,7 +385,6 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
       float vcl[4], vch[4];
       codes4<RB>(*(const uint32_t*)&S.kcode[key][dl], vcl);
       codes4<RB>(*(const uint32_t*)&S.kcode[key][64 + dl], vch);
-      const float4v cv = cosv[nb], sv = sinv[nb];
       half2v yl[2], yh[2], zl[2], zh[2];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
