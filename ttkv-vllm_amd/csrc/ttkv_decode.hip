@@ -1,15 +1,18 @@
 // K1: fused paged decode read over compressed (pre-RoPE, tensor-train) KV slots, one launch per
 // layer for the whole decode batch. gfx950 / CDNA4.
 //
-// Work item = (request r, KV head h, token chunk c). A 256-thread workgroup (4 waves) walks its
-// chunk in 64-token tiles with the next tile's raw bytes prefetched into registers while the
-// current one is computed:
+// Work item = (request r, KV head h, token chunk c). The chunk length comes from the batch's own
+// lengths, computed on the device by every workgroup (the work plan below), so a ragged batch
+// spreads its total tokens over one round of resident workgroups. A 256-thread workgroup (4
+// waves) walks its chunk in 64-token tiles with the next tile's raw bytes prefetched into
+// registers while the current one is computed:
 //   commit  : prefetched bytes -> LDS: coefficients as fp16 MFMA B-fragments (int8 is exact in
 //             fp16); this head's K and V rows realigned, the code streams byte-reversed per dword
 //             (one v_perm each) so that a code window is one v_alignbit.
 //   decode  : one thread per half row. Per bitmap byte, the next 8 codes are spread one per byte
 //             through a 4096-entry table (3-bit) or nibble perms (4-bit) and scattered onto their
-//             lanes with one v_perm driven by a 256-entry selector table. 3-bit codes come out as
+//             lanes with one v_perm driven by a 256-entry selector table (both tables built in
+//             LDS by the workgroup at start). 3-bit codes come out as
 //             fp8 bytes of the signed value c - 4 (0 outside the bitmap), which the arithmetic
 //             reads two at a time with v_cvt_pk_f32_fp8.
 //   recon   : K_pre^T[128 x 16 tokens] = Dec^T[128 x r1] * coeff^T[r1 x 16] on MFMA 16x16x32 f16.
@@ -31,7 +34,9 @@
 //             dot products over token pairs (codes as exact fp16 integers, P' * 2^-8 rounded
 //             to nearest fp16); 4-bit codes: fp32.
 // Chunks of one (r, h) are combined in the same launch by the last workgroup to finish
-// (device-scope fence + counter), which also resets the counter to zero.
+// (device-scope fence + counter), which also resets the counter to zero. The counters sit at the
+// workspace's fixed 64 KiB head, the partials after it, indexed by (chunk item) so their count
+// follows the plan.
 //
 // Reference semantics: vllm_ttkv/reference.py:63-163 (dense K, per-row RoPE, scores, softmax,
 // V readout), vllm_ttkv/impl.py:511-540 (scale then softmax), decode.py:54-122 (vLLM cos/sin
