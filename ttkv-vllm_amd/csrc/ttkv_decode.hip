@@ -429,6 +429,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
 
   for (int tt = t0; tt < t1; tt += kTile) {
     const int ntile = min(kTile, t1 - tt);
+    // the next tile's slot address first: its block-id read overlaps the commit
+    const uint8_t* next_base = tt + kTile < t1 ? slot_base(tt + kTile) : nullptr;
     // ---------------------------------------------------------------- commit prefetched bytes
     {
       uint32_t* cdst = (uint32_t*)&S.coef[ptok][part * kCPP];
@@ -449,7 +451,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
       }
     }
     // ---------------------------------------------------------------- prefetch the next tile
-    if (tt + kTile < t1) fetch_raw_slot<KU>(P, slot_base(tt + kTile), part, g, k_row_off, v_row_off);
+    if (tt + kTile < t1) fetch_raw_slot<KU>(P, next_base, part, g, k_row_off, v_row_off);
     __syncthreads();
     // ---------------------------------------------------------------- decode (thread = half row)
     {
