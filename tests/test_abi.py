@@ -185,3 +185,21 @@ def test_container_host_refusals_before_launch():
     assert vout(ph=63) == 1 and b"strides" in L.ttkv_last_error()
     assert vout(o=0) == 1
     assert vout(bits=2) == 2
+
+
+def test_header_compiles_as_plain_c(tmp_path):
+    """include/ttkv_hip.h is a C header (no C++ or HIP types): a C99 translation unit that
+    includes it and takes every entry point's address compiles with gcc."""
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc is not installed")
+    src = tmp_path / "use_header.c"
+    refs = "\n".join(f"  (entry_fn){name}," for name in _declared())
+    src.write_text('#include "ttkv_hip.h"\n'
+                   "typedef void (*entry_fn)(void);\n"
+                   "entry_fn entry_points[] = {\n" + refs + "\n};\n")
+    r = subprocess.run([gcc, "-std=c99", "-Wall", "-Werror", "-pedantic", "-fsyntax-only",
+                        "-I", str(HEADER.parent), str(src)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
