@@ -1,5 +1,6 @@
 // extern "C" entry points of libttkv_hip (declared in include/ttkv_hip.h).
 #include <mutex>
+#include <unordered_map>
 #include <vector>
 
 #include "ttkv_host.h"
@@ -28,6 +29,22 @@ int device_cu_count() {
     cache[dev] = cu;
   }
   return cache[dev];
+}
+
+int raise_smem_limit(const void* kfn, size_t smem) {
+  static std::mutex mu;
+  static std::unordered_map<const void*, uint64_t> raised;  // kernel -> bit per device ordinal
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return host_fail(TTKV_E_LAUNCH, "hipGetDevice failed");
+  const uint64_t bit = 1ull << (dev & 63);
+  std::lock_guard<std::mutex> lk(mu);
+  uint64_t& mask = raised[kfn];
+  if (mask & bit) return TTKV_OK;
+  if (hipFuncSetAttribute(kfn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) !=
+      hipSuccess)
+    return host_fail(TTKV_E_LAUNCH, "hipFuncSetAttribute(MaxDynamicSharedMemorySize) failed");
+  mask |= bit;
+  return TTKV_OK;
 }
 
 }  // namespace ttkv

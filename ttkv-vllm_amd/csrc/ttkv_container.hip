@@ -337,9 +337,7 @@ static int tiles_per_wg(int ntiles, int pairs) {
 template <typename K>
 static int launch_with_smem(K kfn, size_t smem, dim3 grid, hipStream_t st, const ContainerArgs& a,
                             const char* what) {
-  if (hipFuncSetAttribute((const void*)kfn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)smem) != hipSuccess)
-    return host_fail(TTKV_E_LAUNCH, std::string(what) + ": hipFuncSetAttribute failed");
+  if (int rc = raise_smem_limit((const void*)kfn, smem)) return rc;
   hipLaunchKernelGGL(kfn, grid, dim3(kCThreads), smem, st, a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess)

@@ -769,13 +769,7 @@ template <int G, int RB, int VB, int KU>
 static int launch_decode_t(const DecodeArgs& a, int grid, hipStream_t st) {
   const size_t smem = sizeof(DecodeSmem<KU, G>);
   auto kfn = decode_paged_kernel<G, RB, VB, KU>;
-  static bool attr_set = false;  // per instantiation; benign race (idempotent)
-  if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)kfn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)smem) != hipSuccess)
-      return host_fail(TTKV_E_LAUNCH, "hipFuncSetAttribute(MaxDynamicSharedMemorySize) failed");
-    attr_set = true;
-  }
+  if (int rc = raise_smem_limit((const void*)kfn, smem)) return rc;
   hipLaunchKernelGGL(kfn, dim3(grid), dim3(kThreads), smem, st, a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return host_fail(TTKV_E_LAUNCH, std::string("decode launch: ") +

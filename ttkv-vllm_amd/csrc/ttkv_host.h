@@ -12,6 +12,10 @@ namespace ttkv {
 int host_fail(int code, const std::string& msg);
 int device_cu_count();
 
+// Raise a kernel's dynamic LDS limit to `smem` bytes on the current device, once per (kernel,
+// device): the attribute is per device.
+int raise_smem_limit(const void* kfn, size_t smem);
+
 // Every workspace starts with a fixed region of arrival counters: zero before first use (a fresh
 // zero-filled buffer), left zero by every call. It sits at the same offset with the same size
 // whatever the call's shape, so one buffer can serve calls of any shape in turn: a call's data

@@ -594,13 +594,7 @@ template <int G, int RB, int VB, int KSTEPS, bool SCORES>
 static int launch_prefill_t(const PrefillArgs& a, int grid, hipStream_t st) {
   const size_t smem = sizeof(PrefillSmem<KSTEPS, true>);
   auto kfn = prefill_paged_kernel<G, RB, VB, KSTEPS, SCORES>;
-  static bool attr_set = false;  // per instantiation; benign race (idempotent)
-  if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)kfn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)smem) != hipSuccess)
-      return host_fail(TTKV_E_LAUNCH, "hipFuncSetAttribute(MaxDynamicSharedMemorySize) failed");
-    attr_set = true;
-  }
+  if (int rc = raise_smem_limit((const void*)kfn, smem)) return rc;
   hipLaunchKernelGGL(kfn, dim3(grid), dim3(kPThreads), smem, st, a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess)
