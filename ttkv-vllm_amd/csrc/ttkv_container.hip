@@ -50,42 +50,44 @@ struct ContainerArgs {
   float* o;
 };
 
-// Stage source dwords [c0, c0 + 4] of a byte row at `src` (any alignment, `len` valid bytes) as 4
-// realigned dwords, byte-reversed when `reverse` (big-endian code words). Reads stay inside the
-// row's dwords (the bytes past `len` are never decoded).
-__device__ __forceinline__ void stage4(const uint8_t* src, int len, int c0, bool reverse,
-                                       uint32_t out[4]) {
-  const uintptr_t A = (uintptr_t)src;
-  const uint32_t* w = (const uint32_t*)(A & ~(uintptr_t)3);
-  const int sh = (int)(A & 3);
-  const int nsrc = (sh + len + 3) >> 2;
-  const uint32_t sel = stage_selector(sh, reverse);
-  uint32_t x[5];
+// One quarter of a token's residual / V row in registers, unaligned: part 0 the 16 bitmap bytes,
+// parts 1..3 the five source dwords c0 .. c0 + 4 (c0 = 4 * (part - 1)) of its code stream. Loads
+// stay inside the row's dwords (bytes past the row are never decoded). Zero for an invalid row.
+// `commit_row_quarter` writes it in the staged format the table decoder reads: dwords 0..3 the
+// bitmap as stored, dwords 4.. the code stream realigned with each dword byte-reversed.
+__device__ __forceinline__ void load_row_quarter(const ContainerArgs& a, int64_t row, bool valid,
+                                                 int part, uint32_t x[5], int& sh) {
+  sh = 0;
 #pragma unroll
-  for (int i = 0; i < 5; ++i) x[i] = w[min(c0 + i, nsrc - 1)];
+  for (int i = 0; i < 5; ++i) x[i] = 0u;
+  if (!valid) return;
+  if (part == 0) {
+    const uint4 b = *(const uint4*)(a.bm + row * kBitmapBytes);
+    x[0] = b.x;
+    x[1] = b.y;
+    x[2] = b.z;
+    x[3] = b.w;
+  } else {
+    const uintptr_t A = (uintptr_t)(a.pk + row * a.PB);
+    const uint32_t* w = (const uint32_t*)(A & ~(uintptr_t)3);
+    sh = (int)(A & 3);
+    const int nsrc = (sh + a.PB + 3) >> 2;
+    const int c0 = 4 * (part - 1);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) out[i] = __builtin_amdgcn_perm(x[i + 1], x[i], sel);
+    for (int i = 0; i < 5; ++i) x[i] = w[min(c0 + i, nsrc - 1)];
+  }
 }
 
-// One token's residual / V row into the staged LDS format the table decoder reads: dwords 0..3
-// the bitmap as stored, dwords 4.. the code stream with each dword byte-reversed. `part` 0..3 of
-// the token's four stager threads writes dwords 4*part .. 4*part+3 (part 0: the bitmap).
-__device__ __forceinline__ void stage_row4(const ContainerArgs& a, int64_t row, bool valid,
-                                           int part, uint32_t* dst) {
-  uint32_t v[4] = {0u, 0u, 0u, 0u};
-  if (valid) {
-    if (part == 0) {
-      const uint4 b = *(const uint4*)(a.bm + row * kBitmapBytes);
-      v[0] = b.x;
-      v[1] = b.y;
-      v[2] = b.z;
-      v[3] = b.w;
-    } else {
-      stage4(a.pk + row * a.PB, a.PB, 4 * (part - 1), true, v);
-    }
-  }
+__device__ __forceinline__ void commit_row_quarter(int part, int sh, const uint32_t x[5],
+                                                   uint32_t* dst) {
+  if (part == 0) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) dst[4 * part + i] = v[i];
+    for (int i = 0; i < 4; ++i) dst[i] = x[i];
+  } else {
+    const uint32_t sel = stage_selector(sh, true);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dst[4 * part + i] = __builtin_amdgcn_perm(x[i + 1], x[i], sel);
+  }
   if (part == 3) dst[16] = 0u;
 }
 
@@ -149,53 +151,84 @@ __global__ __launch_bounds__(kCThreads, 2) void container_krt_kernel(ContainerAr
     qlo[j] = (_Float16)(x - (float)hi);
   }
 
+  // ---- the next tile's bytes in registers while the current one computes: this thread's share
+  // of a token's coefficient row (KS / 2 rounded up groups of 5 unaligned source dwords), one
+  // quarter of its residual row, and its rulers
+  const int ptok = tid >> 2, part = tid & 3;
+  constexpr int kCG = (KS + 1) / 2;
+  uint32_t cx[kCG][5], rx[5];
+  int csh = 0, rsh = 0;
+  float csv = 0.f, rsv = 0.f;
+  auto fetch = [&](int tile) {
+    const int i = tile * kCTile + ptok;
+    const bool valid = i < a.n;
+    const int64_t crow = (int64_t)bz * a.n + i;
+    const uintptr_t A = (uintptr_t)(a.cq + crow * a.r1);
+    const uint32_t* w = (const uint32_t*)(A & ~(uintptr_t)3);
+    csh = (int)(A & 3);
+    const int nsrc = (csh + a.r1 + 3) >> 2;
+#pragma unroll
+    for (int gi = 0; gi < kCG; ++gi)
+#pragma unroll
+      for (int j = 0; j < 5; ++j)
+        cx[gi][j] = valid ? w[min(2 * KS * part + 4 * gi + j, nsrc - 1)] : 0u;
+    const int64_t rrow = ((int64_t)bz * a.H + hv) * a.n + i;
+    load_row_quarter(a, rrow, valid && a.has_res, part, rx, rsh);
+    csv = valid && part == 0 ? a.cs[crow] : 0.f;
+    rsv = valid && part == 0 && a.has_res ? a.rs[rrow] : 0.f;
+  };
+  fetch(tile0);
+  // 3-bit codes decode as fp8 (c - 4) * unit: the ruler takes the 1 / unit
+  const float rscale = BITS == 3 ? 1.0f / __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0] : 1.0f;
+
   for (int tile = tile0; tile < tile1; ++tile) {
     const int i0 = tile * kCTile;
-    // ---- stage: coefficients (exact fp16), coefficient ruler, residual row
-    const int ptok = tid >> 2, part = tid & 3;
-    const bool tvalid = i0 + ptok < a.n;
+    // ---- commit: coefficients as exact fp16, the residual row staged big-endian, rulers
     {
-      const int64_t crow = (int64_t)bz * a.n + i0 + ptok;
       uint32_t* cdst = (uint32_t*)&S.coef[ptok][part * (8 * KS)];
-      // this part's 8*KS coefficient bytes: source dwords 2*KS*part .. in groups of 4
+      const uint32_t sel = stage_selector(csh, false);
 #pragma unroll
-      for (int g4 = 0; g4 < KS; g4 += 2) {
-        uint32_t v[4] = {0u, 0u, 0u, 0u};
-        if (tvalid) stage4((const uint8_t*)(a.cq + crow * a.r1), a.r1, 2 * KS * part + 2 * g4, false, v);
-        const int nd = KS - g4 >= 2 ? 4 : 2;  // dwords of this group that belong to the part
+      for (int gi = 0; gi < kCG; ++gi) {
+        const int nd = KS - 2 * gi >= 2 ? 4 : 2;  // dwords of this group that belong to the part
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if (i < nd) {
+        for (int j = 0; j < 4; ++j) {
+          if (j < nd) {
             uint32_t p01, p23;
-            i8x4_to_f16(v[i], p01, p23);
-            cdst[2 * (2 * g4 + i)] = p01;
-            cdst[2 * (2 * g4 + i) + 1] = p23;
+            i8x4_to_f16(__builtin_amdgcn_perm(cx[gi][j + 1], cx[gi][j], sel), p01, p23);
+            cdst[2 * (4 * gi + j)] = p01;
+            cdst[2 * (4 * gi + j) + 1] = p23;
           }
         }
       }
-      const int64_t rrow = ((int64_t)bz * a.H + hv) * a.n + i0 + ptok;
-      stage_row4(a, rrow, tvalid && a.has_res, part, S.raw[ptok]);
+      commit_row_quarter(part, rsh, rx, S.raw[ptok]);
       if (part == 0) {
-        S.cs[ptok] = tvalid ? a.cs[crow] : 0.f;
-        // 3-bit codes decode as fp8 (c - 4) * unit: the ruler takes the 1 / unit
-        const float unit = __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0];
-        S.kr[ptok] = tvalid && a.has_res ? a.rs[rrow] * (BITS == 3 ? 1.0f / unit : 1.0f) : 0.f;
+        S.cs[ptok] = csv;
+        S.kr[ptok] = rsv * rscale;
       }
     }
+    if (tile + 1 < tile1) fetch(tile + 1);
     __syncthreads();
 
-    // ---- decode the residual rows (threads 0..127: token tid/2, half tid&1)
-    if (tid < 2 * kCTile) {
-      const int tok = tid >> 1, half = tid & 1;
-      decode_half_row_be<BITS>(S.raw[tok], half, S.lut, S.lut3, &S.code[tok][64 * half]);
-    }
+    // ---- decode the residual rows (thread = token tid/4, quarter tid&3)
+    decode_quarter_row_be<BITS>(S.raw[ptok], part, S.lut, S.lut3, &S.code[ptok][32 * part]);
     __syncthreads();
 
-    // ---- reconstruct + residual + RoPE + scores, 16 tokens at a time
+    // ---- reconstruct + residual + RoPE + scores, 16 tokens at a time; the angle rows (L2
+    // resident) are requested one block ahead
+    auto angle_row = [&](int nb, float4v r[4]) {
+      const int64_t pos = min(i0 + 16 * nb + n, a.n - 1);
+      r[0] = *(const float4v*)&a.cosv[pos * kD + dl];
+      r[1] = *(const float4v*)&a.cosv[pos * kD + 64 + dl];
+      r[2] = *(const float4v*)&a.sinv[pos * kD + dl];
+      r[3] = *(const float4v*)&a.sinv[pos * kD + 64 + dl];
+    };
+    float4v ang_next[4];
+    angle_row(0, ang_next);
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
       const int tok = 16 * nb + n;
-      const int pos = min(i0 + tok, a.n - 1);
+      const float4v cl = ang_next[0], ch = ang_next[1], sl = ang_next[2], sh = ang_next[3];
+      if (nb < 3) angle_row(nb + 1, ang_next);
       float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int st = 0; st < KS; ++st) {
@@ -210,10 +243,6 @@ __global__ __launch_bounds__(kCThreads, 2) void container_krt_kernel(ContainerAr
       float vl[4], vh[4];
       codes4<BITS>(*(const uint32_t*)&S.code[tok][dl], vl);
       codes4<BITS>(*(const uint32_t*)&S.code[tok][64 + dl], vh);
-      const float4v cl = *(const float4v*)&a.cosv[(int64_t)pos * kD + dl];
-      const float4v ch = *(const float4v*)&a.cosv[(int64_t)pos * kD + 64 + dl];
-      const float4v sl = *(const float4v*)&a.sinv[(int64_t)pos * kD + dl];
-      const float4v sh = *(const float4v*)&a.sinv[(int64_t)pos * kD + 64 + dl];
       float y[8];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -232,6 +261,8 @@ __global__ __launch_bounds__(kCThreads, 2) void container_krt_kernel(ContainerAr
       if (4 * gq < G) *(float4v*)&S.spart[wv][tok][4 * gq] = sacc;
     }
     __syncthreads();
+    // the partial scores are next written past the following tile's two barriers, so no barrier
+    // follows this read-out
     for (int idx = tid; idx < G * kCTile; idx += kCThreads) {
       const int tok = idx & (kCTile - 1), p = idx / kCTile;
       if (i0 + tok < a.n) {
@@ -239,7 +270,6 @@ __global__ __launch_bounds__(kCThreads, 2) void container_krt_kernel(ContainerAr
         a.s[((int64_t)bz * a.H * G + hv * G + p) * a.n + i0 + tok] = v;
       }
     }
-    __syncthreads();  // the next tile overwrites the staged rows, codes and partial scores
   }
 }
 
@@ -247,75 +277,129 @@ __global__ __launch_bounds__(kCThreads, 2) void container_krt_kernel(ContainerAr
 struct VoutSmem {
   uint32_t raw[kCVTile][kCRawDw];
   uint8_t code[kCVTile][kCCode];
-  float pw[8][kCVTile];
-  float vr[kCVTile];
-  float part[8][kD];
+  float pw[2][8][kCVTile];  // double-buffered by tile parity
+  float vr[2][kCVTile];
+  float part[4][8][kD];  // per-wave sums [wave][head][dim]
   uint2 lut[256];
   uint32_t lut3[4096];
 };
 
+// 128-token tiles. The next tile's rows, rulers and weights are in registers while the current
+// tile decodes and accumulates. Accumulation: thread = (4 consecutive dims, 16 consecutive
+// tokens), so each code dword read serves 4 dims and each weight read 4 tokens.
 template <int G, int BITS>
-__global__ __launch_bounds__(kCThreads) void container_v_out_kernel(ContainerArgs a) {
+__global__ __launch_bounds__(kCThreads, 2) void container_v_out_kernel(ContainerArgs a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   VoutSmem& S = *reinterpret_cast<VoutSmem*>(smem_raw);
+  constexpr int kPw = (G * kCVTile + kCThreads - 1) / kCThreads;  // weights per thread per tile
   const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = tid >> 6;
   const int hv = blockIdx.y;
   const int bz = blockIdx.z;
   const int ntiles = (a.n + kCVTile - 1) / kCVTile;
   const int tile0 = blockIdx.x * a.tiles_per_wg;
   const int tile1 = min(ntiles, tile0 + a.tiles_per_wg);
   if (tile0 >= tile1) return;
-  build_luts(S.lut, BITS == 3 ? S.lut3 : nullptr, tid, kCThreads);
-  const int dim = tid & (kD - 1), par = tid >> 7;
-  float acc[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) acc[g] = 0.f;
+  const int ptok = tid >> 2, part = tid & 3;  // staging: tokens ptok and 64 + ptok, one quarter
+  const int dg = tid & 31, ph = tid >> 5;     // accumulation: dims 4dg.., tokens 16ph..
+  const int64_t row0 = ((int64_t)bz * a.H + hv) * a.n;
+  const float* pb = a.p + (int64_t)bz * a.p_batch_stride + (int64_t)hv * G * a.p_head_stride;
 
-  for (int tile = tile0; tile < tile1; ++tile) {
+  uint32_t x[2][5];
+  int sh[2];
+  float rsv[2], pwv[kPw];
+  auto fetch = [&](int tile) {
     const int i0 = tile * kCVTile;
-    // ---- stage the tile's V rows (4 threads per token, two passes), rulers and weights
 #pragma unroll
     for (int pass = 0; pass < 2; ++pass) {
-      const int tok = (tid >> 2) + 64 * pass, part = tid & 3;
+      const int tok = ptok + 64 * pass;
       const bool valid = i0 + tok < a.n;
-      const int64_t row = ((int64_t)bz * a.H + hv) * a.n + i0 + tok;
-      stage_row4(a, row, valid, part, S.raw[tok]);
-      if (part == 0) {
-        const float unit = __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0];
-        S.vr[tok] = valid ? a.rs[row] * (BITS == 3 ? 1.0f / unit : 1.0f) : 0.f;
-      }
+      load_row_quarter(a, row0 + i0 + tok, valid, part, x[pass], sh[pass]);
+      rsv[pass] = part == 0 && valid ? a.rs[row0 + i0 + tok] : 0.f;
     }
-    for (int idx = tid; idx < G * kCVTile; idx += kCThreads) {
-      const int tok = idx & (kCVTile - 1), g = idx / kCVTile;
-      S.pw[g][tok] = i0 + tok < a.n
-                         ? a.p[(int64_t)bz * a.p_batch_stride + (int64_t)(hv * G + g) * a.p_head_stride + i0 + tok]
-                         : 0.f;
+#pragma unroll
+    for (int k = 0; k < kPw; ++k) {
+      const int idx = tid + kCThreads * k, tok = idx & (kCVTile - 1), g = idx / kCVTile;
+      pwv[k] = g < G && i0 + tok < a.n ? pb[(int64_t)g * a.p_head_stride + i0 + tok] : 0.f;
     }
+  };
+  fetch(tile0);
+  build_luts(S.lut, BITS == 3 ? S.lut3 : nullptr, tid, kCThreads);
+  // 3-bit codes decode as fp8 (c - 4) * unit: the ruler takes the 1 / unit
+  const float rscale = BITS == 3 ? 1.0f / __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0] : 1.0f;
+  float acc[G][4], wsum[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    wsum[g] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[g][i] = 0.f;
+  }
+
+  for (int tile = tile0; tile < tile1; ++tile) {
+    // ---- commit the prefetched tile, then request the next one. The rulers and weights are
+    // double-buffered: a thread still accumulating the previous tile reads the other buffer, and
+    // the staged rows and codes are only rewritten past a barrier that follows its reads.
+    const int buf = (tile - tile0) & 1;
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+      const int tok = ptok + 64 * pass;
+      commit_row_quarter(part, sh[pass], x[pass], S.raw[tok]);
+      if (part == 0) S.vr[buf][tok] = rsv[pass] * rscale;
+    }
+#pragma unroll
+    for (int k = 0; k < kPw; ++k) {
+      const int idx = tid + kCThreads * k;
+      if (idx < G * kCVTile) S.pw[buf][idx / kCVTile][idx & (kCVTile - 1)] = pwv[k];
+    }
+    if (tile + 1 < tile1) fetch(tile + 1);
     __syncthreads();
     // ---- decode (thread = token tid/2, half tid&1)
-    decode_half_row_be<BITS>(S.raw[tid >> 1], tid & 1, S.lut, S.lut3, &S.code[tid >> 1][64 * (tid & 1)]);
+    decode_half_row_be<BITS>(S.raw[tid >> 1], tid & 1, S.lut, S.lut3,
+                             &S.code[tid >> 1][64 * (tid & 1)]);
     __syncthreads();
-    // ---- o[g][dim] over this tile: thread = (dim, token parity)
-    for (int tok = par; tok < kCVTile; tok += 2) {
-      const uint32_t c = S.code[tok][dim];
-      float v;
-      if constexpr (BITS == 3) v = __builtin_amdgcn_cvt_f32_fp8((int)c, 0);
-      else v = (float)c - 8.f;
-      const float w = v * S.vr[tok];
+    // ---- acc[g][i] += p[g][tok] * ruler[tok] * code[tok][4dg + i] over this thread's tokens
 #pragma unroll
-      for (int g = 0; g < G; ++g) acc[g] = fmaf(S.pw[g][tok], w, acc[g]);
+    for (int k4 = 0; k4 < 4; ++k4) {
+      const int t0 = 16 * ph + 4 * k4;
+      const float4v vr4 = *(const float4v*)&S.vr[buf][t0];
+      float4v pw4[G];
+#pragma unroll
+      for (int g = 0; g < G; ++g) pw4[g] = *(const float4v*)&S.pw[buf][g][t0];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float v[4];
+        codes4<BITS>(*(const uint32_t*)&S.code[t0 + j][4 * dg], v);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float w = pw4[g][j] * vr4[j];
+          if constexpr (BITS == 4) wsum[g] += w;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[g][i] = fmaf(w, v[i], acc[g][i]);
+        }
+      }
     }
-    __syncthreads();  // the next tile overwrites the staged rows, codes and weights
   }
-  if (par == 1) {
+  // ---- 4-bit codes arrive as c: remove the 8 * sum(w) offset; sum the 8 token ranges
 #pragma unroll
-    for (int g = 0; g < G; ++g) S.part[g][dim] = acc[g];
-  }
-  __syncthreads();
-  if (par == 0) {
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float t = acc[g][i] - (BITS == 4 ? 8.f * wsum[g] : 0.f);
+      t += __shfl_xor(t, 32);
+      acc[g][i] = t;
+    }
+  if (lane < 32) {
 #pragma unroll
     for (int g = 0; g < G; ++g)
-      atomicAdd(&a.o[((int64_t)bz * a.H * G + hv * G + g) * kD + dim], acc[g] + S.part[g][dim]);
+      *(float4v*)&S.part[wv][g][4 * dg] = float4v{acc[g][0], acc[g][1], acc[g][2], acc[g][3]};
+  }
+  __syncthreads();
+  if (tid < kD) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+      atomicAdd(&a.o[((int64_t)bz * a.H * G + hv * G + g) * kD + tid],
+                (S.part[0][g][tid] + S.part[1][g][tid]) + (S.part[2][g][tid] + S.part[3][g][tid]));
   }
 }
 

@@ -277,58 +277,76 @@ __device__ __forceinline__ void build_luts(uint2* lut, uint32_t* lut3, int tid, 
   }
 }
 
-// Decode dims [64*half, 64*half+64) of one big-endian staged head row into one byte per lane at
-// dst[0..63].
+// Decode the 32 lanes of bitmap dword `bm` of one big-endian staged head row (code stream at
+// `st`, this dword's first code at rank `rank`, advanced past it) into one byte per lane at
+// dst[0..31].
 //   BITS == 3: fp8 signed bytes (c - 4), 0 outside the bitmap; needs lut3 (build_luts).
 //   BITS == 4: offset-binary code bytes c, 8 outside the bitmap.
 // Per bitmap byte: the code window at bit offset bp is one v_alignbit of the words holding bits
 // bp-1 and bp+31 (shift (-bp) mod 32; word -1 is the last bitmap dword, read but unused).
 template <int BITS>
+__device__ __forceinline__ void decode_dword_be(const uint32_t* st, uint32_t bm, int& rank,
+                                                const uint2* lut, const uint32_t* lut3,
+                                                uint8_t* dst) {
+  uint32_t B[4];
+  int bp[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    B[m] = __builtin_amdgcn_ubfe(bm, 8 * m, 8);
+    bp[m] = rank * BITS;
+    rank += __builtin_popcount(B[m]);
+  }
+  uint2 sel[4];
+  uint32_t w[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    sel[m] = lut[B[m]];
+    const uint32_t* wp = st + ((bp[m] - 1) >> 5);
+    w[m] = __builtin_amdgcn_alignbit(wp[0], wp[1], (uint32_t)(-bp[m]));
+  }
+  uint32_t e0[4], e1[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    if constexpr (BITS == 3) {
+      e0[m] = lut3[w[m] >> 20];
+      e1[m] = lut3[(w[m] >> 8) & 0xfffu];
+    } else {
+      spread8<4>(w[m] ^ 0x88888888u, e0[m], e1[m]);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    uint2 out;
+    out.x = __builtin_amdgcn_perm(e1[m], e0[m], sel[m].x);
+    out.y = __builtin_amdgcn_perm(e1[m], e0[m], sel[m].y);
+    if constexpr (BITS == 4) {
+      out.x ^= 0x08080808u;
+      out.y ^= 0x08080808u;
+    }
+    *(uint2*)(dst + 8 * m) = out;
+  }
+}
+
+// Decode dims [64*half, 64*half+64) of one big-endian staged head row (dwords 0..3 the bitmap,
+// dwords 4.. the code stream) into one byte per lane at dst[0..63].
+template <int BITS>
 __device__ __forceinline__ void decode_half_row_be(const uint32_t* row, int half, const uint2* lut,
                                                    const uint32_t* lut3, uint8_t* dst) {
   const uint32_t bm0 = row[2 * half], bm1 = row[2 * half + 1];
   int rank = half ? __builtin_popcount(row[0]) + __builtin_popcount(row[1]) : 0;
-  const uint32_t* st = row + 4;
+  decode_dword_be<BITS>(row + 4, bm0, rank, lut, lut3, dst);
+  decode_dword_be<BITS>(row + 4, bm1, rank, lut, lut3, dst + 32);
+}
+
+// Decode dims [32*qr, 32*qr+32) of one staged head row into dst[0..31] (four threads per row).
+template <int BITS>
+__device__ __forceinline__ void decode_quarter_row_be(const uint32_t* row, int qr,
+                                                      const uint2* lut, const uint32_t* lut3,
+                                                      uint8_t* dst) {
+  int rank = 0;
 #pragma unroll
-  for (int m0 = 0; m0 < 8; m0 += 4) {
-    uint32_t B[4];
-    int bp[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      B[m] = __builtin_amdgcn_ubfe(m0 < 4 ? bm0 : bm1, 8 * m, 8);
-      bp[m] = rank * BITS;
-      rank += __builtin_popcount(B[m]);
-    }
-    uint2 sel[4];
-    uint32_t w[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      sel[m] = lut[B[m]];
-      const uint32_t* wp = st + ((bp[m] - 1) >> 5);
-      w[m] = __builtin_amdgcn_alignbit(wp[0], wp[1], (uint32_t)(-bp[m]));
-    }
-    uint32_t e0[4], e1[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      if constexpr (BITS == 3) {
-        e0[m] = lut3[w[m] >> 20];
-        e1[m] = lut3[(w[m] >> 8) & 0xfffu];
-      } else {
-        spread8<4>(w[m] ^ 0x88888888u, e0[m], e1[m]);
-      }
-    }
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      uint2 out;
-      out.x = __builtin_amdgcn_perm(e1[m], e0[m], sel[m].x);
-      out.y = __builtin_amdgcn_perm(e1[m], e0[m], sel[m].y);
-      if constexpr (BITS == 4) {
-        out.x ^= 0x08080808u;
-        out.y ^= 0x08080808u;
-      }
-      *(uint2*)(dst + 8 * (m0 + m)) = out;
-    }
-  }
+  for (int i = 0; i < 3; ++i) rank += i < qr ? __builtin_popcount(row[i]) : 0;
+  decode_dword_be<BITS>(row + 4, row[qr], rank, lut, lut3, dst);
 }
 
 // Four decoded code bytes -> floats. BITS == 3: fp8 signed bytes -> (c - 4) * unit, two per
