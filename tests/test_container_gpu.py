@@ -104,6 +104,27 @@ def test_krt_rotation_is_per_row():
     assert float((good - rolled).abs().max() / good.abs().max()) > 1e-2
 
 
+def test_krt_reads_the_first_half_of_the_angle_rows():
+    """Rotate-half tables duplicate their d/2 ramp (column j == column j + d/2). Like the codec
+    kernel (ttkv_kernels.cu:472-491) the launch reads columns [0, d/2) only: poisoning the second
+    half leaves the scores bit-identical."""
+    n = 80
+    cfg, kl, _ = _store("safe", n, seed=61)
+    cos, sin = _angles(n)
+    assert torch.equal(cos[:, :D // 2], cos[:, D // 2:]) and torch.equal(sin[:, :D // 2], sin[:, D // 2:])
+    q = (torch.randn(32, D, generator=torch.Generator().manual_seed(7)) * 0.1).to(DEV)
+    base = (kl["coeff_q"].to(DEV), kl["coeff_scale"].to(DEV), kl["dec_q"].to(DEV),
+            kl["dec_scale"].to(DEV), _rows(kl["resid"], 3))
+    good = container.krt(*base, cos.to(DEV), sin.to(DEV), q, n, 32, 4, D)
+    cp, sp = cos.clone(), sin.clone()
+    cp[:, D // 2:] = float("nan")
+    sp[:, D // 2:] = float("nan")
+    poisoned = container.krt(*base, cp.to(DEV), sp.to(DEV), q, n, 32, 4, D)
+    torch.cuda.synchronize()
+    assert torch.isfinite(good).all()
+    assert torch.equal(good, poisoned)
+
+
 @pytest.mark.parametrize("cfg_name,B,n,HQ", [("safe", 1, 300, 24), ("campaign4x", 2, 129, 32),
                                              ("tight", 2, 64, 8), ("safe", 1, 1, 24)])
 def test_v_out_matches_the_oracle(cfg_name, B, n, HQ):

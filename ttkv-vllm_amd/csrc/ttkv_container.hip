@@ -213,21 +213,20 @@ __global__ __launch_bounds__(kCThreads, 2) void container_krt_kernel(ContainerAr
     decode_quarter_row_be<BITS>(S.raw[ptok], part, S.lut, S.lut3, &S.code[ptok][32 * part]);
     __syncthreads();
 
-    // ---- reconstruct + residual + RoPE + scores, 16 tokens at a time; the angle rows (L2
-    // resident) are requested one block ahead
-    auto angle_row = [&](int nb, float4v r[4]) {
+    // ---- reconstruct + residual + RoPE + scores, 16 tokens at a time. The pair (j, j + 64)
+    // rotates by one angle: the tables duplicate their d/2 ramp, so only the first half of each
+    // row is read, as the codec kernel does. The rows (L2 resident) are requested one block ahead.
+    auto angle_row = [&](int nb, float4v r[2]) {
       const int64_t pos = min(i0 + 16 * nb + n, a.n - 1);
       r[0] = *(const float4v*)&a.cosv[pos * kD + dl];
-      r[1] = *(const float4v*)&a.cosv[pos * kD + 64 + dl];
-      r[2] = *(const float4v*)&a.sinv[pos * kD + dl];
-      r[3] = *(const float4v*)&a.sinv[pos * kD + 64 + dl];
+      r[1] = *(const float4v*)&a.sinv[pos * kD + dl];
     };
-    float4v ang_next[4];
+    float4v ang_next[2];
     angle_row(0, ang_next);
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
       const int tok = 16 * nb + n;
-      const float4v cl = ang_next[0], ch = ang_next[1], sl = ang_next[2], sh = ang_next[3];
+      const float4v cv = ang_next[0], sv = ang_next[1];
       if (nb < 3) angle_row(nb + 1, ang_next);
       float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -248,8 +247,8 @@ __global__ __launch_bounds__(kCThreads, 2) void container_krt_kernel(ContainerAr
       for (int i = 0; i < 4; ++i) {
         const float xl = fmaf(cs, acc0[i], fmaf(kr, vl[i], kb));
         const float xh = fmaf(cs, acc1[i], fmaf(kr, vh[i], kb));
-        y[i] = xl * cl[i] - xh * sl[i];
-        y[4 + i] = xh * ch[i] + xl * sh[i];
+        y[i] = xl * cv[i] - xh * sv[i];
+        y[4 + i] = xh * cv[i] + xl * sv[i];
       }
       half8 yhi, ylo;
       split8(y, yhi, ylo);

@@ -46,7 +46,8 @@ def krt(coeff_q, coeff_scale, dec_q, dec_scale, resid, cos, sin, q, n, HQ, G, HD
     coeff_q [B*n, r1] int8 (row b*n + i), coeff_scale [B*n]; dec_q [r1, H*HD] int8 (shared) or
     [B, r1, H*HD] with dec_scale [r1] / [B, r1] (the decoder is converted to fp32 here, as the
     codec's launcher does); resid: rows of the K residual or None; cos / sin [n, HD] fp32 at
-    absolute positions; q [HQ, HD] or [B, HQ, HD] fp32 post-RoPE."""
+    absolute positions, halves duplicated as rotate-half tables are (only columns [0, HD/2) are
+    read, as the codec kernel does); q [HQ, HD] or [B, HQ, HD] fp32 post-RoPE."""
     if mode != 7:
         raise NotImplementedError("only the full computation (mode 7) is built; the codec's "
                                   "partial modes exist for timing decomposition")
