@@ -206,7 +206,6 @@ __global__ __launch_bounds__(kCThreads, 2) void container_krt_kernel(ContainerAr
         S.kr[ptok] = rsv * rscale;
       }
     }
-    if (tile + 1 < tile1) fetch(tile + 1);
     __syncthreads();
 
     // ---- decode the residual rows (thread = token tid/4, quarter tid&3)
@@ -259,6 +258,9 @@ __global__ __launch_bounds__(kCThreads, 2) void container_krt_kernel(ContainerAr
       // lane (n, gq) holds heads 4*gq .. 4*gq+3 of token n, over this wave's 32 dims
       if (4 * gq < G) *(float4v*)&S.spart[wv][tok][4 * gq] = sacc;
     }
+    // the next tile's bytes: requested after the last angle wait (loads complete in order, so
+    // that wait would also wait for them), in flight during the read-out and the next commit
+    if (tile + 1 < tile1) fetch(tile + 1);
     __syncthreads();
     // the partial scores are next written past the following tile's two barriers, so no barrier
     // follows this read-out

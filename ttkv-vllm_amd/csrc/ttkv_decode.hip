@@ -427,6 +427,22 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
     for (int i = 0; i < 8; ++i) o[p][i] = 0.f;
   }
 
+  // RoPE angle rows (shared by every request and head, L2-resident): this lane's 4 dims of the
+  // token it reconstructs in block nb, requested one block ahead inside the reconstruction. Block
+  // 0's row of the NEXT tile is requested with that tile's slot bytes, where the registers allow.
+  // Loads complete in order (vmcnt), so the reconstruction's angle loads must not queue behind
+  // the next tile's slot bytes: those are requested only after the reconstruction's last angle
+  // wait, and overlap the softmax and P.V instead.
+  constexpr bool kAngle0Ahead = G <= 4;
+  float4v cv0, sv0;
+  auto angle_row = [&](int ts, int nb, float4v& cv, float4v& sv) {
+    const int tok = 16 * nb + n;
+    const int64_t pos = tok < min(kTile, t1 - ts) ? ts + tok : ts;
+    cv = *gbl((const float4v*)&a.cs_cache[pos * kD + dl]);
+    sv = *gbl((const float4v*)&a.cs_cache[pos * kD + 64 + dl]);
+  };
+  if constexpr (kAngle0Ahead) angle_row(t0, 0, cv0, sv0);
+
   for (int tt = t0; tt < t1; tt += kTile) {
     const int ntile = min(kTile, t1 - tt);
     // the next tile's slot address first: its block-id read overlaps the commit
@@ -450,8 +466,6 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
         S.rawv[ptok][part * 4 + i] = __builtin_amdgcn_perm(P.vrow[i + 1], P.vrow[i], vsel);
       }
     }
-    // ---------------------------------------------------------------- prefetch the next tile
-    if (tt + kTile < t1) fetch_raw_slot<KU>(P, next_base, part, g, k_row_off, v_row_off);
     __syncthreads();
     // ---------------------------------------------------------------- decode (thread = half row)
     {
@@ -476,20 +490,18 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
     }
     __syncthreads();
     // ---------------------------------------------------------------- recon + rope + q.k
-    // RoPE angles (shared by every request and head, L2-resident), fetched one block ahead
-    auto angle_row = [&](int nb, float4v& cv, float4v& sv) {
-      const int tok = 16 * nb + n;
-      const int64_t pos = tok < ntile ? tt + tok : tt;
-      cv = *gbl((const float4v*)&a.cs_cache[pos * kD + dl]);
-      sv = *gbl((const float4v*)&a.cs_cache[pos * kD + 64 + dl]);
-    };
     float4v cvn, svn;
-    angle_row(0, cvn, svn);
+    if constexpr (kAngle0Ahead) {
+      cvn = cv0;
+      svn = sv0;
+    } else {
+      angle_row(tt, 0, cvn, svn);
+    }
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
       const int tok = 16 * nb + n;
       const float4v cv = cvn, sv = svn;
-      if (nb < 3) angle_row(nb + 1, cvn, svn);
+      if (nb < 3) angle_row(tt, nb + 1, cvn, svn);
       const float krp = S.kr[tok];
       // 4-bit codes arrive as c: the -8 * ruler offset enters as the accumulator's start
       const float kb = RB == 4 ? -8.f * krp : 0.f;
@@ -528,6 +540,11 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
       sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qlo, yhi, sacc, 0, 0, 0);
       // lane (n, gq) holds heads 4*gq .. 4*gq+3 of token n
       if (4 * gq < G) *(float4v*)&S.spart[wv][tok][4 * gq] = sacc;
+    }
+    // ---------------------------------------------------------------- prefetch the next tile
+    if (tt + kTile < t1) {
+      if constexpr (kAngle0Ahead) angle_row(tt + kTile, 0, cv0, sv0);
+      fetch_raw_slot<KU>(P, next_base, part, g, k_row_off, v_row_off);
     }
     __syncthreads();
     // ---------------------------------------------------------------- online softmax (every wave)

@@ -292,8 +292,8 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
         S.u.raw.v[ptok][part * 4 + i] = __builtin_amdgcn_perm(P.vrow[i + 1], P.vrow[i], vsel);
       }
     }
-    // the next tile's bytes are in flight while this tile is computed
-    if (tt + kPTile < k1) fetch_raw_slot<2 * KSTEPS>(P, slot_base(tt + kPTile), part, g, k_row_off, v_row_off);
+    if constexpr (SCORES)
+      if (tt + kPTile < k1) fetch_raw_slot<2 * KSTEPS>(P, slot_base(tt + kPTile), part, g, k_row_off, v_row_off);
     __syncthreads();
     // ------------------------------------------------------------ decode (thread = half row)
     {
@@ -411,6 +411,12 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
             __builtin_bit_cast(uint32_t, zh[0]), __builtin_bit_cast(uint32_t, zh[1]));
       }
     }
+    // The next tile's bytes are in flight while this tile's scores, softmax and P.V run. Loads
+    // complete in order (vmcnt), so they are requested only after the reconstruction's last
+    // angle wait, which would otherwise also wait for them. The score-tensor mode requests them
+    // at the commit instead: its score stores count on the same in-order counter (measured).
+    if constexpr (!SCORES)
+      if (tt + kPTile < k1) fetch_raw_slot<2 * KSTEPS>(P, slot_base(tt + kPTile), part, g, k_row_off, v_row_off);
     __syncthreads();
     // ------------------------------------------------------------ scores S^T = Kp Q^T
     float4v sacc[4][G];
