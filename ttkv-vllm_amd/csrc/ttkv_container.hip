@@ -208,7 +208,10 @@ __global__ __launch_bounds__(kCThreads, 2) void container_krt_kernel(ContainerAr
     }
     __syncthreads();
 
-    // ---- decode the residual rows (thread = token tid/4, quarter tid&3)
+    // ---- decode the residual rows (thread = token tid/4, quarter tid&3). The decode and
+    // reconstruction run at raised wave priority: the co-resident workgroup's commit and
+    // read-out fill the issue slots they leave.
+    __builtin_amdgcn_s_setprio(1);
     decode_quarter_row_be<BITS>(S.raw[ptok], part, S.lut, S.lut3, &S.code[ptok][32 * part]);
     __syncthreads();
 
@@ -258,6 +261,7 @@ __global__ __launch_bounds__(kCThreads, 2) void container_krt_kernel(ContainerAr
       // lane (n, gq) holds heads 4*gq .. 4*gq+3 of token n, over this wave's 32 dims
       if (4 * gq < G) *(float4v*)&S.spart[wv][tok][4 * gq] = sacc;
     }
+    __builtin_amdgcn_s_setprio(0);
     // the next tile's bytes: requested after the last angle wait (loads complete in order, so
     // that wait would also wait for them), in flight during the read-out and the next commit
     if (tile + 1 < tile1) fetch(tile + 1);
@@ -355,9 +359,11 @@ __global__ __launch_bounds__(kCThreads, 2) void container_v_out_kernel(Container
     }
     if (tile + 1 < tile1) fetch(tile + 1);
     __syncthreads();
-    // ---- decode (thread = token tid/2, half tid&1)
+    // ---- decode (thread = token tid/2, half tid&1), at raised wave priority
+    __builtin_amdgcn_s_setprio(1);
     decode_half_row_be<BITS>(S.raw[tid >> 1], tid & 1, S.lut, S.lut3,
                              &S.code[tid >> 1][64 * (tid & 1)]);
+    __builtin_amdgcn_s_setprio(0);
     __syncthreads();
     // ---- acc[g][i] += p[g][tok] * ruler[tok] * code[tok][4dg + i] over this thread's tokens
 #pragma unroll

@@ -468,6 +468,10 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
     }
     __syncthreads();
     // ---------------------------------------------------------------- decode (thread = half row)
+    // The decode and reconstruction are each workgroup's critical chain; the co-resident
+    // workgroup's softmax, P.V and commit fill the issue slots they leave. Raising this wave's
+    // priority for these two phases lets them run ahead (headline 172 -> 159 us, measured).
+    __builtin_amdgcn_s_setprio(1);
     {
       const int kind = tid >> 7;  // waves 0,1: K rows; waves 2,3: V rows
       const int tok = (tid >> 1) & 63;
@@ -541,6 +545,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
       // lane (n, gq) holds heads 4*gq .. 4*gq+3 of token n
       if (4 * gq < G) *(float4v*)&S.spart[wv][tok][4 * gq] = sacc;
     }
+    __builtin_amdgcn_s_setprio(0);
     // ---------------------------------------------------------------- prefetch the next tile
     if (tt + kTile < t1) {
       if constexpr (kAngle0Ahead) angle_row(tt + kTile, 0, cv0, sv0);

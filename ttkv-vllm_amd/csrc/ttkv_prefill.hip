@@ -296,6 +296,9 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
       if (tt + kPTile < k1) fetch_raw_slot<2 * KSTEPS>(P, slot_base(tt + kPTile), part, g, k_row_off, v_row_off);
     __syncthreads();
     // ------------------------------------------------------------ decode (thread = half row)
+    // Decode, V transpose and reconstruction run at raised wave priority, so that where two
+    // workgroups share a CU the other one's scores, softmax and P.V fill the slots they leave.
+    __builtin_amdgcn_s_setprio(1);
     {
       const int kind = tid >> 7;
       const int key = (tid >> 1) & 63;
@@ -411,6 +414,7 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
             __builtin_bit_cast(uint32_t, zh[0]), __builtin_bit_cast(uint32_t, zh[1]));
       }
     }
+    __builtin_amdgcn_s_setprio(0);
     // The next tile's bytes are in flight while this tile's scores, softmax and P.V run. Loads
     // complete in order (vmcnt), so they are requested only after the reconstruction's last
     // angle wait, which would otherwise also wait for them. The score-tensor mode requests them
