@@ -65,6 +65,12 @@ __device__ __forceinline__ const __attribute__((address_space(1))) T* gbl(const 
   return (const __attribute__((address_space(1))) T*)p;
 }
 
+// 16 bytes from global memory (16-byte aligned) as uint4, through a global pointer.
+__device__ __forceinline__ uint4 ld_global16(const void* p) {
+  const u32x4 v = *gbl((const u32x4*)p);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 __device__ __forceinline__ float f16_bits_to_float(uint32_t bits16) {
   _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)bits16);
   return (float)h;

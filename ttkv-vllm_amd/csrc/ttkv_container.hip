@@ -62,14 +62,14 @@ __device__ __forceinline__ void load_row_quarter(const ContainerArgs& a, int64_t
   for (int i = 0; i < 5; ++i) x[i] = 0u;
   if (!valid) return;
   if (part == 0) {
-    const uint4 b = *(const uint4*)(a.bm + row * kBitmapBytes);
+    const uint4 b = ld_global16(a.bm + row * kBitmapBytes);
     x[0] = b.x;
     x[1] = b.y;
     x[2] = b.z;
     x[3] = b.w;
   } else {
     const uintptr_t A = (uintptr_t)(a.pk + row * a.PB);
-    const uint32_t* w = (const uint32_t*)(A & ~(uintptr_t)3);
+    const auto* w = gbl((const uint32_t*)(A & ~(uintptr_t)3));
     sh = (int)(A & 3);
     const int nsrc = (sh + a.PB + 3) >> 2;
     const int c0 = 4 * (part - 1);
@@ -164,7 +164,7 @@ __global__ __launch_bounds__(kCThreads, 2) void container_krt_kernel(ContainerAr
     const bool valid = i < a.n;
     const int64_t crow = (int64_t)bz * a.n + i;
     const uintptr_t A = (uintptr_t)(a.cq + crow * a.r1);
-    const uint32_t* w = (const uint32_t*)(A & ~(uintptr_t)3);
+    const auto* w = gbl((const uint32_t*)(A & ~(uintptr_t)3));
     csh = (int)(A & 3);
     const int nsrc = (csh + a.r1 + 3) >> 2;
 #pragma unroll

@@ -89,8 +89,8 @@ __global__ __launch_bounds__(kDThreads) void dense_decode_kernel(DenseArgs a) {
   float q[G][8];
 #pragma unroll
   for (int p = 0; p < G; ++p) {
-    const uint4 x = *(const uint4*)((const uint16_t*)a.q + qrow * a.q_row_stride +
-                                    (int64_t)(h * G + p) * kD + 8 * sub);
+    const uint4 x = ld_global16((const uint16_t*)a.q + qrow * a.q_row_stride +
+                                (int64_t)(h * G + p) * kD + 8 * sub);
     unpack8(x, DT, q[p]);
 #pragma unroll
     for (int i = 0; i < 8; ++i) q[p][i] *= a.scale_log2;
@@ -120,8 +120,8 @@ __global__ __launch_bounds__(kDThreads) void dense_decode_kernel(DenseArgs a) {
   for (int u = 0; u < kDUnroll; ++u) {
     const int t = tb + 4 * u + grp;
     const int64_t off = t < t1 ? slot_off(t) : -1;
-    kx[u] = off >= 0 ? *(const uint4*)(a.kc + off) : zero4;
-    vx[u] = off >= 0 ? *(const uint4*)(a.vc + off) : zero4;
+    kx[u] = off >= 0 ? ld_global16(a.kc + off) : zero4;
+    vx[u] = off >= 0 ? ld_global16(a.vc + off) : zero4;
   }
   for (; tb < t1; tb += 4 * kStep) {
     uint4 kn[kDUnroll], vn[kDUnroll];
@@ -129,8 +129,8 @@ __global__ __launch_bounds__(kDThreads) void dense_decode_kernel(DenseArgs a) {
     for (int u = 0; u < kDUnroll; ++u) {
       const int t = tb + 4 * kStep + 4 * u + grp;
       const int64_t off = t < t1 ? slot_off(t) : -1;
-      kn[u] = off >= 0 ? *(const uint4*)(a.kc + off) : zero4;
-      vn[u] = off >= 0 ? *(const uint4*)(a.vc + off) : zero4;
+      kn[u] = off >= 0 ? ld_global16(a.kc + off) : zero4;
+      vn[u] = off >= 0 ? ld_global16(a.vc + off) : zero4;
     }
     float s[G][kDUnroll];
 #pragma unroll

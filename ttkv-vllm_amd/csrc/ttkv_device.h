@@ -66,12 +66,12 @@ __device__ __forceinline__ void fetch_raw_slot(RawSlot<NCW>& P, const uint8_t* b
     P.rul = 0u;
     return;
   }
-  const uint32_t* cs = (const uint32_t*)(base + part * kCPP);
+  const auto* cs = gbl((const uint32_t*)(base + part * kCPP));
 #pragma unroll
   for (int i = 0; i < NCW; ++i) P.coef[i] = cs[i];
   {
     const uintptr_t A = (uintptr_t)(base + k_row_off);
-    const uint32_t* src = (const uint32_t*)(A & ~(uintptr_t)3);
+    const auto* src = gbl((const uint32_t*)(A & ~(uintptr_t)3));
     const int nsrc = (int)((A & 3) + g.k_row + 3) >> 2;
     // clamped index: every load stays inside the row's dwords (the extra ones are never decoded)
 #pragma unroll
@@ -79,13 +79,13 @@ __device__ __forceinline__ void fetch_raw_slot(RawSlot<NCW>& P, const uint8_t* b
   }
   {
     const uintptr_t A = (uintptr_t)(base + v_row_off);
-    const uint32_t* src = (const uint32_t*)(A & ~(uintptr_t)3);
+    const auto* src = gbl((const uint32_t*)(A & ~(uintptr_t)3));
     const int nsrc = (int)((A & 3) + g.v_row + 3) >> 2;
 #pragma unroll
     for (int i = 0; i < 5; ++i) P.vrow[i] = src[min(part * 4 + i, nsrc - 1)];
   }
   P.rul = 0u;
-  if (part == 0) P.rul = *(const uint16_t*)(base + g.coeff_bytes);  // 2-aligned (r1 even)
+  if (part == 0) P.rul = *gbl((const uint16_t*)(base + g.coeff_bytes));  // 2-aligned (r1 even)
 }
 
 // 2^x on the hardware exp unit (one v_exp_f32). Softmax weights below 2^-126 flush to zero,
