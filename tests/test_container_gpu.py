@@ -126,7 +126,8 @@ def test_krt_reads_the_first_half_of_the_angle_rows():
 
 
 @pytest.mark.parametrize("cfg_name,B,n,HQ", [("safe", 1, 300, 24), ("campaign4x", 2, 129, 32),
-                                             ("tight", 2, 64, 8), ("safe", 1, 1, 24)])
+                                             ("tight", 2, 64, 8), ("safe", 1, 1, 24),
+                                             ("campaign4x", 3, 517, 64), ("safe", 2, 255, 16)])
 def test_v_out_matches_the_oracle(cfg_name, B, n, HQ):
     cfg = codec.CONFIGS[cfg_name]
     stores = [_store(cfg_name, n, seed=50 + b)[2] for b in range(B)]
@@ -141,3 +142,23 @@ def test_v_out_matches_the_oracle(cfg_name, B, n, HQ):
     rel = _rel(o, want)
     print(f"v_out {cfg_name} B={B} n={n}: rel {rel:.2e}")
     assert rel < 1e-5
+
+
+def test_long_sequence_walks_several_tiles_per_workgroup():
+    """At 8,300 tokens each workgroup walks several tiles (krt 3 of 64 tokens, v_out 2 of 128 on
+    a 256-CU part), so the next-tile prefetch and the double-buffered weights are exercised."""
+    n, HQ = 8300, 24
+    cfg, kl, vr = _store("safe", n, seed=71, rank=200, noise=0.05, max_rank=110)
+    cos, sin = _angles(n)
+    q = torch.randn(HQ, D, generator=torch.Generator().manual_seed(8)) * 0.1
+    s = container.krt(kl["coeff_q"].to(DEV), kl["coeff_scale"].to(DEV), kl["dec_q"].to(DEV),
+                      kl["dec_scale"].to(DEV), _rows(kl["resid"], 3), cos.to(DEV), sin.to(DEV),
+                      q.to(DEV), n, HQ, HQ // H, D)
+    p = torch.softmax(torch.randn(HQ, n, generator=torch.Generator().manual_seed(9)), -1)
+    o = container.v_out(p.to(DEV), _rows(vr, 3), n, HQ, HQ // H, D)
+    torch.cuda.synchronize()
+    want = ocont.krt(kl["coeff_q"], kl["coeff_scale"], kl["decoder_f"], kl["resid"], cos, sin, q,
+                     n, H, D, kl["res_k"], 3)
+    want_o = ocont.v_out(p, vr, n, H, D, cfg["k_lanes"], 3)
+    assert _rel(s, want) < 1e-4
+    assert _rel(o, want_o) < 1e-5
