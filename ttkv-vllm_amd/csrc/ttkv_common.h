@@ -87,6 +87,63 @@ __device__ __forceinline__ float load_act(const void* p, int dt, int64_t i) {
   return dt == TTKV_DTYPE_F16 ? f16_bits_to_float(b) : bf16_bits_to_float(b);
 }
 
+// N (4 or 8) consecutive activations from element i0 of p, as floats, with every load issued
+// before any conversion (one memory round trip instead of one per element). `vec`: element i0
+// is aligned to the group (N * element bytes, 16 at most), so each group is one or two wide loads.
+template <int N>
+__device__ __forceinline__ void load_act_n(const void* p, int dt, int64_t i0, bool vec,
+                                           float v[N]) {
+  static_assert(N == 4 || N == 8, "groups of 4 or 8");
+  if (dt == TTKV_DTYPE_F32) {
+    const float* q = (const float*)p + i0;
+    if (vec) {
+#pragma unroll
+      for (int k = 0; k < N / 4; ++k) {
+        const float4v x = *gbl((const float4v*)q + k);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[4 * k + j] = x[j];
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < N; ++k) v[k] = *gbl(q + k);
+    }
+    return;
+  }
+  const uint16_t* q = (const uint16_t*)p + i0;
+  uint32_t bits[N];
+  if (vec) {
+    if constexpr (N == 8) {
+      const u32x4 x = *gbl((const u32x4*)q);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        bits[2 * k] = x[k] & 0xffffu;
+        bits[2 * k + 1] = x[k] >> 16;
+      }
+    } else {
+      typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+      const u32x2 x = *gbl((const u32x2*)q);
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        bits[2 * k] = x[k] & 0xffffu;
+        bits[2 * k + 1] = x[k] >> 16;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < N; ++k) bits[k] = *gbl(q + k);
+  }
+#pragma unroll
+  for (int k = 0; k < N; ++k)
+    v[k] = dt == TTKV_DTYPE_F16 ? f16_bits_to_float(bits[k]) : bf16_bits_to_float(bits[k]);
+}
+
+// Whether element offsets that are multiples of 8 (fp32: 4) are 16-byte aligned in an
+// activation tensor with this base and row stride (elements).
+__device__ __forceinline__ bool act_rows_aligned(const void* p, int dt, int64_t row_stride) {
+  const int64_t eb = dt == TTKV_DTYPE_F32 ? 4 : 2;
+  return ((uintptr_t)p % 16 == 0) && ((row_stride * eb) % 16 == 0);
+}
+
 // Round-to-nearest-even fp32 -> bf16 bits (NaN kept quiet).
 __device__ __forceinline__ uint16_t float_to_bf16_bits(float f) {
   uint32_t u = __builtin_bit_cast(uint32_t, f);

@@ -338,13 +338,16 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
       draw[mi][8 * KSTEPS + j] = KTAIL && ar < g.r1 ? dec[(int64_t)ar * HD + dim] : 0.f;
     }
   }
+  // (rows n >= G of the fragment are zero: they load head G - 1 and discard it, so the loads
+  // carry no branch and go out together)
   float qraw[8];
+  {
+    const bool qvec = act_rows_aligned(a.q, a.q_dtype, a.q_row_stride);
+    const int64_t qb = qrow * a.q_row_stride + (int64_t)(h * G + min(n, G - 1)) * kD;
+    load_act_n<4>(a.q, a.q_dtype, qb + dl, qvec, qraw);
+    load_act_n<4>(a.q, a.q_dtype, qb + 64 + dl, qvec, qraw + 4);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int dim = (j < 4 ? dl + j : 64 + dl + j - 4);
-    qraw[j] = n < G ? load_act(a.q, a.q_dtype,
-                               qrow * a.q_row_stride + (int64_t)(h * G + n) * kD + dim)
-                    : 0.f;
+    for (int j = 0; j < 8; ++j) qraw[j] = n < G ? qraw[j] : 0.f;
   }
 
   // ---- code tables, and this chunk's block ids

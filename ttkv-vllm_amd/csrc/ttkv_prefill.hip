@@ -194,18 +194,23 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
   // ---- query fragments (B operand of S^T = Kp Q^T): column = query 16*wv + n of the block
   const int qj = qa + 16 * wv + n;
   const bool qvalid = qj < qe;
+  // (a column past the chunk loads the chunk's first query and discards it, so the loads carry
+  // no branch and go out together)
   half8 qf[G][4];
+  {
+    const bool qvec = act_rows_aligned(a.q, a.q_dtype, a.q_row_stride);
+    const int64_t qb = (int64_t)(q0 + (qvalid ? qj : qa)) * a.q_row_stride + (int64_t)h * G * kD +
+                       8 * gq;
 #pragma unroll
-  for (int gg = 0; gg < G; ++gg)
+    for (int gg = 0; gg < G; ++gg)
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
+      for (int ks = 0; ks < 4; ++ks) {
+        float t[8];
+        load_act_n<8>(a.q, a.q_dtype, qb + (int64_t)gg * kD + 32 * ks, qvec, t);
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        qf[gg][ks][i] = qvalid ? (_Float16)load_act(a.q, a.q_dtype,
-                                                    (int64_t)(q0 + qj) * a.q_row_stride +
-                                                        (int64_t)(h * G + gg) * kD + 32 * ks +
-                                                        8 * gq + i)
-                               : (_Float16)0.0f;
+        for (int i = 0; i < 8; ++i) qf[gg][ks][i] = qvalid ? (_Float16)t[i] : (_Float16)0.0f;
+      }
+  }
 
   // ---- decoder fragments (A operand of the reconstruction, M = dims), resident in registers
   const int HD = g.H * kD;
