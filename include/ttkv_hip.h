@@ -216,7 +216,7 @@ int ttkv_dense_decode_paged(int32_t H, int32_t num_heads, int32_t d, float scale
  *   h = p / (num_heads / H); cos / sin [n, d] fp32 in rope_apply's frame (absolute position i)
  *   with duplicated halves (column j == column j + d/2, as rotate-half tables are built): only
  *   columns [0, d/2) are read, as the codec kernel does (codec/ttkv_kernels.cu:472-491);
- *   query [B, num_heads, d] fp32 post-RoPE. res_bitmap = NULL: no residual (mode without rows).
+ *   query [B, num_heads, d] fp32 post-RoPE. cos, sin, query and the bitmaps are 16-byte aligned. res_bitmap = NULL: no residual (mode without rows).
  *   Carried at fp32 accuracy (hi + lo fp16 MFMA operands).
  * ttkv_container_v_out: out [B, num_heads, d] fp32 += sum_i p[b, p, i] * V[b, h, i, :];
  *   p[b, p, i] at p + b*p_batch_stride + p*p_head_stride + i. `out` must be zero-filled: the

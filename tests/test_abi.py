@@ -180,6 +180,7 @@ def test_container_host_refusals_before_launch():
     assert krt(q=0) == 1 and b"null" in L.ttkv_last_error()
     assert krt(pk=0) == 1 and b"residual" in L.ttkv_last_error()
     assert krt(cos=8) == 1 and b"aligned" in L.ttkv_last_error()
+    assert krt(q=24) == 1 and b"aligned" in L.ttkv_last_error()
     assert krt(HQ=40, H=8) == 2                                    # 5 heads per KV head
     assert krt(n=0) == 0                                           # nothing to do
     assert vout(ph=63) == 1 and b"strides" in L.ttkv_last_error()

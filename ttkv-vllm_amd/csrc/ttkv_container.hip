@@ -141,14 +141,19 @@ __global__ __launch_bounds__(kCThreads, 2) void container_krt_kernel(ContainerAr
   }
   // ---- query fragments (A operand of q.k, M = heads, K = this wave's 32 dims in the order of
   // the rotated-key fragments), hi + lo fp16; rows >= G are zero
+  // (rows n >= G load head G - 1 and discard it: no branch around the loads, one round trip)
   half8 qhi, qlo;
+  {
+    const float* qr = a.q + ((int64_t)bz * a.H * G + hv * G + min(n, G - 1)) * kD;
+    const float4v x0 = *gbl((const float4v*)(qr + dl));
+    const float4v x1 = *gbl((const float4v*)(qr + 64 + dl));
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int dim = j < 4 ? dl + j : 64 + dl + j - 4;
-    const float x = n < G ? a.q[((int64_t)bz * a.H * G + hv * G + n) * kD + dim] : 0.f;
-    const _Float16 hi = (_Float16)x;
-    qhi[j] = hi;
-    qlo[j] = (_Float16)(x - (float)hi);
+    for (int j = 0; j < 8; ++j) {
+      const float x = n < G ? (j < 4 ? x0[j] : x1[j - 4]) : 0.f;
+      const _Float16 hi = (_Float16)x;
+      qhi[j] = hi;
+      qlo[j] = (_Float16)(x - (float)hi);
+    }
   }
 
   // ---- the next tile's bytes in registers while the current one computes: this thread's share
@@ -488,8 +493,8 @@ int container_krt(int H, int HQ, int d, int B, int n, int r1, const int8_t* cq, 
   if (!cq || !cs || !dec || !cosv || !sinv || !q || !s)
     return host_fail(TTKV_E_INVALID, "null pointer argument");
   if (has_res && (!pk || !rs)) return host_fail(TTKV_E_INVALID, "residual arrays incomplete");
-  if (((uintptr_t)cosv | (uintptr_t)sinv | (uintptr_t)bm) % 16)
-    return host_fail(TTKV_E_INVALID, "cos / sin / bitmap must be 16-byte aligned");
+  if (((uintptr_t)cosv | (uintptr_t)sinv | (uintptr_t)bm | (uintptr_t)q) % 16)
+    return host_fail(TTKV_E_INVALID, "cos / sin / bitmap / query must be 16-byte aligned");
   if (B == 0 || n == 0) return TTKV_OK;
   ContainerArgs a{};
   a.n = n;
