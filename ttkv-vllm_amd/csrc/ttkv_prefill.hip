@@ -277,6 +277,9 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
   RawSlot<2 * KSTEPS> P;
   fetch_raw_slot<2 * KSTEPS>(P, slot_base(k0), part, g, k_row_off, v_row_off);
 
+  // score-tensor rows 16-byte aligned: every 4-key group starts on a 16-byte boundary
+  const bool s_vec = SCORES && ((uintptr_t)a.s_out % 16 == 0) && a.s_q_stride % 4 == 0 &&
+                     a.s_head_stride % 4 == 0 && k0 % 4 == 0;
   for (int tt = k0; tt < k1; tt += kPTile) {
     const int ntile = min(kPTile, k1 - tt);
     // ------------------------------------------------------------ commit this tile's bytes
@@ -449,18 +452,27 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
     }
     const int lim = p0 + qj;  // last key this lane's query may see
     if constexpr (SCORES) {
-      // lane holds keys tt + 16kt + 4gq + jj of query qj
+      // lane holds keys tt + 16kt + 4gq + jj of query qj: one 16-byte store per 4 keys where the
+      // rows are 16-byte aligned and all 4 keys are in range, single stores otherwise
       if (qvalid) {
 #pragma unroll
         for (int gg = 0; gg < G; ++gg) {
           float* srow = a.s_out + (int64_t)(h * G + gg) * a.s_head_stride + (int64_t)qj * a.s_q_stride;
 #pragma unroll
-          for (int kt = 0; kt < 4; ++kt)
+          for (int kt = 0; kt < 4; ++kt) {
+            const int key0 = tt + 16 * kt + 4 * gq;
+            float4v v;
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-              const int key = tt + 16 * kt + 4 * gq + jj;
-              if (key < k1) srow[key] = key <= lim ? sacc[kt][gg][jj] * a.scale : -INFINITY;
+            for (int jj = 0; jj < 4; ++jj)
+              v[jj] = key0 + jj <= lim ? sacc[kt][gg][jj] * a.scale : -INFINITY;
+            if (s_vec && key0 + 3 < k1) {
+              *(float4v*)&srow[key0] = v;
+            } else {
+#pragma unroll
+              for (int jj = 0; jj < 4; ++jj)
+                if (key0 + jj < k1) srow[key0 + jj] = v[jj];
             }
+          }
         }
       }
     } else {
