@@ -654,8 +654,16 @@ static int prefill_dispatch_k(const PrefillArgs& a, int ksteps, int grid, hipStr
 
 // Key range per split: enough splits that the grid fills the chip about once at two resident
 // workgroups per CU, each split at least 256 keys.
-static int prefill_kchunk(int items, int max_seq_len, int block_size) {
-  const int64_t target = 2LL * device_cu_count();
+// Workgroups resident per CU (the kernel's launch bound): the G <= 2 kernels and the score-mode
+// kernels up to G = 3 fit two, the others one.
+static int prefill_blocks_per_cu(int G, bool scores) {
+  return ((scores && G <= 3) || G <= 2) ? 2 : 1;
+}
+
+// Key range per work item: the items fill about one round of resident workgroups (fewer key
+// splits where only one workgroup fits a CU: each split's partials cost a write and a read).
+static int prefill_kchunk(int items, int max_seq_len, int block_size, int per_cu) {
+  const int64_t target = (int64_t)per_cu * device_cu_count();
   const int64_t want = std::max<int64_t>(1, (target + items - 1) / std::max(items, 1));
   int64_t kc = (std::max(max_seq_len, 1) + want - 1) / want;
   kc = (kc + kPTile - 1) / kPTile * kPTile;
@@ -676,7 +684,7 @@ static int64_t prefill_part_bytes(const Geom& g, int G, int nr, int max_q_len, i
                                   int block_size) {
   const int n_qb = (max_q_len + kPQ - 1) / kPQ;
   const int items = nr * g.H * n_qb;
-  const int kc = prefill_kchunk(items, max_seq_len, block_size);
+  const int kc = prefill_kchunk(items, max_seq_len, block_size, prefill_blocks_per_cu(G, false));
   const int nsplit = std::max(1, (max_seq_len + kc - 1) / kc);
   if (nsplit == 1) return 0;
   return (int64_t)items * nsplit * G * kPQ * (kD + 2) * 4;
@@ -788,7 +796,7 @@ int prefill_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype
     b.ri0 = ri0;
     b.num_reqs = std::min(slice, num_reqs - ri0);
     const int items = b.num_reqs * g.H * a.n_qb;
-    b.kchunk = prefill_kchunk(items, max_seq_len, block_size);
+    b.kchunk = prefill_kchunk(items, max_seq_len, block_size, prefill_blocks_per_cu(G, scores));
     b.nsplit = std::max(1, (max_seq_len + b.kchunk - 1) / b.kchunk);
     if (!scores && b.nsplit > 1) {  // counters [item]: items <= kMaxCounters
       b.ws_cnt = (int*)ws;
