@@ -287,8 +287,7 @@ __global__ __launch_bounds__(kCThreads, 2) void container_krt_kernel(ContainerAr
 struct VoutSmem {
   uint32_t raw[kCVTile][kCRawDw];
   uint8_t code[kCVTile][kCCode];
-  float pw[2][8][kCVTile];  // double-buffered by tile parity
-  float vr[2][kCVTile];
+  float pw[2][8][kCVTile];  // p * ruler, double-buffered by tile parity
   float part[4][8][kD];  // per-wave sums [wave][head][dim]
   uint2 lut[256];
   uint32_t lut3[4096];
@@ -318,20 +317,21 @@ __global__ __launch_bounds__(kCThreads, 2) void container_v_out_kernel(Container
 
   uint32_t x[2][5];
   int sh[2];
-  float rsv[2], pwv[kPw];
+  // weights and their token's row ruler: the product p * ruler is what the accumulation uses
+  float pwv[kPw], rwv[kPw];
   auto fetch = [&](int tile) {
     const int i0 = tile * kCVTile;
 #pragma unroll
     for (int pass = 0; pass < 2; ++pass) {
       const int tok = ptok + 64 * pass;
-      const bool valid = i0 + tok < a.n;
-      load_row_quarter(a, row0 + i0 + tok, valid, part, x[pass], sh[pass]);
-      rsv[pass] = part == 0 && valid ? a.rs[row0 + i0 + tok] : 0.f;
+      load_row_quarter(a, row0 + i0 + tok, i0 + tok < a.n, part, x[pass], sh[pass]);
     }
 #pragma unroll
     for (int k = 0; k < kPw; ++k) {
       const int idx = tid + kCThreads * k, tok = idx & (kCVTile - 1), g = idx / kCVTile;
-      pwv[k] = g < G && i0 + tok < a.n ? pb[(int64_t)g * a.p_head_stride + i0 + tok] : 0.f;
+      const bool ok = g < G && i0 + tok < a.n;
+      pwv[k] = ok ? pb[(int64_t)g * a.p_head_stride + i0 + tok] : 0.f;
+      rwv[k] = ok ? a.rs[row0 + i0 + tok] : 0.f;
     }
   };
   fetch(tile0);
@@ -347,20 +347,18 @@ __global__ __launch_bounds__(kCThreads, 2) void container_v_out_kernel(Container
   }
 
   for (int tile = tile0; tile < tile1; ++tile) {
-    // ---- commit the prefetched tile, then request the next one. The rulers and weights are
+    // ---- commit the prefetched tile, then request the next one. The scaled weights are
     // double-buffered: a thread still accumulating the previous tile reads the other buffer, and
     // the staged rows and codes are only rewritten past a barrier that follows its reads.
     const int buf = (tile - tile0) & 1;
 #pragma unroll
-    for (int pass = 0; pass < 2; ++pass) {
-      const int tok = ptok + 64 * pass;
-      commit_row_quarter(part, sh[pass], x[pass], S.raw[tok]);
-      if (part == 0) S.vr[buf][tok] = rsv[pass] * rscale;
-    }
+    for (int pass = 0; pass < 2; ++pass)
+      commit_row_quarter(part, sh[pass], x[pass], S.raw[ptok + 64 * pass]);
 #pragma unroll
     for (int k = 0; k < kPw; ++k) {
       const int idx = tid + kCThreads * k;
-      if (idx < G * kCVTile) S.pw[buf][idx / kCVTile][idx & (kCVTile - 1)] = pwv[k];
+      if (idx < G * kCVTile)
+        S.pw[buf][idx / kCVTile][idx & (kCVTile - 1)] = pwv[k] * (rwv[k] * rscale);
     }
     if (tile + 1 < tile1) fetch(tile + 1);
     __syncthreads();
@@ -370,11 +368,10 @@ __global__ __launch_bounds__(kCThreads, 2) void container_v_out_kernel(Container
                              &S.code[tid >> 1][64 * (tid & 1)]);
     __builtin_amdgcn_s_setprio(0);
     __syncthreads();
-    // ---- acc[g][i] += p[g][tok] * ruler[tok] * code[tok][4dg + i] over this thread's tokens
+    // ---- acc[g][i] += (p[g][tok] * ruler[tok]) * code[tok][4dg + i] over this thread's tokens
 #pragma unroll
     for (int k4 = 0; k4 < 4; ++k4) {
       const int t0 = 16 * ph + 4 * k4;
-      const float4v vr4 = *(const float4v*)&S.vr[buf][t0];
       float4v pw4[G];
 #pragma unroll
       for (int g = 0; g < G; ++g) pw4[g] = *(const float4v*)&S.pw[buf][g][t0];
@@ -384,7 +381,7 @@ __global__ __launch_bounds__(kCThreads, 2) void container_v_out_kernel(Container
         codes4<BITS>(*(const uint32_t*)&S.code[t0 + j][4 * dg], v);
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-          const float w = pw4[g][j] * vr4[j];
+          const float w = pw4[g][j];
           if constexpr (BITS == 4) wsum[g] += w;
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[g][i] = fmaf(w, v[i], acc[g][i]);
