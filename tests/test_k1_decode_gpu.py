@@ -80,6 +80,22 @@ def test_bf16_query_and_output():
     assert e.max() <= 1e-2 and e.mean() <= 2e-3  # bf16 output rounding (8-bit mantissa)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_queries_in_rows_that_are_not_16_byte_aligned(dtype):
+    """Query rows at a stride of HQ*d + 2 elements (a view into a wider buffer) are not 16-byte
+    aligned, so the kernel loads them element by element instead of in wide loads: same result."""
+    lens = [300, 130, 64]
+    stores = [fitted_store("safe", n, seed=90 + i) for i, n in enumerate(lens)]
+    q = synth.queries(len(lens), seed=15).to(dtype)
+    wide = torch.zeros(len(lens), q.shape[1] * 128 + 2, dtype=dtype)
+    wide[:, :q.shape[1] * 128] = q.reshape(len(lens), -1)
+    qv = wide.to("cuda")[:, :q.shape[1] * 128].view(len(lens), q.shape[1], 128)
+    assert qv.stride(0) == q.shape[1] * 128 + 2
+    cache = llama3_cache(512)
+    got, pg = _run_k1(stores, qv, cache, seed=16)
+    _check(got, _oracle(stores, q, cache, pg), f"strided {dtype} queries")
+
+
 def test_rotation_is_applied_per_row():
     """Negative control (test_reference.py:81-113 restated on the kernel): rotating every row by
     its neighbour's position must change the output by far more than the tolerance."""
