@@ -92,6 +92,38 @@ def test_attend_mode_ragged_batch_with_splits():
         _check(out[s:e].float(), want[r], f"attend req {r} {shapes[r]}", exact_inf=False)
 
 
+def test_attend_mode_queries_in_rows_that_are_not_16_byte_aligned():
+    """Query rows at a stride of HQ*d + 2 elements (a view into a wider buffer): the kernel loads
+    them element by element instead of in wide loads, with the same result."""
+    shapes = [(500, 70), (900, 130)]
+    stores = [fitted_store("safe", n, seed=17 + i) for i, (n, _) in enumerate(shapes)]
+    cache = llama3_cache(2048)
+    pg, dec_pool, dec_map = _dev_inputs(stores, seed=5)
+    q = torch.cat([synth.queries(Q, seed=200 + i).reshape(Q, HQ, 128)
+                   for i, (_, Q) in enumerate(shapes)])
+    wide = torch.zeros(q.shape[0], HQ * 128 + 2, dtype=q.dtype)
+    wide[:, :HQ * 128] = q.reshape(q.shape[0], -1)
+    qv = wide.cuda()[:, :HQ * 128].view(q.shape[0], HQ, 128)
+    assert qv.stride(0) == HQ * 128 + 2
+    qsl = torch.tensor([0] + list(torch.tensor([Q for _, Q in shapes]).cumsum(0)),
+                       dtype=torch.int32)
+    out = torch.zeros_like(q, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    lay = stores[0]["lay"]
+    kernels.prefill_paged(lay, qv, pg["page"].cuda(), 16, pg["block_table"].cuda(),
+                          pg["seq_lens"].cuda(), qsl.cuda(), max(Q for _, Q in shapes),
+                          max(n for n, _ in shapes), dec_map, dec_pool, cache.cuda(), SCALE,
+                          out=out, error_word=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    want = attend.paged_continuation(lay, pg["page"], pg["block_table"], pg["seq_lens"], qsl,
+                                     q.double(), [s["decoder"] for s in stores], cache, 16, SCALE,
+                                     dtype=torch.float64)
+    for r in range(len(shapes)):
+        s, e = int(qsl[r]), int(qsl[r + 1])
+        _check(out[s:e].float(), want[r], f"strided queries req {r}", exact_inf=False)
+
+
 def test_attend_mode_req_index_subset_bf16():
     """`req_index` selects batch rows (decodes at the front are skipped); bf16 in and out."""
     shapes = [(50, 1), (600, 70), (1200, 200)]
