@@ -45,3 +45,79 @@ def paged(stores, block_size: int = 16, seed: int = 0, width_pad: int = 0):
 def llama3_cache(max_pos: int):
     inv = orope.inv_freq_llama3(D, **orope.LLAMA32_3B_ROPE)
     return orope.vllm_cos_sin_cache(inv, max_pos)
+
+
+def device_store(cfg_name: str, lens, seed: int, r1: int = 110, block_size: int = 16,
+                 fit_on: int = 2048, dev: str = "cuda"):
+    """A paged store for requests of `lens` tokens, built the way serving builds it: each
+    request's first `fit_on` tokens fitted on the device (`vllm_ttkv.encode.fit_into_budget`) and
+    every token packed by the K3 write kernel (the first chunk from the fit's coefficients, the
+    rest by frozen projection). Full-size stores in seconds, where the CPU oracle's fit would take
+    minutes; the oracle then reads the SAME slot bytes, so K1/K2 are checked against it exactly
+    as on a store the oracle built.
+
+    Returns dict(lay (oracle Layout), play (product TTKLayout), page [n_slots, C] u8 (device),
+    block_table, seq_lens, dec_map, dec_pool, pinv_pool (device), decoders (CPU list), num_blocks).
+    """
+    from vllm_ttkv import encode as penc, kernels
+    from vllm_ttkv.layout import CONFIGS as PCONFIGS, layout_for_config as play_for
+
+    cfg = codec.CONFIGS[cfg_name]
+    lay = layout_for_config(cfg, r1=r1)
+    play = play_for(PCONFIGS[cfg_name], r1)
+    B = len(lens)
+    bt, nblk = synth.shuffled_block_table(lens, block_size, seed=seed, extra_blocks=3)
+    C = lay.compressed_bytes_per_token()
+    page = torch.zeros(nblk * block_size, C, dtype=torch.uint8, device=dev)
+    dec_pool = torch.zeros(B, r1, H * D, dtype=torch.float32, device=dev)
+    pinv_pool = torch.zeros(B, H * D, r1, dtype=torch.float32, device=dev)
+    dec_map = torch.full((nblk,), -1, dtype=torch.int32)
+    for r in range(B):
+        dec_map[bt[r, 0]] = r
+    bt_d, dec_map_d = bt.to(dev), dec_map.to(dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    fk_all, rest = [], []
+    for r, n in enumerate(lens):
+        s = seed * 1000003 + r
+        K = synth.keys(n, seed=s, device=dev).permute(1, 0, 2)      # [n, H, d]
+        V = synth.values(n, seed=s, device=dev).permute(1, 0, 2)
+        f = min(fit_on, n)
+        fk = penc.fit_into_budget(K[:f].permute(1, 0, 2).contiguous(), play, PCONFIGS[cfg_name])
+        dec_pool[r] = fk.decoder.decoder_f
+        pinv_pool[r] = fk.decoder.pinv
+        p = torch.arange(n)
+        slot = (bt[r, p // block_size].long() * block_size + p % block_size).to(dev)
+        fk_all.append((K[:f], V[:f], slot[:f], fk.coeff_q, fk.coeff_scale))
+        rest.append((K[f:], V[f:], slot[f:]))
+
+    def _write(parts, cq=None, cs=None):
+        ln = [x[0].shape[0] for x in parts]
+        if not sum(ln):
+            return
+        reqs = [i for i, l in enumerate(ln) if l]
+        qsl = torch.tensor([0] + list(torch.tensor([ln[i] for i in reqs]).cumsum(0)),
+                           dtype=torch.int32, device=dev)
+        kernels.write_paged(play, torch.cat([parts[i][0] for i in reqs]).contiguous(),
+                            torch.cat([parts[i][1] for i in reqs]).contiguous(),
+                            torch.cat([parts[i][2] for i in reqs]), qsl,
+                            bt_d[torch.tensor(reqs, device=dev)].contiguous(), dec_map_d,
+                            dec_pool, pinv_pool, page,
+                            coeff_q_in=None if cq is None else torch.cat([cq[i] for i in reqs]),
+                            coeff_scale_in=None if cs is None else torch.cat([cs[i] for i in reqs]),
+                            error_word=err)
+
+    _write(fk_all, [x[3] for x in fk_all], [x[4] for x in fk_all])
+    _write(rest)
+    torch.cuda.synchronize()
+    if int(err.item()):
+        raise RuntimeError(f"store build: device error word {int(err.item())}")
+    return dict(lay=lay, play=play, page=page, block_table=bt_d, seq_lens=torch.tensor(
+        lens, dtype=torch.int32, device=dev), dec_map=dec_map_d, dec_pool=dec_pool,
+        pinv_pool=pinv_pool, decoders=[dec_pool[r].cpu() for r in range(B)], num_blocks=nblk,
+        block_size=block_size)
+
+
+def config3_lens(seed: int = 3, B: int = 8):
+    """BASELINE config 3's contexts: 8 lengths drawn uniformly from [1000, 14400], seeded."""
+    g = torch.Generator().manual_seed(seed)
+    return [int(x) for x in torch.randint(1000, 14401, (B,), generator=g)]

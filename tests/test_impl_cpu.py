@@ -142,18 +142,75 @@ def test_backend_flags():
 
 
 def test_decoder_registry_round_trip():
+    """Fixed-capacity pool: registration, release, slot reuse, eviction of the oldest
+    registration that is not live, and refusal when every slot is live. The pools are never
+    reallocated (a captured graph keeps valid pointers)."""
     lay = layout_for_config(CONFIGS["safe"], 16)
     from vllm_ttkv.encode import KDecoder
-    st = rope_store.TTKVRopeStore("L0", torch.zeros(8, 128), lay, num_blocks=10, capacity=1)
+    rope_store.clear_stores()
+    st = rope_store.TTKVRopeStore(24, 8, 128, torch.zeros(8, 128), "L0", lay, num_blocks=10,
+                                  capacity=2)
+    pools = (st.dec_pool.data_ptr(), st.pinv_pool.data_ptr(), st.dec_map.data_ptr())
     d1 = KDecoder(torch.randn(16, 8 * 128))
     d2 = KDecoder(torch.randn(16, 8 * 128))
+    d3 = KDecoder(torch.randn(16, 8 * 128))
     s1 = st.register(3, d1)
-    s2 = st.register(7, d2)                       # grows the pool
+    s2 = st.register(7, d2)
     assert st.dec_map[3] == s1 and st.dec_map[7] == s2 and s1 != s2
     assert torch.equal(st.dec_pool[s2], d2.decoder_f)
+    assert torch.allclose(st.pinv_pool[s2], d2.pinv)
     st.release(3)
     assert st.dec_map[3] == -1 and 3 not in st.decoders
-    assert st.register(5, d1) == s1               # slot reused
+    assert st.register(5, d1) == s1               # freed slot reused
+    assert st.register(5, d3) == s1               # re-registering a key keeps its slot
+    assert torch.equal(st.dec_pool[s1], d3.decoder_f)
+    # full: the oldest registration not named live is evicted (7, registered before 5)
+    s9 = st.register(9, d1, live=[5, 9])
+    assert s9 == s2 and st.dec_map[7] == -1 and 7 not in st.decoders and st.dec_map[9] == s9
+    with pytest.raises(RuntimeError, match="live requests"):
+        st.register(2, d2, live=[5, 9, 2])
     with pytest.raises(IndexError):
         st.register(10, d1)
+    assert (st.dec_pool.data_ptr(), st.pinv_pool.data_ptr(), st.dec_map.data_ptr()) == pools
     rope_store.clear_stores()
+
+
+def test_reference_calling_sequence_binds():
+    """The reference's own adapter-test sequence (tests/test_impl_decode.py:218-225): build the
+    store with its constructor, then `register_decoder(name, request_key(row), KDecoder(dec))`
+    through the module functions. Registrations made before a store exists are adopted by it;
+    the device map is bound when the cache's block count is known."""
+    from vllm_ttkv.encode import KDecoder
+    lay = layout_for_config(CONFIGS["safe"], 16)
+    rope_store.clear_stores()
+    name = "model.layers.4.self_attn"
+    dec_a, dec_b = torch.randn(16, 1024), torch.randn(16, 1024)
+    bt = torch.tensor([[6, 2, 9], [4, 0, -1]], dtype=torch.int32)
+    rope_store.register_decoder(name, rope_store.request_key(bt[0]), KDecoder(dec_a))  # pending
+    assert rope_store.decoder_for_request(name, 6).decoder_f is not None
+    store = rope_store.TTKVRopeStore(24, 8, 128, torch.zeros(64, 128), name, lay)
+    assert rope_store.store_for_layer(name) is store and rope_store.layout_for_layer(name) is lay
+    rope_store.register_decoder(name, rope_store.request_key_host(bt[1].tolist()),
+                                KDecoder(dec_b))
+    assert store.dec_map is None                                   # not bound yet
+    again = rope_store.ensure_store(name, torch.zeros(64, 128), 24, 8, 128, lay, num_blocks=12)
+    assert again is store and store.dec_map.numel() == 12
+    for key, dec in ((6, dec_a), (4, dec_b)):
+        slot = int(store.dec_map[key])
+        assert slot >= 0 and torch.equal(store.dec_pool[slot], dec)
+        assert rope_store.decoder_for_request(name, key).decoder_f is not None
+    assert rope_store.decoder_for_layer(name) is None              # no layer-level decoder
+    rope_store.release_decoder(name, 6)
+    assert int(store.dec_map[6]) == -1 and rope_store.decoder_for_request(name, 6) is None
+    with pytest.raises(ValueError):
+        rope_store.request_key(torch.zeros(0, dtype=torch.int32))
+    with pytest.raises(RuntimeError):
+        rope_store.ensure_store("model.layers.99.x", torch.zeros(4, 128), 24, 8, 128, None)
+    rope_store.clear_stores()
+
+
+def test_layer_index_of_vllm_names():
+    li = rope_store._layer_index
+    assert li("model.layers.7.self_attn.attn") == 7
+    assert li("model.decoder_layers.3.attn.5") == 3
+    assert li("layers.12") == 12 and li("attn_9") == 9 and li("attn") is None

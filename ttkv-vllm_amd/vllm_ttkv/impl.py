@@ -32,7 +32,7 @@ from . import _hip, kernels
 from . import encode as enc
 from .layout import CONFIGS, TTKLayout
 from .patch import take_raw_k
-from .rope_store import ensure_store, layout_for_layer
+from .rope_store import decoder_for_layer, ensure_store, layout_for_layer
 
 logger = logging.getLogger("vllm.ttkv")
 
@@ -154,10 +154,13 @@ class TTKVAttentionImpl(_ImplBase):
 
         name = getattr(layer, "layer_name", None)
         stash = take_raw_k(name)                # pops: the write comes first, unconditionally
-        store = ensure_store(name, self._cos_sin_cache(layer, stash), lay, cache.shape[0])
+        store = ensure_store(name, self._cos_sin_cache(layer, stash), self.num_heads,
+                             self.num_kv_heads, self.head_size, lay,
+                             num_blocks=int(cache.shape[0]))
         self._write_store(lay, cache, stash, value, md, plan, store)
 
         q3 = query.view(n_tokens, self.num_heads, self.head_size)
+        self._layer_decoder = getattr(layer, "ttkv_decoder_f", None)
         if plan.n_decodes:
             nd = plan.n_decodes
             self._decode(lay, cache, store, q3, md, nd, output)
@@ -195,8 +198,12 @@ class TTKVAttentionImpl(_ImplBase):
                                 store.pinv_pool, cache, error_word=self.error_word,
                                 workspace=self._write_workspace(lay, N, K.device))
             return
-        # A step with prefill chunks: a request without a decoder is on its first chunk and is
-        # fitted (encode.py:257-298); one host read of the first block ids and lengths decides.
+        # A step with prefill chunks. A request whose whole context arrives in this step
+        # (seq_len == q_len) is on its first chunk and is fitted (encode.py:257-298) -- ALWAYS,
+        # even when its key already has a decoder: keys are first block ids, and a finished
+        # request's recycled first block must not hand its basis to the next request. The fit
+        # re-registers the key (its slot is reused). One host read of the first block ids and
+        # lengths decides.
         keys = [int(x) for x in md.block_table[:plan.n_reqs, 0].tolist()]
         seq_lens = [int(x) for x in md.seq_lens[:plan.n_reqs].tolist()]
         cfg = CONFIGS[os.environ.get("VLLM_TTKV_CONFIG", "safe")]
@@ -205,15 +212,15 @@ class TTKVAttentionImpl(_ImplBase):
             s, e = plan.qsl[r], plan.qsl[r + 1]
             if e <= s:
                 continue
-            if store.decoders.get(keys[r]) is None:
-                if seq_lens[r] != e - s:
-                    raise RuntimeError(
-                        f"request {keys[r]} arrives with seq_len={seq_lens[r]} but {e - s} tokens "
-                        f"in this step and has no fitted decoder: a continuation of a request "
-                        f"whose first chunk never reached the writer")
+            if seq_lens[r] == e - s:
                 fk = enc.fit_into_budget(K[s:e].permute(1, 0, 2), lay, cfg)
-                store.register(keys[r], fk.decoder)
+                store.register(keys[r], fk.decoder, live=keys)
                 fitted.append((r, fk))
+            elif store.decoders.get(keys[r]) is None:
+                raise RuntimeError(
+                    f"request {keys[r]} arrives with seq_len={seq_lens[r]} but {e - s} tokens "
+                    f"in this step and has no fitted decoder: a continuation of a request "
+                    f"whose first chunk never reached the writer")
             else:
                 frozen.append(r)
         dev = K.device
@@ -261,6 +268,8 @@ class TTKVAttentionImpl(_ImplBase):
 
     def _decode(self, lay, cache, store, q3, md, nd, output):
         bs = self._block_size(cache)
+        if nd == 1:
+            self._single_request_fallback(store, md)
         max_len = int(md.max_seq_len) if md.max_seq_len else int(md.seq_lens[:nd].max())
         kernels.decode_paged(lay, q3, cache, bs, md.block_table[:nd].to(torch.int32),
                              md.seq_lens[:nd].to(torch.int32),
@@ -268,6 +277,20 @@ class TTKVAttentionImpl(_ImplBase):
                              store.dec_pool, store.cos_sin_cache, self.scale, out=output,
                              workspace=self._workspace(lay, nd, max_len, bs, q3.device),
                              error_word=self.error_word)
+
+    def _single_request_fallback(self, store, md):
+        """With ONE decode request, a layer-level decoder (`layer.ttkv_decoder_f` or
+        `store.decoder_f`) is that request's decoder when none is registered under its key
+        (reference impl.py:463-477, 891-901). Only when such a decoder exists is the key read
+        back to the host; the ordinary path reads nothing."""
+        dec = getattr(self, "_layer_decoder", None)
+        if dec is None:
+            dec = decoder_for_layer(store.layer_name)
+        if dec is None:
+            return
+        key = int(md.block_table[0, 0])
+        if store.decoders.get(key) is None:
+            store.register(key, enc.KDecoder(dec), live=(key,))
 
     def _prefill(self, lay, cache, store, q3, key, value, md, plan, output):
         seq_lens = [int(x) for x in md.seq_lens[:plan.n_reqs].tolist()]

@@ -8,13 +8,17 @@ working. The byte format is the reference's, unchanged:
     K slot = r1 int8 coefficients | fp16 coefficient ruler | H x (bitmap d/8 | codes | fp16 ruler)
     V slot = H x (bitmap d/8 | codes | fp16 ruler)
 
-Packing and unpacking are done on the GPU by `libttkv_hip` (the write and read kernels); this
-module only owns the arithmetic that sizes the cache and addresses the fields.
+On the serving path, packing and unpacking are done on the GPU by `libttkv_hip` (the write and
+read kernels). This module owns the arithmetic that sizes the cache and addresses the fields, and
+the same byte moves as tensor operations (`pack_k_slots` and friends) for callers that hold a
+store as separate row arrays.
 """
 from __future__ import annotations
 
 import math
 from dataclasses import dataclass
+
+import torch
 
 # The three shipped allocations (codec/ttkv_codec.py:272-298). `res_frac` is a FRACTION of d;
 # `k_lanes` (the V lane count) is ABSOLUTE.
@@ -103,3 +107,102 @@ def layout_for_config(cfg: dict, r1: int, H: int = 8, d: int = 128) -> TTKLayout
     return TTKLayout(H=H, d=d, r1=r1, qbits=cfg["qbits"],
                      res_k=max(int(d * cfg["res_frac"]), 1), res_bits=cfg["res_bits"],
                      v_lanes=cfg["k_lanes"], v_bits=cfg["vbits"])
+
+
+# ---------------------------------------------------------------- host-side slot (un)packing
+# The write kernel packs slots on the device; these are the same byte moves as torch tensor
+# operations, for callers that hold a store as separate row arrays (the reference's
+# `pack_k_slots` / `unpack_k_slots` / `pack_v_slots` / `unpack_v_slots`, layout.py:161-261).
+# A "row store" is any object with `rows` (H*n), `bitmap` [H*n, d/8] u8, `packed` [H*n, PB] u8
+# and `scale` [H*n] fp16, rows in (head, token) order h*n + i. Each field of all H heads moves as
+# ONE strided copy through a [n, H, row_bytes] view of the slot, not a loop over heads.
+
+def _head_rows(slots, off: int, H: int, row: int):
+    """`slots[:, off + h*row + b]` as a [n, H, row] view (no copy)."""
+    return slots[:, off:off + H * row].unflatten(1, (H, row))
+
+
+def _put_rows(view, bitmap, packed, scale, n: int, H: int, bm: int, pb: int):
+    """Scatter (head, token)-ordered row fields into a [n, H, row] slot view."""
+    view[:, :, :bm] = bitmap.reshape(H, n, bm).transpose(0, 1)
+    view[:, :, bm:bm + pb] = packed.reshape(H, n, pb).transpose(0, 1)
+    view[:, :, bm + pb:bm + pb + 2] = (scale.to(torch.float16).contiguous().view(torch.uint8)
+                                       .reshape(H, n, 2).transpose(0, 1))
+
+
+def _take_rows(view, n: int, H: int, bm: int, pb: int):
+    """Gather a [n, H, row] slot view back into (head, token)-ordered row fields."""
+    hv = view.transpose(0, 1)                                   # [H, n, row]
+    bitmap = hv[:, :, :bm].reshape(H * n, bm).contiguous()
+    packed = hv[:, :, bm:bm + pb].reshape(H * n, pb).contiguous()
+    scale = hv[:, :, bm + pb:bm + pb + 2].contiguous().view(torch.float16).reshape(H * n)
+    return bitmap, packed, scale
+
+
+def _check_rows(rows, lay: TTKLayout, n: int, pb: int, what: str):
+    if int(rows.rows) != lay.H * n:
+        raise ValueError(f"{what} holds {rows.rows} rows, expected H*n = {lay.H}*{n}")
+    if tuple(rows.bitmap.shape) != (lay.H * n, lay.d // 8) or tuple(rows.packed.shape) != (
+            lay.H * n, pb) or rows.scale.numel() != lay.H * n:
+        raise ValueError(f"{what} fields are bitmap {tuple(rows.bitmap.shape)}, packed "
+                         f"{tuple(rows.packed.shape)}, scale {tuple(rows.scale.shape)}; the "
+                         f"layout needs [{lay.H * n}, {lay.d // 8}], [{lay.H * n}, {pb}], "
+                         f"[{lay.H * n}]")
+
+
+def pack_k_slots(lay: TTKLayout, coeff_q: torch.Tensor, coeff_scale: torch.Tensor,
+                 resid) -> torch.Tensor:
+    """`[n, k_slot_bytes]` uint8 K slots from coefficients `[n, r1]` int8, their ruler `[n]`
+    fp16 and the residual row store over H*n rows (reference layout.py:161-193). Padding bytes
+    are zero."""
+    n = coeff_q.shape[0]
+    pb = packed_row_bytes(lay.res_k, lay.res_bits)
+    _check_rows(resid, lay, n, pb, "the residual")
+    if tuple(coeff_q.shape) != (n, lay.r1) or coeff_q.dtype != torch.int8:
+        raise ValueError(f"coeff_q must be int8 [{n}, {lay.r1}], got {coeff_q.dtype} "
+                         f"{tuple(coeff_q.shape)}")
+    out = torch.zeros(n, lay.k_slot_bytes, dtype=torch.uint8, device=coeff_q.device)
+    cb = lay.coeff_bytes
+    out[:, :cb] = coeff_q.contiguous().view(torch.uint8)
+    out[:, cb:cb + 2] = coeff_scale.to(torch.float16).contiguous().view(torch.uint8).reshape(n, 2)
+    _put_rows(_head_rows(out, cb + 2, lay.H, lay.k_row_bytes), resid.bitmap, resid.packed,
+              resid.scale, n, lay.H, lay.d // 8, pb)
+    return out
+
+
+def unpack_k_slots(lay: TTKLayout, slots: torch.Tensor):
+    """Inverse of `pack_k_slots` (reference layout.py:196-219):
+    `(coeff_q [n, r1] int8, coeff_scale [n] fp16, (bitmap, packed, scale))`, the residual rows in
+    (head, token) order."""
+    n = slots.shape[0]
+    if slots.dtype != torch.uint8 or slots.dim() != 2 or slots.shape[1] < lay.k_slot_bytes:
+        raise ValueError(f"K slots must be uint8 [n, >= {lay.k_slot_bytes}]")
+    cb = lay.coeff_bytes
+    coeff_q = slots[:, :cb].contiguous().view(torch.int8)
+    coeff_scale = slots[:, cb:cb + 2].contiguous().view(torch.float16).reshape(n)
+    rows = _take_rows(_head_rows(slots, cb + 2, lay.H, lay.k_row_bytes), n, lay.H, lay.d // 8,
+                      packed_row_bytes(lay.res_k, lay.res_bits))
+    return coeff_q, coeff_scale, rows
+
+
+def pack_v_slots(lay: TTKLayout, rows) -> torch.Tensor:
+    """`[n, v_slot_bytes]` uint8 V slots from a row store over H*n rows (reference
+    layout.py:222-239). Padding bytes are zero."""
+    if int(rows.rows) % lay.H:
+        raise ValueError(f"V store holds {rows.rows} rows, not a multiple of H={lay.H}")
+    n = int(rows.rows) // lay.H
+    pb = packed_row_bytes(lay.v_lanes, lay.v_bits)
+    _check_rows(rows, lay, n, pb, "the V store")
+    out = torch.zeros(n, lay.v_slot_bytes, dtype=torch.uint8, device=rows.bitmap.device)
+    _put_rows(_head_rows(out, 0, lay.H, lay.v_row_bytes), rows.bitmap, rows.packed, rows.scale,
+              n, lay.H, lay.d // 8, pb)
+    return out
+
+
+def unpack_v_slots(lay: TTKLayout, slots: torch.Tensor):
+    """Inverse of `pack_v_slots` (reference layout.py:242-261): `(bitmap, packed, scale)` over
+    H*n rows in (head, token) order."""
+    if slots.dtype != torch.uint8 or slots.dim() != 2 or slots.shape[1] < lay.v_slot_bytes:
+        raise ValueError(f"V slots must be uint8 [n, >= {lay.v_slot_bytes}]")
+    return _take_rows(_head_rows(slots, 0, lay.H, lay.v_row_bytes), slots.shape[0], lay.H,
+                      lay.d // 8, packed_row_bytes(lay.v_lanes, lay.v_bits))
