@@ -109,6 +109,13 @@ def build_store(torch, lay, cfg, lens, n_layers, seed, dev, fit_on=FIT_ON, disti
                 t_fit=t_fit, t_write=t_write)
 
 
+def config3_lens(seed=3, B=8):
+    """BASELINE config 3's contexts: 8 lengths drawn uniformly from [1000, 14400], seeded."""
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    return [int(x) for x in torch.randint(1000, 14401, (B,), generator=g)]
+
+
 def k1_bytes(lay, lens, r1, cs_rows):
     """Algorithmic HBM bytes of one K1 launch: every slot once, each request's fp32 decoder
     once, the angle table rows once, q and out once (fp16)."""
@@ -117,8 +124,18 @@ def k1_bytes(lay, lens, r1, cs_rows):
             + cs_rows * D * 4 + 2 * B * HQ * D * 2)
 
 
-def time_k1(torch, lay, store, q, cache, steps, warmup, n_layers):
-    """Time `steps` decode steps (n_layers K1 launches each). Returns (ms/step, ms/launch)."""
+def cache_flusher(torch, dev, mib=768):
+    """A callable that streams a 768 MiB buffer through the memory hierarchy (read + write),
+    evicting the 256 MB Infinity Cache and every XCD's L2, so the next launch reads cold HBM."""
+    buf = torch.zeros(mib << 20, dtype=torch.uint8, device=dev)
+    return lambda: buf.add_(1)
+
+
+def time_k1(torch, lay, store, q, cache, steps, warmup, n_layers, flush=None):
+    """Time `steps` decode steps (n_layers K1 launches each, layer li reading its own pages).
+    Returns (ms/step, ms/launch). With `flush`, the caches are flushed between launches (outside
+    the per-launch events), so every launch reads cold HBM; ms/step then includes the flushes
+    and only ms/launch is meaningful."""
     from vllm_ttkv import kernels
     dev = q.device
     B = store["B"]
@@ -130,6 +147,8 @@ def time_k1(torch, lay, store, q, cache, steps, warmup, n_layers):
     def step(evs=None):
         for li in range(n_layers):
             L = store["layers"][li % len(store["layers"])]
+            if flush is not None:
+                flush()
             if evs is not None:
                 evs[li][0].record()
             kernels.decode_paged(lay, q, L["page"], BS, store["bt"], store["seq_lens"], qsl,
@@ -279,31 +298,36 @@ def bench_config4(torch, lay, cfg, cache, dev, steps=10, warmup=3, cpu=False):
     return res
 
 
-def bench_dense(torch, lens, q, dev, steps=10, warmup=3):
+def bench_dense(torch, lens, q, dev, steps=3, warmup=1, n_layers=L_LAYERS):
     """Dense fp16 paged attention of the same shapes (the per-cached-token comparison): this
-    build's dense HIP comparator over a shuffled paged cache, and torch SDPA over contiguous
-    per-request K/V (no paging)."""
+    build's dense HIP comparator over a shuffled paged cache, one K/V cache per layer (28, so
+    the cycled bytes far exceed the caches, as the compressed read's are), and torch SDPA over
+    contiguous per-request K/V (no paging)."""
     from vllm_ttkv import kernels, synth
     B = len(lens)
     bt, nblk = synth.shuffled_block_table(lens, BS, seed=11, extra_blocks=2)
     g = torch.Generator(device=dev).manual_seed(12)
-    kc = torch.randn(nblk * BS, H, D, generator=g, device=dev).to(torch.float16)
-    vc = torch.randn(nblk * BS, H, D, generator=g, device=dev).to(torch.float16)
+    kcs, vcs = [], []
+    for _ in range(n_layers):
+        kcs.append(torch.randn(nblk * BS, H, D, generator=g, device=dev).to(torch.float16))
+        vcs.append(torch.randn(nblk * BS, H, D, generator=g, device=dev).to(torch.float16))
     bt_d = bt.to(dev)
     sl = torch.tensor(lens, dtype=torch.int32, device=dev)
     qsl = torch.arange(B + 1, dtype=torch.int32, device=dev)
     out = torch.empty_like(q)
     n = kernels._hip.lib().ttkv_dense_workspace_bytes(H, HQ, B, max(lens), BS)
     ws = torch.zeros(max(int(n), 256), dtype=torch.uint8, device=dev)
+    li = [0]
 
     def run():
-        kernels.dense_decode_paged(q, kc, vc, BS, bt_d, sl, qsl, max(lens), D ** -0.5, out=out,
-                                   workspace=ws)
+        kernels.dense_decode_paged(q, kcs[li[0]], vcs[li[0]], BS, bt_d, sl, qsl, max(lens),
+                                   D ** -0.5, out=out, workspace=ws)
+        li[0] = (li[0] + 1) % n_layers
 
-    ms = time_launches(torch, run, steps, warmup)
-    del kc, vc
+    ms = time_launches(torch, run, steps * n_layers, warmup * n_layers)
+    del kcs, vcs
     res = dict(us_per_layer=ms * 1e3, hbm_gbps=sum(lens) * H * D * 2 * 2 / (ms * 1e-3) / 1e9,
-               ns_per_cached_token=ms * 1e6 / sum(lens))
+               ns_per_cached_token=ms * 1e6 / sum(lens), layers_cycled=n_layers)
     try:
         import torch.nn.functional as F
         kd = torch.randn(B, H, max(lens), D, generator=g, device=dev).to(torch.float16)
@@ -577,33 +601,40 @@ def main():
     log(f"K1 B=8x14402: {ms_launch * 1e3:.1f} us/launch, {achieved:.0f} GB/s")
 
     if not args.no_extra:
+        # Cold-HBM extras: 28 layers of distinct pages each, and the caches flushed between
+        # launches (a batch-1 layer of 1-13 MB would otherwise stay in the 256 MB Infinity Cache
+        # across a 28-layer cycle; in serving, the model's weights pass between two reads of a
+        # layer's cache)
+        flush = cache_flusher(torch, dev)
         sweep = []
         for n in (1082, 4322, 8642, 14402):
-            st = build_store(torch, lay, cfg, [n], 2, seed=2, dev=dev)
+            st = build_store(torch, lay, cfg, [n], L_LAYERS, seed=2, dev=dev)
             q1 = synth.queries(1, seed=6, device=dev)
-            _, ml = time_k1(torch, lay, st, q1, cache, 20, 3, 2)
+            _, ml = time_k1(torch, lay, st, q1, cache, 3, 1, L_LAYERS, flush=flush)
             b = k1_bytes(lay, [n], R1, n)
-            log(f"K1 B=1x{n}: {ml * 1e3:.1f} us/launch")
+            log(f"K1 B=1x{n}: {ml * 1e3:.1f} us/launch (cold)")
             sweep.append(dict(context=n, us_per_layer=ml * 1e3,
                               hbm_gbps=b / (ml * 1e-3) / 1e9,
-                              tokens_per_s=1.0 / (ml * 1e-3 * L_LAYERS)))
+                              tokens_per_s=1.0 / (ml * 1e-3 * L_LAYERS), cold_hbm=True,
+                              layers_cycled=L_LAYERS))
             del st
         extra["batch1_sweep"] = sweep
-        g = torch.Generator().manual_seed(3)
-        lens3 = [int(x) for x in torch.randint(1000, 14401, (8,), generator=g)]
-        st = build_store(torch, lay, cfg, lens3, 2, seed=3, dev=dev)
-        _, ml = time_k1(torch, lay, st, q, cache, 20, 3, 2)
+        lens3 = config3_lens()
+        st = build_store(torch, lay, cfg, lens3, L_LAYERS, seed=3, dev=dev)
+        _, ml = time_k1(torch, lay, st, q, cache, 3, 1, L_LAYERS, flush=flush)
         b = k1_bytes(lay, lens3, R1, max(lens3))
-        log(f"K1 config3 ({sum(lens3)} tokens, longest {max(lens3)}): {ml * 1e3:.1f} us/layer")
+        log(f"K1 config3 ({sum(lens3)} tokens, longest {max(lens3)}): {ml * 1e3:.1f} us/layer "
+            f"(cold)")
         extra["config3_b8_random"] = dict(contexts=lens3, us_per_layer=ml * 1e3,
                                           hbm_gbps=b / (ml * 1e-3) / 1e9,
-                                          tokens_per_s=8 / (ml * 1e-3 * L_LAYERS))
+                                          tokens_per_s=8 / (ml * 1e-3 * L_LAYERS), cold_hbm=True,
+                                          layers_cycled=L_LAYERS)
+        del st
         dn = bench_dense(torch, lens3, q, dev)
         dn["compressed_ns_per_cached_token"] = ml * 1e6 / sum(lens3)
         extra["config3_dense_fp16_comparator"] = dn
         log(f"dense fp16 comparator (config 3 shapes): {dn['us_per_layer']:.1f} us/layer, "
             f"{dn['hbm_gbps']:.0f} GB/s")
-        del st
         dh = bench_dense(torch, lens, q, dev)
         dh["compressed_ns_per_cached_token"] = ms_launch * 1e6 / sum(lens)
         extra["headline_dense_fp16_comparator"] = dh
@@ -631,7 +662,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "fp16 in/out; fp16 MFMA on exact hi+lo splits, fp32 accumulate and softmax",
         "data": "synthetic (seeded low-rank keys with outlier channels, N(0,1) values, fp16 "
                 "queries; stores fitted and packed on the GPU by this package; 4 distinct layer "
                 "stores, each copied into its own pages for the other 24 layers)",
