@@ -98,6 +98,26 @@ int ttkv_decode_paged(const ttkv_layout* lay, int32_t num_heads, float scale,
                       void* workspace, int64_t workspace_bytes, int32_t* error_word,
                       ttkv_stream_t stream);
 
+/* K1 without a workspace -- NO COUNTERPART IN THE REFERENCE. For callers that cannot allocate
+ * (code under HIP graph capture, serving loops or harnesses that forbid hipMalloc): the same
+ * read as ttkv_decode_paged, same arguments minus `workspace`/`workspace_bytes`, same kernels and
+ * results, with the split-K counters and partials in a file-scope device array of 8 MiB that
+ * each device holds until the process ends. Allocates nothing (no hipMalloc / hipFree / torch).
+ * A batch whose split-K state exceeds 8 MiB (ttkv_decode_workspace_bytes) is refused with
+ * TTKV_E_WORKSPACE. Calls on one device share the array: calls that overlap in time on one
+ * device race (issue them on one stream). Every call leaves the array's counters zero. */
+int ttkv_decode_paged_noalloc(const ttkv_layout* lay, int32_t num_heads, float scale,
+                              const void* query, int32_t q_dtype, int64_t q_row_stride,
+                              const uint8_t* page, int64_t n_slots, int64_t slot_stride,
+                              int32_t block_size, const int32_t* block_table,
+                              int64_t bt_row_stride, int32_t max_blocks, const int32_t* seq_lens,
+                              const int32_t* query_start_loc, int32_t num_reqs,
+                              int32_t max_seq_len, const int32_t* dec_slot_of_block,
+                              int64_t num_blocks, const float* dec_pool, int64_t n_dec_slots,
+                              const float* cos_sin_cache, int64_t max_position, void* out,
+                              int32_t out_dtype, int64_t out_row_stride, int32_t* error_word,
+                              ttkv_stream_t stream);
+
 /* K3 -- write/encode of `num_tokens` new tokens into their slots, one launch per layer.
  *
  * Replaces the reference's per-request write (vllm_ttkv/impl.py:543-653): `encode_frozen(_batch)`

@@ -88,6 +88,27 @@ int ttkv_decode_paged(const ttkv_layout* lay, int32_t num_heads, float scale, co
                       (hipStream_t)stream);
 }
 
+int ttkv_decode_paged_noalloc(const ttkv_layout* lay, int32_t num_heads, float scale,
+                              const void* query, int32_t q_dtype, int64_t q_row_stride,
+                              const uint8_t* page, int64_t n_slots, int64_t slot_stride,
+                              int32_t block_size, const int32_t* block_table,
+                              int64_t bt_row_stride, int32_t max_blocks, const int32_t* seq_lens,
+                              const int32_t* query_start_loc, int32_t num_reqs,
+                              int32_t max_seq_len, const int32_t* dec_slot_of_block,
+                              int64_t num_blocks, const float* dec_pool, int64_t n_dec_slots,
+                              const float* cos_sin_cache, int64_t max_position, void* out,
+                              int32_t out_dtype, int64_t out_row_stride, int32_t* error_word,
+                              ttkv_stream_t stream) {
+  Geom g;
+  if (!make_geom(lay, &g)) return host_fail(TTKV_E_INVALID, "invalid layout");
+  return decode_paged_noalloc(g, num_heads, scale, query, q_dtype, q_row_stride, page, n_slots,
+                              slot_stride, block_size, block_table, bt_row_stride, max_blocks,
+                              seq_lens, query_start_loc, num_reqs, max_seq_len,
+                              dec_slot_of_block, num_blocks, dec_pool, n_dec_slots, cos_sin_cache,
+                              max_position, out, out_dtype, out_row_stride, error_word,
+                              (hipStream_t)stream);
+}
+
 int ttkv_write_paged(const ttkv_layout* lay, const void* key, int32_t k_dtype, int64_t k_row_stride,
                      const void* value, int32_t v_dtype, int64_t v_row_stride,
                      const int64_t* slot_mapping, int32_t num_tokens,

@@ -942,6 +942,7 @@ int decode_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype,
   }
   const int slice = decode_slice_reqs(num_reqs, max_seq_len);
   for (int r0 = 0; r0 < num_reqs; r0 += slice) {
+    // (slices run in stream order on one workspace: each leaves the counters zero for the next)
     DecodeArgs b = a;
     b.num_reqs = std::min(slice, num_reqs - r0);
     b.seq_lens = seq_lens + r0;
@@ -960,6 +961,89 @@ int decode_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype,
     if (rc != TTKV_OK) return rc;
   }
   return TTKV_OK;
+}
+
+}  // namespace ttkv
+
+// ---------------------------------------------------------------- no-allocation variant
+// For callers that cannot allocate (code under graph capture, serving loops that forbid it): the
+// split-K counters and partials live in a file-scope device array instead of a caller workspace.
+// Each device holds its own copy for the life of the process. Host code never passes `scratch`
+// itself (its host-side name is not a device address): the device address is looked up once per
+// device with hipGetSymbolAddress and kept. Calls on one device share the array, so calls that
+// overlap in time on one device race; the counters are left zero by every call.
+#include <mutex>
+
+namespace ttkv {
+
+constexpr int64_t kScratchBytes = 8ll << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+constexpr int kMaxDevices = 64;
+
+__global__ void clear_counters_kernel(int* cnt, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+    cnt[i] = 0;
+}
+
+// Device address of `scratch` on the current device, looked up (and its counter region cleared
+// by a kernel on `st`) on the first call there; null on failure, with the error recorded.
+static void* scratch_address(hipStream_t st) {
+  static std::mutex mu;
+  static void* addr[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    host_fail(TTKV_E_LAUNCH, "hipGetDevice failed");
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    host_fail(TTKV_E_UNSUPPORTED, "device ordinal " + std::to_string(dev) + " >= 64");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      host_fail(TTKV_E_LAUNCH, std::string("hipGetSymbolAddress(scratch): ") +
+                                   hipGetErrorString(e));
+      return nullptr;
+    }
+    hipLaunchKernelGGL(clear_counters_kernel, dim3(16), dim3(256), 0, st, (int*)p, kMaxCounters);
+    const hipError_t le = hipGetLastError();
+    if (le != hipSuccess) {
+      host_fail(TTKV_E_LAUNCH, std::string("scratch clear launch: ") + hipGetErrorString(le));
+      return nullptr;
+    }
+    addr[dev] = p;
+  }
+  return addr[dev];
+}
+
+int64_t decode_noalloc_scratch_bytes() { return kScratchBytes; }
+
+int decode_paged_noalloc(const Geom& g, int HQ, float scale, const void* q, int q_dtype,
+                         int64_t q_row_stride, const uint8_t* page, int64_t n_slots,
+                         int64_t slot_stride, int block_size, const int32_t* bt,
+                         int64_t bt_row_stride, int max_blocks, const int32_t* seq_lens,
+                         const int32_t* qsl, int num_reqs, int max_seq_len,
+                         const int32_t* dec_map, int64_t num_blocks, const float* dec_pool,
+                         int64_t n_dec_slots, const float* cs_cache, int64_t max_pos, void* out,
+                         int out_dtype, int64_t out_row_stride, int32_t* err, hipStream_t st) {
+  if (g.H <= 0 || HQ <= 0 || HQ % g.H) return host_fail(TTKV_E_INVALID, "num_heads is not a multiple of H");
+  if (block_size <= 0 || num_reqs < 0 || max_seq_len < 0)
+    return host_fail(TTKV_E_INVALID, "block_size / batch size");
+  const int64_t need = decode_workspace_bytes(g, HQ / g.H, num_reqs, max_seq_len, block_size);
+  if (need > kScratchBytes)
+    return host_fail(TTKV_E_WORKSPACE,
+                     "this batch needs " + std::to_string(need) + " bytes of split-K scratch; "
+                     "the no-allocation entry point holds " + std::to_string(kScratchBytes) +
+                     " (use ttkv_decode_paged with a workspace)");
+  void* ws = scratch_address(st);
+  if (!ws) return TTKV_E_LAUNCH;
+  return decode_paged(g, HQ, scale, q, q_dtype, q_row_stride, page, n_slots, slot_stride,
+                      block_size, bt, bt_row_stride, max_blocks, seq_lens, qsl, num_reqs,
+                      max_seq_len, dec_map, num_blocks, dec_pool, n_dec_slots, cs_cache, max_pos,
+                      out, out_dtype, out_row_stride, ws, kScratchBytes, err, st);
 }
 
 }  // namespace ttkv

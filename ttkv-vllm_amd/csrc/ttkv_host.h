@@ -34,6 +34,15 @@ int decode_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype,
                  int64_t n_dec_slots, const float* cs_cache, int64_t max_pos, void* out,
                  int out_dtype, int64_t out_row_stride, void* ws, int64_t ws_bytes, int32_t* err,
                  hipStream_t st);
+// decode_paged with its split-K scratch in a file-scope device array (no workspace argument)
+int decode_paged_noalloc(const Geom& g, int HQ, float scale, const void* q, int q_dtype,
+                         int64_t q_row_stride, const uint8_t* page, int64_t n_slots,
+                         int64_t slot_stride, int block_size, const int32_t* bt,
+                         int64_t bt_row_stride, int max_blocks, const int32_t* seq_lens,
+                         const int32_t* qsl, int num_reqs, int max_seq_len,
+                         const int32_t* dec_map, int64_t num_blocks, const float* dec_pool,
+                         int64_t n_dec_slots, const float* cs_cache, int64_t max_pos, void* out,
+                         int out_dtype, int64_t out_row_stride, int32_t* err, hipStream_t st);
 
 }  // namespace ttkv
 

@@ -73,6 +73,19 @@ def lib():
         P, I64, P,                    # workspace, workspace_bytes, error_word
         P,                            # stream
     ]
+    L.ttkv_decode_paged_noalloc.restype = ctypes.c_int
+    L.ttkv_decode_paged_noalloc.argtypes = [
+        LP, I32, F32,                 # layout, num_heads, scale
+        P, I32, I64,                  # query, q_dtype, q_row_stride
+        P, I64, I64,                  # page, n_slots, slot_stride
+        I32, P, I64, I32,             # block_size, block_table, bt_row_stride, max_blocks
+        P, P, I32, I32,               # seq_lens, query_start_loc, num_reqs, max_seq_len
+        P, I64, P, I64,               # dec_slot_of_block, num_blocks, dec_pool, n_dec_slots
+        P, I64,                       # cos_sin_cache, max_position
+        P, I32, I64,                  # out, out_dtype, out_row_stride
+        P,                            # error_word
+        P,                            # stream
+    ]
     L.ttkv_write_paged.restype = ctypes.c_int
     L.ttkv_write_paged.argtypes = [
         LP, P, I32, I64,              # layout, key, k_dtype, k_row_stride
@@ -147,7 +160,7 @@ def lib():
 
 # Every symbol include/ttkv_hip.h declares (checked by tests/test_abi.py).
 EXPORTS = ("ttkv_last_error", "ttkv_blob_bytes", "ttkv_decode_workspace_bytes",
-           "ttkv_decode_paged", "ttkv_write_paged", "ttkv_prefill_workspace_bytes",
+           "ttkv_decode_paged", "ttkv_decode_paged_noalloc", "ttkv_write_paged", "ttkv_prefill_workspace_bytes",
            "ttkv_prefill_paged", "ttkv_multi_scores_paged", "ttkv_dense_workspace_bytes",
            "ttkv_dense_decode_paged", "ttkv_write_workspace_bytes", "ttkv_container_krt",
            "ttkv_container_v_out")
