@@ -30,9 +30,10 @@
 //   softmax : online, base 2, evaluated redundantly by every wave (lane = token, no barrier). The
 //             reference point moves only when some score exceeds it by more than 2^8 (a ballot),
 //             so the wave-wide max is rarely computed; sums stay per lane until the end.
-//   P.V     : o[p] += P'[p,t] * (code - 2^(b-1)) with P' = P * ruler_v. 3-bit codes: packed fp16
-//             dot products over token pairs (codes as exact fp16 integers, P' * 2^-8 rounded
-//             to nearest fp16); 4-bit codes: fp32.
+//   P.V     : on MFMA, O^T[dims, heads] += V^T[dims, tokens] * P'^T[tokens, heads] with
+//             P' = P * ruler_v rounded to fp16 once and the codes as exact fp16 integers
+//             (c - 2^(b-1)). The V^T operand is read straight from the decoded code rows with
+//             the gfx950 LDS transpose read (ds_read_tr8_b64); P'^T from a per-wave LDS row.
 // Chunks of one (r, h) are combined in the same launch by the last workgroup to finish
 // (device-scope fence + counter), which also resets the counter to zero. The counters sit at the
 // workspace's fixed 64 KiB head, the partials after it, indexed by (chunk item) so their count
@@ -101,12 +102,13 @@ struct DecodeSmem {
   uint8_t kcode[kTile][kCodeStride];
   uint8_t vcode[kTile][kCodeStride];
   float spart[kWaves][kTile][kSP];  // per wave partial q.k [wave][token][head]
+  _Float16 pw[kWaves][G][kTile];    // per wave P' = P * ruler_v (fp16), the P.V B operand
   uint2 lut[256];
   uint32_t lut3[4096];
   int32_t seg[kSegMax];
   float cs[kTile];  // coefficient ruler
   float kr[kTile];  // K residual ruler / (cs * unit)
-  float vr[kTile];  // V ruler / unit
+  float vr[kTile];  // V ruler
   float f[kTile];   // cs * scale * log2(e)
   float m[G], l[G];
   int is_last;
@@ -299,14 +301,16 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   if (blk0 >= 0 && blk0 < a.num_blocks) dslot = a.dec_map[blk0];
   const int k_row_off = g.k_field + h * g.k_row;
   const int v_row_off = g.k_slot + h * g.v_row;
-  RawSlot<KU> P;
+  // the rows' 64-byte windows (16-aligned; each row lies inside its window, host-checked)
+  const int k_win = k_row_off & ~15, v_win = v_row_off & ~15;
+  RawSlotW<KU> P;
   {
     const uint8_t* base = nullptr;
     if (ptok < min(kTile, t1 - t0) && blk_t0 >= 0 && blk_t0 < a.num_blocks) {
       const int64_t slot = (int64_t)blk_t0 * a.block_size + (pos0 - bi0 * a.block_size);
       if (slot < a.n_slots) base = a.page + slot * a.slot_stride;
     }
-    fetch_raw_slot<KU>(P, base, part, g, k_row_off, v_row_off);
+    fetch_raw_slot_w<KU>(P, base, part, g, k_win, v_win);
   }
   if (dslot < 0 || dslot >= a.n_dec_slots) {
     if (tid == 0) atomicOr(a.err, TTKV_ERR_NO_DECODER);
@@ -370,9 +374,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   // bits are converted as plain bytes
   const float inv_unit = 1.0f / __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0];
   const float inv_unit_k = RB == 3 ? inv_unit : 1.0f;
-  // 3-bit V codes are read as exact integers (c - 4) and P' carries ruler_v * 2^-8; 4-bit codes
-  // are read as c with ruler_v
-  const float vr_scale = VB == 3 ? 1.0f / 256.f : 1.0f;
+
   __syncthreads();  // seg
 
   auto slot_base = [&](int tt) -> const uint8_t* {
@@ -420,15 +422,21 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
     qlo[j] = (_Float16)(qraw[j] - (float)hi);
   }
 
-  float o[G][8], m_run[G], l_lane[G], psum[G];
+  // P.V accumulators on MFMA: O^T[dims, heads] for the wave's two dim tiles; lane (n, gq) holds
+  // dims 4gq..4gq+3 of the tile for query head n (n < G; the other columns stay zero)
+  float4v oacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  float m_run[G], l_lane[G];
 #pragma unroll
   for (int p = 0; p < G; ++p) {
     m_run[p] = -INFINITY;
     l_lane[p] = 0.f;
-    psum[p] = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o[p][i] = 0.f;
   }
+  // V^T A-fragments come from the decoded code rows through the LDS transpose read: in each
+  // 16-lane group, lanes 2j and 2j+1 address the two 8-byte halves of row j (token 8gq + j) of
+  // the tile's 16 dims, and lane n receives column n (dim n) of those 8 rows, i.e. exactly
+  // A[dim n][tokens 8gq .. 8gq+7].
+  const int tr_tok = 8 * gq + (n >> 1);
+  const int tr_col = 8 * (n & 1);
 
   // RoPE angle rows (shared by every request and head, L2-resident): this lane's 4 dims of the
   // token it reconstructs in block nb, requested one block ahead inside the reconstruction. Block
@@ -452,22 +460,25 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
     const uint8_t* next_base = tt + kTile < t1 ? slot_base(tt + kTile) : nullptr;
     // ---------------------------------------------------------------- commit prefetched bytes
     {
-      uint32_t* cdst = (uint32_t*)&S.coef[ptok][part * kCPP];
+      uint32_t* crow = (uint32_t*)&S.coef[ptok][0];
 #pragma unroll
-      for (int dw = 0; dw < KU; ++dw) {
-        // bytes past r1 (the ruler, head 0's row) are converted too: they are finite, and the
-        // decoder fragments are zero for k >= r1, so they contribute exactly 0
-        uint32_t p01, p23;
-        i8x4_to_f16(P.coef[dw], p01, p23);
-        cdst[2 * dw] = p01;
-        cdst[2 * dw + 1] = p23;
-      }
-      if (part == 0) S.cs[ptok] = f16_bits_to_float(P.rul);
+      for (int i = 0; i < RawSlotW<KU>::kChunks; ++i) {
+        // coefficient chunk part + 4i -> 16 fp16 values; bytes past r1 (the ruler, head 0's row)
+        // are converted too: they are finite, and the decoder fragments are zero for k >= r1,
+        // so they contribute exactly 0
+        const int cch = part + 4 * i;
+        if (cch < KU) {
+          uint32_t h[8];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        S.rawk[ptok][part * 4 + i] = __builtin_amdgcn_perm(P.krow[i + 1], P.krow[i], ksel);
-        S.rawv[ptok][part * 4 + i] = __builtin_amdgcn_perm(P.vrow[i + 1], P.vrow[i], vsel);
+          for (int j = 0; j < 4; ++j) i8x4_to_f16(P.coef[i][j], h[2 * j], h[2 * j + 1]);
+          *(u32x4*)&crow[8 * cch] = u32x4{h[0], h[1], h[2], h[3]};
+          *(u32x4*)&crow[8 * cch + 4] = u32x4{h[4], h[5], h[6], h[7]};
+        }
       }
+      if (part == 0)
+        S.cs[ptok] = f16_bits_to_float((g.coeff_bytes & 2) ? P.rul >> 16 : P.rul & 0xffffu);
+      stage_row_w(P.krow, (k_row_off & 15) >> 2, ksel, &S.rawk[ptok][part * 4]);
+      stage_row_w(P.vrow, (v_row_off & 15) >> 2, vsel, &S.rawv[ptok][part * 4]);
     }
     __syncthreads();
     // ---------------------------------------------------------------- decode (thread = half row)
@@ -492,7 +503,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
         const uint32_t* row = S.rawv[tok];
         decode_half_row_be<VB>(row, half, S.lut, S.lut3, &S.vcode[tok][64 * half]);
         if (half == 0)
-          S.vr[tok] = f16_bits_to_float(staged_u16(row, kBitmapBytes + g.v_pb)) * vr_scale;
+          S.vr[tok] = f16_bits_to_float(staged_u16(row, kBitmapBytes + g.v_pb));
       }
     }
     __syncthreads();
@@ -552,11 +563,10 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
     // ---------------------------------------------------------------- prefetch the next tile
     if (tt + kTile < t1) {
       if constexpr (kAngle0Ahead) angle_row(tt + kTile, 0, cv0, sv0);
-      fetch_raw_slot<KU>(P, next_base, part, g, k_row_off, v_row_off);
+      fetch_raw_slot_w<KU>(P, next_base, part, g, k_win, v_win);
     }
     __syncthreads();
     // ---------------------------------------------------------------- online softmax (every wave)
-    float pv[G];
     {
       const bool valid = lane < ntile;
       const float ft = S.f[lane];
@@ -575,6 +585,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
           sum[i + 3] += x[3];
         }
       }
+      float amul = 1.f;  // this lane's factor for its head column n of the P.V accumulators
 #pragma unroll
       for (int p = 0; p < G; ++p) {
         const float s = valid ? sum[p] * ft : -INFINITY;
@@ -587,75 +598,70 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
           const float alpha = exp2f(m_run[p] - mt);
           m_run[p] = mt;
           l_lane[p] *= alpha;
-          psum[p] *= alpha;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) o[p][i] *= alpha;
+          amul = n == p ? alpha : amul;
         }
         const float pr = fast_exp2(s - m_run[p]);
         l_lane[p] += pr;
-        pv[p] = pr * vrt;
+        // P' = P * ruler_v, rounded to fp16 once (the V codes are exact integers); tokens past
+        // the tile's end have P = 0 and all-zero decoded rows
+        S.pw[wv][p][lane] = (_Float16)(pr * vrt);
       }
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi) oacc[mi] *= amul;
     }
-    // ---------------------------------------------------------------- P.V
-    float pwb[G][4];
+    // ---------------------------------------------------------------- P.V on MFMA
+    // O^T[dims, heads] += V^T[dims, tokens] * P'^T[tokens, heads], 32 tokens per k-step. The B
+    // operand (lane (n, gq): P' of head n, tokens 8gq..8gq+7) is this wave's own LDS row, written
+    // just above by other lanes of the wave: LDS accesses of one wave complete in order, and the
+    // wavefront fence keeps the compiler from reordering them.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-    for (int p = 0; p < G; ++p) bcast_rows(pv[p], pwb[p]);
-    if constexpr (VB == 3) {
-      // Packed fp16 dot products over token pairs (16nb + n, 16nb + 16 + n): the two tokens'
-      // fp8 codes of one dim are interleaved by v_perm and converted to an exact fp16 integer
-      // pair; P' = P * ruler_v * 2^-8 is rounded to nearest fp16 (<= ruler_v, so in range).
+    for (int kk = 0; kk < 2; ++kk) {
+      half8 bp = {};
+      if (n < G) bp = *(const half8*)&S.pw[wv][n][32 * kk + 8 * gq];
 #pragma unroll
-      for (int pp = 0; pp < 2; ++pp) {
-        const int ta = 32 * pp + n, tb = ta + 16;
-        const uint32_t al = *(const uint32_t*)&S.vcode[ta][dl];
-        const uint32_t bl = *(const uint32_t*)&S.vcode[tb][dl];
-        const uint32_t ah = *(const uint32_t*)&S.vcode[ta][64 + dl];
-        const uint32_t bh = *(const uint32_t*)&S.vcode[tb][64 + dl];
-        const uint32_t il[4] = {__builtin_amdgcn_perm(bl, al, 0x05010400u),
-                                __builtin_amdgcn_perm(bl, al, 0x07030602u),
-                                __builtin_amdgcn_perm(bh, ah, 0x05010400u),
-                                __builtin_amdgcn_perm(bh, ah, 0x07030602u)};
-        half2v cp[8];
+      for (int mi = 0; mi < 2; ++mi) {
+        const uint8_t* src = &S.vcode[32 * kk + tr_tok][16 * (wv + 4 * mi) + tr_col];
+        typedef int v2i __attribute__((ext_vector_type(2)));
+        const v2i raw = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            (__attribute__((address_space(3))) v2i*)(src));
+        half8 av;
+        if constexpr (VB == 3) {
+          // fp8 bytes of (c - 4) scaled by the fp8 unit's inverse: exact small integers
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          cp[2 * m] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(il[m], inv_unit, false);
-          cp[2 * m + 1] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(il[m], inv_unit, true);
+          for (int w = 0; w < 2; ++w) {
+            const half2v lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(raw[w], inv_unit, false);
+            const half2v hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(raw[w], inv_unit, true);
+            av[4 * w] = lo[0];
+            av[4 * w + 1] = lo[1];
+            av[4 * w + 2] = hi[0];
+            av[4 * w + 3] = hi[1];
+          }
+        } else {
+          // offset-binary code bytes c -> fp16 (c - 8), exact: 1024 + c from the byte placed
+          // under the fp16 exponent of 1024, minus 1032
+          const half2v bias = {(_Float16)1032.0f, (_Float16)1032.0f};
+#pragma unroll
+          for (int w = 0; w < 2; ++w) {
+            const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, (uint32_t)raw[w], 0x04010400u);
+            const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, (uint32_t)raw[w], 0x04030402u);
+            const half2v a = __builtin_bit_cast(half2v, lo) - bias;
+            const half2v b = __builtin_bit_cast(half2v, hi) - bias;
+            av[4 * w] = a[0];
+            av[4 * w + 1] = a[1];
+            av[4 * w + 2] = b[0];
+            av[4 * w + 3] = b[1];
+          }
         }
-#pragma unroll
-        for (int p = 0; p < G; ++p) {
-          const half2v pp2 =
-              __builtin_convertvector(float2v{pwb[p][2 * pp], pwb[p][2 * pp + 1]}, half2v);
-#pragma unroll
-          for (int k = 0; k < 8; ++k) o[p][k] = __builtin_amdgcn_fdot2(cp[k], pp2, o[p][k], false);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb) {
-        const int tok = 16 * nb + n;
-        float v[8];
-        codes4<VB>(*(const uint32_t*)&S.vcode[tok][dl], v);
-        codes4<VB>(*(const uint32_t*)&S.vcode[tok][64 + dl], v + 4);
-#pragma unroll
-        for (int p = 0; p < G; ++p) {
-          const float pw = pwb[p][nb];
-          psum[p] += pw;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) o[p][i] = fmaf(pw, v[i], o[p][i]);
-        }
+        oacc[mi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bp, oacc[mi], 0, 0, 0);
       }
     }
   }
 
-  // ---- reduce o over the 16 token lanes of each lane group (4-bit: remove the code offset)
+  // ---- normalisers: the per-lane partial sums over the wave (every wave holds the same)
 #pragma unroll
-  for (int p = 0; p < G; ++p) {
-    const float off = VB == 4 ? 8.f * row_sum(psum[p]) : 0.f;
-    const float osc = VB == 3 ? 256.f : 1.f;  // undo the 2^-8 of P'
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o[p][i] = row_sum(o[p][i]) * osc - off;
-    l_lane[p] = wave_sum(l_lane[p]);
-  }
+  for (int p = 0; p < G; ++p) l_lane[p] = wave_sum(l_lane[p]);
   if (tid == 0) {
 #pragma unroll
     for (int p = 0; p < G; ++p) {
@@ -666,16 +672,13 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   __syncthreads();
 
   if (n_chunks == 1) {
-    if (n == 0) {
+    if (n < G) {
+      const float inv = 1.f / S.l[n];
+      const int64_t ob = qrow * a.out_row_stride + (int64_t)(h * G + n) * kD;
 #pragma unroll
-      for (int p = 0; p < G; ++p) {
-        const float inv = 1.f / S.l[p];
-        const int64_t ob = qrow * a.out_row_stride + (int64_t)(h * G + p) * kD;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          store_act(a.out, a.out_dtype, ob + dl + i, o[p][i] * inv);
-          store_act(a.out, a.out_dtype, ob + 64 + dl + i, o[p][4 + i] * inv);
-        }
+      for (int i = 0; i < 4; ++i) {
+        store_act(a.out, a.out_dtype, ob + dl + i, oacc[0][i] * inv);
+        store_act(a.out, a.out_dtype, ob + 64 + dl + i, oacc[1][i] * inv);
       }
     }
     return;
@@ -689,14 +692,12 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   auto st_agent = [](float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
-  if (n == 0) {
+  if (n < G) {
 #pragma unroll
-    for (int p = 0; p < G; ++p)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        st_agent(&partp[p * (kD + 2) + dl + i], o[p][i]);
-        st_agent(&partp[p * (kD + 2) + 64 + dl + i], o[p][4 + i]);
-      }
+    for (int i = 0; i < 4; ++i) {
+      st_agent(&partp[n * (kD + 2) + dl + i], oacc[0][i]);
+      st_agent(&partp[n * (kD + 2) + 64 + dl + i], oacc[1][i]);
+    }
   }
   if (tid < G) {
     st_agent(&partp[tid * (kD + 2) + kD], S.m[tid]);
@@ -884,6 +885,11 @@ int decode_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype,
   if (!ku) return host_fail(TTKV_E_UNSUPPORTED, "r1 > 160 is not built");
   if (ku * 16 > g.k_slot)
     return host_fail(TTKV_E_UNSUPPORTED, "padded coefficient block exceeds the K slot");
+  for (int h = 0; h < g.H; ++h)  // every head row inside its 64-byte load window
+    if (((g.k_field + h * g.k_row) & 15) + g.k_row > 64 || ((g.k_slot + h * g.v_row) & 15) + g.v_row > 64)
+      return host_fail(TTKV_E_UNSUPPORTED, "a head row of " + std::to_string(g.k_row) + "/" +
+                                               std::to_string(g.v_row) +
+                                               " bytes straddles its 64-byte load window");
   if (!q || !page || !bt || !seq_lens || !qsl || !dec_map || !dec_pool || !cs_cache || !out || !err)
     return host_fail(TTKV_E_INVALID, "null pointer argument");
   if ((uintptr_t)page % 16 || slot_stride % 16 || slot_stride < g.blob)

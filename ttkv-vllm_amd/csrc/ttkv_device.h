@@ -84,8 +84,72 @@ __device__ __forceinline__ void fetch_raw_slot(RawSlot<NCW>& P, const uint8_t* b
 #pragma unroll
     for (int i = 0; i < 5; ++i) P.vrow[i] = src[min(part * 4 + i, nsrc - 1)];
   }
-  P.rul = 0u;
-  if (part == 0) P.rul = *gbl((const uint16_t*)(base + g.coeff_bytes));  // 2-aligned (r1 even)
+  // every part loads the ruler (the 4 loads of a token hit one line), so the load is not
+  // conditional and the compiler's wait counts stay exact across the prefetch pipeline
+  P.rul = *gbl((const uint16_t*)(base + g.coeff_bytes));  // 2-aligned (r1 even)
+}
+
+// Wide fetch of the slot bytes one of a token's 4 loader threads needs for one KV head: 16-byte
+// loads only (5 per thread instead of one per dword). Part p loads coefficient chunks p, p+4,
+// p+8 (bytes 16c .. 16c+15 of the 16*KU-byte window; a chunk past the window is clamped to the
+// window's last one and never committed), chunk p of the 64-byte-aligned windows holding this
+// head's K row and V row (each row lies inside its window: misalignment + row length <= 64,
+// checked by the host; a chunk past the blob is clamped inside it and covers no row byte), and
+// the dword holding the coefficient ruler.
+template <int KU>
+struct RawSlotW {
+  static constexpr int kChunks = (KU + 3) / 4;  // coefficient chunks per part
+  u32x4 coef[kChunks];
+  u32x4 krow, vrow;
+  uint32_t rul;
+};
+
+template <int KU>
+__device__ __forceinline__ void fetch_raw_slot_w(RawSlotW<KU>& P, const uint8_t* base, int part,
+                                                 const Geom& g, int k_win, int v_win) {
+  using R = RawSlotW<KU>;
+  if (!base) {
+#pragma unroll
+    for (int i = 0; i < R::kChunks; ++i) P.coef[i] = u32x4{0u, 0u, 0u, 0u};
+    P.krow = P.vrow = u32x4{0u, 0u, 0u, 0u};
+    P.rul = 0u;
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < R::kChunks; ++i)
+    P.coef[i] = *gbl((const u32x4*)(base + 16 * min(part + 4 * i, KU - 1)));
+  P.krow = *gbl((const u32x4*)(base + min(k_win + 16 * part, g.blob - 16)));
+  P.vrow = *gbl((const u32x4*)(base + min(v_win + 16 * part, g.blob - 16)));
+  P.rul = *gbl((const uint32_t*)(base + (g.coeff_bytes & ~3)));
+}
+
+// Stage dwords 4*part .. 4*part+3 of a head row for the decode (the big-endian staged layout
+// below): this thread holds chunk `part` of the row's 64-byte window, the quad neighbour (lane
+// + 1) chunk part + 1, fetched with one DPP move per dword. `m4`/`sel`: the row's misalignment in
+// the window in dwords (wave-uniform) and the v_perm selector for its byte part and this part's
+// byte reversal (stage_selector). Part 3's neighbour is itself: those staged bytes lie past the
+// row and are never decoded.
+__device__ __forceinline__ void stage_row_w(const u32x4& mine, int m4, uint32_t sel, uint32_t* dst) {
+  uint32_t w[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    w[i] = mine[i];
+    // quad_perm [1, 2, 3, 3]: each lane reads lane + 1 of its quad
+    w[4 + i] = (uint32_t)__builtin_amdgcn_mov_dpp((int)mine[i], 0xF9, 0xF, 0xF, false);
+  }
+  switch (m4) {  // wave-uniform
+#define TTKV_STAGE_CASE(M)                                                          \
+  case M:                                                                           \
+    _Pragma("unroll") for (int i = 0; i < 4; ++i) dst[i] =                          \
+        __builtin_amdgcn_perm(w[(M) + i + 1], w[(M) + i], sel);                     \
+    break;
+    TTKV_STAGE_CASE(0)
+    TTKV_STAGE_CASE(1)
+    TTKV_STAGE_CASE(2)
+    default:
+      TTKV_STAGE_CASE(3)
+#undef TTKV_STAGE_CASE
+  }
 }
 
 // 2^x on the hardware exp unit (one v_exp_f32). Softmax weights below 2^-126 flush to zero,
