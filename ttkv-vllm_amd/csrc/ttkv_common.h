@@ -57,6 +57,18 @@ __host__ inline bool make_geom(const ttkv_layout* l, Geom* g) {
   return true;
 }
 
+// The read kernels fetch each head row through the 16-byte-aligned 64-byte window that starts at
+// the row's first byte rounded down: every row must lie inside its window (misalignment + row
+// bytes <= 64). All shipped allocations satisfy it (safe 49 B rows at offsets = h mod 16,
+// campaign4x 50 B at 2h mod 16, tight 30/35 B).
+__host__ inline bool rows_in_windows(const Geom& g) {
+  for (int h = 0; h < g.H; ++h)
+    if (((g.k_field + h * g.k_row) & 15) + g.k_row > 64 ||
+        ((g.k_slot + h * g.v_row) & 15) + g.v_row > 64)
+      return false;
+  return true;
+}
+
 // A pointer known to be in global memory, so loads through it are global_load_* (vector memory
 // counter only). Loads through a generic pointer become flat_load_*, which also count against the
 // LDS counter, so every later LDS wait would also wait for them.

@@ -885,11 +885,10 @@ int decode_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype,
   if (!ku) return host_fail(TTKV_E_UNSUPPORTED, "r1 > 160 is not built");
   if (ku * 16 > g.k_slot)
     return host_fail(TTKV_E_UNSUPPORTED, "padded coefficient block exceeds the K slot");
-  for (int h = 0; h < g.H; ++h)  // every head row inside its 64-byte load window
-    if (((g.k_field + h * g.k_row) & 15) + g.k_row > 64 || ((g.k_slot + h * g.v_row) & 15) + g.v_row > 64)
-      return host_fail(TTKV_E_UNSUPPORTED, "a head row of " + std::to_string(g.k_row) + "/" +
-                                               std::to_string(g.v_row) +
-                                               " bytes straddles its 64-byte load window");
+  if (!rows_in_windows(g))
+    return host_fail(TTKV_E_UNSUPPORTED, "a head row of " + std::to_string(g.k_row) + "/" +
+                                             std::to_string(g.v_row) +
+                                             " bytes straddles its 64-byte load window");
   if (!q || !page || !bt || !seq_lens || !qsl || !dec_map || !dec_pool || !cs_cache || !out || !err)
     return host_fail(TTKV_E_INVALID, "null pointer argument");
   if ((uintptr_t)page % 16 || slot_stride % 16 || slot_stride < g.blob)

@@ -119,7 +119,6 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
   constexpr bool EXACT = true;  // see the precision note at the top
   extern __shared__ __align__(16) unsigned char smem_raw[];
   PrefillSmem<KSTEPS, EXACT>& S = *reinterpret_cast<PrefillSmem<KSTEPS, EXACT>*>(smem_raw);
-  constexpr int kCPP = KSTEPS * 8;
   const Geom& g = a.g;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -274,8 +273,10 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
     const int64_t slot = (int64_t)blk * a.block_size + (pos - bi * a.block_size);
     return slot < a.n_slots ? a.page + slot * a.slot_stride : nullptr;
   };
-  RawSlot<2 * KSTEPS> P;
-  fetch_raw_slot<2 * KSTEPS>(P, slot_base(k0), part, g, k_row_off, v_row_off);
+  // the rows' 64-byte windows (16-aligned; each row lies inside its window, host-checked)
+  const int k_win = k_row_off & ~15, v_win = v_row_off & ~15;
+  RawSlotW<2 * KSTEPS> P;
+  fetch_raw_slot_w<2 * KSTEPS>(P, slot_base(k0), part, g, k_win, v_win);
 
   // score-tensor rows 16-byte aligned: every 4-key group starts on a 16-byte boundary
   const bool s_vec = SCORES && ((uintptr_t)a.s_out % 16 == 0) && a.s_q_stride % 4 == 0 &&
@@ -284,24 +285,27 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
     const int ntile = min(kPTile, k1 - tt);
     // ------------------------------------------------------------ commit this tile's bytes
     {
-      uint32_t* cdst = (uint32_t*)&S.coef[ptok][part * kCPP];
+      uint32_t* crow = (uint32_t*)&S.coef[ptok][0];
 #pragma unroll
-      for (int dw = 0; dw < KSTEPS * 2; ++dw) {
-        // bytes past r1 are finite int8 values and meet zero decoder rows: they contribute 0
-        uint32_t p01, p23;
-        i8x4_to_f16(P.coef[dw], p01, p23);
-        cdst[2 * dw] = p01;
-        cdst[2 * dw + 1] = p23;
-      }
-      if (part == 0) S.cs[ptok] = f16_bits_to_float(P.rul);
+      for (int i = 0; i < RawSlotW<2 * KSTEPS>::kChunks; ++i) {
+        // coefficient chunk part + 4i -> 16 fp16 values; bytes past r1 are finite int8 values
+        // and meet zero decoder rows: they contribute 0
+        const int cch = part + 4 * i;
+        if (cch < 2 * KSTEPS) {
+          uint32_t hh[8];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        S.u.raw.k[ptok][part * 4 + i] = __builtin_amdgcn_perm(P.krow[i + 1], P.krow[i], ksel);
-        S.u.raw.v[ptok][part * 4 + i] = __builtin_amdgcn_perm(P.vrow[i + 1], P.vrow[i], vsel);
+          for (int j = 0; j < 4; ++j) i8x4_to_f16(P.coef[i][j], hh[2 * j], hh[2 * j + 1]);
+          *(u32x4*)&crow[8 * cch] = u32x4{hh[0], hh[1], hh[2], hh[3]};
+          *(u32x4*)&crow[8 * cch + 4] = u32x4{hh[4], hh[5], hh[6], hh[7]};
+        }
       }
+      if (part == 0)
+        S.cs[ptok] = f16_bits_to_float((g.coeff_bytes & 2) ? P.rul >> 16 : P.rul & 0xffffu);
+      stage_row_w(P.krow, (k_row_off & 15) >> 2, ksel, &S.u.raw.k[ptok][part * 4]);
+      stage_row_w(P.vrow, (v_row_off & 15) >> 2, vsel, &S.u.raw.v[ptok][part * 4]);
     }
     if constexpr (SCORES)
-      if (tt + kPTile < k1) fetch_raw_slot<2 * KSTEPS>(P, slot_base(tt + kPTile), part, g, k_row_off, v_row_off);
+      if (tt + kPTile < k1) fetch_raw_slot_w<2 * KSTEPS>(P, slot_base(tt + kPTile), part, g, k_win, v_win);
     __syncthreads();
     // ------------------------------------------------------------ decode (thread = half row)
     // Decode, V transpose and reconstruction run at raised wave priority, so that where two
@@ -428,7 +432,7 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
     // angle wait, which would otherwise also wait for them. The score-tensor mode requests them
     // at the commit instead: its score stores count on the same in-order counter (measured).
     if constexpr (!SCORES)
-      if (tt + kPTile < k1) fetch_raw_slot<2 * KSTEPS>(P, slot_base(tt + kPTile), part, g, k_row_off, v_row_off);
+      if (tt + kPTile < k1) fetch_raw_slot_w<2 * KSTEPS>(P, slot_base(tt + kPTile), part, g, k_win, v_win);
     __syncthreads();
     // ------------------------------------------------------------ scores S^T = Kp Q^T
     float4v sacc[4][G];
@@ -720,6 +724,10 @@ int prefill_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype
   if (!ksteps) return host_fail(TTKV_E_UNSUPPORTED, "r1 > 160 is not built");
   if (ksteps * 32 > g.k_slot)
     return host_fail(TTKV_E_UNSUPPORTED, "padded coefficient block exceeds the K slot");
+  if (!rows_in_windows(g))
+    return host_fail(TTKV_E_UNSUPPORTED, "a head row of " + std::to_string(g.k_row) + "/" +
+                                             std::to_string(g.v_row) +
+                                             " bytes straddles its 64-byte load window");
   if (!q || !page || !bt || !seq_lens || !qsl || !dec_map || !dec_pool || !cs_cache || !err)
     return host_fail(TTKV_E_INVALID, "null pointer argument");
   if (!scores && !out) return host_fail(TTKV_E_INVALID, "out is null");
