@@ -1,0 +1,160 @@
+"""The product's first-chunk fit (`vllm_ttkv.encode.fit_into_budget`) against the exact fit.
+
+The product computes only the leading singular triplets (subspace iteration on a Gram matrix); the
+oracle runs the reference's full SVD (codec/ttkv_codec.py:78-109). Pins:
+  * the rank rule itself, on random spectra, equals the reference's reversed-cumsum form over the
+    full spectrum (including the no-hit and all-zero cases);
+  * the UNQUANTISED factorisation (`encode._tt_factors`) equals the float64 exact TT-SVD
+    (`oracle.codec.tt_svd` on float64 input): same ranks, rank-r approximation within 1e-6
+    (relative) -- below the ~3e-6 by which the reference's own fp32 LAPACK SVD misses it -- and
+    singular values within 1e-6;
+  * the quantised fit against the oracle's (fp32 SVD, as the reference runs it): same rank, exact
+    zero padding beyond it, and, once each component's sign is aligned, coefficient codes within
+    one code in under 2% of entries and a decoder within two code steps, off by more than its
+    fp16 ruler's ulp in under 1% of entries (rounding ties: the oracle's fp32 SVD noise moves
+    values across half-codes); fitted keys whose error against the raw keys is within 1e-3
+    (relative) of the exact fit's -- the least-squares optimum at that rank.
+The GPU test runs the product fit on the device (the serving path), checks the same, and that its
+signs are the ones the CPU run picks (the fit fixes a sign convention)."""
+import time
+
+import pytest
+import torch
+
+from oracle import codec as oc
+from oracle import encode as oe
+from oracle.layout import layout_for_config as oracle_layout
+from vllm_ttkv import encode as penc, synth
+from vllm_ttkv.layout import CONFIGS, layout_for_config
+
+R1 = 110
+
+
+def _keys_err(cq, cs, dec, K):
+    H, n, d = K.shape
+    mine = (cq.double().cpu() * cs.double().cpu().reshape(-1, 1)) @ dec.double().cpu()
+    return float((mine.reshape(n, H, d) - K.permute(1, 0, 2).double().cpu()).norm())
+
+
+def _compare(fit, K, cfg_name):
+    cfg = CONFIGS[cfg_name]
+    lay = layout_for_config(cfg, R1)
+    ref = oe.fit_into_budget(K.cpu().float(), oracle_layout(oc.CONFIGS[cfg_name], R1),
+                             oc.CONFIGS[cfg_name])
+    r = fit.fitted_rank
+    assert r == ref["fitted_rank"]
+    cq, dec = fit.coeff_q.cpu(), fit.decoder.decoder_f.cpu()
+    assert not bool(cq[:, r:].any()) and not bool(dec[r:].any())
+    sign = torch.where((dec * ref["decoder_f"]).sum(1) < 0, -1.0, 1.0)
+    qm = 2 ** (lay.qbits - 1) - 1
+    step = ref["decoder_f"].abs().amax(1, keepdim=True) / qm
+    derr = (dec * sign[:, None] - ref["decoder_f"]).abs()
+    assert bool((derr <= 2.01 * step + 1e-6).all())
+    ulp = 2e-3 * ref["decoder_f"].abs() + 1e-3 * step
+    assert float((derr > ulp).float().mean()) < 1e-2
+    dq = (cq.to(torch.int32) * sign.to(torch.int32) - ref["coeff_q"].to(torch.int32)).abs()
+    assert int(dq.max()) <= 1 and float((dq != 0).float().mean()) < 0.02
+    e_mine = _keys_err(fit.coeff_q, fit.coeff_scale, fit.decoder.decoder_f, K)
+    e_ref = _keys_err(ref["coeff_q"], ref["coeff_scale"], ref["decoder_f"], K)
+    assert e_mine <= e_ref * (1 + 1e-3)
+    return sign
+
+
+def _approx(cores, n):
+    r = cores[0].shape[2]
+    right = torch.einsum("ajb,bh->ajh", cores[1].double(), cores[2][:, :, 0].double())
+    return cores[0].reshape(n, r).double() @ right.reshape(r, -1)
+
+
+def _check_factors(K, tol):
+    X = K.permute(1, 2, 0).contiguous()
+    n = X.shape[0]
+    mine = penc._tt_factors(X, tol, R1)
+    exact, ranks = oc.tt_svd(X.double(), tol, R1)
+    assert [c.shape[2] for c in mine] == ranks
+    A = _approx(exact, n)
+    assert float((_approx(mine, n) - A).norm() / A.norm()) < 1e-6
+    sv_exact = torch.linalg.svdvals(X.reshape(n, -1).double())[:ranks[0]]
+    sv_mine = torch.linalg.svdvals(_approx(mine, n))[:ranks[0]]
+    assert float(((sv_mine - sv_exact).abs() / sv_exact).max()) < 1e-6
+
+
+def _reference_rank(e, tol, cap):
+    """The reference's rule, literally: reversed cumulative energy over the FULL spectrum."""
+    tail = torch.flip(torch.cumsum(torch.flip(e, [0]), 0), [0]) / (e.sum() + 1e-30)
+    hit = torch.nonzero(tail <= tol ** 2, as_tuple=False)
+    r = int(hit[0].item()) + 1 if hit.numel() else int(e.numel())
+    return max(1, min(r, e.numel(), cap))
+
+
+def test_energy_rank_rule_matches_reference_form():
+    g = torch.Generator().manual_seed(4)
+    for trial in range(200):
+        m = int(torch.randint(1, 300, (1,), generator=g))
+        e = torch.rand(m, generator=g, dtype=torch.float64).pow(6).sort(descending=True).values
+        if trial % 17 == 0:
+            e[m // 2:] = 0.0
+        tol = float(torch.rand(1, generator=g)) * 0.3
+        cap = int(torch.randint(1, 200, (1,), generator=g))
+        lead = min(m, cap + 5)                      # only the leading values, as the product has
+        r = penc._energy_rank(e[:lead], float(e.sum()), tol)
+        r = lead if r is None else r
+        assert max(1, min(r, cap)) == _reference_rank(e, tol, cap)
+    zero = torch.zeros(7, dtype=torch.float64)
+    assert penc._energy_rank(zero, 0.0, 0.05) == 1 == _reference_rank(zero, 0.05, 110)
+
+
+@pytest.mark.parametrize("cfg_name", ["safe", "campaign4x"])
+@pytest.mark.parametrize("T", [40, 600, 2048])
+def test_product_fit_matches_exact_fit(cfg_name, T):
+    K = synth.keys(T, seed=5)
+    _check_factors(K, CONFIGS[cfg_name]["tols"])
+    fit = penc.fit_into_budget(K, layout_for_config(CONFIGS[cfg_name], R1), CONFIGS[cfg_name])
+    _compare(fit, K, cfg_name)
+
+
+def test_low_rank_keys():
+    """Keys of exact rank 7. The reference's rule keeps the first component whose tail energy is
+    below tol^2, here the 8th, of zero energy, whose left vector is arbitrary (LAPACK returns some
+    unit vector orthogonal to the rest; the product a zero column): same rank as the oracle, same
+    rank-7 approximation, fitted keys as good as the oracle's."""
+    g = torch.Generator().manual_seed(9)
+    A = torch.randn(900, 7, generator=g, dtype=torch.float64)
+    B = torch.randn(7, 1024, generator=g, dtype=torch.float64)
+    K = (A @ B).float().reshape(900, 8, 128).permute(1, 0, 2).contiguous()
+    cfg = CONFIGS["safe"]
+    fit = penc.fit_into_budget(K, layout_for_config(cfg, R1), cfg)
+    ref = oe.fit_into_budget(K, oracle_layout(oc.CONFIGS["safe"], R1), oc.CONFIGS["safe"])
+    assert fit.fitted_rank == ref["fitted_rank"] == 8
+    assert not bool(fit.coeff_q[:, 8:].any()) and not bool(fit.decoder.decoder_f[8:].any())
+    assert bool(torch.isfinite(fit.decoder.decoder_f).all())
+    X = K.permute(1, 2, 0).contiguous()
+    mine = _approx(penc._tt_factors(X, cfg["tols"], R1), 900)
+    exact = _approx(oc.tt_svd(X.double(), cfg["tols"], R1)[0], 900)
+    assert float((mine - exact).norm() / exact.norm()) < 1e-6
+    e_mine = _keys_err(fit.coeff_q, fit.coeff_scale, fit.decoder.decoder_f, K)
+    e_ref = _keys_err(ref["coeff_q"], ref["coeff_scale"], ref["decoder_f"], K)
+    assert e_mine <= e_ref * 1.05 + 1e-3 * float(K.norm())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("cfg_name", ["safe", "campaign4x"])
+def test_product_fit_on_device(cfg_name):
+    T = 2048
+    K = synth.keys(T, seed=5)
+    lay = layout_for_config(CONFIGS[cfg_name], R1)
+    Kd = K.cuda()
+    penc.fit_into_budget(Kd, lay, CONFIGS[cfg_name])                  # warm the solvers
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    fit = penc.fit_into_budget(Kd, lay, CONFIGS[cfg_name])
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3
+    print(f"[fit] {cfg_name} T={T} rank={fit.fitted_rank} device fit {ms:.1f} ms", flush=True)
+    assert fit.coeff_q.is_cuda and fit.decoder.decoder_f.is_cuda
+    sign = _compare(fit, K, cfg_name)
+    cpu = penc.fit_into_budget(K, lay, CONFIGS[cfg_name])
+    sign_cpu = torch.where((cpu.decoder.decoder_f * fit.decoder.decoder_f.cpu()).sum(1) < 0,
+                           -1.0, 1.0)
+    assert bool((sign_cpu == 1).all())                                 # same convention
+    assert ms < 2000

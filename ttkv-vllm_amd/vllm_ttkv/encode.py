@@ -1,10 +1,12 @@
 """The write half: raw K and V of new tokens into packed slots.
 
 Two phases, as in the reference (vllm_ttkv/encode.py:1-36):
-  * a request's FIRST chunk is fitted -- TT-SVD of the [n, d, H] key block, tokens first, capped
-    at the layer's rank budget and zero-padded to it (`fit_into_budget`, encode.py:257-298). The
-    fit runs on the device through torch's linear algebra (rocSOLVER on ROCm); it happens once
-    per request and layer and its bits are LAPACK-dependent, as they are in the reference.
+  * a request's FIRST chunk is fitted -- the energy-truncated tensor-train factorisation of the
+    [n, d, H] key block, tokens first, capped at the layer's rank budget and zero-padded to it
+    (`fit_into_budget`, encode.py:257-298). It runs on the device as GEMMs plus small dense
+    factorisations (subspace iteration on a Gram matrix, see `_leading_factors`), once per
+    request and layer; like the reference's SVD-based fit, its bits depend on the linear algebra
+    underneath, and it is pinned by invariants (rank rule, zero padding, least squares).
   * every later token is projected onto that frozen decoder and packed by the HIP write kernel
     (`kernels.write_paged`, K3), which also packs the first chunk from the fit's coefficients.
 
@@ -57,26 +59,134 @@ class FittedK:
     budget: int
 
 
-def _tt_svd(X: torch.Tensor, tol: float, max_rank: int | None):
-    """Energy-truncated TT-SVD (codec/ttkv_codec.py:78-109)."""
-    dims = list(X.shape)
-    rest = X.reshape(dims[0], -1)
-    cores, r_prev = [], 1
-    for k in range(len(dims) - 1):
-        M = rest.reshape(r_prev * dims[k], -1)
-        U, S, Vh = torch.linalg.svd(M, full_matrices=False)
-        e = S.pow(2)
-        tail = torch.flip(torch.cumsum(torch.flip(e, [0]), 0), [0]) / (e.sum() + 1e-30)
-        hit = torch.nonzero(tail <= tol ** 2, as_tuple=False)
-        r = int(hit[0].item()) + 1 if hit.numel() else int(S.numel())
-        r = max(1, min(r, int(S.numel())))
-        if max_rank is not None:
-            r = max(1, min(r, max_rank))
-        cores.append(U[:, :r].reshape(r_prev, dims[k], r))
-        rest = (S[:r].unsqueeze(1) * Vh[:r, :]).reshape(r, *dims[k + 1:])
-        r_prev = r
-    cores.append(rest.reshape(r_prev, dims[-1], 1))
-    return cores
+# ---------------------------------------------------------------- the fit's factorisation
+# The first-chunk fit is the reference's energy-truncated tensor-train decomposition of the
+# [n, d, H] key block (codec/ttkv_codec.py:78-109): a rank-r1 factorisation of the n x (d*H)
+# unfolding M, then of the (r1*d) x H remainder. Only the LEADING r1 singular triplets of M
+# (r1 <= the layer's budget, 110) and its total energy are used, so no full SVD is computed. In
+# float64, the smaller Gram matrix of M (M^T M, d*H = 1024 wide, or M M^T for a chunk of fewer
+# tokens) is formed with one GEMM; randomized subspace iteration on it with a Rayleigh-Ritz step
+# (Halko, Martinsson & Tropp, SIAM Review 53(2), 2011, sections 4.5 and 5) gives the leading
+# eigenpairs, i.e. the leading singular values and vectors of M. Squaring the condition number is
+# harmless here: the kept components lie within tol of the top of the spectrum and the arithmetic
+# is float64. The rank follows the reference's energy rule from the leading spectrum and the
+# exact total (the Gram trace). The second stage has only H columns and is solved through its
+# H x H Gram matrix exactly. Singular vectors are defined up to sign; a sign flip of a component
+# flips the coefficient column and the decoder row together and leaves the fitted keys unchanged.
+# Each component's sign is fixed here so that the largest-magnitude entry of its left vector is
+# positive, which makes the fit's signs the same on every device.
+
+_OVERSAMPLE = 128     # extra subspace columns beyond the rank budget
+_ITERS = 24           # subspace iterations: the error decays like (s_{r+p+1} / s_r)^(2 * iters)
+_RANGE_SEED = 0x7E5   # fixed start-block seed: the fit is deterministic
+
+
+def _chol_qr(Y: torch.Tensor, infos: list) -> torch.Tensor:
+    """One Cholesky QR step, Y R^-1 with R^T R = Y^T Y, on a tall float64 Y. The factorisation's
+    status stays on the device (appended to `infos`) so the iteration never waits on the host."""
+    R, info = torch.linalg.cholesky_ex(Y.T @ Y, upper=True)
+    infos.append(info)
+    return torch.linalg.solve_triangular(R, Y, upper=True, left=False)
+def _energy_rank(e: torch.Tensor, total: float, tol: float) -> int | None:
+    """The reference's rank rule on a descending energy spectrum e (squared singular values):
+    r = 1 + the first index i at which the energy of components i, i+1, ... is <= tol^2 of the
+    total (codec/ttkv_codec.py:97-100). `e` may hold only the leading values: the energy from i on
+    is the total minus the leading partial sum. None when no index of `e` qualifies."""
+    before = torch.cumsum(e, 0) - e                      # energy of components < i
+    tail = (total - before) / (total + 1e-30)
+    hit = torch.nonzero(tail <= tol ** 2, as_tuple=False)
+    return int(hit[0].item()) + 1 if hit.numel() else None
+
+
+def _fix_signs(U: torch.Tensor, SVh: torch.Tensor):
+    """Flip each component so the largest-magnitude entry of its column of U is positive."""
+    pick = U.abs().argmax(0, keepdim=True)
+    s = torch.where(torch.gather(U, 0, pick) < 0, -1.0, 1.0).to(U.dtype)   # [1, r]
+    return U * s, SVh * s.T
+
+
+def _nonzero(S: torch.Tensor) -> torch.Tensor:
+    """Divisors for U = M V / S. The energy rule can keep one component of (numerically) zero
+    energy -- the first one whose tail is below tol^2 -- whose left vector is arbitrary; dividing
+    its rounding noise by ~0 would blow it up, so it gets a zero column instead (its decoder row
+    is zero too: the fitted keys are the same)."""
+    return torch.where(S > S[:1] * 1e-12, S, torch.full_like(S, float("inf")))
+
+
+def _leading_eigh(G: torch.Tensor, count: int):
+    """Leading `count` eigenpairs (descending) of a symmetric positive semidefinite float64 G,
+    from randomized subspace iteration with a Rayleigh-Ritz step; exact when `count` spans G.
+    Inside the iteration one Cholesky QR per step keeps the block well conditioned (only its span
+    matters); the final basis gets a second one (CholeskyQR2: orthonormal to working precision).
+    If any Cholesky factorisation met a numerically rank-deficient block, the iteration is redone
+    with Householder QR."""
+    dim = G.shape[0]
+    p = min(count + _OVERSAMPLE, dim)
+    if p == dim:
+        lam, V = torch.linalg.eigh(G)
+        return lam.flip(0).clamp(min=0.0), V.flip(1)
+    gen = torch.Generator(device=G.device)
+    gen.manual_seed(_RANGE_SEED)
+    Y0 = G @ torch.randn(dim, p, generator=gen, dtype=torch.float64, device=G.device)
+    infos = []
+    Q = _chol_qr(Y0, infos)
+    for _ in range(_ITERS):
+        Q = _chol_qr(G @ Q, infos)
+    Q = _chol_qr(Q, infos)
+    if bool(torch.stack(infos).any()):                    # one host sync for the whole loop
+        Q = torch.linalg.qr(Y0, mode="reduced")[0]
+        for _ in range(_ITERS):
+            Q = torch.linalg.qr(G @ Q, mode="reduced")[0]
+    lam, W = torch.linalg.eigh(Q.T @ G @ Q)               # Rayleigh-Ritz on span(Q)
+    return lam.flip(0).clamp(min=0.0), (Q @ W).flip(1)
+
+
+def _leading_factors(M: torch.Tensor, tol: float, max_rank: int):
+    """Rank-r factorisation M ~ U_r diag(S_r) Vh_r of a [m, k] matrix by the energy rule, capped at
+    max_rank: the leading r singular triplets only. Returns (U_r fp32 [m, r], SVh_r fp32 [r, k])
+    with SVh_r = diag(S_r) Vh_r."""
+    Md = M.to(torch.float64)
+    m, k = Md.shape
+    right = k <= m                                        # eigenvectors of M^T M are V
+    G = Md.T @ Md if right else Md @ Md.T
+    lam, E = _leading_eigh(G, max_rank)
+    r = _energy_rank(lam, float(torch.trace(G)), tol)
+    r = max(1, min(lam.numel() if r is None else r, max_rank))
+    if right:
+        S = lam[:r].sqrt()
+        U = (Md @ E[:, :r]) / _nonzero(S)                 # left singular vectors
+        SVh = S[:, None] * E[:, :r].T
+    else:
+        U = E[:, :r]
+        SVh = U.T @ Md                                    # diag(S) Vh = U^T M
+    U, SVh = _fix_signs(U, SVh)
+    return U.to(torch.float32), SVh.to(torch.float32)
+
+
+def _narrow_factors(M: torch.Tensor, tol: float):
+    """The same factorisation for a [m, c] matrix with few columns (c = H), uncapped, through the
+    c x c Gram matrix: M = U diag(S) Vh with M^T M = V diag(S^2) V^T."""
+    Md = M.to(torch.float64)
+    lam, V = torch.linalg.eigh(Md.T @ Md)
+    lam, V = lam.flip(0).clamp(min=0.0), V.flip(1)
+    total = float(lam.sum())
+    r = _energy_rank(lam, total, tol)
+    r = max(1, int(lam.numel()) if r is None else r)
+    S = lam[:r].sqrt()
+    U = (Md @ V[:, :r]) / _nonzero(S)                     # left singular vectors
+    SVh = S[:, None] * V[:, :r].T
+    U, SVh = _fix_signs(U, SVh)
+    return U.to(torch.float32), SVh.to(torch.float32)
+
+
+def _tt_factors(X: torch.Tensor, tol: float, max_rank: int):
+    """Cores [1, n, r1], [r1, d, r2], [r2, H, 1] of X [n, d, H] (tokens first)."""
+    n, d, H = X.shape
+    U1, R1 = _leading_factors(X.reshape(n, d * H), tol, max_rank)
+    r1 = int(U1.shape[1])
+    U2, R2 = _narrow_factors(R1.reshape(r1 * d, H), tol)
+    r2 = int(U2.shape[1])
+    return [U1.reshape(1, n, r1), U2.reshape(r1, d, r2), R2.reshape(r2, H, 1)]
 
 
 def _quant_core(c: torch.Tensor, qbits: int) -> torch.Tensor:
@@ -98,7 +208,7 @@ def fit_into_budget(K: torch.Tensor, lay: TTKLayout, cfg: dict) -> FittedK:
         raise TypeError(f"raw keys arrived as {K.dtype}")
     K = K.to(torch.float32)
     qm = 2 ** (lay.qbits - 1) - 1
-    cores = _tt_svd(K.permute(1, 2, 0).contiguous(), cfg["tols"], lay.r1)   # [n, d, H]
+    cores = _tt_factors(K.permute(1, 2, 0).contiguous(), cfg["tols"], lay.r1)  # [n, d, H]
     r1 = int(cores[0].shape[2])
     c = cores[0].reshape(n, r1)
     cs = _ruler(c.abs().amax(1, keepdim=True), qm)
