@@ -214,3 +214,75 @@ def test_layer_index_of_vllm_names():
     assert li("model.layers.7.self_attn.attn") == 7
     assert li("model.decoder_layers.3.attn.5") == 3
     assert li("layers.12") == 12 and li("attn_9") == 9 and li("attn") is None
+
+
+class _NoRead:
+    """A device tensor stand-in that fails if the host reads it."""
+
+    def __getitem__(self, item):
+        raise AssertionError("seq_lens was read back")
+
+
+def test_prefill_plan_from_host_metadata():
+    """With `num_computed_tokens_cpu`, first chunks and exact lengths come from the host: the
+    device `seq_lens` is never read. Without it, one read of `seq_lens` decides."""
+    md = _md([0, 1, 41, 141], [9, 40, 300])
+    plan = impl.BatchPlan.of(md)
+    im = impl.TTKVAttentionImpl(24, 128, 128 ** -0.5, 8)
+    assert im._first_chunks(md, plan) == [False, True, False]
+    assert im._seq_lens_host(md, plan) == [9, 40, 300]
+    md.num_computed_tokens_cpu = torch.tensor([8, 0, 200], dtype=torch.int32)
+    md.seq_lens = _NoRead()
+    assert im._first_chunks(md, plan) == [False, True, False]
+    assert im._seq_lens_host(md, plan) == [9, 40, 300]
+
+
+def test_builder_declares_uniform_decode_graphs(monkeypatch):
+    from types import SimpleNamespace
+    from vllm_ttkv.metadata import AttentionCGSupport
+    assert (TTKVAttentionMetadataBuilder.cudagraph_support
+            == AttentionCGSupport.UNIFORM_SINGLE_TOKEN_DECODE)
+    monkeypatch.setenv("VLLM_TTKV_MAX_MODEL_LEN", "4096")
+    b = TTKVAttentionMetadataBuilder()
+    qsl = torch.arange(4, dtype=torch.int32)
+    cam = SimpleNamespace(seq_lens=torch.ones(3, dtype=torch.int32),
+                          slot_mapping=torch.zeros(3, dtype=torch.int64),
+                          block_table_tensor=torch.zeros(3, 4, dtype=torch.int32),
+                          query_start_loc=qsl, query_start_loc_cpu=qsl, num_actual_tokens=3,
+                          max_query_len=1, max_seq_len=17,
+                          _num_computed_tokens_cpu=torch.tensor([16, 3, 0]))
+    md = b.build_for_cudagraph_capture(cam)
+    assert md.max_seq_len == 4096 and md.ttkv_serial > 0
+    assert md.num_computed_tokens_cpu.tolist() == [16, 3, 0]
+    assert b.can_run_in_cudagraph(cam)
+    cam.max_query_len = 5
+    assert not b.can_run_in_cudagraph(cam)
+    with pytest.raises(RuntimeError, match="uniform single-token decode"):
+        b.build_for_cudagraph_capture(cam)
+    monkeypatch.delenv("VLLM_TTKV_MAX_MODEL_LEN")
+    cam.max_query_len = 1
+    with pytest.raises(RuntimeError, match="maximum length"):
+        TTKVAttentionMetadataBuilder().build_for_cudagraph_capture(cam)
+
+
+def test_fixed_workspaces_are_never_replaced_once_frozen():
+    ws = impl.DeviceWorkspaces("cpu")
+    a = ws.get("decode", 1000, capacity=4096, fixed=True)
+    assert a.numel() == 4096 and ws.get("decode", 4000, fixed=True) is a
+    b = ws.get("decode", 5000, fixed=True)           # before any capture: may grow
+    assert b.numel() == 5000
+    p = ws.get("prefill", 100)
+    ws.frozen = True                                 # a graph now holds the decode buffers
+    assert ws.get("decode", 5000, fixed=True) is b
+    with pytest.raises(RuntimeError, match="captured graph"):
+        ws.get("decode", 5001, fixed=True)
+    assert ws.get("prefill", 10 ** 4).numel() == 10 ** 4 and ws.get("prefill", 1) is not p
+
+
+def test_serving_limits_from_environment(monkeypatch):
+    monkeypatch.delenv("VLLM_TTKV_MAX_NUM_SEQS", raising=False)
+    monkeypatch.delenv("VLLM_TTKV_MAX_MODEL_LEN", raising=False)
+    assert impl.serving_limits(1234) == (256, 1234)
+    monkeypatch.setenv("VLLM_TTKV_MAX_NUM_SEQS", "12")
+    monkeypatch.setenv("VLLM_TTKV_MAX_MODEL_LEN", "777")
+    assert impl.serving_limits(1234) == (12, 777)

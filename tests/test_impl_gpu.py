@@ -3,6 +3,7 @@ mixed decode / continuation / first-chunk step, each checked against the CPU ora
 cache bytes the step wrote (reference test: test_impl_decode.py:259-873 -- real forward vs
 attend_raw_store, write->decode loop, continuation over the whole store, mixed batch)."""
 from dataclasses import dataclass
+from types import SimpleNamespace
 
 import pytest
 import torch
@@ -11,10 +12,11 @@ from helpers import HQ, H, D
 from oracle import attend
 from oracle.layout import layout_for_config as oracle_layout
 from oracle.rope import cos_sin_from_cache, rope_apply
+from vllm_ttkv import impl as impl_mod
 from vllm_ttkv import patch, rope_store, synth
 from vllm_ttkv.impl import TTKVAttentionImpl
 from vllm_ttkv.layout import CONFIGS, layout_for_config
-from vllm_ttkv.metadata import TTKVAttentionMetadata
+from vllm_ttkv.metadata import TTKVAttentionMetadata, TTKVAttentionMetadataBuilder
 from vllm_ttkv.rope import cos_sin_cache
 
 pytestmark = pytest.mark.gpu
@@ -215,3 +217,172 @@ def test_decode_steps_replayed_from_one_captured_graph(monkeypatch):
                                    SCALE, dtype=torch.float64)
         _check(out.float().cpu(), want, f"graph replay {t}")
     rope_store.clear_stores()
+    impl_mod.release_workspaces()
+
+
+class _DecodeBatch:
+    """A decode batch over rows `rows` of the block table, with static input buffers (as vLLM's
+    runner keeps them for a captured graph) and metadata from the builder's capture path."""
+
+    def __init__(self, rows, bt, builder, csc_d, dev="cuda"):
+        n = len(rows)
+        self.rows, self.bt, self.csc_d = rows, bt, csc_d
+        self.q = torch.zeros(n, HQ, D, dtype=torch.float16, device=dev)
+        self.k = torch.zeros(n, H * D, dtype=torch.float16, device=dev)
+        self.v = torch.zeros(n, H * D, dtype=torch.float16, device=dev)
+        self.raw = torch.zeros(n, H * D, dtype=torch.float32, device=dev)
+        self.out = torch.zeros(n, HQ, D, dtype=torch.float16, device=dev)
+        qsl = torch.arange(n + 1, dtype=torch.int32)
+        cam = SimpleNamespace(
+            seq_lens=torch.ones(n, dtype=torch.int32, device=dev),
+            slot_mapping=torch.zeros(n, dtype=torch.int64, device=dev),
+            block_table_tensor=bt[rows].to(torch.int32).to(dev), query_start_loc=qsl.to(dev),
+            query_start_loc_cpu=qsl, num_actual_tokens=n, max_query_len=1, max_seq_len=1)
+        self.md = builder.build_for_cudagraph_capture(cam)
+
+    def fill(self, seqs, pos, csc):
+        """Next token of each row's request at positions `pos` (one per row)."""
+        raw = torch.stack([seqs[r].K[p] for r, p in zip(self.rows, pos)])      # [n, H, d]
+        c, s_ = cos_sin_from_cache(csc, torch.tensor(pos), D)
+        kp = rope_apply(raw, c.unsqueeze(1), s_.unsqueeze(1))
+        n = len(self.rows)
+        self.q.copy_(torch.stack([seqs[r].Q[p] for r, p in zip(self.rows, pos)]).half())
+        self.k.copy_(kp.reshape(n, H * D).half())
+        self.v.copy_(torch.stack([seqs[r].V[p] for r, p in zip(self.rows, pos)])
+                     .reshape(n, H * D).half())
+        self.raw.copy_(raw.reshape(n, H * D))
+        self.md.seq_lens.copy_(torch.tensor([p + 1 for p in pos], dtype=torch.int32))
+        self.md.slot_mapping.copy_(torch.stack([self.bt[r, p // BS].long() * BS + p % BS
+                                                for r, p in zip(self.rows, pos)]))
+
+    def stash(self):
+        patch.stash_raw_k(NAME, self.raw, cos_sin_cache=self.csc_d)
+
+
+def _oracle_decode(olay, cache, C, bt, rows, pos, q, csc):
+    flat = cache.view(torch.uint8).reshape(-1, C).cpu()
+    st = rope_store.store_for_layer(NAME)
+    decs = [st.decoders[int(bt[r, 0])].decoder_f.cpu() for r in rows]
+    n = len(rows)
+    return attend.paged_decode(olay, flat, bt[rows], torch.tensor([p + 1 for p in pos]),
+                               torch.arange(n + 1), q.float().cpu(), decs, csc, BS, SCALE,
+                               dtype=torch.float64)
+
+
+def test_graphs_at_two_batch_sizes_then_a_larger_eager_batch(monkeypatch):
+    """vLLM's capture pattern for uniform decode: graphs captured at two batch sizes (2 and 4
+    requests) from the builder's capture metadata (`max_seq_len` = the model's maximum), then a
+    LARGER batch (all 6 requests) run eagerly, then both graphs replayed twice more. Every step is
+    checked against the oracle over the cache bytes it wrote, and the decode-step workspaces are
+    the same buffers before and after the larger batch (nothing a graph holds was replaced). The
+    first chunks arrive in one prefill step whose fit decisions come from
+    `num_computed_tokens_cpu` (no read of `seq_lens`)."""
+    monkeypatch.delenv("VLLM_TTKV_CHECK", raising=False)
+    monkeypatch.setenv("VLLM_TTKV_MAX_NUM_SEQS", "8")
+    monkeypatch.setenv("VLLM_TTKV_MAX_MODEL_LEN", "2048")
+    impl_mod.release_workspaces()
+    lay = layout_for_config(CONFIGS["safe"], 110)
+    olay = oracle_layout(CONFIGS["safe"], 110)
+    rope_store.clear_stores()
+    csc = cos_sin_cache(2048)
+    csc_d = csc.cuda()
+    lens = [700, 400, 900, 300, 520, 610]
+    seqs = [_Seq(L + 8, 40 + i) for i, L in enumerate(lens)]
+    bt0, nblk = synth.shuffled_block_table([L + 8 for L in lens], BS, seed=41, extra_blocks=2)
+    # as vLLM's: ceil(max_model_len / block_size) columns, unused entries padded (-1 here, so a
+    # read past a request's length would set the device error bit)
+    bt = torch.full((6, 2048 // BS), -1, dtype=torch.int32)
+    bt[:, :bt0.shape[1]] = bt0
+    C = lay.compressed_bytes_per_token()
+    cache = torch.zeros(nblk, 1, BS, C // 2, dtype=torch.bfloat16, device="cuda")
+    im = TTKVAttentionImpl(HQ, D, SCALE, H)
+    layer = _Layer(NAME, lay)
+    builder = TTKVAttentionMetadataBuilder()
+    assert builder.max_model_len == 2048
+
+    # one prefill step: all six first chunks, planned from host metadata
+    dev = "cuda"
+    qsl = [0]
+    for L in lens:
+        qsl.append(qsl[-1] + L)
+    N = qsl[-1]
+    raw_k = torch.cat([sq.K[:L] for sq, L in zip(seqs, lens)])
+    pos = torch.cat([torch.arange(L) for L in lens])
+    c, s_ = cos_sin_from_cache(csc, pos, D)
+    k_post = rope_apply(raw_k, c.unsqueeze(1), s_.unsqueeze(1)).half()
+    slots = torch.cat([bt[r, torch.arange(L) // BS].long() * BS + torch.arange(L) % BS
+                       for r, L in enumerate(lens)])
+    md = TTKVAttentionMetadata(
+        seq_lens=torch.tensor(lens, dtype=torch.int32, device=dev), slot_mapping=slots.to(dev),
+        block_table=bt[:6].to(dev), query_start_loc=torch.tensor(qsl, dtype=torch.int32,
+                                                                 device=dev),
+        query_start_loc_cpu=torch.tensor(qsl, dtype=torch.int32), num_actual_tokens=N,
+        num_computed_tokens_cpu=torch.zeros(6, dtype=torch.int32),
+        max_query_len=max(lens), max_seq_len=max(lens))
+    patch.stash_raw_k(NAME, raw_k.reshape(N, H * D).to(dev), cos_sin_cache=csc_d)
+    out = torch.zeros(N, HQ, D, dtype=torch.float16, device=dev)
+    im.forward(layer, torch.cat([sq.Q[:L] for sq, L in zip(seqs, lens)]).half().to(dev),
+               k_post.reshape(N, H * D).to(dev),
+               torch.cat([sq.V[:L] for sq, L in zip(seqs, lens)]).reshape(N, H * D).half()
+               .to(dev), cache, md, output=out)
+    torch.cuda.synchronize()
+    assert int(im.error_word.item()) == 0
+    assert len(rope_store.store_for_layer(NAME).decoders) == 6
+    nxt = list(lens)                       # next position of each request
+
+    batches = {"A": _DecodeBatch([0, 1], bt, builder, csc_d),
+               "B": _DecodeBatch([2, 3, 4, 5], bt, builder, csc_d)}
+    assert batches["A"].md.max_seq_len == 2048
+    graphs = {}
+    for name, b in batches.items():        # eager warm-up step, then capture
+        p = [nxt[r] for r in b.rows]
+        b.fill(seqs, p, csc)
+        b.stash()
+        im.forward(layer, b.q, b.k, b.v, cache, b.md, output=b.out)
+        torch.cuda.synchronize()
+        _check(b.out.float().cpu(), _oracle_decode(olay, cache, C, bt, b.rows, p, b.q, csc),
+               f"warm-up {name}")
+        for r in b.rows:
+            nxt[r] += 1
+        g = torch.cuda.CUDAGraph()
+        b.stash()
+        with torch.cuda.graph(g):
+            im.forward(layer, b.q, b.k, b.v, cache, b.md, output=b.out)
+        graphs[name] = g
+    ws = impl_mod.workspaces(dev)
+    assert ws.frozen
+    held = {k: v.data_ptr() for k, v in ws.bufs.items() if k.startswith("decode")}
+    assert set(held) == {"decode", "decode_write"}
+
+    # a larger batch, eagerly: all six requests
+    rows = list(range(6))
+    big = _DecodeBatch(rows, bt, builder, csc_d)
+    big.md.max_seq_len = max(nxt) + 1      # an eager step carries the exact maximum
+    p = [nxt[r] for r in rows]
+    big.fill(seqs, p, csc)
+    big.stash()
+    im.forward(layer, big.q, big.k, big.v, cache, big.md, output=big.out)
+    torch.cuda.synchronize()
+    assert int(im.error_word.item()) == 0
+    _check(big.out.float().cpu(), _oracle_decode(olay, cache, C, bt, rows, p, big.q, csc),
+           "eager batch of 6")
+    for r in rows:
+        nxt[r] += 1
+    assert {k: v.data_ptr() for k, v in ws.bufs.items() if k in held} == held
+
+    # both graphs replayed, twice each, interleaved
+    for t in range(2):
+        for name in ("A", "B"):
+            b = batches[name]
+            p = [nxt[r] for r in b.rows]
+            b.fill(seqs, p, csc)
+            b.out.fill_(float("nan"))
+            graphs[name].replay()
+            torch.cuda.synchronize()
+            assert int(im.error_word.item()) == 0
+            _check(b.out.float().cpu(), _oracle_decode(olay, cache, C, bt, b.rows, p, b.q, csc),
+                   f"replay {name} {t}")
+            for r in b.rows:
+                nxt[r] += 1
+    rope_store.clear_stores()
+    impl_mod.release_workspaces()

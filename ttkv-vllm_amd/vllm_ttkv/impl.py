@@ -19,6 +19,17 @@ issued:
   * a continuation chunk (seq_len > q_len) uses the multi-query kernel K2 over the whole store;
     a first chunk attends over its own post-RoPE q/k/v with SDPA, as in the reference
     (impl.py:684-723, decode.py:363-389).
+
+Graph capture (uniform single-token decode steps only; the reference captures nothing,
+metadata.py:96-102): a decode step's launches read only device tensors, and the buffers they hold
+are never replaced. The decoder pools have a fixed capacity (`rope_store`), and the decode-step
+workspaces are shared by all layers of a device and allocated at the serving limits
+(`max_num_seqs` x `max_model_len`, `serving_limits`). Once a step has been captured on the
+device, a step that would need more raises instead of reallocating. K1's grid is sized by the
+metadata's `max_seq_len`, and its work plan follows the actual lengths on the device, so a
+graph captured with `max_seq_len = max_model_len`
+(`TTKVAttentionMetadataBuilder.build_for_cudagraph_capture`) is valid for every later batch of
+its size. A step with prefill chunks refuses to run under capture.
 """
 from __future__ import annotations
 
@@ -44,6 +55,82 @@ except Exception:  # noqa: BLE001
     AttentionType = None
 
 CHECK_ENV = "VLLM_TTKV_CHECK"
+MAX_SEQS_ENV = "VLLM_TTKV_MAX_NUM_SEQS"
+MAX_LEN_ENV = "VLLM_TTKV_MAX_MODEL_LEN"
+DEFAULT_MAX_SEQS = 256
+
+
+def serving_limits(fallback_len: int | None = None) -> tuple[int, int | None]:
+    """(max_num_seqs, max_model_len) the fixed buffers are sized for: the environment
+    (`VLLM_TTKV_MAX_NUM_SEQS`, `VLLM_TTKV_MAX_MODEL_LEN`) over the running vLLM config, else 256
+    sequences and `fallback_len` (the RoPE table's length: no position beyond it has an angle)."""
+    seqs = lens = None
+    try:  # pragma: no cover - vLLM is not installed in the build container
+        from vllm.config import get_current_vllm_config
+        vc = get_current_vllm_config()
+        seqs = getattr(getattr(vc, "scheduler_config", None), "max_num_seqs", None)
+        lens = getattr(getattr(vc, "model_config", None), "max_model_len", None)
+    except Exception:  # noqa: BLE001
+        pass
+    seqs = int(os.environ.get(MAX_SEQS_ENV) or seqs or DEFAULT_MAX_SEQS)
+    lens = os.environ.get(MAX_LEN_ENV) or lens or fallback_len
+    return seqs, (None if lens is None else int(lens))
+
+
+class DeviceWorkspaces:
+    """Kernel scratch for one device, shared by every layer (the layers of a step run one after
+    another on one stream; each kernel leaves its counters at zero). The decode step's buffers
+    (`fixed=True`) are allocated at the capacity the caller states for the serving limits. Once
+    any step has been captured on this device (`frozen`), they are never replaced: a graph holds
+    their addresses, and a step that needs more raises. Before that, an eager step may still
+    replace them with larger ones. The prefill buffers may be replaced at any time outside
+    capture (prefill steps are never captured). Nothing is allocated under capture."""
+
+    def __init__(self, device):
+        self.device = torch.device(device)
+        self.bufs: dict[str, torch.Tensor] = {}
+        self.frozen = False
+
+    def get(self, kind: str, need: int, capacity: int = 0, fixed: bool = False) -> torch.Tensor:
+        buf = self.bufs.get(kind)
+        if buf is not None and buf.numel() >= need:
+            return buf
+        if buf is not None and fixed and self.frozen:
+            raise RuntimeError(
+                f"the {kind} workspace ({buf.numel()} bytes, sized for the serving limits) is "
+                f"held by a captured graph and cannot be replaced, but this step needs {need}; "
+                f"raise {MAX_SEQS_ENV} / {MAX_LEN_ENV}")
+        if _capturing():
+            raise RuntimeError(f"the {kind} workspace would be allocated during graph capture; "
+                               f"run one eager step of the captured shape first")
+        buf = torch.zeros(max(int(need), int(capacity), 256), dtype=torch.uint8,
+                          device=self.device)
+        self.bufs[kind] = buf
+        return buf
+
+
+_WORKSPACES: dict = {}
+
+
+def _capturing() -> bool:
+    """Is the current stream recording a graph? (False where there is no device.)"""
+    return torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
+
+
+def workspaces(device) -> DeviceWorkspaces:
+    """The workspaces of `device` ("cuda" means the current device)."""
+    dev = torch.device(device)
+    if dev.type == "cuda" and dev.index is None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+    if dev not in _WORKSPACES:
+        _WORKSPACES[dev] = DeviceWorkspaces(dev)
+    return _WORKSPACES[dev]
+
+
+def release_workspaces() -> None:
+    """Drop every device's workspaces and their frozen state. Only for when no captured graph
+    that used them will be replayed again (tests, a model reload)."""
+    _WORKSPACES.clear()
 
 
 @dataclass
@@ -116,9 +203,6 @@ class TTKVAttentionImpl(_ImplBase):
             raise ValueError(f"num_heads={num_heads} is not a multiple of "
                              f"num_kv_heads={self.num_kv_heads}")
         self.error_word = None
-        self._ws = None
-        self._pws = None
-        self._wws = None
 
     # ------------------------------------------------------------------ entry point
     def forward(self, layer, query, key, value, kv_cache, attn_metadata, output=None,
@@ -152,11 +236,17 @@ class TTKVAttentionImpl(_ImplBase):
         if self.error_word is None or self.error_word.device != query.device:
             self.error_word = torch.zeros(1, dtype=torch.int32, device=query.device)
 
+        if _capturing():
+            if plan.prefills:
+                raise RuntimeError("only uniform single-token decode steps can be captured in a "
+                                   "graph; this step has prefill chunks")
+            workspaces(query.device).frozen = True
         name = getattr(layer, "layer_name", None)
         stash = take_raw_k(name)                # pops: the write comes first, unconditionally
-        store = ensure_store(name, self._cos_sin_cache(layer, stash), self.num_heads,
-                             self.num_kv_heads, self.head_size, lay,
-                             num_blocks=int(cache.shape[0]))
+        csc = self._cos_sin_cache(layer, stash)
+        self._limits = serving_limits(int(csc.shape[0]))
+        store = ensure_store(name, csc, self.num_heads, self.num_kv_heads, self.head_size, lay,
+                             num_blocks=int(cache.shape[0]), capacity=self._limits[0])
         self._write_store(lay, cache, stash, value, md, plan, store)
 
         q3 = query.view(n_tokens, self.num_heads, self.head_size)
@@ -196,31 +286,31 @@ class TTKVAttentionImpl(_ImplBase):
             # decode-only step: every request has a decoder; one launch, no host reads
             kernels.write_paged(lay, K, V, slots, qsl_d, bt, store.dec_map, store.dec_pool,
                                 store.pinv_pool, cache, error_word=self.error_word,
-                                workspace=self._write_workspace(lay, N, K.device))
+                                workspace=self._write_workspace(lay, N, K.device, fixed=True))
             return
         # A step with prefill chunks. A request whose whole context arrives in this step
         # (seq_len == q_len) is on its first chunk and is fitted (encode.py:257-298) -- ALWAYS,
         # even when its key already has a decoder: keys are first block ids, and a finished
         # request's recycled first block must not hand its basis to the next request. The fit
-        # re-registers the key (its slot is reused). One host read of the first block ids and
-        # lengths decides.
-        keys = [int(x) for x in md.block_table[:plan.n_reqs, 0].tolist()]
-        seq_lens = [int(x) for x in md.seq_lens[:plan.n_reqs].tolist()]
+        # re-registers the key (its slot is reused). Which requests start here comes from the
+        # host metadata when the engine provides it (`num_computed_tokens_cpu`). Only a step that
+        # fits reads the first block ids back (the fit synchronises anyway): all of them, since
+        # every key of the batch is live and must survive an eviction. A continuation whose key
+        # has no decoder is refused on the device (error bit 1, NaN output rows).
+        first = self._first_chunks(md, plan)
         cfg = CONFIGS[os.environ.get("VLLM_TTKV_CONFIG", "safe")]
         frozen, fitted = [], []
+        keys = []
+        if any(first):
+            keys = [int(x) for x in md.block_table[:plan.n_reqs, 0].tolist()]
         for r in range(plan.n_reqs):
             s, e = plan.qsl[r], plan.qsl[r + 1]
             if e <= s:
                 continue
-            if seq_lens[r] == e - s:
+            if first[r]:
                 fk = enc.fit_into_budget(K[s:e].permute(1, 0, 2), lay, cfg)
                 store.register(keys[r], fk.decoder, live=keys)
                 fitted.append((r, fk))
-            elif store.decoders.get(keys[r]) is None:
-                raise RuntimeError(
-                    f"request {keys[r]} arrives with seq_len={seq_lens[r]} but {e - s} tokens "
-                    f"in this step and has no fitted decoder: a continuation of a request "
-                    f"whose first chunk never reached the writer")
             else:
                 frozen.append(r)
         dev = K.device
@@ -246,29 +336,51 @@ class TTKVAttentionImpl(_ImplBase):
                    torch.cat([fk.coeff_scale for _, fk in fitted]))
 
     # ------------------------------------------------------------------ read
-    def _workspace(self, lay, num_reqs, max_seq_len, block_size, device):
-        need = _hip.lib().ttkv_decode_workspace_bytes(_hip.Layout.of(lay), self.num_heads,
-                                                      num_reqs, max_seq_len, block_size)
-        if self._ws is None or self._ws.numel() < need or self._ws.device != device:
-            self._ws = torch.zeros(max(int(need), 256), dtype=torch.uint8, device=device)
-        return self._ws
+    def _first_chunks(self, md, plan) -> list:
+        """Per request: does its whole context arrive in this step (seq_len == q_len)? From
+        `num_computed_tokens_cpu` when present (no device read), else from one read of
+        `seq_lens`."""
+        q_len = [plan.qsl[r + 1] - plan.qsl[r] for r in range(plan.n_reqs)]
+        ncomp = getattr(md, "num_computed_tokens_cpu", None)
+        if ncomp is not None:
+            return [int(c) == 0 for c in ncomp[:plan.n_reqs].tolist()]
+        seq = md.seq_lens[:plan.n_reqs].tolist()
+        return [int(sl) == q for sl, q in zip(seq, q_len)]
 
-    def _write_workspace(self, lay, num_tokens, device):
-        need = _hip.lib().ttkv_write_workspace_bytes(_hip.Layout.of(lay), num_tokens)
-        if self._wws is None or self._wws.numel() < need or self._wws.device != device:
-            self._wws = torch.zeros(max(int(need), 256), dtype=torch.uint8, device=device)
-        return self._wws
+    def _seq_lens_host(self, md, plan) -> list:
+        """Exact per-request context lengths on the host: computed tokens + this step's."""
+        ncomp = getattr(md, "num_computed_tokens_cpu", None)
+        if ncomp is not None:
+            return [int(c) + plan.qsl[r + 1] - plan.qsl[r]
+                    for r, c in enumerate(ncomp[:plan.n_reqs].tolist())]
+        return [int(x) for x in md.seq_lens[:plan.n_reqs].tolist()]
+
+    def _workspace(self, lay, num_reqs, max_seq_len, block_size, device):
+        L = _hip.lib()
+        g = _hip.Layout.of(lay)
+        need = L.ttkv_decode_workspace_bytes(g, self.num_heads, num_reqs, max_seq_len, block_size)
+        seqs, lens = self._limits
+        cap = L.ttkv_decode_workspace_bytes(g, self.num_heads, max(seqs, num_reqs),
+                                            max(lens or 0, max_seq_len), block_size)
+        return workspaces(device).get("decode", need, cap, fixed=True)
+
+    def _write_workspace(self, lay, num_tokens, device, fixed=False):
+        L = _hip.lib()
+        g = _hip.Layout.of(lay)
+        need = L.ttkv_write_workspace_bytes(g, num_tokens)
+        if fixed:   # a decode step's tokens: one per sequence
+            cap = L.ttkv_write_workspace_bytes(g, max(self._limits[0], num_tokens))
+            return workspaces(device).get("decode_write", need, cap, fixed=True)
+        return workspaces(device).get("prefill_write", need)
 
     def _prefill_workspace(self, lay, num_reqs, max_q, max_seq, device, block_size):
         need = _hip.lib().ttkv_prefill_workspace_bytes(_hip.Layout.of(lay), self.num_heads,
                                                        num_reqs, max_q, max_seq, block_size)
-        if self._pws is None or self._pws.numel() < need or self._pws.device != device:
-            self._pws = torch.zeros(max(int(need), 256), dtype=torch.uint8, device=device)
-        return self._pws
+        return workspaces(device).get("prefill", need)
 
     def _decode(self, lay, cache, store, q3, md, nd, output):
         bs = self._block_size(cache)
-        if nd == 1:
+        if nd == 1 and not _capturing():
             self._single_request_fallback(store, md)
         max_len = int(md.max_seq_len) if md.max_seq_len else int(md.seq_lens[:nd].max())
         kernels.decode_paged(lay, q3, cache, bs, md.block_table[:nd].to(torch.int32),
@@ -293,7 +405,7 @@ class TTKVAttentionImpl(_ImplBase):
             store.register(key, enc.KDecoder(dec), live=(key,))
 
     def _prefill(self, lay, cache, store, q3, key, value, md, plan, output):
-        seq_lens = [int(x) for x in md.seq_lens[:plan.n_reqs].tolist()]
+        seq_lens = self._seq_lens_host(md, plan)
         cont = []
         for r in plan.prefills:
             s, e = plan.qsl[r], plan.qsl[r + 1]

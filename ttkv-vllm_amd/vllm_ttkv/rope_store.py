@@ -225,16 +225,22 @@ class TTKVRopeStore:
 
 def ensure_store(layer_name: str, cos_sin_cache: torch.Tensor, num_heads: int,
                  num_kv_heads: int, head_dim: int, layout: TTKLayout | None, *,
-                 num_blocks: int | None = None) -> TTKVRopeStore:
+                 num_blocks: int | None = None, capacity: int | None = None) -> TTKVRopeStore:
     """The layer's store, created on first use by the writer (reference rope_store.py:280-300).
-    `num_blocks` binds the device key map if it is not bound yet."""
+    `num_blocks` binds the device key map if it is not bound yet. A new store's pool holds
+    `VLLM_TTKV_MAX_DECODERS` decoders when that is set, else max(64, `capacity`) -- the writer
+    passes the engine's `max_num_seqs`, so every running request keeps its slot."""
     st = _STORES.get(layer_name)
     if st is None:
         if layout is None:
             raise RuntimeError(f"cannot create a TT-KV store for layer {layer_name!r}: no "
                                f"calibrated layout (point VLLM_TTKV_CALIBRATION at a calibration "
                                f"artifact)")
-        st = TTKVRopeStore(num_heads, num_kv_heads, head_dim, cos_sin_cache, layer_name, layout)
+        cap = None
+        if not os.environ.get(CAPACITY_ENV) and capacity is not None:
+            cap = max(DEFAULT_CAPACITY, int(capacity))
+        st = TTKVRopeStore(num_heads, num_kv_heads, head_dim, cos_sin_cache, layer_name, layout,
+                           capacity=cap)
     if num_blocks is not None:
         st.bind_blocks(num_blocks)
     return st
