@@ -386,3 +386,40 @@ def test_graphs_at_two_batch_sizes_then_a_larger_eager_batch(monkeypatch):
                 nxt[r] += 1
     rope_store.clear_stores()
     impl_mod.release_workspaces()
+
+
+def test_recycled_first_block_gets_a_new_fit(monkeypatch):
+    """A finished request's blocks, first block included, go to a new request (vLLM recycles
+    them). The key (first block id) is the same, but the new request's first chunk is fitted
+    and re-registered: its decoder is the fit of ITS keys, not the old request's basis, and its
+    decode step matches the oracle."""
+    from vllm_ttkv import encode as penc
+    monkeypatch.delenv("VLLM_TTKV_CHECK", raising=False)
+    lay = layout_for_config(CONFIGS["safe"], 110)
+    olay = oracle_layout(CONFIGS["safe"], 110)
+    rope_store.clear_stores()
+    csc = cos_sin_cache(1024)
+    old, new = _Seq(400, 51), _Seq(400, 52)
+    bt, nblk = synth.shuffled_block_table([400], BS, seed=53, extra_blocks=1)
+    C = lay.compressed_bytes_per_token()
+    cache = torch.zeros(nblk, 1, BS, C // 2, dtype=torch.bfloat16, device="cuda")
+    im = TTKVAttentionImpl(HQ, D, SCALE, H)
+    layer = _Layer(NAME, lay)
+    key = int(bt[0, 0])
+    _step(im, layer, cache, csc, bt, [(old, 0, 300)])
+    _step(im, layer, cache, csc, bt, [(old, 300, 301)])
+    dec_old = rope_store.store_for_layer(NAME).decoders[key].decoder_f.clone()
+    # the old request ends; a new one arrives on the same blocks
+    _step(im, layer, cache, csc, bt, [(new, 0, 250)])
+    st = rope_store.store_for_layer(NAME)
+    dec_new = st.decoders[key].decoder_f
+    want_dec = penc.fit_into_budget(new.K[:250].permute(1, 0, 2).contiguous().cuda(), lay,
+                                    CONFIGS["safe"]).decoder.decoder_f
+    assert torch.equal(dec_new, want_dec)
+    assert not torch.equal(dec_new, dec_old)
+    out, q, _, qsl, seq_lens = _step(im, layer, cache, csc, bt, [(new, 250, 251)])
+    flat = cache.view(torch.uint8).reshape(-1, C).cpu()
+    want = attend.paged_decode(olay, flat, bt[:1], torch.tensor(seq_lens), torch.tensor(qsl),
+                               q.float(), [dec_new.cpu()], csc, BS, SCALE, dtype=torch.float64)
+    _check(out, want, "decode after recycling")
+    rope_store.clear_stores()
