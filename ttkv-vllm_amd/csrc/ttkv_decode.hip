@@ -15,8 +15,8 @@
 //             LDS by the workgroup at start). 3-bit codes come out as
 //             fp8 bytes of the signed value c - 4 (0 outside the bitmap), which the arithmetic
 //             reads two at a time with v_cvt_pk_f32_fp8.
-//   recon   : K_pre^T[128 x 16 tokens] = Dec^T[128 x r1] * coeff^T[r1 x 16] on MFMA 16x16x32 f16.
-//             The decoder is split hi + lo in fp16 and both halves are applied; decoder_f values
+//   recon   : K_pre^T[128 x 16 tokens] = Dec^T[128 x r1] * coeff^T[r1 x 16] on MFMA 16x16x32 f16
+//             (only that shape). The decoder is split hi + lo in fp16 and both halves are applied; decoder_f values
 //             are int8 * fp16 row rulers (<= 19 significant bits), so hi + lo is exact and the
 //             products are exact in the fp32 accumulator. Wave w owns dims {16w..16w+15} and
 //             {64+16w..64+16w+15}, so each RoPE pair (j, j+64) sits in one lane and the decoder
@@ -390,7 +390,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
 
   // ---- decoder fragments (A operand, M = dims, K = r1), hi/lo fp16, resident in registers.
   half8 ahi[2][KSTEPS], alo[2][KSTEPS];
-  half4 thi[2], tlo[2];  // k = 16 tail step (odd KU)
+  half8 thi[2], tlo[2];  // k = 16 tail step (odd KU), upper halves zero
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi) {
 #pragma unroll
@@ -403,8 +403,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
         alo[mi][s][j] = (_Float16)(f - (float)hi);
       }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float f = draw[mi][8 * KSTEPS + j];
+    for (int j = 0; j < 8; ++j) {
+      const float f = j < 4 ? draw[mi][8 * KSTEPS + j] : 0.f;
       const _Float16 hi = (_Float16)f;
       thi[mi][j] = hi;
       tlo[mi][j] = (_Float16)(f - (float)hi);
@@ -533,11 +533,17 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
         acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[1][s], b, acc1, 0, 0, 0);
       }
       if constexpr (KTAIL) {
-        const half4 b = *(const half4*)&S.coef[tok][32 * KSTEPS + 4 * gq];
-        acc0 = __builtin_amdgcn_mfma_f32_16x16x16f16(thi[0], b, acc0, 0, 0, 0);
-        acc0 = __builtin_amdgcn_mfma_f32_16x16x16f16(tlo[0], b, acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x16f16(thi[1], b, acc1, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x16f16(tlo[1], b, acc1, 0, 0, 0);
+        // The k = 16 tail runs as a 16x16x32 step whose upper k half is zero in A and B (lane
+        // (n, gq) holds k 8gq..8gq+7 of a 32-wide step; the tail's k 4gq..4gq+3 sit in its first
+        // four). One MFMA shape per accumulator chain: on gfx950 a 16x16x16 step reading a
+        // 16x16x32 step's result as its accumulator gave wrong sums when the compiler placed the
+        // two a few instructions apart (measured; extra wait states between them also fixed it).
+        const half4 b4 = *(const half4*)&S.coef[tok][32 * KSTEPS + 4 * gq];
+        const half8 b = {b4[0], b4[1], b4[2], b4[3], 0, 0, 0, 0};
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(thi[0], b, acc0, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(tlo[0], b, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(thi[1], b, acc1, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(tlo[1], b, acc1, 0, 0, 0);
       }
       float vl[4], vh[4];
       codes4<RB>(*(const uint32_t*)&S.kcode[tok][dl], vl);
