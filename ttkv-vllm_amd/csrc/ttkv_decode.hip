@@ -294,6 +294,19 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   }
   const int t1 = min(seq, t0 + chunk);
 
+  // This chunk's block ids (at most kSegMax, host-bounded), requested in the same round trip as
+  // the first tile's block id and the decoder slot: they depend on the plan only, and are staged
+  // into LDS after the code tables are built.
+  const int bfirst = t0 / a.block_size;
+  const int nseg = (t1 - 1) / a.block_size - bfirst + 1;
+  constexpr int kSegPer = (kSegMax + kThreads - 1) / kThreads;
+  int segv[kSegPer];
+#pragma unroll
+  for (int k = 0; k < kSegPer; ++k) {
+    const int i = tid + kThreads * k;
+    segv[k] = i < nseg ? a.bt[bt_row + bfirst + i] : -1;
+  }
+
   // Decoder slot via the device registry keyed by the request's first block, requested together
   // with the first tile's block ids; the first tile's bytes follow with the decoder (bad block ids
   // are flagged when the chunk's ids are staged)
@@ -356,15 +369,17 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
 
   // ---- code tables, and this chunk's block ids
   build_luts(S.lut, (RB == 3 || VB == 3) ? S.lut3 : nullptr, tid, kThreads);
-  const int bfirst = t0 / a.block_size;
-  const int nseg = (t1 - 1) / a.block_size - bfirst + 1;
-  for (int i = tid; i < nseg; i += kThreads) {
-    int blk = a.bt[(int64_t)r * a.bt_row_stride + bfirst + i];
-    if (blk < 0 || blk >= a.num_blocks) {
-      atomicOr(a.err, TTKV_ERR_BAD_BLOCK);
-      blk = -1;
+#pragma unroll
+  for (int k = 0; k < kSegPer; ++k) {
+    const int i = tid + kThreads * k;
+    if (i < nseg) {
+      int blk = segv[k];
+      if (blk < 0 || blk >= a.num_blocks) {
+        atomicOr(a.err, TTKV_ERR_BAD_BLOCK);
+        blk = -1;
+      }
+      S.seg[i] = blk;
     }
-    S.seg[i] = blk;
   }
 
   // slot bases are 16-aligned, so a row's byte misalignment is fixed per head
