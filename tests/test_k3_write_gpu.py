@@ -169,6 +169,45 @@ def test_frozen_write_against_reference_vectors(case):
     assert float((vg - vr).abs().max()) <= 0.3 * float(V.abs().max())
 
 
+@pytest.mark.parametrize("case", ["ref_encode_safe_r16", "ref_encode_campaign4x_r64"])
+def test_device_pinv_against_reference_vectors(case):
+    """The product's pinv (`vllm_ttkv.encode.KDecoder.pinv`, torch.linalg.pinv on the device, as
+    the reference's encode.py:197-211 on its CUDA path) against the pinv the reference wrote on the
+    CPU for the same decoder. The campaign4x decoder has rank 26 of 64 rows (the rest exactly
+    zero), so the zero rows' pinv columns must come out exactly zero. Then the Moore-Penrose
+    identities on the device result, and a frozen write driven by the device pinv against the
+    reference's bytes, at the bar of the reference-pinv test above."""
+    import pathlib
+    import numpy as np
+    from vllm_ttkv.encode import KDecoder
+    z = np.load(pathlib.Path(__file__).parent / "golden" / f"{case}.npz")
+    dec = torch.from_numpy(z["fit_decoder_f"])
+    want = torch.from_numpy(z["pinv"]).double()
+    got = KDecoder(dec.to(DEV)).pinv.cpu()
+    assert got.shape == want.shape and got.dtype == torch.float32
+    scale = float(want.abs().max())
+    err = float((got.double() - want).abs().max())
+    assert err <= 1e-4 * scale, f"{case}: pinv off by {err:.3e} (max |pinv| {scale:.3e})"
+    zero_rows = (dec.abs().sum(dim=1) == 0).nonzero().flatten()
+    if case.startswith("ref_encode_campaign4x"):
+        assert len(zero_rows) == 64 - 26
+    assert torch.equal(got[:, zero_rows], torch.zeros(got.shape[0], len(zero_rows)))
+    D64, P64 = dec.double(), got.double()
+    assert float((D64 @ P64 @ D64 - D64).abs().max()) <= 1e-5 * float(D64.abs().max())
+    assert float((P64 @ D64 @ P64 - P64).abs().max()) <= 1e-4 * scale
+    # frozen write with the device pinv: the reference's bytes almost everywhere
+    lay = layout_for_config(codec.CONFIGS[str(z["config"])], r1=int(z["r1"]))
+    K1 = torch.from_numpy(z["K1"]).float()
+    n = K1.shape[1]
+    V = torch.from_numpy(z["V0"]).float()[:, :n].contiguous()
+    page, _, _, e = _run(lay, dec, got, K1, V, torch.arange(n, dtype=torch.int64), n)
+    assert e == 0
+    ref = torch.cat([torch.from_numpy(z["frozen_k_slots"]), torch.from_numpy(z["v_slots"])[:n]],
+                    dim=1)
+    frac = float((page != ref).float().mean())
+    assert frac < 0.01, f"{case}: {frac:.4f} of bytes differ with the device pinv"
+
+
 def test_workspace_shared_across_token_counts():
     """One workspace serves writes of different sizes in turn (a serving loop's token count
     changes every step): each write's bytes equal those of the same write with a fresh

@@ -22,6 +22,7 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef float float2v __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
 
 constexpr int kD = 128;           // head dim the kernels are built for
 constexpr int kBitmapBytes = kD / 8;
@@ -75,6 +76,12 @@ __host__ inline bool rows_in_windows(const Geom& g) {
 template <typename T>
 __device__ __forceinline__ const __attribute__((address_space(1))) T* gbl(const T* p) {
   return (const __attribute__((address_space(1))) T*)p;
+}
+
+// The same for stores: global_store_* instead of flat_store_*.
+template <typename T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* gblw(T* p) {
+  return (__attribute__((address_space(1))) T*)p;
 }
 
 // 16 bytes from global memory (16-byte aligned) as uint4, through a global pointer.

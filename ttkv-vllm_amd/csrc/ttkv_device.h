@@ -18,6 +18,17 @@ __device__ __forceinline__ void i8x4_to_f16(uint32_t x, uint32_t& p01, uint32_t&
   p23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, hi) - bias);
 }
 
+// 4 code bytes (little-endian) -> two fp16 pairs holding code - off, exact.
+__device__ __forceinline__ void u8x4_to_f16_minus(uint32_t x, float off, uint32_t& p01,
+                                                  uint32_t& p23) {
+  const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u);  // 1024 + b0, 1024 + b1
+  const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u);
+  const _Float16 bias = (_Float16)(1024.0f + off);
+  const half2v b2 = {bias, bias};
+  p01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, lo) - b2);
+  p23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, hi) - b2);
+}
+
 // Spread the 8 codes at the top of a 32-bit MSB-first window (code k at bits 31-B*k-B+1 ..
 // 31-B*k) into bytes: e0 = codes 0..3, e1 = codes 4..7 (byte i of e0 = code i).
 template <int BITS>

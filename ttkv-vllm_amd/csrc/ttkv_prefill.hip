@@ -103,17 +103,6 @@ struct PrefillSmem {
   int is_last;
 };
 
-// 4 code bytes (little-endian) -> two fp16 pairs holding code - off, exact.
-__device__ __forceinline__ void u8x4_to_f16_minus(uint32_t x, float off, uint32_t& p01,
-                                                  uint32_t& p23) {
-  const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u);  // 1024 + b0, 1024 + b1
-  const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u);
-  const _Float16 bias = (_Float16)(1024.0f + off);
-  const half2v b2 = {bias, bias};
-  p01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, lo) - b2);
-  p23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, hi) - b2);
-}
-
 template <int G, int RB, int VB, int KSTEPS, bool SCORES>
 __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) void prefill_paged_kernel(PrefillArgs a) {
   constexpr bool EXACT = true;  // see the precision note at the top
@@ -697,6 +686,8 @@ static int64_t prefill_part_bytes(const Geom& g, int G, int nr, int max_q_len, i
 int64_t prefill_workspace_bytes(const Geom& g, int G, int num_reqs, int max_q_len,
                                 int max_seq_len, int block_size) {
   if (num_reqs <= 0 || max_q_len <= 0) return 0;
+  if (continuation_applies(g, G, max_q_len))
+    return continuation_workspace_bytes(g, G, num_reqs, max_q_len, max_seq_len);
   const int slice = prefill_slice_reqs(g, num_reqs, max_q_len);
   const int64_t part = std::max(
       prefill_part_bytes(g, G, slice, max_q_len, max_seq_len, block_size),
@@ -798,6 +789,13 @@ int prefill_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype
     if (need && (uintptr_t)ws % 256)
       return host_fail(TTKV_E_INVALID, "workspace not 256-byte aligned");
   }
+  // chunks of more than one 64-query block: every key expanded once, then attended by all the
+  // chunk's queries (ttkv_continuation.hip)
+  if (!scores && continuation_applies(g, G, max_q_len))
+    return continuation_paged(g, HQ, scale, q, q_dtype, q_row_stride, page, n_slots, slot_stride,
+                              block_size, bt, bt_row_stride, seq_lens, qsl, req_index, num_reqs,
+                              max_q_len, max_seq_len, dec_map, num_blocks, dec_pool, n_dec_slots,
+                              cs_cache, out, out_dtype, out_row_stride, ws, err, st);
   const int slice = prefill_slice_reqs(g, num_reqs, max_q_len);
   for (int ri0 = 0; ri0 < num_reqs; ri0 += slice) {
     PrefillArgs b = a;
