@@ -171,6 +171,20 @@ __device__ __forceinline__ uint16_t float_to_bf16_bits(float f) {
   return (uint16_t)(u >> 16);
 }
 
+// 16 bytes stored write-through to the device-coherent level (the cache policy of an agent-scope
+// atomic store, `sc1`), so that another CU, on any XCD, reads them after an agent-scope acquire
+// with no L2 writeback on this side. A vector-memory store; p must be 16-byte aligned.
+__device__ __forceinline__ void store_agent16(float* p, float4v v) {
+  __asm__ volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void store_agent8(float* p, float2v v) {
+  __asm__ volatile("global_store_dwordx2 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
+
+// Four consecutive activations from element i (a multiple of 4) with one store, where `vec` says
+// the tensor's rows are aligned for it; element stores otherwise.
+__device__ __forceinline__ void store_act4(void* p, int dt, int64_t i, float4v v, bool vec);
+
 __device__ __forceinline__ void store_act(void* p, int dt, int64_t i, float v) {
   if (dt == TTKV_DTYPE_F32) {
     ((float*)p)[i] = v;
@@ -181,4 +195,23 @@ __device__ __forceinline__ void store_act(void* p, int dt, int64_t i, float v) {
   }
 }
 
+__device__ __forceinline__ void store_act4(void* p, int dt, int64_t i, float4v v, bool vec) {
+  if (!vec) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) store_act(p, dt, i + j, v[j]);
+    return;
+  }
+  if (dt == TTKV_DTYPE_F32) {
+    *gblw((float4v*)((float*)p + i)) = v;
+  } else if (dt == TTKV_DTYPE_F16) {
+    const half4 h = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+    *gblw((half4*)((_Float16*)p + i)) = h;
+  } else {
+    const u32x2v b = {(uint32_t)float_to_bf16_bits(v[0]) | ((uint32_t)float_to_bf16_bits(v[1]) << 16),
+                      (uint32_t)float_to_bf16_bits(v[2]) | ((uint32_t)float_to_bf16_bits(v[3]) << 16)};
+    *gblw((u32x2v*)((uint16_t*)p + i)) = b;
+  }
+}
+
 }  // namespace ttkv
+

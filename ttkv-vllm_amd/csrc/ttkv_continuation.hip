@@ -18,12 +18,12 @@
 //                heads of one (request, KV head, key split); wave w owns queries 16w..16w+15.
 //                Per 64-key tile: S^T = K Q^T on MFMA (hi and lo key halves against the fp16
 //                query), causal -inf, online base-2 softmax per query column, O^T += Vt (P *
-//                ruler_v)^T on MFMA with P * ruler_v rounded to fp16 once. The next tile is
-//                copied to LDS through registers while this one is computed (double-buffered
-//                LDS, one barrier per tile): its K half is requested before the scores and
-//                stored after them, its V half requested after the scores and stored after
-//                P.V, so that at most one half is held in registers. Key splits are combined
-//                in the same launch by the last workgroup.
+//                ruler_v)^T on MFMA with P * ruler_v rounded to fp16 once, in 32-key halves.
+//                Waves 4..7 run half a tile behind waves 0..3 (three LDS tile buffers, one
+//                barrier per tile), so each SIMD's two waves overlap MFMA with softmax. The
+//                next tile is copied to LDS while the current ones are
+//                computed, by direct global -> LDS DMA issued at the barrier. Key splits are
+//                combined in the same launch by the last workgroup.
 //
 // The arithmetic is the fused kernel's, so results agree with it to fp32 rounding: the same
 // exact fp16 coefficient / hi+lo decoder reconstruction, k = cs * acc + ruler * code, RoPE in
@@ -355,7 +355,8 @@ struct AttendArgs {
   int n_qb, kchunk, nsplit, max_seq, max_q;
 };
 
-// one 64-key tile in LDS: khi, klo rows of 16 chunks and vt rows of 8 chunks, chunk c of row k at
+// one 64-key tile in LDS (three are resident: see the loop): khi, klo rows of 16 chunks and vt
+// rows of 8 chunks, chunk c of row k at
 // c ^ (k & 7) (rows read by lanes 0..7 of a wave land in 8 different bank groups); then vrul
 struct AttendTile {
   u32x4 khi[kXTile][16];
@@ -364,22 +365,9 @@ struct AttendTile {
   float vrul[kXTile];
 };
 struct AttendSmem {
-  AttendTile t[2];
+  AttendTile t[3];
   int is_last;
 };
-
-// destination of workspace chunk ch (0 .. kTileChunks-1) of a tile inside its LDS image
-__device__ __forceinline__ u32x4* attend_slot(AttendTile& T, int ch) {
-  if (ch < 2048) {
-    const int row = (ch >> 4) & 63, cc = ch & 15;
-    return (ch < 1024 ? &T.khi[row][0] : &T.klo[row][0]) + (cc ^ (row & 7));
-  }
-  if (ch < 3072) {
-    const int row = (ch - 2048) >> 3, cc = ch & 7;
-    return &T.vt[row][cc ^ (row & 7)];
-  }
-  return (u32x4*)&T.vrul[4 * (ch - 3072)];
-}
 
 template <int G>
 __global__ __launch_bounds__(kAThreads, 2) void attend_kernel(AttendArgs a) {
@@ -446,28 +434,34 @@ __global__ __launch_bounds__(kAThreads, 2) void attend_kernel(AttendArgs a) {
   }
 
   const uint8_t* tbase = a.tiles + ((int64_t)ri * g.H + h) * a.ntl * kTileBytes;
-  // tile copies through registers: the K half is chunks 0..2047 (4 per thread), the V half
-  // chunks 2048..3087 (2 per thread, threads 0..15 also the vrul chunks)
-  u32x4 ldk[4], ldv[3];
-  auto load_k = [&](int tile) {
+  // Tile copies global -> LDS by DMA (global_load_lds_dwordx4): one wave instruction fills 64
+  // consecutive 16-byte chunks of a buffer's image, each lane gathering the workspace chunk that
+  // belongs in its slot (chunk c of row k sits at c ^ (k & 7)). Wave w moves image chunks
+  // 64 (w + 8 i): 4 instructions for the K half, 2 for the V half, and wave 0 the 16 vrul
+  // chunks. Each wave waits for its own (vmcnt(0)) before the next barrier.
+  // source chunk of this lane's slot in each of its 6 full instructions (the same every tile)
+  int dsrc[6];
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+    const int P = (i < 4 ? 64 * (wv + 8 * i) : 2048 + 64 * (wv + 8 * (i - 4))) + lane;
+    if (P < 2048) {
+      const int row = (P >> 4) & 63, pc = P & 15;
+      dsrc[i] = (P & ~1023) + row * 16 + (pc ^ (row & 7));
+    } else {
+      const int row = (P - 2048) >> 3, pc = P & 7;
+      dsrc[i] = 2048 + row * 8 + (pc ^ (row & 7));
+    }
+  }
+  auto dma_tile = [&](AttendTile& T, int tile) {
     const u32x4* src = (const u32x4*)(tbase + (int64_t)tile * kTileBytes);
+    typedef __attribute__((address_space(3))) void* lds_ptr;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ldk[i] = *gbl(src + tid + kAThreads * i);
-  };
-  auto store_k = [&](AttendTile& T) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) *attend_slot(T, tid + kAThreads * i) = ldk[i];
-  };
-  auto load_v = [&](int tile) {
-    const u32x4* src = (const u32x4*)(tbase + (int64_t)tile * kTileBytes) + 2048;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) ldv[i] = *gbl(src + tid + kAThreads * i);
-    if (tid < kTileChunks - 3072) ldv[2] = *gbl(src + 1024 + tid);
-  };
-  auto store_v = [&](AttendTile& T) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) *attend_slot(T, 2048 + tid + kAThreads * i) = ldv[i];
-    if (tid < kTileChunks - 3072) *attend_slot(T, 3072 + tid) = ldv[2];
+    for (int i = 0; i < 6; ++i) {
+      const int c0 = i < 4 ? 64 * (wv + 8 * i) : 2048 + 64 * (wv + 8 * (i - 4));
+      __builtin_amdgcn_global_load_lds(gbl(src + dsrc[i]), (lds_ptr)((u32x4*)&T + c0), 16, 0, 0);
+    }
+    if (wv == 0 && lane < kTileChunks - 3072)  // the 16 vrul chunks, unswizzled
+      __builtin_amdgcn_global_load_lds(gbl(src + 3072 + lane), (lds_ptr)((u32x4*)&T + 3072), 16, 0, 0);
   };
 
   // query fragments (B operand of S^T = K Q^T): column n = query qa + 16 wv + n of head h*G+gg
@@ -498,101 +492,130 @@ __global__ __launch_bounds__(kAThreads, 2) void attend_kernel(AttendArgs a) {
     for (int dt = 0; dt < 8; ++dt) o[dt][gg] = float4v{0.f, 0.f, 0.f, 0.f};
   }
 
-  const int tl0 = k0 / kXTile, tl1 = (k1 + kXTile - 1) / kXTile;
-  load_k(tl0);
-  load_v(tl0);
-  store_k(S.t[0]);
-  store_v(S.t[0]);
+  const int tl0 = k0 / kXTile, ntl_item = (k1 + kXTile - 1) / kXTile - tl0;
   const int lim = p0 + qj;  // last key this lane's query may see
-  for (int tl = tl0; tl < tl1; ++tl) {
-    AttendTile& T = S.t[(tl - tl0) & 1];
-    AttendTile& Tn = S.t[(tl + 1 - tl0) & 1];
-    const bool more = tl + 1 < tl1;
-    __syncthreads();  // tile tl is in LDS; every wave is done with the other buffer
-    if (more) load_k(tl + 1);
+  const float sl2 = a.scale_log2;
+
+  // One half step: keys 32 hf .. 32 hf + 31 of tile tl (buffer T): scores, softmax, P.V.
+  // LDS byte offsets of this lane's fragments inside a tile image: the swizzle only involves
+  // row & 7 = n & 7, so they are fixed per lane (rows add multiples of 16 rows)
+  uint32_t koff[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) koff[ks] = n * 256 + (((4 * ks + gq) ^ (n & 7)) << 4);
+  uint32_t voff[2];
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) voff[hf] = 32768 + n * 128 + (((4 * hf + gq) ^ (n & 7)) << 4);
+  float l_lane[G];  // per-lane partial normalisers, summed over the column at the end
+#pragma unroll
+  for (int gg = 0; gg < G; ++gg) l_lane[gg] = 0.f;
+
+  auto half_step = [&](const AttendTile& T, int tl, int hf) {
     const int tt = tl * kXTile;
-    // Two 32-key halves, each scores -> softmax -> P.V, so that only half a tile's score and
-    // probability fragments are live at once.
-    const bool full = tt + kXTile <= k1 && tt + kXTile - 1 <= p0 + qa;  // no key masked
+    const char* tb = (const char*)&T;
+    // -------------------------------------------------------- scores S^T = K Q^T
+    float4v sacc[2][G];
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      // -------------------------------------------------------- scores S^T = K Q^T
-      float4v sacc[2][G];
+    for (int k2 = 0; k2 < 2; ++k2) {
+      const char* rb = tb + (32 * hf + 16 * k2) * 256;
 #pragma unroll
-      for (int k2 = 0; k2 < 2; ++k2) {
+      for (int ks = 0; ks < 4; ++ks) {
+        const half8 ka = *(const half8*)(rb + koff[ks]);
+        const half8 kl = *(const half8*)(rb + 16384 + koff[ks]);
 #pragma unroll
-        for (int gg = 0; gg < G; ++gg) sacc[k2][gg] = float4v{0.f, 0.f, 0.f, 0.f};
-        const int row = 32 * hf + 16 * k2 + n;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const int cc = (4 * ks + gq) ^ (row & 7);
-          const half8 ka = __builtin_bit_cast(half8, T.khi[row][cc]);
-          const half8 kl = __builtin_bit_cast(half8, T.klo[row][cc]);
-#pragma unroll
-          for (int gg = 0; gg < G; ++gg) {
-            sacc[k2][gg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qf[gg][ks], sacc[k2][gg], 0, 0, 0);
-            sacc[k2][gg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qf[gg][ks], sacc[k2][gg], 0, 0, 0);
-          }
+        for (int gg = 0; gg < G; ++gg) {
+          sacc[k2][gg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              ka, qf[gg][ks], ks ? sacc[k2][gg] : float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          sacc[k2][gg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qf[gg][ks], sacc[k2][gg], 0, 0, 0);
         }
-      }
-      if (hf == 1 && more) {  // every K read of this tile is issued
-        store_k(Tn);
-        load_v(tl + 1);
-      }
-      // -------------------------------------------------------- online softmax per column
-      float4v vr[2];
-#pragma unroll
-      for (int k2 = 0; k2 < 2; ++k2) vr[k2] = *(const float4v*)&T.vrul[32 * hf + 16 * k2 + 4 * gq];
-      half8 pb[G];
-#pragma unroll
-      for (int gg = 0; gg < G; ++gg) {
-        float mt = -INFINITY;
-#pragma unroll
-        for (int k2 = 0; k2 < 2; ++k2)
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) {
-            const int key = tt + 32 * hf + 16 * k2 + 4 * gq + jj;
-            const float sv = sacc[k2][gg][jj] * a.scale_log2;
-            const float tv = (full || (key < k1 && key <= lim)) ? sv : -INFINITY;
-            sacc[k2][gg][jj] = tv;
-            mt = fmaxf(mt, tv);
-          }
-        mt = cross_row_max(mt);
-        // lazy rescaling: the reference point moves only when the column max grows by more
-        // than 2^8 (p <= 256 otherwise); a fully masked column leaves it at -inf
-        if (mt > m_run[gg] + 8.f) {
-          const float alpha = exp2f(m_run[gg] - mt);
-          m_run[gg] = mt;
-          l_run[gg] *= alpha;
-#pragma unroll
-          for (int dt = 0; dt < 8; ++dt) o[dt][gg] *= alpha;
-        }
-        const float mref = m_run[gg] == -INFINITY ? 0.f : m_run[gg];
-        float ps = 0.f;
-#pragma unroll
-        for (int k2 = 0; k2 < 2; ++k2)
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) {
-            const float pr = fast_exp2(sacc[k2][gg][jj] - mref);
-            ps += pr;
-            pb[gg][4 * k2 + jj] = (_Float16)(pr * vr[k2][jj]);
-          }
-        l_run[gg] += cross_row_sum(ps);
-      }
-      // -------------------------------------------------------- O^T += Vt (P ruler_v)^T
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const int row = 16 * dt + n;
-        const half8 va = __builtin_bit_cast(half8, T.vt[row][(4 * hf + gq) ^ (row & 7)]);
-#pragma unroll
-        for (int gg = 0; gg < G; ++gg)
-          o[dt][gg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[gg], o[dt][gg], 0, 0, 0);
       }
     }
-    if (more) store_v(Tn);
+    // -------------------------------------------------------- causal mask (boundary tiles only)
+    // key t is visible to this lane's query iff t <= min(k1 - 1, p0 + qj); a tile whose every
+    // key is visible to the block's first query needs no mask (a uniform branch)
+    if (!(tt + kXTile <= k1 && tt + kXTile - 1 <= p0 + qa)) {
+      const int last = min(k1 - 1, lim) - (tt + 32 * hf + 4 * gq);
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+          for (int gg = 0; gg < G; ++gg)
+            sacc[k2][gg][jj] = 16 * k2 + jj <= last ? sacc[k2][gg][jj] : -INFINITY;
+    }
+    // -------------------------------------------------------- online softmax per column
+    // (raw scores; the scale enters the exponent's fma, and m_run is in scaled units)
+    const float4v vr0 = *(const float4v*)(tb + 49152 + (32 * hf + 4 * gq) * 4);
+    const float4v vr1 = *(const float4v*)(tb + 49152 + (32 * hf + 16 + 4 * gq) * 4);
+    half8 pb[G];
+#pragma unroll
+    for (int gg = 0; gg < G; ++gg) {
+      float mt = fmaxf(fmaxf(fmaxf(sacc[0][gg][0], sacc[0][gg][1]), fmaxf(sacc[0][gg][2], sacc[0][gg][3])),
+                       fmaxf(fmaxf(sacc[1][gg][0], sacc[1][gg][1]), fmaxf(sacc[1][gg][2], sacc[1][gg][3])));
+      mt *= sl2;
+      // Lazy rescaling: the reference point moves only when a column max grows by more than 2^8
+      // (p <= 256 otherwise), which is rare after a column's first tile, so the column max and
+      // the rescale sit behind a wave-uniform ballot. A fully masked column stays at -inf.
+      if (__builtin_amdgcn_ballot_w64(mt > m_run[gg] + 8.f) != 0) {
+        const float cm = cross_row_max(mt);
+        const bool up = cm > m_run[gg] + 8.f;  // the same in the column's 4 lanes
+        const float alpha = up ? exp2f(m_run[gg] - cm) : 1.f;
+        m_run[gg] = up ? cm : m_run[gg];
+        l_lane[gg] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) o[dt][gg] *= alpha;
+      }
+      const float nref = m_run[gg] == -INFINITY ? 0.f : -m_run[gg];
+      float ps = 0.f;
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const float pr = fast_exp2(fmaf(sacc[k2][gg][jj], sl2, nref));
+          ps += pr;
+          pb[gg][4 * k2 + jj] = (_Float16)(pr * (k2 ? vr1[jj] : vr0[jj]));
+        }
+      l_lane[gg] += ps;
+    }
+    // -------------------------------------------------------- O^T += Vt (P ruler_v)^T
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const half8 va = *(const half8*)(tb + dt * 2048 + voff[hf]);
+#pragma unroll
+      for (int gg = 0; gg < G; ++gg)
+        o[dt][gg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[gg], o[dt][gg], 0, 0, 0);
+    }
+  };
+
+  // Waves 4..7 run half a tile behind waves 0..3, so that the two waves sharing a SIMD are in
+  // different phases (one's MFMAs beside the other's softmax). Barrier k: waves 0..3 have
+  // finished tiles < k, waves 4..7 tiles < k - 1 and half 0 of tile k - 1. Between barriers k
+  // and k + 1 tiles k - 1 and k are read and tile k + 1 is written, into buffer (k + 1) % 3,
+  // whose last reader (tile k - 2) finished before barrier k.
+  dma_tile(S.t[0], tl0);
+  const bool late = wv >= 4;
+  for (int k = 0; k <= ntl_item; ++k) {
+    // this wave's DMA writes have landed (the barrier's workgroup-scope fence does not wait for
+    // them), then every wave's have
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (k + 1 < ntl_item) dma_tile(S.t[(k + 1) % 3], tl0 + k + 1);
+    if (!late) {
+      if (k < ntl_item) {
+        half_step(S.t[k % 3], tl0 + k, 0);
+        half_step(S.t[k % 3], tl0 + k, 1);
+      }
+    } else {
+      if (k >= 1) half_step(S.t[(k - 1) % 3], tl0 + k - 1, 1);
+      if (k < ntl_item) half_step(S.t[k % 3], tl0 + k, 0);
+    }
   }
 
+#pragma unroll
+  for (int gg = 0; gg < G; ++gg) l_run[gg] = cross_row_sum(l_lane[gg]);
+
   // ---------------------------------------------------------------- output / split-K hand-off
+  // out rows aligned for 4-element stores (16 bytes fp32, 8 bytes fp16 / bf16)
+  const bool ovec = (uintptr_t)a.out % 16 == 0 && a.out_row_stride % 4 == 0;
   if (nparts == 1) {
     if (qvalid) {
 #pragma unroll
@@ -601,9 +624,7 @@ __global__ __launch_bounds__(kAThreads, 2) void attend_kernel(AttendArgs a) {
         const int64_t ob = (int64_t)(q0 + qj) * a.out_row_stride + (int64_t)(h * G + gg) * kD;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj)
-            store_act(a.out, a.out_dtype, ob + 16 * dt + 4 * gq + jj, o[dt][gg][jj] * inv);
+          store_act4(a.out, a.out_dtype, ob + 16 * dt + 4 * gq, o[dt][gg] * inv, ovec);
       }
     }
     return;
@@ -618,12 +639,13 @@ __global__ __launch_bounds__(kAThreads, 2) void attend_kernel(AttendArgs a) {
     for (int gg = 0; gg < G; ++gg) {
       const int row = gg * kAQ + 16 * wv + n;
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) *gblw((float4v*)&po[(int64_t)row * kD + 16 * dt + 4 * gq]) = o[dt][gg];
-      if (gq == 0) *gblw((float2v*)&pml[2 * row]) = float2v{m_run[gg], l_run[gg]};
+      for (int dt = 0; dt < 8; ++dt) store_agent16(&po[(int64_t)row * kD + 16 * dt + 4 * gq], o[dt][gg]);
+      if (gq == 0) store_agent8(&pml[2 * row], float2v{m_run[gg], l_run[gg]});
     }
   }
-  // each thread's partial stores complete at the device-coherent level before the counter update
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  // the write-through partial stores are complete at the device-coherent level before the
+  // counter update (no L2 writeback needed on this side)
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (tid == 0) {
     const int prev = __hip_atomic_fetch_add(&a.ws_cnt[item], 1, __ATOMIC_ACQ_REL,
@@ -682,8 +704,7 @@ __global__ __launch_bounds__(kAThreads, 2) void attend_kernel(AttendArgs a) {
       const int gg = rowv[u] / kAQ, qq = rowv[u] % kAQ;
       const int64_t ob = (int64_t)(q0 + qa + qq) * a.out_row_stride + (int64_t)(h * G + gg) * kD +
                          4 * (it & 31);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) store_act(a.out, a.out_dtype, ob + j, acc[u][j]);
+      store_act4(a.out, a.out_dtype, ob, acc[u], ovec);
     }
   }
   if (tid == 0)
