@@ -208,6 +208,19 @@ __global__ __launch_bounds__(kXThreads, 2) void expand_kernel(ExpandArgs a) {
       stage_row_w(P.krow, (k_row_off & 15) >> 2, ksel, &S.rawk[ptok][part * 4]);
       stage_row_w(P.vrow, (v_row_off & 15) >> 2, vsel, &S.rawv[ptok][part * 4]);
     }
+    // This tile's angle rows, then the next tile's slot bytes, are requested before any of the
+    // tile's stores: loads and stores complete in order (vmcnt), so a load issued after the
+    // stores could only be waited on together with them.
+    float4v cvA[4], svA[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      const int key = 16 * nb + n;
+      const int pos = key < ntile ? tt + key : tt;
+      cvA[nb] = *gbl((const float4v*)&a.cs_cache[(int64_t)pos * kD + dl]);
+      svA[nb] = *gbl((const float4v*)&a.cs_cache[(int64_t)pos * kD + 64 + dl]);
+    }
+    if (tt + kXTile < k1)
+      fetch_raw_slot_w<2 * KSTEPS>(P, slot_base(tt + kXTile), part, g, k_win, v_win);
     __syncthreads();
     __builtin_amdgcn_s_setprio(1);
     // ------------------------------------------------------------ decode (thread = half row)
@@ -271,19 +284,10 @@ __global__ __launch_bounds__(kXThreads, 2) void expand_kernel(ExpandArgs a) {
     if (tid < kXTile / 4)
       gblw((u32x4*)(tile_out + kTileVrul))[tid] = *(const u32x4*)&S.vrul[4 * tid];
     // ------------------------------------------------------------ recon + residual + RoPE -> K
-    auto angle_row = [&](int nb, float4v& cv, float4v& sv) {
-      const int key = 16 * nb + n;
-      const int pos = key < ntile ? tt + key : tt;
-      cv = *gbl((const float4v*)&a.cs_cache[(int64_t)pos * kD + dl]);
-      sv = *gbl((const float4v*)&a.cs_cache[(int64_t)pos * kD + 64 + dl]);
-    };
-    float4v cvn, svn;
-    angle_row(0, cvn, svn);
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
       const int key = 16 * nb + n;
-      const float4v cv = cvn, sv = svn;
-      if (nb < 3) angle_row(nb + 1, cvn, svn);
+      const float4v cv = cvA[nb], sv = svA[nb];
       float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < KSTEPS; ++s) {
@@ -321,9 +325,6 @@ __global__ __launch_bounds__(kXThreads, 2) void expand_kernel(ExpandArgs a) {
       kl_out[(64 + dl) >> 2] = u32x2v{__builtin_bit_cast(uint32_t, zh[0]), __builtin_bit_cast(uint32_t, zh[1])};
     }
     __builtin_amdgcn_s_setprio(0);
-    // the next tile's bytes are in flight while the other workgroup on the CU computes
-    if (tt + kXTile < k1)
-      fetch_raw_slot_w<2 * KSTEPS>(P, slot_base(tt + kXTile), part, g, k_win, v_win);
     __syncthreads();  // coef / kcode / vcode / rulers are overwritten by the next tile
   }
 }
