@@ -114,12 +114,13 @@ struct DecodeSmem {
   int is_last;
 };
 
-template <int G, int RB, int VB, int KU>
+// QLO: the query's low fp16 part can be non-zero (fp32 / bf16 queries), so the scores take the
+// third product qlo * yhi; an fp16 query is its own hi part and skips it.
+template <int G, int RB, int VB, int KU, bool QLO>
 __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   using Smem = DecodeSmem<KU, G>;
   Smem& S = *reinterpret_cast<Smem*>(smem_raw);
-  constexpr int kCPP = KU * 4;
   constexpr int KSTEPS = KU / 2;  // k = 32 steps
   constexpr bool KTAIL = KU & 1;  // one more k = 16 step
   constexpr int kSP = Smem::kSP;
@@ -576,7 +577,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
       float4v sacc = {0.f, 0.f, 0.f, 0.f};
       sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qhi, yhi, sacc, 0, 0, 0);
       sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qhi, ylo, sacc, 0, 0, 0);
-      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qlo, yhi, sacc, 0, 0, 0);
+      if constexpr (QLO) sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qlo, yhi, sacc, 0, 0, 0);
       // lane (n, gq) holds heads 4*gq .. 4*gq+3 of token n
       if (4 * gq < G) *(float4v*)&S.spart[wv][tok][4 * gq] = sacc;
     }
@@ -815,7 +816,8 @@ namespace ttkv {
 template <int G, int RB, int VB, int KU>
 static int launch_decode_t(const DecodeArgs& a, int grid, hipStream_t st) {
   const size_t smem = sizeof(DecodeSmem<KU, G>);
-  auto kfn = decode_paged_kernel<G, RB, VB, KU>;
+  auto kfn = a.q_dtype == TTKV_DTYPE_F16 ? decode_paged_kernel<G, RB, VB, KU, false>
+                                         : decode_paged_kernel<G, RB, VB, KU, true>;
   if (int rc = raise_smem_limit((const void*)kfn, smem)) return rc;
   hipLaunchKernelGGL(kfn, dim3(grid), dim3(kThreads), smem, st, a);
   const hipError_t e = hipGetLastError();
