@@ -152,8 +152,10 @@ int ttkv_write_paged(const ttkv_layout* lay, const void* key, int32_t k_dtype, i
  * coefficients come from coeff_q_in); see the workspace note above ttkv_decode_workspace_bytes. */
 int64_t ttkv_write_workspace_bytes(const ttkv_layout* lay, int32_t num_tokens);
 
-/* Workspace bytes `ttkv_prefill_paged` needs for this batch shape (0 when one key split covers
- * every query block); see the workspace note above ttkv_decode_workspace_bytes. */
+/* Workspace bytes `ttkv_prefill_paged` needs for this batch shape: the split-K counters and
+ * partials, and for chunks of more than 64 queries the expanded key tiles (49,408 B per request,
+ * KV head and 64 keys, at most 1 GiB per request slice); 0 when one key split covers every query
+ * block of a fused launch. See the workspace note above ttkv_decode_workspace_bytes. */
 int64_t ttkv_prefill_workspace_bytes(const ttkv_layout* lay, int32_t num_heads, int32_t num_reqs,
                                      int32_t max_q_len, int32_t max_seq_len, int32_t block_size);
 
@@ -166,8 +168,11 @@ int64_t ttkv_prefill_workspace_bytes(const ttkv_layout* lay, int32_t num_heads, 
  * stored keys (the chunk's own keys included, written before the read), p0 = n - Q:
  *   s[p, j, t] = scale * q[qsl[r]+j, p] . RoPE_t(K_pre[t]),   -inf where t > p0 + j
  *   out[qsl[r]+j, p] = sum_t softmax_t(s[p, j, :]) * V[h(p), t]
- * Key tiles are reconstructed once per 64-query block and reused by all its queries and GQA
- * heads on MFMA; the scores never leave the chip.
+ * Chunks of more than 64 queries (G <= 3, r1 <= 128) run as two launches: every stored key is
+ * decoded and reconstructed once into the workspace (rotated key hi + lo fp16, exact V codes, V
+ * rulers), then flash attention on MFMA reads it for every 128-query block. Shorter chunks run one
+ * fused launch that reconstructs each key tile once per 64-query block. Scores never leave the
+ * chip.
  * req_index    optional [num_reqs] int32: batch rows to process (block_table / seq_lens /
  *              query_start_loc are indexed by it); NULL = rows 0..num_reqs-1.
  * max_q_len / max_seq_len bound Q and n over the processed rows (they size the grid).
