@@ -270,11 +270,15 @@ def bench_config4(torch, lay, cfg, cache, dev, steps=10, warmup=3, cpu=False):
 
     ms = time_launches(torch, attend, steps, warmup)
     scores = torch.empty(HQ, Q, n, dtype=torch.float32, device=dev)
+    from vllm_ttkv import _hip
+    sws = torch.empty(max(1, _hip.lib().ttkv_multi_scores_workspace_bytes(_hip.Layout.of(lay), HQ,
+                                                                           Q, n)),
+                      dtype=torch.uint8, device=dev)
 
     def score1():
         kernels.multi_scores_paged(lay, q[:Q], L["page"], BS, st["bt"][:1], st["seq_lens"][:1],
                                    qsl[:2], Q, n, st["dec_map"], L["dec_pool"], cache,
-                                   D ** -0.5, scores=scores, error_word=err)
+                                   D ** -0.5, scores=scores, error_word=err, workspace=sws)
 
     ms_s = time_launches(torch, score1, steps, warmup)
     torch.cuda.synchronize()

@@ -196,7 +196,9 @@ int ttkv_prefill_paged(const ttkv_layout* lay, int32_t num_heads, float scale,
  * `krt_multi_from_slots` returns it (krt_triton.py:268-317; reference.py:112-146):
  *   scores[p * s_head_stride + j * s_q_stride + t] = s[p, j, t]   fp32, -inf where t > p0 + j
  * for p < num_heads, j < Q, t < n. Reconstruction and rotated keys are carried at fp32 accuracy
- * (hi + lo fp16 MFMA operands); the query is taken as fp16. */
+ * (hi + lo fp16 MFMA operands); the query is taken as fp16. With a workspace of
+ * ttkv_multi_scores_workspace_bytes (256-byte aligned; NULL / 0 allowed), a chunk of more than 64
+ * queries is computed from every stored key expanded once; otherwise by the fused kernel. */
 int ttkv_multi_scores_paged(const ttkv_layout* lay, int32_t num_heads, float scale,
                             const void* query, int32_t q_dtype, int64_t q_row_stride,
                             const uint8_t* page, int64_t n_slots, int64_t slot_stride,
@@ -206,8 +208,15 @@ int ttkv_multi_scores_paged(const ttkv_layout* lay, int32_t num_heads, float sca
                             int32_t max_seq_len, const int32_t* dec_slot_of_block,
                             int64_t num_blocks, const float* dec_pool, int64_t n_dec_slots,
                             const float* cos_sin_cache, int64_t max_position, float* scores,
-                            int64_t s_head_stride, int64_t s_q_stride, int32_t* error_word,
-                            ttkv_stream_t stream);
+                            int64_t s_head_stride, int64_t s_q_stride, void* workspace,
+                            int64_t workspace_bytes, int32_t* error_word, ttkv_stream_t stream);
+
+/* Workspace bytes with which `ttkv_multi_scores_paged` computes a chunk of more than 64 queries
+ * (G <= 3, r1 <= 128) from every stored key expanded once (49,408 B per KV head and 64 keys);
+ * 0 when the chunk takes the fused kernel. With a NULL or smaller workspace the call runs the
+ * fused kernel, with the same results. -1 for an invalid layout / head count. */
+int64_t ttkv_multi_scores_workspace_bytes(const ttkv_layout* lay, int32_t num_heads,
+                                          int32_t max_q_len, int32_t max_seq_len);
 
 /* Benchmark comparator (no counterpart in the compressed path): dense paged decode attention over
  * an uncompressed fp16/bf16 KV cache of the same shapes and launch structure as

@@ -65,6 +65,39 @@ def test_scores_mode_vs_raw_scores_multi(cfg, n, Q):
     _check(got, want, f"scores {cfg} n={n} Q={Q}")
 
 
+@pytest.mark.parametrize("cfg,n,Q", [("safe", 2100, 257), ("campaign4x", 1030, 200)])
+def test_scores_from_expanded_keys_equal_the_fused_kernel(cfg, n, Q):
+    """A chunk of more than 64 queries with a workspace is scored from every stored key expanded
+    once (expand launch + scores kernel); without one, by the fused kernel. Both reconstruct and
+    rotate with the same fp32 arithmetic (up to the compiler's fma contraction, an ulp) and take
+    the same fp16 MFMA operands, so the -inf pattern is identical and the finite scores agree to
+    fp32 rounding. Rows past the tensor's n keys and Q queries stay untouched."""
+    st = fitted_store(cfg, n, seed=3 * n + Q)
+    cache = llama3_cache(4096)
+    pg, dec_pool, dec_map = _dev_inputs([st], seed=9)
+    q = synth.queries(Q, seed=Q + 1).reshape(Q, HQ, 128)
+    qsl = torch.tensor([0, Q], dtype=torch.int32).cuda()
+    args = (st["lay"], q.cuda(), pg["page"].cuda(), 16, pg["block_table"].cuda(),
+            pg["seq_lens"].cuda(), qsl, Q, n, dec_map, dec_pool, cache.cuda(), SCALE)
+    outs = []
+    for ws in (None, False):
+        err = torch.zeros(1, dtype=torch.int32, device="cuda")
+        sc = torch.full((HQ, Q + 3, n + 5), 7.0, dtype=torch.float32, device="cuda")
+        kernels.multi_scores_paged(*args, scores=sc, error_word=err, workspace=ws)
+        torch.cuda.synchronize()
+        assert int(err.item()) == 0
+        outs.append(sc.cpu())
+    expanded, fused = outs
+    assert torch.equal(torch.isneginf(expanded), torch.isneginf(fused))
+    fin = torch.isfinite(fused)
+    assert torch.isfinite(expanded[fin]).all()
+    d = (expanded[fin].double() - fused[fin].double()).abs().max()
+    print(f"expanded vs fused scores {cfg} n={n} Q={Q}: max-abs {d:.3e}")
+    assert d <= 1e-5 * float(fused[fin].abs().max())
+    assert (expanded[:, Q:, :] == 7.0).all() and (expanded[:, :, n:] == 7.0).all()
+    assert torch.isneginf(expanded[:, :Q, :n]).any()
+
+
 def test_attend_mode_ragged_batch_with_splits():
     """Three continuation requests of different lengths in one launch (several key splits per
     query block, so the in-launch combine runs), fp16 queries and output."""

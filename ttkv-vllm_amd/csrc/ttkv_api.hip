@@ -172,17 +172,27 @@ int ttkv_multi_scores_paged(const ttkv_layout* lay, int32_t num_heads, float sca
                             int32_t max_seq_len, const int32_t* dec_slot_of_block,
                             int64_t num_blocks, const float* dec_pool, int64_t n_dec_slots,
                             const float* cos_sin_cache, int64_t max_position, float* scores,
-                            int64_t s_head_stride, int64_t s_q_stride, int32_t* error_word,
-                            ttkv_stream_t stream) {
+                            int64_t s_head_stride, int64_t s_q_stride, void* workspace,
+                            int64_t workspace_bytes, int32_t* error_word, ttkv_stream_t stream) {
   Geom g;
   if (!make_geom(lay, &g)) return host_fail(TTKV_E_INVALID, "invalid layout");
   if (!scores) return host_fail(TTKV_E_INVALID, "scores is null");
+  if (workspace_bytes < 0) return host_fail(TTKV_E_INVALID, "negative workspace_bytes");
   return prefill_paged(g, num_heads, scale, query, q_dtype, q_row_stride, page, n_slots,
                        slot_stride, block_size, block_table, bt_row_stride, max_blocks, seq_lens,
                        query_start_loc, nullptr, 1, max_q_len, max_seq_len, dec_slot_of_block,
                        num_blocks, dec_pool, n_dec_slots, cos_sin_cache, max_position, nullptr, 0,
-                       0, scores, s_head_stride, s_q_stride, nullptr, 0, error_word,
-                       (hipStream_t)stream);
+                       0, scores, s_head_stride, s_q_stride, workspace, workspace_bytes,
+                       error_word, (hipStream_t)stream);
+}
+
+int64_t ttkv_multi_scores_workspace_bytes(const ttkv_layout* lay, int32_t num_heads,
+                                          int32_t max_q_len, int32_t max_seq_len) {
+  Geom g;
+  if (!make_geom(lay, &g) || num_heads <= 0 || num_heads % g.H || max_q_len < 0 ||
+      max_seq_len < 0)
+    return -1;
+  return continuation_scores_workspace_bytes(g, num_heads / g.H, max_q_len, max_seq_len);
 }
 
 int64_t ttkv_dense_workspace_bytes(int32_t H, int32_t num_heads, int32_t num_reqs,

@@ -712,6 +712,186 @@ __global__ __launch_bounds__(kAThreads, 2) void attend_kernel(AttendArgs a) {
     __hip_atomic_store(&a.ws_cnt[item], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ------------------------------------------------------------------------------------ scores
+// The score tensor of one request (krt_multi_from_slots) from the expanded tiles:
+//   s[p, j, t] = scale * q[j, p] . k_t,   -inf where t > p0 + j
+// for a 512-thread workgroup per (KV head, 128 queries, key range); wave w owns queries
+// 16w..16w+15 for all G heads. Per 64-key tile: the tile's K halves by DMA (double-buffered, one
+// barrier per tile), S^T = K Q^T on MFMA (hi and lo key halves against the fp16 query), then 16-byte
+// stores of 4 keys per lane. Nothing is reduced, so key ranges need no combine.
+struct ScoresArgs {
+  Geom g;
+  int G;
+  float scale;
+  const void* q;
+  int q_dtype;
+  int64_t q_row_stride;
+  const int32_t* bt;
+  const int32_t* seq_lens;
+  const int32_t* qsl;
+  const int32_t* dec_map;
+  int64_t num_blocks, n_dec_slots;
+  const uint8_t* tiles;
+  int ntl;
+  float* s_out;
+  int64_t s_head_stride, s_q_stride;
+  int* err;
+  int n_qb, kchunk, nsplit, max_seq, max_q;
+};
+
+struct ScoresTile {
+  u32x4 khi[kXTile][16];
+  u32x4 klo[kXTile][16];
+};
+struct ScoresSmem {
+  ScoresTile t[2];
+};
+
+template <int G>
+__global__ __launch_bounds__(kAThreads, 2) void scores_kernel(ScoresArgs a) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  ScoresSmem& S = *reinterpret_cast<ScoresSmem*>(smem_raw);
+  const Geom& g = a.g;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = tid >> 6;
+  const int n = lane & 15;
+  const int gq = lane >> 4;
+
+  // items (head, key range, query block), the query blocks of one key range consecutive on one
+  // XCD so they read the same tiles through its L2
+  const int nwork = g.H * a.nsplit * a.n_qb;
+  const int per_xcd = gridDim.x >> 3;
+  const int w = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  if (w >= nwork) return;
+  const int qb = w % a.n_qb;
+  const int sp = (w / a.n_qb) % a.nsplit;
+  const int h = w / a.n_qb / a.nsplit;
+  const int q0 = a.qsl[0];
+  int qlen = a.qsl[1] - q0;
+  int seq = a.seq_lens[0];
+  const bool lead = tid == 0 && sp == 0 && qb == 0 && h == 0;
+  if (seq > a.max_seq || qlen > a.max_q) {
+    if (lead) atomicOr(a.err, TTKV_ERR_SEQ_LEN);
+    seq = min(seq, a.max_seq);
+    qlen = min(qlen, a.max_q);
+  }
+  const int p0 = seq - qlen;
+  const int qa = qb * kAQ;
+  if (qlen <= 0 || qa >= qlen) return;
+  if (p0 < 0) {
+    if (lead) atomicOr(a.err, TTKV_ERR_SEQ_LEN);
+    return;
+  }
+  const int qe = min(qlen, qa + kAQ);
+  const int k0 = sp * a.kchunk;
+  const int k1 = min(seq, k0 + a.kchunk);
+  if (k0 >= k1) return;
+
+  const int blk0 = a.bt[0];
+  int dslot = -1;
+  if (blk0 >= 0 && blk0 < a.num_blocks) dslot = a.dec_map[blk0];
+  if (dslot < 0 || dslot >= a.n_dec_slots) {  // expand skipped the request: NaN scores
+    if (tid == 0) atomicOr(a.err, TTKV_ERR_NO_DECODER);
+    for (int i = tid; i < G * (qe - qa) * (k1 - k0); i += kAThreads) {
+      const int kk = i % (k1 - k0);
+      const int rest = i / (k1 - k0);
+      const int qj = qa + rest % (qe - qa);
+      const int gg = rest / (qe - qa);
+      a.s_out[(int64_t)(h * G + gg) * a.s_head_stride + (int64_t)qj * a.s_q_stride + k0 + kk] = NAN;
+    }
+    return;
+  }
+
+  const uint8_t* tbase = a.tiles + (int64_t)h * a.ntl * kTileBytes;
+  // K-half DMA: wave w moves image chunks 64 (w + 8 i), i < 4 (see attend_kernel's dma_tile)
+  int dsrc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int P = 64 * (wv + 8 * i) + lane;
+    const int row = (P >> 4) & 63, pc = P & 15;
+    dsrc[i] = (P & ~1023) + row * 16 + (pc ^ (row & 7));
+  }
+  auto dma_k = [&](ScoresTile& T, int tile) {
+    const u32x4* src = (const u32x4*)(tbase + (int64_t)tile * kTileBytes);
+    typedef __attribute__((address_space(3))) void* lds_ptr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_global_load_lds(gbl(src + dsrc[i]), (lds_ptr)((u32x4*)&T + 64 * (wv + 8 * i)),
+                                       16, 0, 0);
+  };
+
+  const int qj = qa + 16 * wv + n;
+  const bool qvalid = qj < qe;
+  half8 qf[G][4];
+  {
+    const bool qvec = act_rows_aligned(a.q, a.q_dtype, a.q_row_stride);
+    const int64_t qrow = (int64_t)(q0 + (qvalid ? qj : qa)) * a.q_row_stride + (int64_t)h * G * kD +
+                         8 * gq;
+#pragma unroll
+    for (int gg = 0; gg < G; ++gg)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        float tq[8];
+        load_act_n<8>(a.q, a.q_dtype, qrow + (int64_t)gg * kD + 32 * ks, qvec, tq);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qf[gg][ks][i] = qvalid ? (_Float16)tq[i] : (_Float16)0.0f;
+      }
+  }
+  uint32_t koff[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) koff[ks] = n * 256 + (((4 * ks + gq) ^ (n & 7)) << 4);
+  // score rows 16-byte aligned: a lane's 4 consecutive keys are one store
+  const bool s_vec = ((uintptr_t)a.s_out % 16 == 0) && a.s_q_stride % 4 == 0 &&
+                     a.s_head_stride % 4 == 0;
+  const int lim = p0 + qj;  // last key this lane's query may see
+
+  const int tl0 = k0 / kXTile, ntl_item = (k1 + kXTile - 1) / kXTile - tl0;
+  dma_k(S.t[0], tl0);
+  for (int k = 0; k < ntl_item; ++k) {
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's DMA has landed
+    __syncthreads();  // every wave's has; every wave is done with the other buffer
+    if (k + 1 < ntl_item) dma_k(S.t[(k + 1) & 1], tl0 + k + 1);
+    const char* tb = (const char*)&S.t[k & 1];
+    const int tt = (tl0 + k) * kXTile;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      float4v sacc[G];
+      const char* rb = tb + 16 * kt * 256;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const half8 ka = *(const half8*)(rb + koff[ks]);
+        const half8 kl = *(const half8*)(rb + 16384 + koff[ks]);
+#pragma unroll
+        for (int gg = 0; gg < G; ++gg) {
+          sacc[gg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              ka, qf[gg][ks], ks ? sacc[gg] : float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          sacc[gg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qf[gg][ks], sacc[gg], 0, 0, 0);
+        }
+      }
+      // lane holds keys key0 .. key0 + 3 of query qj, head h*G + gg
+      const int key0 = tt + 16 * kt + 4 * gq;
+      if (qvalid) {
+#pragma unroll
+        for (int gg = 0; gg < G; ++gg) {
+          float* srow = a.s_out + (int64_t)(h * G + gg) * a.s_head_stride + (int64_t)qj * a.s_q_stride;
+          float4v v;
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj)
+            v[jj] = key0 + jj <= lim ? sacc[gg][jj] * a.scale : -INFINITY;
+          if (s_vec && key0 + 3 < k1) {
+            *gblw((float4v*)&srow[key0]) = v;
+          } else {
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+              if (key0 + jj < k1) srow[key0 + jj] = v[jj];
+          }
+        }
+      }
+    }
+  }
+}
+
 }  // namespace ttkv
 
 // ------------------------------------------------------------------------------------ host side
@@ -801,7 +981,120 @@ int launch_attend_t(const AttendArgs& a, int grid, hipStream_t st) {
   return TTKV_OK;
 }
 
+template <int G>
+int launch_scores_t(const ScoresArgs& a, int grid, hipStream_t st) {
+  const size_t smem = sizeof(ScoresSmem);
+  auto kfn = scores_kernel<G>;
+  if (int rc = raise_smem_limit((const void*)kfn, smem)) return rc;
+  hipLaunchKernelGGL(kfn, dim3(grid), dim3(kAThreads), smem, st, a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return host_fail(TTKV_E_LAUNCH, std::string("scores launch: ") + hipGetErrorString(e));
+  return TTKV_OK;
+}
+
+// shared by the attention and score paths: the expand launch over rows ri0 .. ri0 + nr - 1
+int expand_rows(const Geom& g, const uint8_t* page, int64_t n_slots, int64_t slot_stride,
+                int block_size, const int32_t* bt, int64_t bt_row_stride, const int32_t* seq_lens,
+                const int32_t* req_index, int ri0, int nr, int ntl, int max_seq_len,
+                const int32_t* dec_map, int64_t num_blocks, const float* dec_pool,
+                int64_t n_dec_slots, const float* cs_cache, uint8_t* tiles, int32_t* err,
+                hipStream_t st) {
+  ExpandArgs e{};
+  e.g = g;
+  e.page = page;
+  e.n_slots = n_slots;
+  e.slot_stride = slot_stride;
+  e.block_size = block_size;
+  e.bt = bt;
+  e.bt_row_stride = bt_row_stride;
+  e.seq_lens = seq_lens;
+  e.req_index = req_index;
+  e.ri0 = ri0;
+  e.num_reqs = nr;
+  e.dec_map = dec_map;
+  e.num_blocks = num_blocks;
+  e.dec_pool = dec_pool;
+  e.n_dec_slots = n_dec_slots;
+  e.cs_cache = cs_cache;
+  e.tiles = tiles;
+  e.ntl = ntl;
+  e.max_seq = max_seq_len;
+  e.err = err;
+  // tiles per item: about one round of two workgroups per CU, and the item's block ids fit the
+  // LDS stage
+  const int64_t total = (int64_t)nr * g.H * ntl;
+  int tpi = ceil_div(total, 2 * (int64_t)device_cu_count());
+  tpi = std::min(tpi, std::max(1, (kXSeg - 2) * block_size / kXTile));
+  tpi = std::max(1, std::min(tpi, ntl));
+  e.tpi = tpi;
+  e.nchunk = ceil_div(ntl, tpi);
+  const int ework = nr * e.nchunk * g.H;
+  return launch_expand(e, g.r1 <= 64 ? 2 : 4, (ework + 7) / 8 * 8, st);
+}
 }  // namespace
+
+int64_t continuation_scores_workspace_bytes(const Geom& g, int G, int max_q_len,
+                                            int max_seq_len) {
+  if (!continuation_eligible(g, G, max_q_len)) return 0;
+  return (int64_t)g.H * ceil_div(max_seq_len, kXTile) * kTileBytes;
+}
+
+// The score tensor of one request through the expand launch and the scores kernel (caller:
+// prefill_paged in scores mode, which has checked the arguments and the workspace size).
+int continuation_scores(const Geom& g, int HQ, float scale, const void* q, int q_dtype,
+                        int64_t q_row_stride, const uint8_t* page, int64_t n_slots,
+                        int64_t slot_stride, int block_size, const int32_t* bt,
+                        int64_t bt_row_stride, const int32_t* seq_lens, const int32_t* qsl,
+                        int max_q_len, int max_seq_len, const int32_t* dec_map, int64_t num_blocks,
+                        const float* dec_pool, int64_t n_dec_slots, const float* cs_cache,
+                        float* s_out, int64_t s_head_stride, int64_t s_q_stride, void* ws,
+                        int32_t* err, hipStream_t st) {
+  const int G = HQ / g.H;
+  const int ntl = ceil_div(max_seq_len, kXTile);
+  uint8_t* tiles = (uint8_t*)ws;
+  if (int rc = expand_rows(g, page, n_slots, slot_stride, block_size, bt, bt_row_stride, seq_lens,
+                           nullptr, 0, 1, ntl, max_seq_len, dec_map, num_blocks, dec_pool,
+                           n_dec_slots, cs_cache, tiles, err, st))
+    return rc;
+  ScoresArgs b{};
+  b.g = g;
+  b.G = G;
+  b.scale = scale;
+  b.q = q;
+  b.q_dtype = q_dtype;
+  b.q_row_stride = q_row_stride;
+  b.bt = bt;
+  b.seq_lens = seq_lens;
+  b.qsl = qsl;
+  b.dec_map = dec_map;
+  b.num_blocks = num_blocks;
+  b.n_dec_slots = n_dec_slots;
+  b.tiles = tiles;
+  b.ntl = ntl;
+  b.s_out = s_out;
+  b.s_head_stride = s_head_stride;
+  b.s_q_stride = s_q_stride;
+  b.err = err;
+  b.n_qb = ceil_div(max_q_len, kAQ);
+  b.max_seq = max_seq_len;
+  b.max_q = max_q_len;
+  // key ranges: about one round of two workgroups per CU, each at least 4 tiles
+  const int items = g.H * b.n_qb;
+  const int64_t want = std::max<int64_t>(1, (2 * (int64_t)device_cu_count() + items - 1) / items);
+  int64_t kc = (std::max(max_seq_len, 1) + want - 1) / want;
+  kc = std::max<int64_t>((kc + kXTile - 1) / kXTile * kXTile, 4 * kXTile);
+  b.kchunk = (int)kc;
+  b.nsplit = std::max(1, ceil_div(max_seq_len, kc));
+  const int work = g.H * b.nsplit * b.n_qb;
+  const int grid = (work + 7) / 8 * 8;
+  switch (G) {
+    case 1: return launch_scores_t<1>(b, grid, st);
+    case 2: return launch_scores_t<2>(b, grid, st);
+    case 3: return launch_scores_t<3>(b, grid, st);
+  }
+  return host_fail(TTKV_E_UNSUPPORTED, "scores: G > 3");
+}
 
 bool continuation_applies(const Geom& g, int G, int max_q_len) {
   return continuation_eligible(g, G, max_q_len);
@@ -830,44 +1123,16 @@ int continuation_paged(const Geom& g, int HQ, float scale, const void* q, int q_
                        int64_t n_dec_slots, const float* cs_cache, void* out, int out_dtype,
                        int64_t out_row_stride, void* ws, int32_t* err, hipStream_t st) {
   const int G = HQ / g.H;
-  const int ksteps = g.r1 <= 64 ? 2 : 4;
   const int slice = cont_slice_reqs(g, num_reqs, max_q_len, max_seq_len);
   for (int ri0 = 0; ri0 < num_reqs; ri0 += slice) {
     const int nr = std::min(slice, num_reqs - ri0);
     const ContShape s = cont_shape(g, G, nr, max_q_len, max_seq_len);
     uint8_t* tiles = (uint8_t*)ws + kCounterBytes + align256(s.part_bytes);
 
-    ExpandArgs e{};
-    e.g = g;
-    e.page = page;
-    e.n_slots = n_slots;
-    e.slot_stride = slot_stride;
-    e.block_size = block_size;
-    e.bt = bt;
-    e.bt_row_stride = bt_row_stride;
-    e.seq_lens = seq_lens;
-    e.req_index = req_index;
-    e.ri0 = ri0;
-    e.num_reqs = nr;
-    e.dec_map = dec_map;
-    e.num_blocks = num_blocks;
-    e.dec_pool = dec_pool;
-    e.n_dec_slots = n_dec_slots;
-    e.cs_cache = cs_cache;
-    e.tiles = tiles;
-    e.ntl = s.ntl;
-    e.max_seq = max_seq_len;
-    e.err = err;
-    // tiles per expand item: about one round of two workgroups per CU, and the item's block ids
-    // fit the LDS stage
-    const int64_t total = (int64_t)nr * g.H * s.ntl;
-    int tpi = ceil_div(total, 2 * (int64_t)device_cu_count());
-    tpi = std::min(tpi, std::max(1, (kXSeg - 2) * block_size / kXTile));
-    tpi = std::max(1, std::min(tpi, s.ntl));
-    e.tpi = tpi;
-    e.nchunk = ceil_div(s.ntl, tpi);
-    const int ework = nr * e.nchunk * g.H;
-    if (int rc = launch_expand(e, ksteps, (ework + 7) / 8 * 8, st)) return rc;
+    if (int rc = expand_rows(g, page, n_slots, slot_stride, block_size, bt, bt_row_stride,
+                             seq_lens, req_index, ri0, nr, s.ntl, max_seq_len, dec_map,
+                             num_blocks, dec_pool, n_dec_slots, cs_cache, tiles, err, st))
+      return rc;
 
     AttendArgs b{};
     b.g = g;

@@ -65,6 +65,16 @@ int64_t prefill_workspace_bytes(const Geom& g, int G, int num_reqs, int max_q_le
 bool continuation_applies(const Geom& g, int G, int max_q_len);
 int64_t continuation_workspace_bytes(const Geom& g, int G, int num_reqs, int max_q_len,
                                      int max_seq_len);
+int64_t continuation_scores_workspace_bytes(const Geom& g, int G, int max_q_len,
+                                            int max_seq_len);
+int continuation_scores(const Geom& g, int HQ, float scale, const void* q, int q_dtype,
+                        int64_t q_row_stride, const uint8_t* page, int64_t n_slots,
+                        int64_t slot_stride, int block_size, const int32_t* bt,
+                        int64_t bt_row_stride, const int32_t* seq_lens, const int32_t* qsl,
+                        int max_q_len, int max_seq_len, const int32_t* dec_map, int64_t num_blocks,
+                        const float* dec_pool, int64_t n_dec_slots, const float* cs_cache,
+                        float* s_out, int64_t s_head_stride, int64_t s_q_stride, void* ws,
+                        int32_t* err, hipStream_t st);
 int continuation_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype,
                        int64_t q_row_stride, const uint8_t* page, int64_t n_slots,
                        int64_t slot_stride, int block_size, const int32_t* bt,

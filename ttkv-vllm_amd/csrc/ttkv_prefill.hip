@@ -791,6 +791,17 @@ int prefill_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype
   }
   // chunks of more than one 64-query block: every key expanded once, then attended by all the
   // chunk's queries (ttkv_continuation.hip)
+  // the score tensor of a long chunk from the expanded tiles, when the caller gave a workspace
+  // for them (without one, the fused kernel below)
+  if (scores && ws) {
+    const int64_t need = continuation_scores_workspace_bytes(g, G, max_q_len, max_seq_len);
+    if (need && ws_bytes >= need && (uintptr_t)ws % 256 == 0)
+      return continuation_scores(g, HQ, scale, q, q_dtype, q_row_stride, page, n_slots,
+                                 slot_stride, block_size, bt, bt_row_stride, seq_lens, qsl,
+                                 max_q_len, max_seq_len, dec_map, num_blocks, dec_pool,
+                                 n_dec_slots, cs_cache, s_out, s_head_stride, s_q_stride, ws, err,
+                                 st);
+  }
   if (!scores && continuation_applies(g, G, max_q_len))
     return continuation_paged(g, HQ, scale, q, q_dtype, q_row_stride, page, n_slots, slot_stride,
                               block_size, bt, bt_row_stride, seq_lens, qsl, req_index, num_reqs,

@@ -126,8 +126,10 @@ def lib():
         P, I64, P, I64,               # dec_slot_of_block, num_blocks, dec_pool, n_dec_slots
         P, I64,                       # cos_sin_cache, max_position
         P, I64, I64,                  # scores, s_head_stride, s_q_stride
-        P, P,                         # error_word, stream
+        P, I64, P, P,                 # workspace, workspace_bytes, error_word, stream
     ]
+    L.ttkv_multi_scores_workspace_bytes.restype = I64
+    L.ttkv_multi_scores_workspace_bytes.argtypes = [LP, I32, I32, I32]
     L.ttkv_dense_workspace_bytes.restype = I64
     L.ttkv_dense_workspace_bytes.argtypes = [I32, I32, I32, I32, I32]
     L.ttkv_dense_decode_paged.restype = ctypes.c_int
@@ -161,7 +163,8 @@ def lib():
 # Every symbol include/ttkv_hip.h declares (checked by tests/test_abi.py).
 EXPORTS = ("ttkv_last_error", "ttkv_blob_bytes", "ttkv_decode_workspace_bytes",
            "ttkv_decode_paged", "ttkv_decode_paged_noalloc", "ttkv_write_paged", "ttkv_prefill_workspace_bytes",
-           "ttkv_prefill_paged", "ttkv_multi_scores_paged", "ttkv_dense_workspace_bytes",
+           "ttkv_prefill_paged", "ttkv_multi_scores_paged", "ttkv_multi_scores_workspace_bytes",
+           "ttkv_dense_workspace_bytes",
            "ttkv_dense_decode_paged", "ttkv_write_workspace_bytes", "ttkv_container_krt",
            "ttkv_container_v_out")
 

@@ -272,10 +272,13 @@ def multi_scores_paged(lay: TTKLayout, query: torch.Tensor, page: torch.Tensor,
                        dec_slot_of_block: torch.Tensor, dec_pool: torch.Tensor,
                        cos_sin_cache: torch.Tensor, scale: float,
                        scores: torch.Tensor | None = None,
-                       error_word: torch.Tensor | None = None) -> torch.Tensor:
+                       error_word: torch.Tensor | None = None,
+                       workspace: torch.Tensor | None | bool = None) -> torch.Tensor:
     """K2 scores mode for ONE request (row 0 of block_table / seq_lens / query_start_loc):
     returns `scores` [HQ, Q, n] fp32 with -inf where key t > p0 + j (`krt_multi_from_slots`).
-    Q and n are `max_q_len` / `max_seq_len`, which must equal the request's own lengths."""
+    Q and n are `max_q_len` / `max_seq_len`, which must equal the request's own lengths.
+    `workspace`: None allocates `ttkv_multi_scores_workspace_bytes` (a chunk of more than 64
+    queries then reads every stored key expanded once), False runs the fused kernel."""
     flat = _read_checks(lay, query, page, block_table, seq_lens, query_start_loc,
                         dec_slot_of_block, dec_pool, cos_sin_cache)
     HQ = query.shape[1]
@@ -289,6 +292,13 @@ def multi_scores_paged(lay: TTKLayout, query: torch.Tensor, page: torch.Tensor,
                          f"contiguous key rows")
     if error_word is None:
         error_word = torch.zeros(1, dtype=torch.int32, device=query.device)
+    if workspace is None:
+        n = _hip.lib().ttkv_multi_scores_workspace_bytes(_hip.Layout.of(lay), HQ, int(max_q_len),
+                                                         int(max_seq_len))
+        if n < 0:
+            raise ValueError("invalid layout / head count for the scores workspace")
+        workspace = torch.empty(int(n), dtype=torch.uint8, device=query.device) if n else False
+    ws_ptr, ws_bytes = (0, 0) if workspace is False else (workspace.data_ptr(), workspace.numel())
     rc = _hip.lib().ttkv_multi_scores_paged(
         _hip.Layout.of(lay), HQ, float(scale),
         query.data_ptr(), _hip.DTYPE_CODE[query.dtype], query.stride(0),
@@ -297,8 +307,8 @@ def multi_scores_paged(lay: TTKLayout, query: torch.Tensor, page: torch.Tensor,
         seq_lens.data_ptr(), query_start_loc.data_ptr(), int(max_q_len), int(max_seq_len),
         dec_slot_of_block.data_ptr(), dec_slot_of_block.numel(), dec_pool.data_ptr(),
         dec_pool.shape[0], cos_sin_cache.data_ptr(), cos_sin_cache.shape[0],
-        scores.data_ptr(), scores.stride(0), scores.stride(1), error_word.data_ptr(),
-        _hip.stream_ptr(query.device))
+        scores.data_ptr(), scores.stride(0), scores.stride(1), ws_ptr, ws_bytes,
+        error_word.data_ptr(), _hip.stream_ptr(query.device))
     _hip.check(rc, "ttkv_multi_scores_paged")
     return scores
 
