@@ -456,10 +456,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
 
   // RoPE angle rows (shared by every request and head, L2-resident): this lane's 4 dims of the
   // token it reconstructs in block nb, requested one block ahead inside the reconstruction. Block
-  // 0's row of the NEXT tile is requested with that tile's slot bytes, where the registers allow.
-  // Loads complete in order (vmcnt), so the reconstruction's angle loads must not queue behind
-  // the next tile's slot bytes: those are requested only after the reconstruction's last angle
-  // wait, and overlap the softmax and P.V instead.
+  // 0's row of the NEXT tile is requested after the reconstruction, where the registers allow.
   constexpr bool kAngle0Ahead = G <= 4;
   float4v cv0, sv0;
   auto angle_row = [&](int ts, int nb, float4v& cv, float4v& sv) {
@@ -497,6 +494,11 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
       stage_row_w(P.vrow, (v_row_off & 15) >> 2, vsel, &S.rawv[ptok][part * 4]);
     }
     __syncthreads();
+    // The next tile's slot bytes, requested as soon as the commit has freed P: they arrive during
+    // the decode and reconstruction instead of stalling the next commit (measured: the bytes took
+    // ~2k cycles, longer than the softmax and P.V they used to overlap). The reconstruction's
+    // angle loads queue behind them (loads complete in order) but are issued a decode later.
+    if (tt + kTile < t1) fetch_raw_slot_w<KU>(P, next_base, part, g, k_win, v_win);
     // ---------------------------------------------------------------- decode (thread = half row)
     // The decode and reconstruction are each workgroup's critical chain; the co-resident
     // workgroup's softmax, P.V and commit fill the issue slots they leave. Raising this wave's
@@ -531,15 +533,15 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
     } else {
       angle_row(tt, 0, cvn, svn);
     }
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
+    // Software-pipelined over the 4 token blocks: block nb + 1's MFMAs are issued before block nb's
+    // epilogue (residual, RoPE, hi/lo split, scores), which has no dependence on them, so the two
+    // overlap within the wave (reconstruction phase 3.65k -> 3.17k cycles per tile, measured).
+    auto recon_mfma = [&](int nb, float krp, float4v& acc0, float4v& acc1) {
       const int tok = 16 * nb + n;
-      const float4v cv = cvn, sv = svn;
-      if (nb < 3) angle_row(tt, nb + 1, cvn, svn);
-      const float krp = S.kr[tok];
       // 4-bit codes arrive as c: the -8 * ruler offset enters as the accumulator's start
       const float kb = RB == 4 ? -8.f * krp : 0.f;
-      float4v acc0 = {kb, kb, kb, kb}, acc1 = {kb, kb, kb, kb};
+      acc0 = float4v{kb, kb, kb, kb};
+      acc1 = float4v{kb, kb, kb, kb};
 #pragma unroll
       for (int s = 0; s < KSTEPS; ++s) {
         const half8 b = *(const half8*)&S.coef[tok][32 * s + 8 * gq];
@@ -561,14 +563,29 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
         acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(thi[1], b, acc1, 0, 0, 0);
         acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(tlo[1], b, acc1, 0, 0, 0);
       }
+    };
+    float krA = S.kr[n];
+    float4v accA0, accA1;
+    recon_mfma(0, krA, accA0, accA1);
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      const int tok = 16 * nb + n;
+      const float4v cv = cvn, sv = svn;
+      if (nb < 3) angle_row(tt, nb + 1, cvn, svn);
+      float4v accB0 = accA0, accB1 = accA1;
+      float krB = krA;
+      if (nb < 3) {
+        krB = S.kr[tok + 16];
+        recon_mfma(nb + 1, krB, accB0, accB1);
+      }
       float vl[4], vh[4];
       codes4<RB>(*(const uint32_t*)&S.kcode[tok][dl], vl);
       codes4<RB>(*(const uint32_t*)&S.kcode[tok][64 + dl], vh);
       float y[8];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float kl = fmaf(krp, vl[i], acc0[i]);
-        const float kh = fmaf(krp, vh[i], acc1[i]);
+        const float kl = fmaf(krA, vl[i], accA0[i]);
+        const float kh = fmaf(krA, vh[i], accA1[i]);
         y[i] = kl * cv[i] - kh * sv[i];
         y[4 + i] = kh * cv[i] + kl * sv[i];
       }
@@ -580,13 +597,14 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
       if constexpr (QLO) sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qlo, yhi, sacc, 0, 0, 0);
       // lane (n, gq) holds heads 4*gq .. 4*gq+3 of token n
       if (4 * gq < G) *(float4v*)&S.spart[wv][tok][4 * gq] = sacc;
+      accA0 = accB0;
+      accA1 = accB1;
+      krA = krB;
     }
     __builtin_amdgcn_s_setprio(0);
-    // ---------------------------------------------------------------- prefetch the next tile
-    if (tt + kTile < t1) {
-      if constexpr (kAngle0Ahead) angle_row(tt + kTile, 0, cv0, sv0);
-      fetch_raw_slot_w<KU>(P, next_base, part, g, k_win, v_win);
-    }
+    // ---------------------------------------------------------------- next tile's first angle row
+    if constexpr (kAngle0Ahead)
+      if (tt + kTile < t1) angle_row(tt + kTile, 0, cv0, sv0);
     __syncthreads();
     // ---------------------------------------------------------------- online softmax (every wave)
     {
@@ -744,7 +762,10 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   // Many chunks: weights in LDS (the tile buffers are free now) -- every chunk's (max, sum) in
   // one round of loads, the per-head max and normaliser by one wave per head, then each output's
   // chunk loads issued together: a few memory round trips whatever the chunk count. Up to 8
-  // chunks, one pass per output (two round trips, no barriers) is shorter.
+  // chunks, every value a thread's outputs need is requested in one round and combined in
+  // registers: one round trip. (Partials live past this XCD's L2; a round trip took ~2.8 us at
+  // the headline, and the former two rounds per output, four per thread, made this combine
+  // ~11.5 us of the launch's tail.)
   float* wsh = reinterpret_cast<float*>(&S.coef[0][0]);
   constexpr int kWCap = (int)(sizeof(S.coef) / sizeof(float));
   const int ncp = n_chunks * G;
@@ -783,7 +804,43 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
       }
       store_act(a.out, a.out_dtype, qrow * a.out_row_stride + (int64_t)(h * G + p) * kD + dim, O);
     }
-  } else {
+  } else if (n_chunks <= 8) {
+    constexpr int kOut = (G * kD + kThreads - 1) / kThreads;  // outputs per thread
+    float mv[kOut][8], lv[kOut][8], ov[kOut][8];
+#pragma unroll
+    for (int u = 0; u < kOut; ++u) {
+      const int it = min(tid + u * kThreads, G * kD - 1);
+      const int p = it / kD;
+      const int dim = it - p * kD;
+#pragma unroll
+      for (int cc = 0; cc < 8; ++cc) {  // chunks past n_chunks re-read the last one, unused
+        const float* pc = pbase + min(cc, n_chunks - 1) * cstride + p * (kD + 2);
+        mv[u][cc] = ld_agent(&pc[kD]);
+        lv[u][cc] = ld_agent(&pc[kD + 1]);
+        ov[u][cc] = ld_agent(&pc[dim]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kOut; ++u) {
+      const int it = tid + u * kThreads;
+      if (it < G * kD) {
+        const int p = it / kD;
+        const int dim = it - p * kD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int cc = 0; cc < 8; ++cc) M = cc < n_chunks ? fmaxf(M, mv[u][cc]) : M;
+        float L = 0.f, O = 0.f;
+#pragma unroll
+        for (int cc = 0; cc < 8; ++cc) {
+          const float f = cc < n_chunks ? exp2f(mv[u][cc] - M) : 0.f;
+          L = fmaf(lv[u][cc], f, L);
+          O = fmaf(ov[u][cc], f, O);
+        }
+        store_act(a.out, a.out_dtype, qrow * a.out_row_stride + (int64_t)(h * G + p) * kD + dim,
+                  O / L);
+      }
+    }
+  } else {  // more chunks than the LDS weights hold: two passes per output
     for (int it = tid; it < G * kD; it += kThreads) {
       const int p = it / kD;
       const int dim = it - p * kD;
