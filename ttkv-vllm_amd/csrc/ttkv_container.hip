@@ -212,6 +212,10 @@ __global__ __launch_bounds__(kCThreads, 2) void container_krt_kernel(ContainerAr
       }
     }
     __syncthreads();
+    // the next tile's bytes, requested as soon as the commit has freed their registers: they
+    // arrive during the decode and reconstruction (kernel 159-161 -> 157-158 us at 8 x 14,402;
+    // the angle loads then queue behind them, a decode later)
+    if (tile + 1 < tile1) fetch(tile + 1);
 
     // ---- decode the residual rows (thread = token tid/4, quarter tid&3). The decode and
     // reconstruction run at raised wave priority: the co-resident workgroup's commit and
@@ -267,9 +271,6 @@ __global__ __launch_bounds__(kCThreads, 2) void container_krt_kernel(ContainerAr
       if (4 * gq < G) *(float4v*)&S.spart[wv][tok][4 * gq] = sacc;
     }
     __builtin_amdgcn_s_setprio(0);
-    // the next tile's bytes: requested after the last angle wait (loads complete in order, so
-    // that wait would also wait for them), in flight during the read-out and the next commit
-    if (tile + 1 < tile1) fetch(tile + 1);
     __syncthreads();
     // the partial scores are next written past the following tile's two barriers, so no barrier
     // follows this read-out
