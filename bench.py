@@ -17,6 +17,12 @@ contexts U[1000, 14400] (config 3), the multi-query continuation score (config 4
 dense fp16 paged-attention comparator, the K1 roofline (HBM bytes per launch / measured launch
 time vs 8 TB/s) and the CPU baseline (the torch-CPU oracle timed on a bounded sample on this
 host).
+
+Timing: the headline's K steps (and config 3's, and the dense comparator's launches) run back to
+back with HIP events only around the timed region, so a launch's time includes the gap to the
+next launch but no per-launch event packets; the per-launch event-pair figure is reported beside
+it. The batch-1 sweep flushes the caches between launches (its layers would otherwise stay in
+the Infinity Cache) and so is timed per launch.
 """
 from __future__ import annotations
 
@@ -131,11 +137,13 @@ def cache_flusher(torch, dev, mib=768):
     return lambda: buf.add_(1)
 
 
-def time_k1(torch, lay, store, q, cache, steps, warmup, n_layers, flush=None):
+def time_k1(torch, lay, store, q, cache, steps, warmup, n_layers, flush=None, per_launch=True):
     """Time `steps` decode steps (n_layers K1 launches each, layer li reading its own pages).
     Returns (ms/step, ms/launch). With `flush`, the caches are flushed between launches (outside
     the per-launch events), so every launch reads cold HBM; ms/step then includes the flushes
-    and only ms/launch is meaningful."""
+    and only ms/launch is meaningful. With per_launch=False the steps run back to back with events
+    only around the whole timed region (per-launch event pairs add ~8 us of packet processing
+    per launch between kernels), and ms/launch is ms/step / n_layers."""
     from vllm_ttkv import kernels
     dev = q.device
     B = store["B"]
@@ -160,6 +168,18 @@ def time_k1(torch, lay, store, q, cache, steps, warmup, n_layers, flush=None):
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
+    if not per_launch:
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(steps):
+            step()
+        t1.record()
+        torch.cuda.synchronize()
+        if int(err.item()):
+            raise RuntimeError(f"K1: device error word {int(err.item())}")
+        ms_step = t0.elapsed_time(t1) / steps
+        return ms_step, ms_step / n_layers
     evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
             for _ in range(n_layers)] for _ in range(steps)]
     t0 = torch.cuda.Event(enable_timing=True)
@@ -175,6 +195,22 @@ def time_k1(torch, lay, store, q, cache, steps, warmup, n_layers, flush=None):
     ms_step = t0.elapsed_time(t1) / steps
     per = [a.elapsed_time(b) for st in evs for (a, b) in st]
     return ms_step, sum(per) / len(per)
+
+
+def time_back_to_back(torch, fn, steps, warmup):
+    """Average ms per call of `fn` with the calls back to back and events only around the whole
+    timed region (the calls' own launch gaps included, no per-call event packets)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
 
 
 def time_launches(torch, fn, steps, warmup):
@@ -328,10 +364,12 @@ def bench_dense(torch, lens, q, dev, steps=3, warmup=1, n_layers=L_LAYERS):
                                    D ** -0.5, out=out, workspace=ws)
         li[0] = (li[0] + 1) % n_layers
 
-    ms = time_launches(torch, run, steps * n_layers, warmup * n_layers)
+    ms = time_back_to_back(torch, run, steps * n_layers, warmup * n_layers)
+    ms_ev = time_launches(torch, run, steps * n_layers, warmup * n_layers)
     del kcs, vcs
     res = dict(us_per_layer=ms * 1e3, hbm_gbps=sum(lens) * H * D * 2 * 2 / (ms * 1e-3) / 1e9,
-               ns_per_cached_token=ms * 1e6 / sum(lens), layers_cycled=n_layers)
+               ns_per_cached_token=ms * 1e6 / sum(lens), layers_cycled=n_layers,
+               us_per_layer_launch_events=ms_ev * 1e3)
     try:
         import torch.nn.functional as F
         kd = torch.randn(B, H, max(lens), D, generator=g, device=dev).to(torch.float16)
@@ -597,12 +635,16 @@ def main():
     log(f"build B=8x14402: {time.perf_counter() - t0:.1f}s (fit {store['t_fit']:.1f}s, "
         f"write {store['t_write']:.1f}s)")
     q = synth.queries(8, seed=5, device=dev)
+    # the timed region: K steps back to back, events only around it; then the same steps with an
+    # event pair around every launch, for the per-launch figure alone
     ms_step, ms_launch = time_k1(torch, lay, store, q, cache, args.steps, args.warmup,
-                                 args.layers)
+                                 args.layers, per_launch=False)
+    _, ms_launch_ev = time_k1(torch, lay, store, q, cache, args.steps, 1, args.layers)
     nbytes = k1_bytes(lay, lens, R1, max(lens))
     achieved = nbytes / (ms_launch * 1e-3) / 1e9
     step_ms = ms_step * L_LAYERS / args.layers
-    log(f"K1 B=8x14402: {ms_launch * 1e3:.1f} us/launch, {achieved:.0f} GB/s")
+    log(f"K1 B=8x14402: {ms_launch * 1e3:.1f} us/launch back to back ({ms_launch_ev * 1e3:.1f} "
+        f"with an event pair per launch), {achieved:.0f} GB/s")
 
     if not args.no_extra:
         # Cold-HBM extras: 28 layers of distinct pages each, and the caches flushed between
@@ -625,14 +667,18 @@ def main():
         extra["batch1_sweep"] = sweep
         lens3 = config3_lens()
         st = build_store(torch, lay, cfg, lens3, L_LAYERS, seed=3, dev=dev)
-        _, ml = time_k1(torch, lay, st, q, cache, 3, 1, L_LAYERS, flush=flush)
+        # 28 layers of ~42 MB each cycle far past the 256 MB Infinity Cache: timed back to back
+        # like the headline (and the dense comparator below); the flushed per-launch figure too
+        _, ml = time_k1(torch, lay, st, q, cache, 10, 3, L_LAYERS, per_launch=False)
+        _, mlf = time_k1(torch, lay, st, q, cache, 3, 1, L_LAYERS, flush=flush)
         b = k1_bytes(lay, lens3, R1, max(lens3))
         log(f"K1 config3 ({sum(lens3)} tokens, longest {max(lens3)}): {ml * 1e3:.1f} us/layer "
-            f"(cold)")
+            f"back to back ({mlf * 1e3:.1f} flushed, event pair per launch)")
         extra["config3_b8_random"] = dict(contexts=lens3, us_per_layer=ml * 1e3,
                                           hbm_gbps=b / (ml * 1e-3) / 1e9,
                                           tokens_per_s=8 / (ml * 1e-3 * L_LAYERS), cold_hbm=True,
-                                          layers_cycled=L_LAYERS)
+                                          layers_cycled=L_LAYERS,
+                                          us_per_layer_flushed_event_pairs=mlf * 1e3)
         del st
         dn = bench_dense(torch, lens3, q, dev)
         dn["compressed_ns_per_cached_token"] = ml * 1e6 / sum(lens3)
@@ -675,6 +721,7 @@ def main():
                    "global_batch": 8, "seq_len": 14402, "layers": L_LAYERS,
                    "layers_timed": args.layers, "parallelism": "single GPU"},
         "us_per_layer": ms_launch * 1e3,
+        "us_per_launch_event_pairs": ms_launch_ev * 1e3,
         "hbm_gbps": achieved,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS,
