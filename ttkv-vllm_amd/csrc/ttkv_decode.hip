@@ -114,6 +114,50 @@ struct DecodeSmem {
   int is_last;
 };
 
+// One-round split-K combine for up to NC chunks: each thread requests every chunk's (max, sum,
+// output) value for its outputs (it = tid + u * kThreads) in one round, then combines them in
+// registers. Chunks past n_chunks re-read the last one and are not used. The partials were
+// written through to the device-coherent level and an agent-scope acquire precedes this.
+template <int G, int NC>
+__device__ __forceinline__ void combine_regs(const float* pbase, int64_t cstride, int n_chunks,
+                                             int tid, void* out, int out_dtype, int64_t orow,
+                                             int h) {
+  constexpr int kOut = (G * kD + kThreads - 1) / kThreads;  // outputs per thread
+  float mv[kOut][NC], lv[kOut][NC], ov[kOut][NC];
+#pragma unroll
+  for (int u = 0; u < kOut; ++u) {
+    const int it = min(tid + u * kThreads, G * kD - 1);
+    const int p = it / kD;
+    const int dim = it - p * kD;
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc) {
+      const float* pc = pbase + min(cc, n_chunks - 1) * cstride + p * (kD + 2);
+      mv[u][cc] = pc[kD];
+      lv[u][cc] = pc[kD + 1];
+      ov[u][cc] = pc[dim];
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kOut; ++u) {
+    const int it = tid + u * kThreads;
+    if (it < G * kD) {
+      const int p = it / kD;
+      const int dim = it - p * kD;
+      float M = -INFINITY;
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc) M = cc < n_chunks ? fmaxf(M, mv[u][cc]) : M;
+      float L = 0.f, O = 0.f;
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc) {
+        const float f = cc < n_chunks ? exp2f(mv[u][cc] - M) : 0.f;
+        L = fmaf(lv[u][cc], f, L);
+        O = fmaf(ov[u][cc], f, O);
+      }
+      store_act(out, out_dtype, orow + (int64_t)(h * G + p) * kD + dim, O / L);
+    }
+  }
+}
+
 // QLO: the query's low fp16 part can be non-zero (fp32 / bf16 queries), so the scores take the
 // third product qlo * yhi; an fp16 query is its own hi part and skips it.
 template <int G, int RB, int VB, int KU, bool QLO>
@@ -762,14 +806,20 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   // Many chunks: weights in LDS (the tile buffers are free now) -- every chunk's (max, sum) in
   // one round of loads, the per-head max and normaliser by one wave per head, then each output's
   // chunk loads issued together: a few memory round trips whatever the chunk count. Up to 8
-  // chunks, every value a thread's outputs need is requested in one round and combined in
-  // registers: one round trip. (Partials live past this XCD's L2; a round trip took ~2.8 us at
+  // chunks (24 for G <= 4), every value a thread's outputs need is requested in one round and
+  // combined in registers (combine_regs): one round trip. (Partials live past this XCD's L2; a round trip took ~2.8 us at
   // the headline, and the former two rounds per output, four per thread, made this combine
   // ~11.5 us of the launch's tail.)
   float* wsh = reinterpret_cast<float*>(&S.coef[0][0]);
   constexpr int kWCap = (int)(sizeof(S.coef) / sizeof(float));
   const int ncp = n_chunks * G;
-  if (n_chunks > 8 && 2 * ncp <= kWCap) {
+  const int64_t orow = qrow * a.out_row_stride;
+  if (n_chunks <= 8) {
+    combine_regs<G, 8>(pbase, cstride, n_chunks, tid, a.out, a.out_dtype, orow, h);
+  } else if (G <= 4 && n_chunks <= 24) {
+    // (batch 1 at ~1k tokens: 17 chunks per head)
+    if constexpr (G <= 4) combine_regs<G, 24>(pbase, cstride, n_chunks, tid, a.out, a.out_dtype, orow, h);
+  } else if (2 * ncp <= kWCap) {
     for (int i = tid; i < ncp; i += kThreads) {
       const int cc = i / G, p = i - cc * G;
       const float* pc = pbase + cc * cstride + p * (kD + 2);
@@ -803,42 +853,6 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
           if (c0 + j < n_chunks) O = fmaf(v[j], wsh[(c0 + j) * G + p], O);
       }
       store_act(a.out, a.out_dtype, qrow * a.out_row_stride + (int64_t)(h * G + p) * kD + dim, O);
-    }
-  } else if (n_chunks <= 8) {
-    constexpr int kOut = (G * kD + kThreads - 1) / kThreads;  // outputs per thread
-    float mv[kOut][8], lv[kOut][8], ov[kOut][8];
-#pragma unroll
-    for (int u = 0; u < kOut; ++u) {
-      const int it = min(tid + u * kThreads, G * kD - 1);
-      const int p = it / kD;
-      const int dim = it - p * kD;
-#pragma unroll
-      for (int cc = 0; cc < 8; ++cc) {  // chunks past n_chunks re-read the last one, unused
-        const float* pc = pbase + min(cc, n_chunks - 1) * cstride + p * (kD + 2);
-        mv[u][cc] = ld_agent(&pc[kD]);
-        lv[u][cc] = ld_agent(&pc[kD + 1]);
-        ov[u][cc] = ld_agent(&pc[dim]);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kOut; ++u) {
-      const int it = tid + u * kThreads;
-      if (it < G * kD) {
-        const int p = it / kD;
-        const int dim = it - p * kD;
-        float M = -INFINITY;
-#pragma unroll
-        for (int cc = 0; cc < 8; ++cc) M = cc < n_chunks ? fmaxf(M, mv[u][cc]) : M;
-        float L = 0.f, O = 0.f;
-#pragma unroll
-        for (int cc = 0; cc < 8; ++cc) {
-          const float f = cc < n_chunks ? exp2f(mv[u][cc] - M) : 0.f;
-          L = fmaf(lv[u][cc], f, L);
-          O = fmaf(ov[u][cc], f, O);
-        }
-        store_act(a.out, a.out_dtype, qrow * a.out_row_stride + (int64_t)(h * G + p) * kD + dim,
-                  O / L);
-      }
     }
   } else {  // more chunks than the LDS weights hold: two passes per output
     for (int it = tid; it < G * kD; it += kThreads) {
