@@ -183,9 +183,10 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   // (request, chunk) read the same coefficient bytes and every request's chunk c the same rows
   // of the angle table (positions are absolute). Blocks are dealt round-robin to the 8 XCDs, so
   // each XCD takes a contiguous range of items and both are fetched from HBM about once per XCD.
-  // Each request's query row and first block id are loaded with its length (one round trip).
+  // Each request's query row and first block id are loaded with its length (one round trip), then
+  // its decoder slot.
   const int nper = (a.num_reqs + 63) >> 6;  // groups of 64 requests in use (uniform)
-  int seql[kPlanLanes], nchl[kPlanLanes], qsll[kPlanLanes], blk0l[kPlanLanes];
+  int seql[kPlanLanes], nchl[kPlanLanes], qsll[kPlanLanes], blk0l[kPlanLanes], decl[kPlanLanes];
   int tot = 0, over = 0;
 #pragma unroll
   for (int i = 0; i < kPlanLanes; ++i) {
@@ -202,6 +203,10 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
       tot += seql[i];                         // host: num_reqs * max_seq < 2^31
     }
   }
+  // each request's decoder slot, requested now: its round trip overlaps the chunk search below
+#pragma unroll
+  for (int i = 0; i < kPlanLanes; ++i)
+    decl[i] = blk0l[i] >= 0 && blk0l[i] < a.num_blocks ? a.dec_map[blk0l[i]] : -1;
   tot = wave_sum_i(tot);
   const bool any_over = __builtin_amdgcn_ballot_w64(over) != 0;
   if (blockIdx.x == 0 && tid == 0 && any_over) atomicOr(a.err, TTKV_ERR_SEQ_LEN);
@@ -312,14 +317,14 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
       if (i < nper) bl += lane + 64 * i < r ? nchl[i] : 0;
     base = wave_sum_i(bl);
   }
-  int n_chunks = 0, seq = 0, qrow_r = 0, blk0 = -1;
+  int n_chunks = 0, seq = 0, qrow_r = 0, dslot = -1;
 #pragma unroll
   for (int i = 0; i < kPlanLanes; ++i) {
     if ((r >> 6) == i) {
       n_chunks = __builtin_amdgcn_readlane(nchl[i], r & 63);
       seq = __builtin_amdgcn_readlane(seql[i], r & 63);
       qrow_r = __builtin_amdgcn_readlane(qsll[i], r & 63);
-      blk0 = __builtin_amdgcn_readlane(blk0l[i], r & 63);
+      dslot = __builtin_amdgcn_readlane(decl[i], r & 63);
     }
   }
 
@@ -352,11 +357,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
     segv[k] = i < nseg ? a.bt[bt_row + bfirst + i] : -1;
   }
 
-  // Decoder slot via the device registry keyed by the request's first block, requested together
-  // with the first tile's block ids; the first tile's bytes follow with the decoder (bad block ids
-  // are flagged when the chunk's ids are staged)
-  int dslot = -1;
-  if (blk0 >= 0 && blk0 < a.num_blocks) dslot = a.dec_map[blk0];
+  // The first tile's bytes (bad block ids are flagged when the chunk's ids are staged); the
+  // decoder slot (the device registry keyed by the request's first block) came with the plan
   const int k_row_off = g.k_field + h * g.k_row;
   const int v_row_off = g.k_slot + h * g.v_row;
   // the rows' 64-byte windows (16-aligned; each row lies inside its window, host-checked)
