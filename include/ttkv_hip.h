@@ -254,7 +254,10 @@ int ttkv_dense_decode_paged(int32_t H, int32_t num_heads, int32_t d, float scale
  *   Carried at fp32 accuracy (hi + lo fp16 MFMA operands).
  * ttkv_container_v_out: out [B, num_heads, d] fp32 += sum_i p[b, p, i] * V[b, h, i, :];
  *   p[b, p, i] at p + b*p_batch_stride + p*p_head_stride + i. `out` must be zero-filled: the
- *   launch accumulates tile partials with atomic adds (the codec kernel's contract).
+ *   launch accumulates tile partials with atomic adds (the codec kernel's contract). Carried at
+ *   fp32 accuracy (MFMA on exact integer codes against p * row scale split hi + lo in fp16 after
+ *   an exact 2^8 scaling), which needs |p * scale| < 256 for every token (beyond it the fp16
+ *   operand overflows and the output reads inf / NaN).
  * Built for d = 128, r1 <= 160, 3- or 4-bit rows of <= 48 packed bytes, num_heads / H in
  * {1, 2, 3, 4, 8}. */
 int ttkv_container_krt(int32_t H, int32_t num_heads, int32_t d, int32_t B, int32_t n, int32_t r1,

@@ -288,15 +288,21 @@ __global__ __launch_bounds__(kCThreads, 2) void container_krt_kernel(ContainerAr
 struct VoutSmem {
   uint32_t raw[kCVTile][kCRawDw];
   uint8_t code[kCVTile][kCCode];
-  float pw[2][8][kCVTile];  // p * ruler, double-buffered by tile parity
-  float part[4][8][kD];  // per-wave sums [wave][head][dim]
+  // p * ruler split hi + lo in fp16 (22 significant bits), [parity][head][token], double-buffered
+  // by tile parity: the P.V MFMA's B operand
+  _Float16 pwh[2][8][kCVTile];
+  _Float16 pwl[2][8][kCVTile];
   uint2 lut[256];
   uint32_t lut3[4096];
 };
 
 // 128-token tiles. The next tile's rows, rulers and weights are in registers while the current
-// tile decodes and accumulates. Accumulation: thread = (4 consecutive dims, 16 consecutive
-// tokens), so each code dword read serves 4 dims and each weight read 4 tokens.
+// tile decodes and accumulates. Accumulation on MFMA, as K1's P.V: O^T[dims, heads] +=
+// V^T[dims, tokens] * W^T[tokens, heads] with the codes as exact fp16 integers (c - 2^(b-1)), read
+// transposed from the decoded rows (ds_read_tr8_b64), and the weights w = p * ruler split hi + lo
+// in fp16 (two products) after an exact 2^8 scaling that keeps small weights out of the fp16
+// subnormals, so the sum keeps fp32-level accuracy. Wave w owns dims 16w.. and 64 + 16w.. for all
+// heads.
 template <int G, int BITS>
 __global__ __launch_bounds__(kCThreads, 2) void container_v_out_kernel(ContainerArgs a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -312,7 +318,7 @@ __global__ __launch_bounds__(kCThreads, 2) void container_v_out_kernel(Container
   const int tile1 = min(ntiles, tile0 + a.tiles_per_wg);
   if (tile0 >= tile1) return;
   const int ptok = tid >> 2, part = tid & 3;  // staging: tokens ptok and 64 + ptok, one quarter
-  const int dg = tid & 31, ph = tid >> 5;     // accumulation: dims 4dg.., tokens 16ph..
+  const int n = lane & 15, gq = lane >> 4;
   const int64_t row0 = ((int64_t)bz * a.H + hv) * a.n;
   const float* pb = a.p + (int64_t)bz * a.p_batch_stride + (int64_t)hv * G * a.p_head_stride;
 
@@ -337,15 +343,13 @@ __global__ __launch_bounds__(kCThreads, 2) void container_v_out_kernel(Container
   };
   fetch(tile0);
   build_luts(S.lut, BITS == 3 ? S.lut3 : nullptr, tid, kCThreads);
-  // 3-bit codes decode as fp8 (c - 4) * unit: the ruler takes the 1 / unit
-  const float rscale = BITS == 3 ? 1.0f / __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0] : 1.0f;
-  float acc[G][4], wsum[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    wsum[g] = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc[g][i] = 0.f;
-  }
+  // 3-bit codes: fp8 bytes of (c - 4) scaled back by 1 / unit to exact integers
+  const float inv_unit = 1.0f / __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0];
+  float4v oacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};  // O^T[dims][head n]
+  // transposed code reads: in each 16-lane group, lanes 2j, 2j+1 address the two 8-byte halves of
+  // row (token) 8gq + j of a 16-dim tile; lane n receives dim n of those 8 tokens
+  const int tr_tok = 8 * gq + (n >> 1);
+  const int tr_col = 8 * (n & 1);
 
   for (int tile = tile0; tile < tile1; ++tile) {
     // ---- commit the prefetched tile, then request the next one. The scaled weights are
@@ -358,8 +362,14 @@ __global__ __launch_bounds__(kCThreads, 2) void container_v_out_kernel(Container
 #pragma unroll
     for (int k = 0; k < kPw; ++k) {
       const int idx = tid + kCThreads * k;
-      if (idx < G * kCVTile)
-        S.pw[buf][idx / kCVTile][idx & (kCVTile - 1)] = pwv[k] * (rwv[k] * rscale);
+      if (idx < G * kCVTile) {
+        // scaled by 2^8 (exact) so that weights down to ~1e-6 stay fp16 normals; the sums are
+        // scaled back at the end. |p * ruler| must stay below 256 (fp16 range after scaling).
+        const float w = pwv[k] * rwv[k] * 256.0f;
+        const _Float16 hi = (_Float16)w;
+        S.pwh[buf][idx / kCVTile][idx & (kCVTile - 1)] = hi;
+        S.pwl[buf][idx / kCVTile][idx & (kCVTile - 1)] = (_Float16)(w - (float)hi);
+      }
     }
     if (tile + 1 < tile1) fetch(tile + 1);
     __syncthreads();
@@ -369,47 +379,61 @@ __global__ __launch_bounds__(kCThreads, 2) void container_v_out_kernel(Container
                              &S.code[tid >> 1][64 * (tid & 1)]);
     __builtin_amdgcn_s_setprio(0);
     __syncthreads();
-    // ---- acc[g][i] += (p[g][tok] * ruler[tok]) * code[tok][4dg + i] over this thread's tokens
+    // ---- O^T += V^T W^T over the tile's 128 tokens, 32 per k-step
 #pragma unroll
-    for (int k4 = 0; k4 < 4; ++k4) {
-      const int t0 = 16 * ph + 4 * k4;
-      float4v pw4[G];
+    for (int kk = 0; kk < kCVTile / 32; ++kk) {
+      half8 bh = {}, bl = {};
+      if (n < G) {
+        bh = *(const half8*)&S.pwh[buf][n][32 * kk + 8 * gq];
+        bl = *(const half8*)&S.pwl[buf][n][32 * kk + 8 * gq];
+      }
 #pragma unroll
-      for (int g = 0; g < G; ++g) pw4[g] = *(const float4v*)&S.pw[buf][g][t0];
+      for (int mi = 0; mi < 2; ++mi) {
+        const uint8_t* src = &S.code[32 * kk + tr_tok][16 * (wv + 4 * mi) + tr_col];
+        typedef int v2i __attribute__((ext_vector_type(2)));
+        const v2i raw = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            (__attribute__((address_space(3))) v2i*)(src));
+        half8 av;
+        if constexpr (BITS == 3) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float v[4];
-        codes4<BITS>(*(const uint32_t*)&S.code[t0 + j][4 * dg], v);
+          for (int w = 0; w < 2; ++w) {
+            const half2v lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(raw[w], inv_unit, false);
+            const half2v hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(raw[w], inv_unit, true);
+            av[4 * w] = lo[0];
+            av[4 * w + 1] = lo[1];
+            av[4 * w + 2] = hi[0];
+            av[4 * w + 3] = hi[1];
+          }
+        } else {
+          // offset-binary code bytes c -> fp16 (c - 8), exact: 1024 + c from the byte placed
+          // under the fp16 exponent of 1024, minus 1032
+          const half2v bias = {(_Float16)1032.0f, (_Float16)1032.0f};
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-          const float w = pw4[g][j];
-          if constexpr (BITS == 4) wsum[g] += w;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[g][i] = fmaf(w, v[i], acc[g][i]);
+          for (int w = 0; w < 2; ++w) {
+            const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, (uint32_t)raw[w], 0x04010400u);
+            const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, (uint32_t)raw[w], 0x04030402u);
+            const half2v x0 = __builtin_bit_cast(half2v, lo) - bias;
+            const half2v x1 = __builtin_bit_cast(half2v, hi) - bias;
+            av[4 * w] = x0[0];
+            av[4 * w + 1] = x0[1];
+            av[4 * w + 2] = x1[0];
+            av[4 * w + 3] = x1[1];
+          }
         }
+        oacc[mi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bh, oacc[mi], 0, 0, 0);
+        oacc[mi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bl, oacc[mi], 0, 0, 0);
       }
     }
   }
-  // ---- 4-bit codes arrive as c: remove the 8 * sum(w) offset; sum the 8 token ranges
+  // ---- this workgroup's sums for its token range: lane (head n, gq) holds dims 4gq.. of each of
+  // the wave's two 16-dim tiles
+  if (n < G) {
+    float* ob = &a.o[((int64_t)bz * a.H * G + hv * G + n) * kD];
 #pragma unroll
-  for (int g = 0; g < G; ++g)
+    for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float t = acc[g][i] - (BITS == 4 ? 8.f * wsum[g] : 0.f);
-      t += __shfl_xor(t, 32);
-      acc[g][i] = t;
-    }
-  if (lane < 32) {
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-      *(float4v*)&S.part[wv][g][4 * dg] = float4v{acc[g][0], acc[g][1], acc[g][2], acc[g][3]};
-  }
-  __syncthreads();
-  if (tid < kD) {
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-      atomicAdd(&a.o[((int64_t)bz * a.H * G + hv * G + g) * kD + tid],
-                (S.part[0][g][tid] + S.part[1][g][tid]) + (S.part[2][g][tid] + S.part[3][g][tid]));
+      for (int i = 0; i < 4; ++i)
+        atomicAdd(&ob[16 * (wv + 4 * mi) + 4 * gq + i], oacc[mi][i] * (1.0f / 256.0f));
   }
 }
 
@@ -420,10 +444,12 @@ __global__ __launch_bounds__(kCThreads, 2) void container_v_out_kernel(Container
 
 namespace ttkv {
 
-// Token tiles per workgroup: about one round of two resident workgroups per CU over the
-// (sequence, head) pairs, so each workgroup builds its tables and decoder fragments once.
-static int tiles_per_wg(int ntiles, int pairs) {
-  const int target = 2 * device_cu_count();
+// Token tiles per workgroup: about one round of `per_cu` resident workgroups per CU over the
+// (sequence, head) pairs, so each workgroup builds its tables and decoder fragments once. krt
+// holds two per CU; v_out (52.5 KB of LDS, < 128 VGPRs) three (8 x 14,402: 52.8 -> 45.6 us; four
+// do not fit the LDS and ran 62 us).
+static int tiles_per_wg(int ntiles, int pairs, int per_cu = 2) {
+  const int target = per_cu * device_cu_count();
   const int per_pair = std::max(1, target / std::max(pairs, 1));
   return std::max(1, (ntiles + per_pair - 1) / per_pair);
 }
@@ -555,7 +581,7 @@ int container_v_out(int H, int HQ, int d, int B, int n, const float* p, int64_t 
   a.p_head_stride = p_head_stride;
   a.p_batch_stride = p_batch_stride;
   a.o = o;
-  a.tiles_per_wg = tiles_per_wg((n + kCVTile - 1) / kCVTile, H * B);
+  a.tiles_per_wg = tiles_per_wg((n + kCVTile - 1) / kCVTile, H * B, 3);
   const dim3 grid(((n + kCVTile - 1) / kCVTile + a.tiles_per_wg - 1) / a.tiles_per_wg, H, B);
   return bits == 4 ? vout_g<4>(a, grid, st) : vout_g<3>(a, grid, st);
 }
