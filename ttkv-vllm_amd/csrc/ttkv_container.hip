@@ -98,7 +98,7 @@ struct KrtSmem {
   uint8_t code[kCTile][kCCode];
   float spart[4][kCTile][8];
   uint2 lut[256];
-  uint32_t lut3[4096];
+  uint16_t lut3[kLut3Entries];
   float cs[kCTile], kr[kCTile];
 };
 
@@ -293,7 +293,7 @@ struct VoutSmem {
   _Float16 pwh[2][8][kCVTile];
   _Float16 pwl[2][8][kCVTile];
   uint2 lut[256];
-  uint32_t lut3[4096];
+  uint16_t lut3[kLut3Entries];
 };
 
 // 128-token tiles. The next tile's rows, rulers and weights are in registers while the current
@@ -446,8 +446,9 @@ namespace ttkv {
 
 // Token tiles per workgroup: about one round of `per_cu` resident workgroups per CU over the
 // (sequence, head) pairs, so each workgroup builds its tables and decoder fragments once. krt
-// holds two per CU; v_out (52.5 KB of LDS, < 128 VGPRs) three (8 x 14,402: 52.8 -> 45.6 us; four
-// do not fit the LDS and ran 62 us).
+// holds three per CU up to r1 = 128 (41 KB of LDS, <= 164 VGPRs; 8 x 14,402 at r1 = 110:
+// 158 -> 138 us against two), two above; v_out (37 KB, < 128 VGPRs) four (its kernel 38.8 us,
+// the same as three per CU with the 16 KB four-code table).
 static int tiles_per_wg(int ntiles, int pairs, int per_cu = 2) {
   const int target = per_cu * device_cu_count();
   const int per_pair = std::max(1, target / std::max(pairs, 1));
@@ -539,7 +540,7 @@ int container_krt(int H, int HQ, int d, int B, int n, int r1, const int8_t* cq, 
   a.sinv = sinv;
   a.q = q;
   a.s = s;
-  a.tiles_per_wg = tiles_per_wg((n + kCTile - 1) / kCTile, H * B);
+  a.tiles_per_wg = tiles_per_wg((n + kCTile - 1) / kCTile, H * B, ks <= 4 ? 3 : 2);
   const dim3 grid(((n + kCTile - 1) / kCTile + a.tiles_per_wg - 1) / a.tiles_per_wg, H, B);
   // without residual rows the staged bitmaps are zero and the 3-bit decode contributes 0
   return (has_res && bits == 4) ? krt_g<4>(a, ks, grid, st) : krt_g<3>(a, ks, grid, st);
@@ -581,7 +582,7 @@ int container_v_out(int H, int HQ, int d, int B, int n, const float* p, int64_t 
   a.p_head_stride = p_head_stride;
   a.p_batch_stride = p_batch_stride;
   a.o = o;
-  a.tiles_per_wg = tiles_per_wg((n + kCVTile - 1) / kCVTile, H * B, 3);
+  a.tiles_per_wg = tiles_per_wg((n + kCVTile - 1) / kCVTile, H * B, 4);
   const dim3 grid(((n + kCVTile - 1) / kCVTile + a.tiles_per_wg - 1) / a.tiles_per_wg, H, B);
   return bits == 4 ? vout_g<4>(a, grid, st) : vout_g<3>(a, grid, st);
 }

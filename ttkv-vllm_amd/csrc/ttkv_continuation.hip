@@ -89,7 +89,7 @@ struct ExpandSmem {
   uint8_t kcode[kXTile][kXCode];       // decode -> recon
   uint8_t vcode[kXTile][kXCode];       // decode -> transpose
   uint2 lut[256];
-  uint32_t lut3[4096];
+  uint16_t lut3[kLut3Entries];
   int32_t seg[kXSeg];
   float cs[kXTile], krul[kXTile], vrul[kXTile];
 };

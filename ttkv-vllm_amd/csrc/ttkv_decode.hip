@@ -10,7 +10,7 @@
 //             fp16); this head's K and V rows realigned, the code streams byte-reversed per dword
 //             (one v_perm each) so that a code window is one v_alignbit.
 //   decode  : one thread per half row. Per bitmap byte, the next 8 codes are spread one per byte
-//             through a 4096-entry table (3-bit) or nibble perms (4-bit) and scattered onto their
+//             through a 64-entry two-code table (3-bit) or nibble perms (4-bit) and scattered onto their
 //             lanes with one v_perm driven by a 256-entry selector table (both tables built in
 //             LDS by the workgroup at start). 3-bit codes come out as
 //             fp8 bytes of the signed value c - 4 (0 outside the bitmap), which the arithmetic
@@ -104,7 +104,7 @@ struct DecodeSmem {
   float spart[kWaves][kTile][kSP];  // per wave partial q.k [wave][token][head]
   _Float16 pw[kWaves][G][kTile];    // per wave P' = P * ruler_v (fp16), the P.V B operand
   uint2 lut[256];
-  uint32_t lut3[4096];
+  uint16_t lut3[kLut3Entries];
   int32_t seg[kSegMax];
   float cs[kTile];  // coefficient ruler
   float kr[kTile];  // K residual ruler / (cs * unit)

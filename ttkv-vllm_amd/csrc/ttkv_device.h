@@ -319,14 +319,18 @@ __device__ __forceinline__ uint32_t staged_u16(const uint32_t* row, int rb) {
 
 // The decode tables, built in LDS by the workgroup itself (a few hundred VALU operations per
 // thread, no memory traffic at kernel start):
-//   lut3[x]  (3-bit codes): x = 12 bits holding 4 codes, the first in the top 3 bits -> the 4
-//            codes as fp8 signed bytes (c - 4), first code in byte 0. The byte map c -> fp8(c - 4)
-//            is one v_perm over the 8-byte table {84 83 82 81 00 01 02 03}.
+//   lut3[x]  (3-bit codes): x = 6 bits holding 2 codes, the first in the top 3 bits -> the 2
+//            codes as fp8 signed bytes (c - 4), first code in the low byte. The byte map
+//            c -> fp8(c - 4) is one v_perm over the 8-byte table {84 83 82 81 00 01 02 03}. The
+//            64 entries fill 32 dwords, one per bank, so any gather by a wave is conflict-free
+//            (a 4096-entry table of 4-code entries takes half the lookups but ~4x the bank
+//            passes per lookup, and 16 KB of LDS).
 //   lut[B]   selectors that move the byte-spread codes of bitmap byte B (MSB = first lane) onto its
 //            set lanes: lane k gets the rank of its bit among B's set bits, 0x0c (zero) if unset.
-__device__ __forceinline__ uint32_t lut3_entry(uint32_t x) {
-  const uint32_t c = (x >> 9) | (((x >> 6) & 7u) << 8) | (((x >> 3) & 7u) << 16) | ((x & 7u) << 24);
-  return __builtin_amdgcn_perm(0x03020100u, 0x81828384u, c);
+constexpr int kLut3Entries = 64;
+__device__ __forceinline__ uint16_t lut3_entry(uint32_t x) {
+  const uint32_t c = (x >> 3) | ((x & 7u) << 8);
+  return (uint16_t)__builtin_amdgcn_perm(0x03020100u, 0x81828384u, c);
 }
 __device__ __forceinline__ uint2 scatter_entry(uint32_t B) {
   uint32_t s0 = 0, s1 = 0;
@@ -340,16 +344,10 @@ __device__ __forceinline__ uint2 scatter_entry(uint32_t B) {
   }
   return make_uint2(s0, s1);
 }
-__device__ __forceinline__ void build_luts(uint2* lut, uint32_t* lut3, int tid, int nthreads) {
+__device__ __forceinline__ void build_luts(uint2* lut, uint16_t* lut3, int tid, int nthreads) {
   for (int i = tid; i < 256; i += nthreads) lut[i] = scatter_entry((uint32_t)i);
-  if (lut3) {
-    for (int i = tid; i < 1024; i += nthreads) {
-      u32x4 e;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) e[k] = lut3_entry((uint32_t)(4 * i + k));
-      ((u32x4*)lut3)[i] = e;
-    }
-  }
+  if (lut3)
+    for (int i = tid; i < kLut3Entries; i += nthreads) lut3[i] = lut3_entry((uint32_t)i);
 }
 
 // Decode the 32 lanes of bitmap dword `bm` of one big-endian staged head row (code stream at
@@ -361,7 +359,7 @@ __device__ __forceinline__ void build_luts(uint2* lut, uint32_t* lut3, int tid, 
 // bp-1 and bp+31 (shift (-bp) mod 32; word -1 is the last bitmap dword, read but unused).
 template <int BITS>
 __device__ __forceinline__ void decode_dword_be(const uint32_t* st, uint32_t bm, int& rank,
-                                                const uint2* lut, const uint32_t* lut3,
+                                                const uint2* lut, const uint16_t* lut3,
                                                 uint8_t* dst) {
   uint32_t B[4];
   int bp[4];
@@ -383,8 +381,8 @@ __device__ __forceinline__ void decode_dword_be(const uint32_t* st, uint32_t bm,
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     if constexpr (BITS == 3) {
-      e0[m] = lut3[w[m] >> 20];
-      e1[m] = lut3[(w[m] >> 8) & 0xfffu];
+      e0[m] = (uint32_t)lut3[w[m] >> 26] | ((uint32_t)lut3[(w[m] >> 20) & 63u] << 16);
+      e1[m] = (uint32_t)lut3[(w[m] >> 14) & 63u] | ((uint32_t)lut3[(w[m] >> 8) & 63u] << 16);
     } else {
       spread8<4>(w[m] ^ 0x88888888u, e0[m], e1[m]);
     }
@@ -406,7 +404,7 @@ __device__ __forceinline__ void decode_dword_be(const uint32_t* st, uint32_t bm,
 // dwords 4.. the code stream) into one byte per lane at dst[0..63].
 template <int BITS>
 __device__ __forceinline__ void decode_half_row_be(const uint32_t* row, int half, const uint2* lut,
-                                                   const uint32_t* lut3, uint8_t* dst) {
+                                                   const uint16_t* lut3, uint8_t* dst) {
   const uint32_t bm0 = row[2 * half], bm1 = row[2 * half + 1];
   int rank = half ? __builtin_popcount(row[0]) + __builtin_popcount(row[1]) : 0;
   decode_dword_be<BITS>(row + 4, bm0, rank, lut, lut3, dst);
@@ -416,7 +414,7 @@ __device__ __forceinline__ void decode_half_row_be(const uint32_t* row, int half
 // Decode dims [32*qr, 32*qr+32) of one staged head row into dst[0..31] (four threads per row).
 template <int BITS>
 __device__ __forceinline__ void decode_quarter_row_be(const uint32_t* row, int qr,
-                                                      const uint2* lut, const uint32_t* lut3,
+                                                      const uint2* lut, const uint16_t* lut3,
                                                       uint8_t* dst) {
   int rank = 0;
 #pragma unroll

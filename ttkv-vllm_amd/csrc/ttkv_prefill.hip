@@ -97,7 +97,7 @@ struct PrefillSmem {
   uint8_t vcode[kPTile][kPCode];  // decode -> transpose
   _Float16 vt[kD][kVtStride];     // transpose -> P.V
   uint2 lut[256];
-  uint32_t lut3[4096];
+  uint16_t lut3[kLut3Entries];
   int32_t seg[kPSeg];
   float cs[kPTile], krul[kPTile], vrul[kPTile];
   int is_last;
