@@ -98,7 +98,6 @@ struct KrtSmem {
   uint8_t code[kCTile][kCCode];
   float spart[4][kCTile][8];
   uint2 lut[256];
-  uint16_t lut3[kLut3Entries];
   float cs[kCTile], kr[kCTile];
 };
 
@@ -106,6 +105,7 @@ struct KrtSmem {
 template <int G, int BITS, int KS>
 __global__ __launch_bounds__(kCThreads, 2) void container_krt_kernel(ContainerArgs a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
+  __shared__ uint16_t lut3s[kLut3Entries];  // static: its address folds into the loads
   KrtSmem<KS>& S = *reinterpret_cast<KrtSmem<KS>*>(smem_raw);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -121,7 +121,7 @@ __global__ __launch_bounds__(kCThreads, 2) void container_krt_kernel(ContainerAr
   const int tile1 = min(ntiles, tile0 + a.tiles_per_wg);
   if (tile0 >= tile1) return;
 
-  build_luts(S.lut, BITS == 3 ? S.lut3 : nullptr, tid, kCThreads);
+  build_luts(S.lut, BITS == 3 ? lut3s : nullptr, tid, kCThreads);
   // ---- decoder fragments (A operand, M = dims, K = r1), hi + lo fp16, resident in registers
   const float* dec = a.dec + (a.dec_per_seq ? (int64_t)bz * a.r1 * HD : 0) + (int64_t)hv * kD;
   half8 ahi[2][KS], alo[2][KS];
@@ -221,7 +221,7 @@ __global__ __launch_bounds__(kCThreads, 2) void container_krt_kernel(ContainerAr
     // reconstruction run at raised wave priority: the co-resident workgroup's commit and
     // read-out fill the issue slots they leave.
     __builtin_amdgcn_s_setprio(1);
-    decode_quarter_row_be<BITS>(S.raw[ptok], part, S.lut, S.lut3, &S.code[ptok][32 * part]);
+    decode_quarter_row_be<BITS>(S.raw[ptok], part, S.lut, lut3s, &S.code[ptok][32 * part]);
     __syncthreads();
 
     // ---- reconstruct + residual + RoPE + scores, 16 tokens at a time. The pair (j, j + 64)
@@ -293,7 +293,6 @@ struct VoutSmem {
   _Float16 pwh[2][8][kCVTile];
   _Float16 pwl[2][8][kCVTile];
   uint2 lut[256];
-  uint16_t lut3[kLut3Entries];
 };
 
 // 128-token tiles. The next tile's rows, rulers and weights are in registers while the current
@@ -306,6 +305,7 @@ struct VoutSmem {
 template <int G, int BITS>
 __global__ __launch_bounds__(kCThreads, 2) void container_v_out_kernel(ContainerArgs a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
+  __shared__ uint16_t lut3s[kLut3Entries];  // static: its address folds into the loads
   VoutSmem& S = *reinterpret_cast<VoutSmem*>(smem_raw);
   constexpr int kPw = (G * kCVTile + kCThreads - 1) / kCThreads;  // weights per thread per tile
   const int tid = threadIdx.x;
@@ -342,7 +342,7 @@ __global__ __launch_bounds__(kCThreads, 2) void container_v_out_kernel(Container
     }
   };
   fetch(tile0);
-  build_luts(S.lut, BITS == 3 ? S.lut3 : nullptr, tid, kCThreads);
+  build_luts(S.lut, BITS == 3 ? lut3s : nullptr, tid, kCThreads);
   // 3-bit codes: fp8 bytes of (c - 4) scaled back by 1 / unit to exact integers
   const float inv_unit = 1.0f / __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0];
   float4v oacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};  // O^T[dims][head n]
@@ -375,7 +375,7 @@ __global__ __launch_bounds__(kCThreads, 2) void container_v_out_kernel(Container
     __syncthreads();
     // ---- decode (thread = token tid/2, half tid&1), at raised wave priority
     __builtin_amdgcn_s_setprio(1);
-    decode_half_row_be<BITS>(S.raw[tid >> 1], tid & 1, S.lut, S.lut3,
+    decode_half_row_be<BITS>(S.raw[tid >> 1], tid & 1, S.lut, lut3s,
                              &S.code[tid >> 1][64 * (tid & 1)]);
     __builtin_amdgcn_s_setprio(0);
     __syncthreads();

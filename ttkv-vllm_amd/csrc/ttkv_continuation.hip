@@ -89,7 +89,6 @@ struct ExpandSmem {
   uint8_t kcode[kXTile][kXCode];       // decode -> recon
   uint8_t vcode[kXTile][kXCode];       // decode -> transpose
   uint2 lut[256];
-  uint16_t lut3[kLut3Entries];
   int32_t seg[kXSeg];
   float cs[kXTile], krul[kXTile], vrul[kXTile];
 };
@@ -97,6 +96,7 @@ struct ExpandSmem {
 template <int RB, int VB, int KSTEPS>
 __global__ __launch_bounds__(kXThreads, 2) void expand_kernel(ExpandArgs a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
+  __shared__ uint16_t lut3s[kLut3Entries];  // static: its address folds into the loads
   ExpandSmem<KSTEPS>& S = *reinterpret_cast<ExpandSmem<KSTEPS>*>(smem_raw);
   const Geom& g = a.g;
   const int tid = threadIdx.x;
@@ -131,7 +131,7 @@ __global__ __launch_bounds__(kXThreads, 2) void expand_kernel(ExpandArgs a) {
     return;
   }
 
-  build_luts(S.lut, (RB == 3 || VB == 3) ? S.lut3 : nullptr, tid, kXThreads);
+  build_luts(S.lut, (RB == 3 || VB == 3) ? lut3s : nullptr, tid, kXThreads);
 
   // decoder fragments (A operand, M = dims), hi + lo fp16, resident in registers
   const int HD = g.H * kD;
@@ -230,7 +230,7 @@ __global__ __launch_bounds__(kXThreads, 2) void expand_kernel(ExpandArgs a) {
       const int half = tid & 1;
       if (kind == 0) {
         const uint32_t* row = S.rawk[key];
-        decode_half_row_be<RB>(row, half, S.lut, S.lut3, &S.kcode[key][64 * half]);
+        decode_half_row_be<RB>(row, half, S.lut, lut3s, &S.kcode[key][64 * half]);
         if (half == 0) {
           // 3-bit codes come out as fp8 (c - 4) * unit: the ruler takes the 1 / unit
           const float kr = f16_bits_to_float(staged_u16(row, kBitmapBytes + g.k_pb));
@@ -238,7 +238,7 @@ __global__ __launch_bounds__(kXThreads, 2) void expand_kernel(ExpandArgs a) {
         }
       } else {
         const uint32_t* row = S.rawv[key];
-        decode_half_row_be<VB>(row, half, S.lut, S.lut3, &S.vcode[key][64 * half]);
+        decode_half_row_be<VB>(row, half, S.lut, lut3s, &S.vcode[key][64 * half]);
         if (half == 0)
           S.vrul[key] = key < ntile ? f16_bits_to_float(staged_u16(row, kBitmapBytes + g.v_pb)) : 0.f;
       }

@@ -104,7 +104,6 @@ struct DecodeSmem {
   float spart[kWaves][kTile][kSP];  // per wave partial q.k [wave][token][head]
   _Float16 pw[kWaves][G][kTile];    // per wave P' = P * ruler_v (fp16), the P.V B operand
   uint2 lut[256];
-  uint16_t lut3[kLut3Entries];
   int32_t seg[kSegMax];
   float cs[kTile];  // coefficient ruler
   float kr[kTile];  // K residual ruler / (cs * unit)
@@ -163,6 +162,7 @@ __device__ __forceinline__ void combine_regs(const float* pbase, int64_t cstride
 template <int G, int RB, int VB, int KU, bool QLO>
 __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
+  __shared__ uint16_t lut3s[kLut3Entries];  // static: its address folds into the loads
   using Smem = DecodeSmem<KU, G>;
   Smem& S = *reinterpret_cast<Smem*>(smem_raw);
   constexpr int KSTEPS = KU / 2;  // k = 32 steps
@@ -415,7 +415,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   }
 
   // ---- code tables, and this chunk's block ids
-  build_luts(S.lut, (RB == 3 || VB == 3) ? S.lut3 : nullptr, tid, kThreads);
+  build_luts(S.lut, (RB == 3 || VB == 3) ? lut3s : nullptr, tid, kThreads);
 #pragma unroll
   for (int k = 0; k < kSegPer; ++k) {
     const int i = tid + kThreads * k;
@@ -556,7 +556,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
       const int half = tid & 1;
       if (kind == 0) {
         const uint32_t* row = S.rawk[tok];
-        decode_half_row_be<RB>(row, half, S.lut, S.lut3, &S.kcode[tok][64 * half]);
+        decode_half_row_be<RB>(row, half, S.lut, lut3s, &S.kcode[tok][64 * half]);
         if (half == 0) {
           const float kr = f16_bits_to_float(staged_u16(row, kBitmapBytes + g.k_pb));
           const float cs = S.cs[tok];
@@ -565,7 +565,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
         }
       } else {
         const uint32_t* row = S.rawv[tok];
-        decode_half_row_be<VB>(row, half, S.lut, S.lut3, &S.vcode[tok][64 * half]);
+        decode_half_row_be<VB>(row, half, S.lut, lut3s, &S.vcode[tok][64 * half]);
         if (half == 0)
           S.vr[tok] = f16_bits_to_float(staged_u16(row, kBitmapBytes + g.v_pb));
       }

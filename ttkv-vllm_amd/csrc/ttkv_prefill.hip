@@ -97,7 +97,6 @@ struct PrefillSmem {
   uint8_t vcode[kPTile][kPCode];  // decode -> transpose
   _Float16 vt[kD][kVtStride];     // transpose -> P.V
   uint2 lut[256];
-  uint16_t lut3[kLut3Entries];
   int32_t seg[kPSeg];
   float cs[kPTile], krul[kPTile], vrul[kPTile];
   int is_last;
@@ -107,6 +106,7 @@ template <int G, int RB, int VB, int KSTEPS, bool SCORES>
 __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) void prefill_paged_kernel(PrefillArgs a) {
   constexpr bool EXACT = true;  // see the precision note at the top
   extern __shared__ __align__(16) unsigned char smem_raw[];
+  __shared__ uint16_t lut3s[kLut3Entries];  // static: its address folds into the loads
   PrefillSmem<KSTEPS, EXACT>& S = *reinterpret_cast<PrefillSmem<KSTEPS, EXACT>*>(smem_raw);
   const Geom& g = a.g;
   const int tid = threadIdx.x;
@@ -177,7 +177,7 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
     return;
   }
 
-  build_luts(S.lut, (RB == 3 || VB == 3) ? S.lut3 : nullptr, tid, kPThreads);
+  build_luts(S.lut, (RB == 3 || VB == 3) ? lut3s : nullptr, tid, kPThreads);
 
   // ---- query fragments (B operand of S^T = Kp Q^T): column = query 16*wv + n of the block
   const int qj = qa + 16 * wv + n;
@@ -306,7 +306,7 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
       const int half = tid & 1;
       if (kind == 0) {
         const uint32_t* row = S.u.raw.k[key];
-        decode_half_row_be<RB>(row, half, S.lut, S.lut3, &S.kcode[key][64 * half]);
+        decode_half_row_be<RB>(row, half, S.lut, lut3s, &S.kcode[key][64 * half]);
         if (half == 0) {
           // 3-bit codes come out as fp8 (c - 4) * unit: the ruler takes the 1 / unit
           const float kr = f16_bits_to_float(staged_u16(row, kBitmapBytes + g.k_pb));
@@ -314,7 +314,7 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
         }
       } else {
         const uint32_t* row = S.u.raw.v[key];
-        decode_half_row_be<VB>(row, half, S.lut, S.lut3, &S.vcode[key][64 * half]);
+        decode_half_row_be<VB>(row, half, S.lut, lut3s, &S.vcode[key][64 * half]);
         if (half == 0)
           S.vrul[key] =
               key < ntile ? f16_bits_to_float(staged_u16(row, kBitmapBytes + g.v_pb)) : 0.f;
