@@ -8,8 +8,10 @@
 //   K2a expand : per (request, KV head, run of 64-key tiles): the commit / decode /
 //                reconstruction of the fused kernel, once per key. Each tile is written to the
 //                workspace as
-//                  khi, klo [64 keys][128 dims] fp16 -- the rotated key split hi + lo (its fp32
-//                                                       value to 22 significant bits)
+//                  khi, klo [64 keys][16 chunks][8] fp16 -- the rotated key split hi + lo (its
+//                                                       fp32 value to 22 significant bits); chunk c
+//                                                       holds dims 4c..4c+3 and 64+4c..64+4c+3
+//                                                       (tile_dims)
 //                  vt       [128 dims][64 keys] fp16 -- the V codes c - 2^(b-1), exact small
 //                                                       integers, keys in MFMA k-slot order
 //                  vrul     [64] fp32               -- the V row rulers
@@ -52,6 +54,11 @@ constexpr int kMaxParts = 48;             // key splits of one attend item (LDS 
 constexpr int kXRawDw = 16;
 constexpr int kXCode = 144;
 
+// tile_dims: the 16-byte chunk c of a workspace key row holds dims 4c..4c+3 then 64+4c..64+4c+3
+// -- exactly the 8 values one lane of the expand's reconstruction holds (dims dl..dl+3 and
+// 64+dl..64+dl+3, dl = 4c), so each lane writes one 16-byte chunk per half. A dot product over
+// all 128 dims does not depend on their order: the attend and scores kernels read the query's
+// dims in the same order into the matching B fragments.
 // Position of key k of a 64-key tile in the MFMA k-slot order of the P.V contraction: a 32-key
 // step's lane group g holds keys 4g..4g+3 and 16+4g..16+4g+3, stored as 8 consecutive slots.
 __host__ __device__ constexpr int vt_slot(int k) {
@@ -316,13 +323,14 @@ __global__ __launch_bounds__(kXThreads, 2) void expand_kernel(ExpandArgs a) {
         zl[i >> 1][i & 1] = (_Float16)(y1 - (float)h1);
         zh[i >> 1][i & 1] = (_Float16)(y2 - (float)h2);
       }
-      // khi / klo [key][dim]: dims dl..dl+3 and 64+dl..64+dl+3 of this key
-      auto* kh_out = gblw((u32x2v*)(tile_out + kTileKhi + key * kD * 2));
-      auto* kl_out = gblw((u32x2v*)(tile_out + kTileKlo + key * kD * 2));
-      kh_out[dl >> 2] = u32x2v{__builtin_bit_cast(uint32_t, yl[0]), __builtin_bit_cast(uint32_t, yl[1])};
-      kh_out[(64 + dl) >> 2] = u32x2v{__builtin_bit_cast(uint32_t, yh[0]), __builtin_bit_cast(uint32_t, yh[1])};
-      kl_out[dl >> 2] = u32x2v{__builtin_bit_cast(uint32_t, zl[0]), __builtin_bit_cast(uint32_t, zl[1])};
-      kl_out[(64 + dl) >> 2] = u32x2v{__builtin_bit_cast(uint32_t, zh[0]), __builtin_bit_cast(uint32_t, zh[1])};
+      // khi / klo [key][chunk]: this lane's dims dl..dl+3 and 64+dl..64+dl+3 are chunk dl / 4
+      // (tile_dims), one 16-byte store each
+      auto* kh_out = gblw((u32x4*)(tile_out + kTileKhi + key * kD * 2));
+      auto* kl_out = gblw((u32x4*)(tile_out + kTileKlo + key * kD * 2));
+      kh_out[dl >> 2] = u32x4{__builtin_bit_cast(uint32_t, yl[0]), __builtin_bit_cast(uint32_t, yl[1]),
+                              __builtin_bit_cast(uint32_t, yh[0]), __builtin_bit_cast(uint32_t, yh[1])};
+      kl_out[dl >> 2] = u32x4{__builtin_bit_cast(uint32_t, zl[0]), __builtin_bit_cast(uint32_t, zl[1]),
+                              __builtin_bit_cast(uint32_t, zh[0]), __builtin_bit_cast(uint32_t, zh[1])};
     }
     __builtin_amdgcn_s_setprio(0);
     __syncthreads();  // coef / kcode / vcode / rulers are overwritten by the next tile
@@ -471,14 +479,16 @@ __global__ __launch_bounds__(kAThreads, 2) void attend_kernel(AttendArgs a) {
   half8 qf[G][4];
   {
     const bool qvec = act_rows_aligned(a.q, a.q_dtype, a.q_row_stride);
+    // k-step ks, lane group gq: the dims of key chunk 4 ks + gq (tile_dims)
     const int64_t qrow = (int64_t)(q0 + (qvalid ? qj : qa)) * a.q_row_stride + (int64_t)h * G * kD +
-                         8 * gq;
+                         4 * gq;
 #pragma unroll
     for (int gg = 0; gg < G; ++gg)
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         float tq[8];
-        load_act_n<8>(a.q, a.q_dtype, qrow + (int64_t)gg * kD + 32 * ks, qvec, tq);
+        load_act_n<4>(a.q, a.q_dtype, qrow + (int64_t)gg * kD + 16 * ks, qvec, tq);
+        load_act_n<4>(a.q, a.q_dtype, qrow + (int64_t)gg * kD + 64 + 16 * ks, qvec, tq + 4);
 #pragma unroll
         for (int i = 0; i < 8; ++i) qf[gg][ks][i] = qvalid ? (_Float16)tq[i] : (_Float16)0.0f;
       }
@@ -826,14 +836,16 @@ __global__ __launch_bounds__(kAThreads, 2) void scores_kernel(ScoresArgs a) {
   half8 qf[G][4];
   {
     const bool qvec = act_rows_aligned(a.q, a.q_dtype, a.q_row_stride);
+    // k-step ks, lane group gq: the dims of key chunk 4 ks + gq (tile_dims)
     const int64_t qrow = (int64_t)(q0 + (qvalid ? qj : qa)) * a.q_row_stride + (int64_t)h * G * kD +
-                         8 * gq;
+                         4 * gq;
 #pragma unroll
     for (int gg = 0; gg < G; ++gg)
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         float tq[8];
-        load_act_n<8>(a.q, a.q_dtype, qrow + (int64_t)gg * kD + 32 * ks, qvec, tq);
+        load_act_n<4>(a.q, a.q_dtype, qrow + (int64_t)gg * kD + 16 * ks, qvec, tq);
+        load_act_n<4>(a.q, a.q_dtype, qrow + (int64_t)gg * kD + 64 + 16 * ks, qvec, tq + 4);
 #pragma unroll
         for (int i = 0; i < 8; ++i) qf[gg][ks][i] = qvalid ? (_Float16)tq[i] : (_Float16)0.0f;
       }
