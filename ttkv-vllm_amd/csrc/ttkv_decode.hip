@@ -560,7 +560,9 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
         if (half == 0) {
           const float kr = f16_bits_to_float(staged_u16(row, kBitmapBytes + g.k_pb));
           const float cs = S.cs[tok];
-          S.kr[tok] = cs != 0.f ? kr * inv_unit_k / cs : 0.f;
+          // the hardware reciprocal (1 ulp) instead of an IEEE divide: this phase's K-row waves
+          // are the ones the V-row waves wait for at the next barrier
+          S.kr[tok] = cs != 0.f ? kr * inv_unit_k * __builtin_amdgcn_rcpf(cs) : 0.f;
           S.f[tok] = cs * a.scale_log2;
         }
       } else {
