@@ -560,8 +560,9 @@ __global__ __launch_bounds__(kAThreads, 2) void attend_kernel(AttendArgs a) {
     half8 pb[G];
 #pragma unroll
     for (int gg = 0; gg < G; ++gg) {
-      float mt = fmaxf(fmaxf(fmaxf(sacc[0][gg][0], sacc[0][gg][1]), fmaxf(sacc[0][gg][2], sacc[0][gg][3])),
-                       fmaxf(fmaxf(sacc[1][gg][0], sacc[1][gg][1]), fmaxf(sacc[1][gg][2], sacc[1][gg][3])));
+      const float m01 = max3_mfma(sacc[0][gg][0], sacc[0][gg][1], sacc[0][gg][2]);
+      const float m23 = max3_mfma(sacc[0][gg][3], sacc[1][gg][0], sacc[1][gg][1]);
+      float mt = max3_mfma(m01, m23, max3_mfma(sacc[1][gg][2], sacc[1][gg][3], sacc[1][gg][3]));
       mt *= sl2;
       // Lazy rescaling: the reference point moves only when a column max grows by more than 2^8
       // (p <= 256 otherwise), which is rare after a column's first tile, so the column max and

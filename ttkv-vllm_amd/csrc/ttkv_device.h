@@ -167,6 +167,15 @@ __device__ __forceinline__ void stage_row_w(const u32x4& mine, int m4, uint32_t 
 // which is far below fp32 resolution of the sums they join; -inf gives 0.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// max(a, b, c) in one v_max3_f32. fmaxf chains compile to v_max with every operand first
+// quieted (v_max_f32 x, x, x) because the compiler cannot rule out signalling NaNs; MFMA results
+// are never signalling NaNs, so the callers skip that.
+__device__ __forceinline__ float max3_mfma(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 // Cross-lane helpers on DPP and the gfx950 permlane swaps (VALU ops, no LDS round trip).
 __device__ __forceinline__ int dpp_i(int iv, int ctrl_sel) {
   switch (ctrl_sel) {  // dpp control must be a constant
