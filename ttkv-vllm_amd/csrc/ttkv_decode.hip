@@ -98,17 +98,18 @@ struct DecodeSmem {
   static constexpr int kSP = G <= 4 ? 4 : 8;           // score slots per token
   _Float16 coef[kTile][kCoefStride];
   uint32_t rawk[kTile][kRawDw];
+  uint32_t rawgap[16];  // V rows 16 dwords off: a wave's K and V rows of one token on other banks
   uint32_t rawv[kTile][kRawDw];
   uint8_t kcode[kTile][kCodeStride];
-  uint8_t vcode[kTile][kCodeStride];
+  uint8_t vcode[2][kTile][kCodeStride];  // by tile parity: the next tile's decode runs beside P.V
   float spart[kWaves][kTile][kSP];  // per wave partial q.k [wave][token][head]
   _Float16 pw[kWaves][G][kTile];    // per wave P' = P * ruler_v (fp16), the P.V B operand
   uint2 lut[256];
   int32_t seg[kSegMax];
   float cs[kTile];  // coefficient ruler
   float kr[kTile];  // K residual ruler / (cs * unit)
-  float vr[kTile];  // V ruler
-  float f[kTile];   // cs * scale * log2(e)
+  float vr[2][kTile];  // V ruler, by tile parity
+  float f[2][kTile];   // cs * scale * log2(e), by tile parity
   float m[G], l[G];
   int is_last;
 };
@@ -165,6 +166,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   __shared__ uint16_t lut3s[kLut3Entries];  // static: its address folds into the loads
   using Smem = DecodeSmem<KU, G>;
   Smem& S = *reinterpret_cast<Smem*>(smem_raw);
+  static_assert(RB == VB, "K and V rows decode with one code path (3/3 and 4/4 are built)");
   constexpr int KSTEPS = KU / 2;  // k = 32 steps
   constexpr bool KTAIL = KU & 1;  // one more k = 16 step
   constexpr int kSP = Smem::kSP;
@@ -513,7 +515,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   };
   if constexpr (kAngle0Ahead) angle_row(t0, 0, cv0, sv0);
 
-  for (int tt = t0; tt < t1; tt += kTile) {
+  for (int tt = t0, tp = 0; tt < t1; tt += kTile, tp ^= 1) {
     const int ntile = min(kTile, t1 - tt);
     // the next tile's slot address first: its block-id read overlaps the commit
     const uint8_t* next_base = tt + kTile < t1 ? slot_base(tt + kTile) : nullptr;
@@ -539,7 +541,13 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
       stage_row_w(P.krow, (k_row_off & 15) >> 2, ksel, &S.rawk[ptok][part * 4]);
       stage_row_w(P.vrow, (v_row_off & 15) >> 2, vsel, &S.rawv[ptok][part * 4]);
     }
-    __syncthreads();
+    // No barrier: wave w commits and decodes the same 16 tokens (16w .. 16w+15), and LDS
+    // accesses of one wave complete in order (the fences only keep the compiler from moving
+    // them). The buffers this tile writes are free: the previous tile's reconstruction read
+    // coef / kcode / kr before the last barrier, and its softmax and P.V read the other parity of
+    // vcode / vr / f.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // The next tile's slot bytes, requested as soon as the commit has freed P: they arrive during
     // the decode and reconstruction instead of stalling the next commit (measured: the bytes took
     // ~2k cycles, longer than the softmax and P.V they used to overlap). The reconstruction's
@@ -551,25 +559,25 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
     // priority for these two phases lets them run ahead (headline 172 -> 159 us, measured).
     __builtin_amdgcn_s_setprio(1);
     {
-      const int kind = tid >> 7;  // waves 0,1: K rows; waves 2,3: V rows
-      const int tok = (tid >> 1) & 63;
-      const int half = tid & 1;
-      if (kind == 0) {
-        const uint32_t* row = S.rawk[tok];
-        decode_half_row_be<RB>(row, half, S.lut, lut3s, &S.kcode[tok][64 * half]);
-        if (half == 0) {
-          const float kr = f16_bits_to_float(staged_u16(row, kBitmapBytes + g.k_pb));
+      // lanes 0..31: K rows, 32..63: V rows of this wave's 16 tokens, two threads per row; one
+      // decode call with per-lane row and destination (the two kinds share the code width)
+      const bool is_v = lane >= 32;
+      const int tok = 16 * wv + ((lane >> 1) & 15);
+      const int half = lane & 1;
+      const uint32_t* row = is_v ? S.rawv[tok] : S.rawk[tok];
+      uint8_t* dst = is_v ? &S.vcode[tp][tok][64 * half] : &S.kcode[tok][64 * half];
+      decode_half_row_be<RB>(row, half, S.lut, lut3s, dst);
+      if (half == 0) {
+        const float rul = f16_bits_to_float(staged_u16(row, kBitmapBytes + (is_v ? g.v_pb : g.k_pb)));
+        if (is_v) {
+          S.vr[tp][tok] = rul;
+        } else {
           const float cs = S.cs[tok];
-          // the hardware reciprocal (1 ulp) instead of an IEEE divide: this phase's K-row waves
-          // are the ones the V-row waves wait for at the next barrier
-          S.kr[tok] = cs != 0.f ? kr * inv_unit_k * __builtin_amdgcn_rcpf(cs) : 0.f;
-          S.f[tok] = cs * a.scale_log2;
+          // the hardware reciprocal (1 ulp) instead of an IEEE divide, which would lengthen the
+          // K lanes' branch
+          S.kr[tok] = cs != 0.f ? rul * inv_unit_k * __builtin_amdgcn_rcpf(cs) : 0.f;
+          S.f[tp][tok] = cs * a.scale_log2;
         }
-      } else {
-        const uint32_t* row = S.rawv[tok];
-        decode_half_row_be<VB>(row, half, S.lut, lut3s, &S.vcode[tok][64 * half]);
-        if (half == 0)
-          S.vr[tok] = f16_bits_to_float(staged_u16(row, kBitmapBytes + g.v_pb));
       }
     }
     __syncthreads();
@@ -657,8 +665,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
     // ---------------------------------------------------------------- online softmax (every wave)
     {
       const bool valid = lane < ntile;
-      const float ft = S.f[lane];
-      const float vrt = S.vr[lane];
+      const float ft = S.f[tp][lane];
+      const float vrt = S.vr[tp][lane];
       float sum[kSP];
 #pragma unroll
       for (int i = 0; i < kSP; ++i) sum[i] = 0.f;
@@ -710,7 +718,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
       if (n < G) bp = *(const half8*)&S.pw[wv][n][32 * kk + 8 * gq];
 #pragma unroll
       for (int mi = 0; mi < 2; ++mi) {
-        const uint8_t* src = &S.vcode[32 * kk + tr_tok][16 * (wv + 4 * mi) + tr_col];
+        const uint8_t* src = &S.vcode[tp][32 * kk + tr_tok][16 * (wv + 4 * mi) + tr_col];
         typedef int v2i __attribute__((ext_vector_type(2)));
         const v2i raw = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
             (__attribute__((address_space(3))) v2i*)(src));
