@@ -51,7 +51,7 @@ constexpr int kTileVrul = 3 * kXTile * kD * 2;
 constexpr int kTileBytes = kTileVrul + kXTile * 4;  // 49,408
 constexpr int kTileChunks = kTileBytes / 16;        // 3088 16-byte chunks
 constexpr int kMaxParts = 48;             // key splits of one attend item (LDS weights)
-constexpr int kXRawDw = 16;
+constexpr int kXRawDw = 17;                // staged row dwords (16 + slack): odd, so rows spread over banks
 constexpr int kXCode = 144;
 
 // tile_dims: the 16-byte chunk c of a workspace key row holds dims 4c..4c+3 then 64+4c..64+4c+3
@@ -92,6 +92,7 @@ struct ExpandSmem {
   static constexpr int kCoefStride = KSTEPS * 32 + 8;
   _Float16 coef[kXTile][kCoefStride];  // commit -> recon
   uint32_t rawk[kXTile][kXRawDw];      // commit -> decode
+  uint32_t rawgap[16];                 // V rows 16 dwords off: a token's K and V rows on other banks
   uint32_t rawv[kXTile][kXRawDw];
   uint8_t kcode[kXTile][kXCode];       // decode -> recon
   uint8_t vcode[kXTile][kXCode];       // decode -> transpose
@@ -105,6 +106,7 @@ __global__ __launch_bounds__(kXThreads, 2) void expand_kernel(ExpandArgs a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   __shared__ uint16_t lut3s[kLut3Entries];  // static: its address folds into the loads
   ExpandSmem<KSTEPS>& S = *reinterpret_cast<ExpandSmem<KSTEPS>*>(smem_raw);
+  static_assert(RB == VB, "K and V rows decode with one code path (3/3 and 4/4 are built)");
   const Geom& g = a.g;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -228,26 +230,30 @@ __global__ __launch_bounds__(kXThreads, 2) void expand_kernel(ExpandArgs a) {
     }
     if (tt + kXTile < k1)
       fetch_raw_slot_w<2 * KSTEPS>(P, slot_base(tt + kXTile), part, g, k_win, v_win);
-    __syncthreads();
+    // No barrier: wave w commits and decodes the same 16 keys (16w .. 16w+15), and LDS accesses
+    // of one wave complete in order (the fences only keep the compiler from moving them); the
+    // previous tile's readers finished before its closing barrier.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     __builtin_amdgcn_s_setprio(1);
     // ------------------------------------------------------------ decode (thread = half row)
     {
-      const int kind = tid >> 7;
-      const int key = (tid >> 1) & 63;
-      const int half = tid & 1;
-      if (kind == 0) {
-        const uint32_t* row = S.rawk[key];
-        decode_half_row_be<RB>(row, half, S.lut, lut3s, &S.kcode[key][64 * half]);
-        if (half == 0) {
+      // lanes 0..31: K rows, 32..63: V rows of this wave's 16 keys, two threads per row; one
+      // decode call with per-lane row and destination (the two kinds share the code width)
+      const bool is_v = lane >= 32;
+      const int key = 16 * wv + ((lane >> 1) & 15);
+      const int half = lane & 1;
+      const uint32_t* row = is_v ? S.rawv[key] : S.rawk[key];
+      decode_half_row_be<RB>(row, half, S.lut, lut3s,
+                             is_v ? &S.vcode[key][64 * half] : &S.kcode[key][64 * half]);
+      if (half == 0) {
+        const float rul = f16_bits_to_float(staged_u16(row, kBitmapBytes + (is_v ? g.v_pb : g.k_pb)));
+        if (is_v) {
+          S.vrul[key] = key < ntile ? rul : 0.f;
+        } else {
           // 3-bit codes come out as fp8 (c - 4) * unit: the ruler takes the 1 / unit
-          const float kr = f16_bits_to_float(staged_u16(row, kBitmapBytes + g.k_pb));
-          S.krul[key] = RB == 3 ? kr * inv_unit : kr;
+          S.krul[key] = RB == 3 ? rul * inv_unit : rul;
         }
-      } else {
-        const uint32_t* row = S.rawv[key];
-        decode_half_row_be<VB>(row, half, S.lut, lut3s, &S.vcode[key][64 * half]);
-        if (half == 0)
-          S.vrul[key] = key < ntile ? f16_bits_to_float(staged_u16(row, kBitmapBytes + g.v_pb)) : 0.f;
       }
     }
     __syncthreads();
