@@ -153,7 +153,7 @@ int ttkv_write_paged(const ttkv_layout* lay, const void* key, int32_t k_dtype, i
 int64_t ttkv_write_workspace_bytes(const ttkv_layout* lay, int32_t num_tokens);
 
 /* Workspace bytes `ttkv_prefill_paged` needs for this batch shape: the split-K counters and
- * partials, and for chunks of more than 64 queries the expanded key tiles (49,408 B per request,
+ * partials, and for chunks of two or more queries the expanded key tiles (49,408 B per request,
  * KV head and 64 keys, at most 1 GiB per request slice); 0 when one key split covers every query
  * block of a fused launch. See the workspace note above ttkv_decode_workspace_bytes. */
 int64_t ttkv_prefill_workspace_bytes(const ttkv_layout* lay, int32_t num_heads, int32_t num_reqs,
@@ -168,11 +168,11 @@ int64_t ttkv_prefill_workspace_bytes(const ttkv_layout* lay, int32_t num_heads, 
  * stored keys (the chunk's own keys included, written before the read), p0 = n - Q:
  *   s[p, j, t] = scale * q[qsl[r]+j, p] . RoPE_t(K_pre[t]),   -inf where t > p0 + j
  *   out[qsl[r]+j, p] = sum_t softmax_t(s[p, j, :]) * V[h(p), t]
- * Chunks of more than 64 queries (G <= 3, r1 <= 128) run as two launches: every stored key is
+ * Chunks of two or more queries (G <= 3, r1 <= 128) run as two launches: every stored key is
  * decoded and reconstructed once into the workspace (rotated key hi + lo fp16, exact V codes, V
- * rulers), then flash attention on MFMA reads it for every 128-query block. Shorter chunks run one
- * fused launch that reconstructs each key tile once per 64-query block. Scores never leave the
- * chip.
+ * rulers), then flash attention on MFMA reads it for every 128-query block. Single queries (and
+ * G = 4, 8 or r1 > 128) run one fused launch that reconstructs each key tile once per 64-query
+ * block. Scores never leave the chip.
  * req_index    optional [num_reqs] int32: batch rows to process (block_table / seq_lens /
  *              query_start_loc are indexed by it); NULL = rows 0..num_reqs-1.
  * max_q_len / max_seq_len bound Q and n over the processed rows (they size the grid).
@@ -197,7 +197,7 @@ int ttkv_prefill_paged(const ttkv_layout* lay, int32_t num_heads, float scale,
  *   scores[p * s_head_stride + j * s_q_stride + t] = s[p, j, t]   fp32, -inf where t > p0 + j
  * for p < num_heads, j < Q, t < n. Reconstruction and rotated keys are carried at fp32 accuracy
  * (hi + lo fp16 MFMA operands); the query is taken as fp16. With a workspace of
- * ttkv_multi_scores_workspace_bytes (256-byte aligned; NULL / 0 allowed), a chunk of more than 64
+ * ttkv_multi_scores_workspace_bytes (256-byte aligned; NULL / 0 allowed), a chunk of two or more
  * queries is computed from every stored key expanded once; otherwise by the fused kernel. */
 int ttkv_multi_scores_paged(const ttkv_layout* lay, int32_t num_heads, float scale,
                             const void* query, int32_t q_dtype, int64_t q_row_stride,
@@ -211,7 +211,7 @@ int ttkv_multi_scores_paged(const ttkv_layout* lay, int32_t num_heads, float sca
                             int64_t s_head_stride, int64_t s_q_stride, void* workspace,
                             int64_t workspace_bytes, int32_t* error_word, ttkv_stream_t stream);
 
-/* Workspace bytes with which `ttkv_multi_scores_paged` computes a chunk of more than 64 queries
+/* Workspace bytes with which `ttkv_multi_scores_paged` computes a chunk of two or more queries
  * (G <= 3, r1 <= 128) from every stored key expanded once (49,408 B per KV head and 64 keys);
  * 0 when the chunk takes the fused kernel. With a NULL or smaller workspace the call runs the
  * fused kernel, with the same results. -1 for an invalid layout / head count. */

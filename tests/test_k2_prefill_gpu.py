@@ -67,7 +67,7 @@ def test_scores_mode_vs_raw_scores_multi(cfg, n, Q):
 
 @pytest.mark.parametrize("cfg,n,Q", [("safe", 2100, 257), ("campaign4x", 1030, 200)])
 def test_scores_from_expanded_keys_equal_the_fused_kernel(cfg, n, Q):
-    """A chunk of more than 64 queries with a workspace is scored from every stored key expanded
+    """A chunk of two or more queries with a workspace is scored from every stored key expanded
     once (expand launch + scores kernel); without one, by the fused kernel. Both reconstruct and
     rotate with the same fp32 arithmetic (up to the compiler's fma contraction, an ulp) and take
     the same fp16 MFMA operands, so the -inf pattern is identical and the finite scores agree to

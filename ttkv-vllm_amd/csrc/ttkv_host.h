@@ -61,7 +61,7 @@ int64_t write_workspace_bytes(const Geom& g, int num_tokens);
 namespace ttkv {
 int64_t prefill_workspace_bytes(const Geom& g, int G, int num_reqs, int max_q_len,
                                 int max_seq_len, int block_size);
-// The two-launch continuation read (expand + attend) for chunks of more than 64 queries.
+// The two-launch continuation read (expand + attend) for chunks of two or more queries.
 bool continuation_applies(const Geom& g, int G, int max_q_len);
 int64_t continuation_workspace_bytes(const Geom& g, int G, int num_reqs, int max_q_len,
                                      int max_seq_len);

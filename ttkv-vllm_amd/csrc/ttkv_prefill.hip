@@ -43,7 +43,7 @@ namespace ttkv {
 constexpr int kPTile = 64;      // keys per tile
 constexpr int kPQ = 64;         // queries per work item
 constexpr int kPThreads = 256;
-constexpr int kPRawDw = 16;     // dwords per staged head row
+constexpr int kPRawDw = 17;     // dwords per staged head row (16 + slack): odd, so rows spread over banks
 constexpr int kPCode = 144;     // bytes per code row
 constexpr int kKpStride = 136;  // halves per reconstructed key row (128 + 8)
 constexpr int kVtStride = 72;   // halves per transposed V row (64 keys + 8)
@@ -89,6 +89,7 @@ struct PrefillSmem {
   union {
     struct {
       uint32_t k[kPTile][kPRawDw];
+      uint32_t gap[16];  // V rows 16 dwords off: a token's K and V rows on other banks
       uint32_t v[kPTile][kPRawDw];
     } raw;                                        // commit -> decode
     _Float16 kp[EXACT ? 2 : 1][kPTile][kKpStride];  // recon -> scores (hi, lo)
@@ -108,6 +109,7 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
   extern __shared__ __align__(16) unsigned char smem_raw[];
   __shared__ uint16_t lut3s[kLut3Entries];  // static: its address folds into the loads
   PrefillSmem<KSTEPS, EXACT>& S = *reinterpret_cast<PrefillSmem<KSTEPS, EXACT>*>(smem_raw);
+  static_assert(RB == VB, "K and V rows decode with one code path (3/3 and 4/4 are built)");
   const Geom& g = a.g;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -295,29 +297,32 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
     }
     if constexpr (SCORES)
       if (tt + kPTile < k1) fetch_raw_slot_w<2 * KSTEPS>(P, slot_base(tt + kPTile), part, g, k_win, v_win);
-    __syncthreads();
+    // No barrier: wave w commits and decodes the same 16 keys (16w .. 16w+15), and LDS accesses
+    // of one wave complete in order (the fences only keep the compiler from moving them); the
+    // previous tile's readers finished before its closing barrier.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // ------------------------------------------------------------ decode (thread = half row)
     // Decode, V transpose and reconstruction run at raised wave priority, so that where two
     // workgroups share a CU the other one's scores, softmax and P.V fill the slots they leave.
     __builtin_amdgcn_s_setprio(1);
     {
-      const int kind = tid >> 7;
-      const int key = (tid >> 1) & 63;
-      const int half = tid & 1;
-      if (kind == 0) {
-        const uint32_t* row = S.u.raw.k[key];
-        decode_half_row_be<RB>(row, half, S.lut, lut3s, &S.kcode[key][64 * half]);
-        if (half == 0) {
+      // lanes 0..31: K rows, 32..63: V rows of this wave's 16 keys, two threads per row; one
+      // decode call with per-lane row and destination (the two kinds share the code width)
+      const bool is_v = lane >= 32;
+      const int key = 16 * (tid >> 6) + ((lane >> 1) & 15);
+      const int half = lane & 1;
+      const uint32_t* row = is_v ? S.u.raw.v[key] : S.u.raw.k[key];
+      decode_half_row_be<RB>(row, half, S.lut, lut3s,
+                             is_v ? &S.vcode[key][64 * half] : &S.kcode[key][64 * half]);
+      if (half == 0) {
+        const float rul = f16_bits_to_float(staged_u16(row, kBitmapBytes + (is_v ? g.v_pb : g.k_pb)));
+        if (is_v) {
+          S.vrul[key] = key < ntile ? rul : 0.f;
+        } else {
           // 3-bit codes come out as fp8 (c - 4) * unit: the ruler takes the 1 / unit
-          const float kr = f16_bits_to_float(staged_u16(row, kBitmapBytes + g.k_pb));
-          S.krul[key] = RB == 3 ? kr * inv_unit : kr;
+          S.krul[key] = RB == 3 ? rul * inv_unit : rul;
         }
-      } else {
-        const uint32_t* row = S.u.raw.v[key];
-        decode_half_row_be<VB>(row, half, S.lut, lut3s, &S.vcode[key][64 * half]);
-        if (half == 0)
-          S.vrul[key] =
-              key < ntile ? f16_bits_to_float(staged_u16(row, kBitmapBytes + g.v_pb)) : 0.f;
       }
     }
     __syncthreads();

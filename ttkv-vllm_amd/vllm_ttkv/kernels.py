@@ -277,7 +277,7 @@ def multi_scores_paged(lay: TTKLayout, query: torch.Tensor, page: torch.Tensor,
     """K2 scores mode for ONE request (row 0 of block_table / seq_lens / query_start_loc):
     returns `scores` [HQ, Q, n] fp32 with -inf where key t > p0 + j (`krt_multi_from_slots`).
     Q and n are `max_q_len` / `max_seq_len`, which must equal the request's own lengths.
-    `workspace`: None allocates `ttkv_multi_scores_workspace_bytes` (a chunk of more than 64
+    `workspace`: None allocates `ttkv_multi_scores_workspace_bytes` (a chunk of two or more
     queries then reads every stored key expanded once), False runs the fused kernel."""
     flat = _read_checks(lay, query, page, block_table, seq_lens, query_start_loc,
                         dec_slot_of_block, dec_pool, cos_sin_cache)
