@@ -317,18 +317,32 @@ def bench_config4(torch, lay, cfg, cache, dev, steps=10, warmup=3, cpu=False):
                                    D ** -0.5, scores=scores, error_word=err, workspace=sws)
 
     ms_s = time_launches(torch, score1, steps, warmup)
+    # a short chunk over the same store: 16 queries per request (the last 16 keys are the chunk's)
+    Qs = 16
+    qs = q[:4 * Qs].contiguous()
+    qsl_s = torch.arange(0, 4 * Qs + 1, Qs, dtype=torch.int32, device=dev)
+    outs = torch.empty_like(qs)
+    ws_s = kernels.prefill_workspace(lay, HQ, 4, Qs, n, dev, BS)
+
+    def attend_short():
+        kernels.prefill_paged(lay, qs, L["page"], BS, st["bt"], st["seq_lens"], qsl_s, Qs, n,
+                              st["dec_map"], L["dec_pool"], cache, D ** -0.5, out=outs,
+                              workspace=ws_s, error_word=err)
+
+    ms_q16 = time_launches(torch, attend_short, steps, warmup)
     torch.cuda.synchronize()
     if int(err.item()):
         raise RuntimeError(f"K2: device error word {int(err.item())}")
     fl = k2_flops(lens, [Q] * 4, lay.r1)
     tf = fl / (ms * 1e-3) / 1e12
     log(f"K2 config4: {ms * 1e3:.1f} us/launch (4 chunks), {tf:.1f} TFLOP/s; scores mode "
-        f"{ms_s * 1e3:.1f} us per chunk")
+        f"{ms_s * 1e3:.1f} us per chunk; 16-query chunks {ms_q16 * 1e3:.1f} us/launch")
     res = dict(requests=4, cached=7400, chunk=Q, us_per_launch=ms * 1e3,
                us_per_chunk_layer=ms * 1e3 / 4, algorithmic_flop_per_launch=fl,
                tflops=tf, mfma_peak_tflops=2500.0, mfma_frac=tf / 2500.0,
                scores_mode_us_per_chunk_layer=ms_s * 1e3,
-               scores_mode_gbps_written=HQ * Q * n * 4 / (ms_s * 1e-3) / 1e9)
+               scores_mode_gbps_written=HQ * Q * n * 4 / (ms_s * 1e-3) / 1e9,
+               us_per_launch_16_query_chunks=ms_q16 * 1e3)
     if cpu:
         cms, cores = cpu_k2_sample(torch, lay, st, L, q[:Q], cache, n, Q)
         res["cpu_baseline"] = dict(value=cms, unit="ms per chunk-layer", cores=cores, kind="port",
