@@ -284,6 +284,69 @@ def cpu_k3_sample(torch, lay, k_new, v_new, dec_pool, pinv_pool):
     return (time.perf_counter() - t0) * 1e3, torch.get_num_threads()
 
 
+def bench_first_chunk(torch, lay, cfg, dev, lengths=(2048, 8192), reps=5):
+    """A request's first chunk, per layer: the attention over the chunk's own post-RoPE q/k/v
+    (the drop-in's `TTKVAttentionImpl._sdpa`: causal SDPA in fp32, as the reference runs it,
+    impl.py:716-721), the fit of its keys on the device (`encode.fit_into_budget`) and the K3
+    write of its tokens with the fit's coefficients. The fp16 SDPA (model dtype, not the
+    reference's arithmetic) is timed beside it for scale."""
+    from vllm_ttkv import encode, kernels, synth
+    from vllm_ttkv.impl import TTKVAttentionImpl
+    im = TTKVAttentionImpl(HQ, D, D ** -0.5, H)
+    out = []
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e3
+
+    for T in lengths:
+        K = synth.keys(T, seed=T, device=dev)                     # [H, T, d] raw
+        V = synth.values(T, seed=T, device=dev).permute(1, 0, 2).contiguous()
+        q = synth.queries(T, seed=T, device=dev)                  # [T, HQ, d] fp16
+        k = K.permute(1, 0, 2).reshape(T, H * D).half()           # stands in for post-RoPE k
+        v = V.reshape(T, H * D).half()
+        us_sdpa = timed(lambda: im._sdpa(q, k, v))
+        qh = q.transpose(0, 1).unsqueeze(0)
+        kh = k.view(T, H, D).repeat_interleave(HQ // H, 1).transpose(0, 1).unsqueeze(0)
+        vh = v.view(T, H, D).repeat_interleave(HQ // H, 1).transpose(0, 1).unsqueeze(0)
+        us_sdpa16 = timed(lambda: torch.nn.functional.scaled_dot_product_attention(
+            qh, kh, vh, is_causal=True, scale=D ** -0.5))
+        fk = [None]
+
+        def fit():
+            fk[0] = encode.fit_into_budget(K, lay, cfg)
+        us_fit = timed(fit)
+        nblk = (T + BS - 1) // BS
+        page = torch.zeros(nblk * BS, lay.compressed_bytes_per_token(), dtype=torch.uint8,
+                           device=dev)
+        bt = torch.arange(nblk, dtype=torch.int32, device=dev).reshape(1, nblk)
+        dec_map = torch.full((nblk,), -1, dtype=torch.int32, device=dev)
+        dec_map[0] = 0
+        dec_pool = fk[0].decoder.decoder_f.unsqueeze(0).contiguous()
+        pinv_pool = fk[0].decoder.pinv.unsqueeze(0).contiguous()
+        qsl = torch.tensor([0, T], dtype=torch.int32, device=dev)
+        slots = torch.arange(T, dtype=torch.int64, device=dev)
+        Kt = K.permute(1, 0, 2).contiguous()
+        us_write = timed(lambda: kernels.write_paged(
+            lay, Kt, V, slots, qsl, bt, dec_map, dec_pool, pinv_pool, page,
+            coeff_q_in=fk[0].coeff_q, coeff_scale_in=fk[0].coeff_scale))
+        row = dict(tokens=T, sdpa_fp32_us=us_sdpa, sdpa_fp16_us=us_sdpa16, fit_us=us_fit,
+                   write_us=us_write, total_us=us_sdpa + us_fit + us_write)
+        log(f"first chunk {T}: SDPA fp32 {us_sdpa:.0f} us (fp16 {us_sdpa16:.0f}), fit "
+            f"{us_fit:.0f} us, write {us_write:.0f} us per layer")
+        out.append(row)
+        del K, V, q, k, v, qh, kh, vh, page
+    return dict(per_layer=out, note="one request's first chunk per layer: attention over the "
+                "chunk (fp32 causal SDPA, the reference's precision), device fit, K3 write")
+
+
 def bench_config4(torch, lay, cfg, cache, dev, steps=10, warmup=3, cpu=False):
     """4 requests, 7400 cached tokens each plus a 256-query chunk whose keys
     are already written (n = 7656), causal over cached + chunk positions; one K2 launch per
@@ -598,6 +661,8 @@ def main():
                     help="only the continuation workload (BASELINE config 4, K2); prints its line")
     ap.add_argument("--container-only", action="store_true",
                     help="only the container-layout reads (krt + v_out at 8 x 14402); prints its line")
+    ap.add_argument("--first-chunk-only", action="store_true",
+                    help="only the first-chunk timings (attention, fit, write at 2048 / 8192)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 1 GiB device copy (HBM-counter calibration for rocprofv3)")
     args = ap.parse_args()
@@ -621,7 +686,9 @@ def main():
         c4 = bench_config4(torch, lay, cfg, cache, dev, args.steps, args.warmup)
         print(json.dumps(dict(metric="continuation chunk us/layer (K2, BASELINE config 4)",
                               value=c4["us_per_chunk_layer"], unit="us", n_gpus=1,
-                              higher_is_better=False, dtype="f16 MFMA, fp32 accumulate",
+                              higher_is_better=False,
+                              dtype="f16 MFMA on exact hi+lo key splits (V readout: P*ruler_v "
+                                    "rounded to fp16 once), fp32 accumulate",
                               data="synthetic", **c4)))
         return
 
@@ -634,12 +701,20 @@ def main():
                               data="synthetic", **cr)))
         return
 
+    if args.first_chunk_only:
+        fc = bench_first_chunk(torch, lay, cfg, dev)
+        print(json.dumps(dict(metric="first chunk us/layer (attention + fit + write)",
+                              value=fc["per_layer"][-1]["total_us"], unit="us", n_gpus=1,
+                              higher_is_better=False, data="synthetic", **fc)))
+        return
+
     if args.config5_only:
         c5 = bench_config5(torch, cache, dev, args.steps, args.warmup)
         print(json.dumps(dict(metric="4-bit decode step us/layer, K3 write + K1 read (BASELINE "
                                      "config 5)", value=c5["us_per_layer"], unit="us",
                               n_gpus=1, higher_is_better=False,
-                              dtype="fp16 in/out; fp16 MFMA on exact hi+lo splits, fp32 "
+                              dtype="fp16 in/out; fp16 MFMA on exact hi+lo splits (V "
+                                    "readout: P*ruler_v rounded to fp16 once), fp32 "
                                     "accumulate and softmax",
                               data="synthetic", **c5)))
         return
@@ -719,6 +794,7 @@ def main():
                                                       cpu=not args.no_cpu)
         extra["config5_4bit_read_write"] = bench_config5(torch, cache, dev, cpu=not args.no_cpu)
         extra["container_reads_b8_ctx14402"] = bench_container(torch, dev)
+        extra["first_chunk"] = bench_first_chunk(torch, lay, cfg, dev)
 
     cpu = None
     if not args.no_cpu:
@@ -737,7 +813,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp16 in/out; fp16 MFMA on exact hi+lo splits, fp32 accumulate and softmax",
+        "dtype": "fp16 in/out; fp16 MFMA: reconstruction and scores on exact hi+lo splits, V "
+                 "readout on exact codes against P*ruler_v rounded to fp16 once (power-of-two "
+                 "scaled below 2^15); fp32 accumulate and softmax",
         "data": "synthetic (seeded low-rank keys with outlier channels, N(0,1) values, fp16 "
                 "queries; stores fitted and packed on the GPU by this package; 4 distinct layer "
                 "stores, each copied into its own pages for the other 24 layers)",

@@ -40,7 +40,7 @@ enum {
 enum {
   TTKV_ERR_NO_DECODER = 1,   /* block_table[r,0] maps to no decoder slot */
   TTKV_ERR_BAD_BLOCK = 2,    /* a block id outside [0, num_blocks) inside a request's used prefix */
-  TTKV_ERR_BAD_SLOT = 4,     /* slot_mapping entry is PAD (<0) or past the cache */
+  TTKV_ERR_BAD_SLOT = 4,     /* slot_mapping entry past the cache (PAD entries, < 0, are skipped) */
   TTKV_ERR_SEQ_LEN = 8,      /* seq_lens[r] (or a query count) beyond what the call was sized for (clamped), or a continuation with seq_len < q_len */
 };
 
@@ -84,7 +84,11 @@ int64_t ttkv_decode_workspace_bytes(const ttkv_layout* lay, int32_t num_heads,
  * dec_pool     [n_dec_slots, r1, H*d] fp32 decoder_f rows (encode.py:178-211).
  * cos_sin_cache [max_position, d] fp32, vLLM layout: cos in columns [0,d/2), sin in [d/2,d)
  *              (decode.py:54-122).
- * out          [N, num_heads, d] (dtype out_dtype); only the decode rows are written. */
+ * out          [N, num_heads, d] (dtype out_dtype); only the decode rows are written.
+ * Precision: the reconstruction and the scores are carried at fp32 accuracy (hi + lo fp16 MFMA
+ * operands; the query is taken as fp16); the softmax weight times the V row ruler is rounded to
+ * fp16 once for the P.V MFMA (the V codes are exact integers), at a power-of-two scale that keeps
+ * it below 2^15 whatever the rulers, so no finite V row overflows it. */
 int ttkv_decode_paged(const ttkv_layout* lay, int32_t num_heads, float scale,
                       const void* query, int32_t q_dtype, int64_t q_row_stride,
                       const uint8_t* page, int64_t n_slots, int64_t slot_stride,
@@ -133,6 +137,10 @@ int ttkv_decode_paged_noalloc(const ttkv_layout* lay, int32_t num_heads, float s
  * Bytes are bit-exact functions of R and value (select_triton.py:24-91): exact top-k by magnitude
  * (ties -> lowest lane), ruler = rowmax * fp32(1/(2^(b-1)-1)), q = rint(x / ruler) (IEEE div).
  * coeff_out [N, r1] and resid_out [N, H*d] (optional, fp32) receive c and R.
+ * dec_slot_used (optional, [n_dec_slots] int32): set to 1 for the decoder slot of every token
+ *   written, so the host registry can evict decoders by last use (the caller clears it).
+ * slot_mapping entries < 0 are vLLM's PAD_SLOT_ID (padded tokens of a replayed graph): skipped
+ *   silently, as vLLM's cache writers do; entries past the cache set TTKV_ERR_BAD_SLOT.
  * key/value: [N, H, d] rows with the given element stride between tokens.
  * Work is spread over (token, KV head) workgroups in two launches: per-head partial projections
  * (the token's last workgroup sums them in head order and quantises) and, per head, the residual
@@ -143,10 +151,10 @@ int ttkv_write_paged(const ttkv_layout* lay, const void* key, int32_t k_dtype, i
                      const int32_t* query_start_loc, int32_t num_reqs, const int32_t* block_table,
                      int64_t bt_row_stride, const int32_t* dec_slot_of_block, int64_t num_blocks,
                      const float* dec_pool, const float* pinv_pool, int64_t n_dec_slots,
-                     const int8_t* coeff_q_in, const float* coeff_scale_in, uint8_t* page,
-                     int64_t n_slots, int64_t slot_stride, float* coeff_out, float* resid_out,
-                     void* workspace, int64_t workspace_bytes, int32_t* error_word,
-                     ttkv_stream_t stream);
+                     int32_t* dec_slot_used, const int8_t* coeff_q_in,
+                     const float* coeff_scale_in, uint8_t* page, int64_t n_slots,
+                     int64_t slot_stride, float* coeff_out, float* resid_out, void* workspace,
+                     int64_t workspace_bytes, int32_t* error_word, ttkv_stream_t stream);
 
 /* Workspace bytes `ttkv_write_paged` needs for `num_tokens` projected tokens (none when the
  * coefficients come from coeff_q_in); see the workspace note above ttkv_decode_workspace_bytes. */
@@ -172,7 +180,8 @@ int64_t ttkv_prefill_workspace_bytes(const ttkv_layout* lay, int32_t num_heads, 
  * decoded and reconstructed once into the workspace (rotated key hi + lo fp16, exact V codes, V
  * rulers), then flash attention on MFMA reads it for every 128-query block. Single queries (and
  * G = 4, 8 or r1 > 128) run one fused launch that reconstructs each key tile once per 64-query
- * block. Scores never leave the chip.
+ * block. Scores never leave the chip. Precision as for ttkv_decode_paged (the softmax weight times
+ * the V ruler rounded to fp16 once, at a power-of-two scale that keeps it below 2^15).
  * req_index    optional [num_reqs] int32: batch rows to process (block_table / seq_lens /
  *              query_start_loc are indexed by it); NULL = rows 0..num_reqs-1.
  * max_q_len / max_seq_len bound Q and n over the processed rows (they size the grid).
@@ -256,8 +265,9 @@ int ttkv_dense_decode_paged(int32_t H, int32_t num_heads, int32_t d, float scale
  *   p[b, p, i] at p + b*p_batch_stride + p*p_head_stride + i. `out` must be zero-filled: the
  *   launch accumulates tile partials with atomic adds (the codec kernel's contract). Carried at
  *   fp32 accuracy (MFMA on exact integer codes against p * row scale split hi + lo in fp16 after
- *   an exact 2^8 scaling), which needs |p * scale| < 256 for every token (beyond it the fp16
- *   operand overflows and the output reads inf / NaN).
+ *   an exact power-of-two scaling: 2^8 while every |p * scale| is below 128, and lowered by the
+ *   workgroup, with its partial sums rescaled exactly, when a larger product arrives, so no
+ *   finite product overflows the fp16 operand).
  * Built for d = 128, r1 <= 160, 3- or 4-bit rows of <= 48 packed bytes, num_heads / H in
  * {1, 2, 3, 4, 8}. */
 int ttkv_container_krt(int32_t H, int32_t num_heads, int32_t d, int32_t B, int32_t n, int32_t r1,

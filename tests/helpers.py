@@ -12,12 +12,16 @@ from vllm_ttkv import synth
 H, D, HQ = 8, 128, 24
 
 
-def fitted_store(cfg_name: str, T: int, seed: int, r1: int = 110, HQ_: int = HQ):
-    """One request's store: fit on the whole context (fit_into_budget), then slots."""
+def fitted_store(cfg_name: str, T: int, seed: int, r1: int = 110, HQ_: int = HQ,
+                 v_scale=None):
+    """One request's store: fit on the whole context (fit_into_budget), then slots. `v_scale`
+    (a number or a [T] tensor of per-token factors) multiplies the values before encoding."""
     cfg = codec.CONFIGS[cfg_name]
     lay = layout_for_config(cfg, r1=r1)
     K = synth.keys(T, seed=seed)
     V = synth.values(T, seed=seed)
+    if v_scale is not None:
+        V = V * (v_scale if not torch.is_tensor(v_scale) else v_scale.reshape(1, T, 1))
     fk = encode.fit_into_budget(K, lay, cfg)
     ks = encode.k_slots_from(lay, fk["coeff_q"], fk["coeff_scale"], fk["resid"])
     vs = encode.v_slots_from(lay, encode.encode_v(V, lay))

@@ -101,7 +101,8 @@ def _write_call(lay, **kw):
     L = _hip.lib()
     a = dict(key=1, k_dtype=1, k_row_stride=1024, value=1, v_dtype=1, v_row_stride=1024,
              slot_mapping=1, num_tokens=4, qsl=1, num_reqs=1, block_table=1, bt_row_stride=1,
-             dec_map=1, num_blocks=1, dec_pool=1, pinv_pool=1, n_dec=1, cq_in=0, cs_in=0,
+             dec_map=1, num_blocks=1, dec_pool=1, pinv_pool=1, n_dec=1, dec_used=0, cq_in=0,
+             cs_in=0,
              page=4096, n_slots=16, slot_stride=912, c_out=0, r_out=0, ws=256, ws_bytes=1 << 20,
              err=1)
     a.update(kw)
@@ -109,7 +110,8 @@ def _write_call(lay, **kw):
                               a["value"], a["v_dtype"], a["v_row_stride"], a["slot_mapping"],
                               a["num_tokens"], a["qsl"], a["num_reqs"], a["block_table"],
                               a["bt_row_stride"], a["dec_map"], a["num_blocks"], a["dec_pool"],
-                              a["pinv_pool"], a["n_dec"], a["cq_in"], a["cs_in"], a["page"],
+                              a["pinv_pool"], a["n_dec"], a["dec_used"], a["cq_in"],
+                              a["cs_in"], a["page"],
                               a["n_slots"], a["slot_stride"], a["c_out"], a["r_out"], a["ws"],
                               a["ws_bytes"], a["err"], None)
 

@@ -175,6 +175,38 @@ def test_decoder_registry_round_trip():
     rope_store.clear_stores()
 
 
+def test_decoder_eviction_follows_last_use():
+    """A full pool evicts the least recently USED key that is not live. Use comes from the write
+    kernel's flags (`dec_used`, one per slot, set here by hand as the kernel would): a running
+    request that decodes every other step keeps its slot while short requests that registered
+    after it, ran their first chunk and finished are evicted, oldest use first. (Registration
+    order alone evicted the running request first.)"""
+    lay = layout_for_config(CONFIGS["safe"], 16)
+    from vllm_ttkv.encode import KDecoder
+    rope_store.clear_stores()
+    st = rope_store.TTKVRopeStore(24, 8, 128, torch.zeros(8, 128), "L0", lay, num_blocks=40,
+                                  capacity=3)
+    dec = KDecoder(torch.randn(16, 8 * 128))
+    a = st.register(1, dec, live=[1])                  # the running request
+    for step, key in enumerate(range(10, 20)):         # 10 short requests, one per even step
+        st.dec_used[a] = 1                             # odd step: request 1 decodes
+        st.register(key, dec, live=[key])              # even step: key's first chunk only
+        assert st.dec_map[1] == a and 1 in st.decoders, f"running request evicted at {key}"
+        assert len(st.decoders) == min(3, 2 + step)
+    assert list(st.decoders) == [1, 18, 19]
+    # every key used at the same tick: the older registration goes first
+    st.dec_used.fill_(1)
+    st.observe_use()
+    assert st.eviction_order() == [1, 18, 19]
+    st.register(30, dec)
+    assert 1 not in st.decoders and list(st.decoders) == [18, 19, 30]
+    # a released key frees its slot without an eviction
+    st.release(18)
+    st.register(31, dec)
+    assert list(st.decoders) == [19, 30, 31]
+    rope_store.clear_stores()
+
+
 def test_reference_calling_sequence_binds():
     """The reference's own adapter-test sequence (tests/test_impl_decode.py:218-225): build the
     store with its constructor, then `register_decoder(name, request_key(row), KDecoder(dec))`

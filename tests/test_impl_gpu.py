@@ -423,3 +423,103 @@ def test_recycled_first_block_gets_a_new_fit(monkeypatch):
                                q.float(), [dec_new.cpu()], csc, BS, SCALE, dtype=torch.float64)
     _check(out, want, "decode after recycling")
     rope_store.clear_stores()
+
+
+def test_running_request_outlives_short_requests_in_a_full_decoder_pool(monkeypatch):
+    """A pool of 3 decoders. A running request decodes every other step and sits out the steps
+    in between, where short requests arrive one at a time (first chunk only, then never seen
+    again). Six of them register, more than the pool holds: eviction follows last use (the write
+    kernel flags every decoder a step uses), so the short requests leave, oldest use first, and
+    the running request keeps its decoder and decodes against the oracle after every one.
+    (Registration order with `live` = the step's own requests evicted it at the third.)"""
+    monkeypatch.delenv("VLLM_TTKV_CHECK", raising=False)
+    monkeypatch.setenv("VLLM_TTKV_MAX_DECODERS", "3")
+    lay = layout_for_config(CONFIGS["safe"], 110)
+    olay = oracle_layout(CONFIGS["safe"], 110)
+    rope_store.clear_stores()
+    csc = cos_sin_cache(1024)
+    run = _Seq(320, 61)
+    shorts = [_Seq(96, 70 + i) for i in range(6)]
+    bt, nblk = synth.shuffled_block_table([320] + [96] * 6, BS, seed=62, extra_blocks=1)
+    C = lay.compressed_bytes_per_token()
+    cache = torch.zeros(nblk, 1, BS, C // 2, dtype=torch.bfloat16, device="cuda")
+    im = TTKVAttentionImpl(HQ, D, SCALE, H)
+    layer = _Layer(NAME, lay)
+    key = int(bt[0, 0])
+    _step(im, layer, cache, csc, bt[[0]], [(run, 0, 300)])
+    st = rope_store.store_for_layer(NAME)
+    assert st.capacity == 3
+    pos = 300
+    for i, sq in enumerate(shorts):
+        _step(im, layer, cache, csc, bt[[1 + i]], [(sq, 0, 96)])        # a short request
+        out, q, _, qsl, seq_lens = _step(im, layer, cache, csc, bt[[0]], [(run, pos, pos + 1)])
+        assert key in st.decoders and len(st.decoders) == min(3, 2 + i)
+        flat = cache.view(torch.uint8).reshape(-1, C).cpu()
+        want = attend.paged_decode(olay, flat, bt[[0]], torch.tensor(seq_lens), torch.tensor(qsl),
+                                   q.float(), [st.decoders[key].decoder_f.cpu()], csc, BS, SCALE,
+                                   dtype=torch.float64)
+        _check(out, want, f"running request after short request {i}")
+        pos += 1
+    assert list(st.decoders) == [key, int(bt[5, 0]), int(bt[6, 0])]
+    rope_store.clear_stores()
+
+
+def test_padded_graph_replay_skips_pad_tokens(monkeypatch):
+    """vLLM replays a graph captured for 4 decode requests with only 2 real ones: the 2 padded
+    entries carry slot id -1 (PAD_SLOT_ID) and sequence length 0. The write skips the pad tokens
+    without a refusal, the read returns zero rows for the empty requests, the error word stays 0
+    (so a later checked step does not inherit a false refusal), and the real rows match the
+    oracle."""
+    monkeypatch.delenv("VLLM_TTKV_CHECK", raising=False)
+    monkeypatch.setenv("VLLM_TTKV_MAX_NUM_SEQS", "8")
+    monkeypatch.setenv("VLLM_TTKV_MAX_MODEL_LEN", "2048")
+    impl_mod.release_workspaces()
+    lay = layout_for_config(CONFIGS["safe"], 110)
+    olay = oracle_layout(CONFIGS["safe"], 110)
+    rope_store.clear_stores()
+    csc = cos_sin_cache(2048)
+    csc_d = csc.cuda()
+    lens = [500, 700, 300, 420]
+    seqs = [_Seq(L + 8, 80 + i) for i, L in enumerate(lens)]
+    bt0, nblk = synth.shuffled_block_table([L + 8 for L in lens], BS, seed=81, extra_blocks=2)
+    bt = torch.full((4, 2048 // BS), -1, dtype=torch.int32)
+    bt[:, :bt0.shape[1]] = bt0
+    C = lay.compressed_bytes_per_token()
+    cache = torch.zeros(nblk, 1, BS, C // 2, dtype=torch.bfloat16, device="cuda")
+    im = TTKVAttentionImpl(HQ, D, SCALE, H)
+    layer = _Layer(NAME, lay)
+    builder = TTKVAttentionMetadataBuilder()
+    for r, L in enumerate(lens):                       # first chunks, one request per step
+        _step(im, layer, cache, csc, bt[[r]], [(seqs[r], 0, L)])
+    b = _DecodeBatch([0, 1, 2, 3], bt, builder, csc_d)
+    nxt = list(lens)
+    b.fill(seqs, nxt, csc)                             # eager warm-up at the full size
+    b.stash()
+    im.forward(layer, b.q, b.k, b.v, cache, b.md, output=b.out)
+    torch.cuda.synchronize()
+    assert int(im.error_word.item()) == 0
+    nxt = [p + 1 for p in nxt]
+    g = torch.cuda.CUDAGraph()
+    b.stash()
+    with torch.cuda.graph(g):
+        im.forward(layer, b.q, b.k, b.v, cache, b.md, output=b.out)
+    for t in range(2):                                 # replays with 2 real requests
+        b.fill(seqs, nxt, csc)
+        b.md.slot_mapping[2:] = -1
+        b.md.seq_lens[2:] = 0
+        page_before = cache.view(torch.uint8).reshape(-1, C).clone()
+        b.out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert int(im.error_word.item()) == 0, f"replay {t}: error word {int(im.error_word.item())}"
+        assert torch.equal(b.out[2:].float().cpu(), torch.zeros(2, HQ, D))
+        # the pad tokens wrote nothing: only the two real tokens' slots changed
+        after = cache.view(torch.uint8).reshape(-1, C)
+        changed = (after != page_before).any(1).nonzero().flatten().cpu().tolist()
+        real = [int(bt[r, nxt[r] // BS]) * BS + nxt[r] % BS for r in (0, 1)]
+        assert set(changed) <= set(real), changed
+        want = _oracle_decode(olay, cache, C, bt, [0, 1], nxt[:2], b.q[:2], csc)
+        _check(b.out[:2].float().cpu(), want, f"padded replay {t}")
+        nxt = [p + 1 for p in nxt[:2]] + nxt[2:]
+    rope_store.clear_stores()
+    impl_mod.release_workspaces()

@@ -279,3 +279,46 @@ def test_workspace_shared_across_batch_shapes():
     for i, shapes in enumerate(calls):
         assert torch.equal(run(shapes, shared, i), run(shapes, None, i)), f"call {shapes}"
     assert int(shared[:65536].abs().sum()) == 0, "counters left non-zero"
+
+
+@pytest.mark.parametrize("hq", [8, 16])
+def test_attend_and_scores_at_one_and_two_query_heads_per_kv_head(hq):
+    """G = 1 and G = 2 (HQ = 8, 16 over 8 KV heads) build their own attend and scores kernels
+    (and the attend's split-K combine over G * 128 rows): a two-request launch with key splits
+    against the oracle, and the scores mode from expanded keys against raw_scores_multi."""
+    shapes = [(2100, 257), (700, 64)]
+    stores = [fitted_store("safe", n, seed=60 + hq + i) for i, (n, _) in enumerate(shapes)]
+    cache = llama3_cache(4096)
+    pg, dec_pool, dec_map = _dev_inputs(stores, seed=8)
+    q = torch.cat([synth.queries(Q, HQ=hq, seed=600 + hq + i) for i, (_, Q) in enumerate(shapes)])
+    qsl = torch.tensor([0] + list(torch.tensor([Q for _, Q in shapes]).cumsum(0)),
+                       dtype=torch.int32)
+    lay = stores[0]["lay"]
+    out = torch.zeros_like(q, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    kernels.prefill_paged(lay, q.cuda(), pg["page"].cuda(), 16, pg["block_table"].cuda(),
+                          pg["seq_lens"].cuda(), qsl.cuda(), 257, 2100, dec_map, dec_pool,
+                          cache.cuda(), SCALE, out=out, error_word=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    want = attend.paged_continuation(lay, pg["page"], pg["block_table"], pg["seq_lens"], qsl,
+                                     q.double(), [s["decoder"] for s in stores], cache, 16, SCALE,
+                                     dtype=torch.float64)
+    for r in range(len(shapes)):
+        s, e = int(qsl[r]), int(qsl[r + 1])
+        _check(out[s:e].float(), want[r], f"attend HQ={hq} req {r}", exact_inf=False)
+
+    n, Q = shapes[0]
+    st = stores[0]
+    pg1, dec_pool1, dec_map1 = _dev_inputs([st], seed=9)
+    q1 = q[:Q]
+    got = kernels.multi_scores_paged(lay, q1.cuda(), pg1["page"].cuda(), 16,
+                                     pg1["block_table"].cuda(), pg1["seq_lens"].cuda(),
+                                     torch.tensor([0, Q], dtype=torch.int32, device="cuda"), Q, n,
+                                     dec_map1, dec_pool1, cache.cuda(), SCALE, error_word=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    cos, sin = cos_sin_from_cache(cache, torch.arange(n), 128)
+    want_s = attend.raw_scores_multi(lay, st["k_slots"], st["decoder"], q1.permute(1, 0, 2).double(),
+                                     cos, sin, SCALE, p0=n - Q, dtype=torch.float64)
+    _check(got, want_s, f"scores HQ={hq}")

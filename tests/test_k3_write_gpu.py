@@ -126,14 +126,18 @@ def test_fit_coefficients_path():
 
 
 def test_slot_refusals_set_the_error_word_and_write_nothing():
+    """A slot id past the cache is refused (error bit 4) and writes nothing; a negative id is
+    vLLM's PAD_SLOT_ID (padded tokens of a replayed graph): skipped silently, as vLLM's own cache
+    writers do, while the other tokens are written."""
     lay, dec, pinv, Knew, V = _setup("safe", 3, seed=5)
-    for bad in ([0, -1, 2], [0, 1, 99]):
+    for bad, want_err in (([0, -1, 2], 0), ([0, 1, 99], 4)):
         page, _, _, err = _run(lay, dec, pinv, Knew, V, torch.tensor(bad, dtype=torch.int64), 8)
-        assert err & 4, f"{bad}: error word {err}"
+        assert err == want_err, f"{bad}: error word {err}"
         bad_i = 1 if bad[1] == -1 else 2
         ok_rows = [j for j in range(3) if j != bad_i]
-        assert int(page.abs().sum()) > 0
         assert all(int(page[bad[j]].abs().sum()) > 0 for j in ok_rows)
+        written = {bad[j] for j in ok_rows}
+        assert all(int(page[s].abs().sum()) == 0 for s in range(8) if s not in written)
 
 
 @pytest.mark.parametrize("case", ["ref_encode_safe_r16", "ref_encode_campaign4x_r64"])
@@ -237,3 +241,25 @@ def test_workspace_shared_across_token_counts():
         want = write(lo, hi, None)
         assert torch.equal(got, want), f"tokens {lo}:{hi} with a shared workspace"
     assert int(shared[:65536].abs().sum()) == 0, "counters left non-zero"
+
+
+def test_write_flags_the_decoder_slots_it_uses():
+    """`dec_used` receives 1 for the decoder slot of every request with a written token, and
+    nothing for the others: the registry's last-use record (rope_store evicts by it)."""
+    lay, dec, pinv, Knew, V = _setup("safe", 4, seed=9)
+    C = lay.compressed_bytes_per_token()
+    page = torch.zeros(16, C, dtype=torch.uint8, device=DEV)
+    bt = torch.tensor([[3], [1]], dtype=torch.int32, device=DEV)   # request keys 3 and 1
+    dec_map = torch.tensor([-1, 4, -1, 2, -1], dtype=torch.int32, device=DEV)
+    pool = dec.unsqueeze(0).repeat(6, 1, 1).to(DEV)
+    pinvs = pinv.unsqueeze(0).repeat(6, 1, 1).to(DEV)
+    used = torch.zeros(6, dtype=torch.int32, device=DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    kernels.write_paged(lay, Knew.permute(1, 0, 2).contiguous().to(DEV),
+                        V.permute(1, 0, 2).contiguous().to(DEV),
+                        torch.tensor([0, 5, -1, 9], dtype=torch.int64, device=DEV),
+                        torch.tensor([0, 3, 4], dtype=torch.int32, device=DEV), bt, dec_map,
+                        pool, pinvs, page, error_word=err, dec_used=used)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    assert used.cpu().tolist() == [0, 0, 1, 0, 1, 0]

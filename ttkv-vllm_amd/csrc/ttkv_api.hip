@@ -115,15 +115,16 @@ int ttkv_write_paged(const ttkv_layout* lay, const void* key, int32_t k_dtype, i
                      const int32_t* query_start_loc, int32_t num_reqs, const int32_t* block_table,
                      int64_t bt_row_stride, const int32_t* dec_slot_of_block, int64_t num_blocks,
                      const float* dec_pool, const float* pinv_pool, int64_t n_dec_slots,
-                     const int8_t* coeff_q_in, const float* coeff_scale_in, uint8_t* page,
-                     int64_t n_slots, int64_t slot_stride, float* coeff_out, float* resid_out,
-                     void* workspace, int64_t workspace_bytes, int32_t* error_word,
-                     ttkv_stream_t stream) {
+                     int32_t* dec_slot_used, const int8_t* coeff_q_in,
+                     const float* coeff_scale_in, uint8_t* page, int64_t n_slots,
+                     int64_t slot_stride, float* coeff_out, float* resid_out, void* workspace,
+                     int64_t workspace_bytes, int32_t* error_word, ttkv_stream_t stream) {
   Geom g;
   if (!make_geom(lay, &g)) return host_fail(TTKV_E_INVALID, "invalid layout");
   return write_paged(g, key, k_dtype, k_row_stride, value, v_dtype, v_row_stride, slot_mapping,
                      num_tokens, query_start_loc, num_reqs, block_table, bt_row_stride,
-                     dec_slot_of_block, num_blocks, dec_pool, pinv_pool, n_dec_slots, coeff_q_in,
+                     dec_slot_of_block, num_blocks, dec_pool, pinv_pool, n_dec_slots,
+                     dec_slot_used, coeff_q_in,
                      coeff_scale_in, page, n_slots, slot_stride, coeff_out, resid_out, workspace,
                      workspace_bytes, error_word, (hipStream_t)stream);
 }

@@ -298,14 +298,17 @@ struct VoutSmem {
   _Float16 pwh[2][8][kCVTile];
   _Float16 pwl[2][8][kCVTile];
   uint2 lut[256];
+  int wexp;  // the weight exponent the workgroup runs at (only grows)
 };
 
 // 128-token tiles. The next tile's rows, rulers and weights are in registers while the current
 // tile decodes and accumulates. Accumulation on MFMA, as K1's P.V: O^T[dims, heads] +=
 // V^T[dims, tokens] * W^T[tokens, heads] with the codes as exact fp16 integers (c - 2^(b-1)), read
 // transposed from the decoded rows (ds_read_tr8_b64), and the weights w = p * ruler split hi + lo
-// in fp16 (two products) after an exact 2^8 scaling that keeps small weights out of the fp16
-// subnormals, so the sum keeps fp32-level accuracy. Wave w owns dims 16w.. and 64 + 16w.. for all
+// in fp16 (two products) after an exact 2^(8 - we) scaling, so the sum keeps fp32-level accuracy:
+// at we = 0 the 2^8 keeps small weights out of the fp16 subnormals, and we grows (the workgroup
+// agrees on it through LDS at the tile's first barrier) when a weight of 2^(7 + we) or more
+// arrives, so every scaled weight stays below 2^15. Wave w owns dims 16w.. and 64 + 16w.. for all
 // heads.
 template <int G, int BITS>
 __global__ __launch_bounds__(kCThreads, 2) void container_v_out_kernel(ContainerArgs a) {
@@ -348,6 +351,12 @@ __global__ __launch_bounds__(kCThreads, 2) void container_v_out_kernel(Container
   };
   fetch(tile0);
   build_luts(S.lut, BITS == 3 ? lut3s : nullptr, tid, kCThreads);
+  if (tid == 0) S.wexp = 0;
+  __syncthreads();  // wexp
+  int we = 0;                 // weights are scaled by 2^(8 - we); the accumulators likewise
+  float w_thr = 128.f;        // |w| >= 2^(7 + we) needs a larger exponent
+  float wsc = 256.f;          // 2^(8 - we)
+  float wreg[kPw];
   // 3-bit codes: fp8 bytes of (c - 4) scaled back by 1 / unit to exact integers
   const float inv_unit = 1.0f / __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0];
   float4v oacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};  // O^T[dims][head n]
@@ -366,18 +375,37 @@ __global__ __launch_bounds__(kCThreads, 2) void container_v_out_kernel(Container
       commit_row_quarter(part, sh[pass], x[pass], S.raw[ptok + 64 * pass]);
 #pragma unroll
     for (int k = 0; k < kPw; ++k) {
+      wreg[k] = pwv[k] * rwv[k];
+      const float aw = fabsf(wreg[k]);
+      if (aw >= w_thr) atomicMax(&S.wexp, (int)(__float_as_uint(aw) >> 23) - 127 - 6);
+    }
+    if (tile + 1 < tile1) fetch(tile + 1);
+    __syncthreads();
+    {
+      // the workgroup's exponent for this tile (every atomicMax above precedes the barrier; the
+      // next ones follow the tile's second barrier)
+      const int we_new = S.wexp;
+      if (we_new != we) {
+        const float f = ldexpf(1.f, we - we_new);
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) oacc[mi] *= f;
+        we = we_new;
+        w_thr = ldexpf(1.f, 7 + we);
+        wsc = ldexpf(1.f, 8 - we);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kPw; ++k) {
       const int idx = tid + kCThreads * k;
       if (idx < G * kCVTile) {
-        // scaled by 2^8 (exact) so that weights down to ~1e-6 stay fp16 normals; the sums are
-        // scaled back at the end. |p * ruler| must stay below 256 (fp16 range after scaling).
-        const float w = pwv[k] * rwv[k] * 256.0f;
+        // scaled by 2^(8 - we) (exact): weights down to ~1e-6 stay fp16 normals at we = 0, and
+        // every scaled weight stays below 2^15; the sums are scaled back at the end
+        const float w = wreg[k] * wsc;
         const _Float16 hi = (_Float16)w;
         S.pwh[buf][idx / kCVTile][idx & (kCVTile - 1)] = hi;
         S.pwl[buf][idx / kCVTile][idx & (kCVTile - 1)] = (_Float16)(w - (float)hi);
       }
     }
-    if (tile + 1 < tile1) fetch(tile + 1);
-    __syncthreads();
     // ---- decode (thread = token tid/2, half tid&1), at raised wave priority
     __builtin_amdgcn_s_setprio(1);
     decode_half_row_be<BITS>(S.raw[tid >> 1], tid & 1, S.lut, lut3s,
@@ -438,7 +466,7 @@ __global__ __launch_bounds__(kCThreads, 2) void container_v_out_kernel(Container
     for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        atomicAdd(&ob[16 * (wv + 4 * mi) + 4 * gq + i], oacc[mi][i] * (1.0f / 256.0f));
+        atomicAdd(&ob[16 * (wv + 4 * mi) + 4 * gq + i], oacc[mi][i] * ldexpf(1.f, we - 8));
   }
 }
 

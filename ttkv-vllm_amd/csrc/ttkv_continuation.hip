@@ -20,7 +20,8 @@
 //                heads of one (request, KV head, key split); wave w owns queries 16w..16w+15.
 //                Per 64-key tile: S^T = K Q^T on MFMA (hi and lo key halves against the fp16
 //                query), causal -inf, online base-2 softmax per query column, O^T += Vt (P *
-//                ruler_v)^T on MFMA with P * ruler_v rounded to fp16 once, in 32-key halves.
+//                ruler_v)^T on MFMA with P * ruler_v * 2^-ve rounded to fp16 once (ve >= 0 grows
+//                with the largest V ruler seen, keeping it below 2^15), in 32-key halves.
 //                Waves 4..7 run half a tile behind waves 0..3 (three LDS tile buffers, one
 //                barrier per tile), so each SIMD's two waves overlap MFMA with softmax. The
 //                next tile is copied to LDS while the current ones are
@@ -525,6 +526,11 @@ __global__ __launch_bounds__(kAThreads, 2) void attend_kernel(AttendArgs a) {
   float l_lane[G];  // per-lane partial normalisers, summed over the column at the end
 #pragma unroll
   for (int gg = 0; gg < G; ++gg) l_lane[gg] = 0.f;
+  // P * ruler_v is carried at scale 2^-ve so that it stays an fp16 normal below 2^15 (P <= 2^8):
+  // ve grows, behind a ballot, when a half step brings a ruler of 2^(7 + ve) or more, and the
+  // wave's accumulators are rescaled by an exact power of two (ve is per wave: its own rows)
+  int ve = 0;
+  float v_thr = 128.f, v_mul = 1.f;
 
   auto half_step = [&](const AttendTile& T, int tl, int hf) {
     const int tt = tl * kXTile;
@@ -561,8 +567,26 @@ __global__ __launch_bounds__(kAThreads, 2) void attend_kernel(AttendArgs a) {
     }
     // -------------------------------------------------------- online softmax per column
     // (raw scores; the scale enters the exponent's fma, and m_run is in scaled units)
-    const float4v vr0 = *(const float4v*)(tb + 49152 + (32 * hf + 4 * gq) * 4);
-    const float4v vr1 = *(const float4v*)(tb + 49152 + (32 * hf + 16 + 4 * gq) * 4);
+    float4v vr0 = *(const float4v*)(tb + 49152 + (32 * hf + 4 * gq) * 4);
+    float4v vr1 = *(const float4v*)(tb + 49152 + (32 * hf + 16 + 4 * gq) * 4);
+    {
+      // rulers are >= 0 (rows past the context carry 0)
+      const float vmx = fmaxf(max3_mfma(vr0[0], vr0[1], vr0[2]),
+                              max3_mfma(vr0[3], vr1[0], fmaxf(vr1[1], fmaxf(vr1[2], vr1[3]))));
+      if (__builtin_amdgcn_ballot_w64(vmx >= v_thr) != 0) {  // rare: a large V ruler
+        const int ve_new = wave_max_i((int)(__float_as_uint(vmx) >> 23) - 127) - 6;
+        const float f = ldexpf(1.f, ve - ve_new);
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+          for (int gg = 0; gg < G; ++gg) o[dt][gg] *= f;
+        ve = ve_new;
+        v_thr = ldexpf(1.f, 7 + ve);
+        v_mul = ldexpf(1.f, -ve);
+      }
+      vr0 *= v_mul;
+      vr1 *= v_mul;
+    }
     half8 pb[G];
 #pragma unroll
     for (int gg = 0; gg < G; ++gg) {
@@ -630,6 +654,13 @@ __global__ __launch_bounds__(kAThreads, 2) void attend_kernel(AttendArgs a) {
 
 #pragma unroll
   for (int gg = 0; gg < G; ++gg) l_run[gg] = cross_row_sum(l_lane[gg]);
+  if (ve != 0) {  // the V-ruler scale taken back (exact)
+    const float vsc = ldexpf(1.f, ve);
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int gg = 0; gg < G; ++gg) o[dt][gg] *= vsc;
+  }
 
   // ---------------------------------------------------------------- output / split-K hand-off
   // out rows aligned for 4-element stores (16 bytes fp32, 8 bytes fp16 / bf16)

@@ -31,7 +31,8 @@
 //             reference point moves only when some score exceeds it by more than 2^8 (a ballot),
 //             so the wave-wide max is rarely computed; sums stay per lane until the end.
 //   P.V     : on MFMA, O^T[dims, heads] += V^T[dims, tokens] * P'^T[tokens, heads] with
-//             P' = P * ruler_v rounded to fp16 once and the codes as exact fp16 integers
+//             P' = P * ruler_v * 2^-ve rounded to fp16 once (ve >= 0 grows with the largest V
+//             ruler seen, so P' stays below 2^15) and the codes as exact fp16 integers
 //             (c - 2^(b-1)). The V^T operand is read straight from the decoded code rows with
 //             the gfx950 LDS transpose read (ds_read_tr8_b64); P'^T from a per-wave LDS row.
 // Chunks of one (r, h) are combined in the same launch by the last workgroup to finish
@@ -495,6 +496,14 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
     m_run[p] = -INFINITY;
     l_lane[p] = 0.f;
   }
+  // P' = P * ruler_v is carried at scale 2^-ve so that it stays an fp16 normal below 2^15: P <=
+  // 2^8 (lazy rescale), so every ruler of a tile must stay below 2^(7 + ve). ve starts at 0 (no
+  // scaling: rulers below 128, i.e. V rows up to |v| ~ 384 at 3 bits) and grows, behind a ballot,
+  // when a tile brings a larger ruler; the accumulators are then rescaled by an exact power of
+  // two, and the output takes 2^ve back at the end. Every wave sees the same rulers, so ve is
+  // the same in all of them.
+  int ve = 0;
+  float v_thr = 128.f, v_mul = 1.f;
   // V^T A-fragments come from the decoded code rows through the LDS transpose read: in each
   // 16-lane group, lanes 2j and 2j+1 address the two 8-byte halves of row j (token 8gq + j) of
   // the tile's 16 dims, and lane n receives column n (dim n) of those 8 rows, i.e. exactly
@@ -682,6 +691,16 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
         }
       }
       float amul = 1.f;  // this lane's factor for its head column n of the P.V accumulators
+      if (__builtin_amdgcn_ballot_w64(vrt >= v_thr) != 0) {  // rare: a large V ruler
+        // rulers are >= 0: the biased exponent field orders them; vrt < 2^(ex + 1)
+        const int ex = wave_max_i((int)(__float_as_uint(vrt) >> 23) - 127);
+        const int ve_new = ex - 6;
+        amul = ldexpf(1.f, ve - ve_new);
+        ve = ve_new;
+        v_thr = ldexpf(1.f, 7 + ve);
+        v_mul = ldexpf(1.f, -ve);
+      }
+      const float vrs = vrt * v_mul;
 #pragma unroll
       for (int p = 0; p < G; ++p) {
         const float s = valid ? sum[p] * ft : -INFINITY;
@@ -694,13 +713,13 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
           const float alpha = exp2f(m_run[p] - mt);
           m_run[p] = mt;
           l_lane[p] *= alpha;
-          amul = n == p ? alpha : amul;
+          amul = n == p ? alpha * amul : amul;
         }
         const float pr = fast_exp2(s - m_run[p]);
         l_lane[p] += pr;
-        // P' = P * ruler_v, rounded to fp16 once (the V codes are exact integers); tokens past
-        // the tile's end have P = 0 and all-zero decoded rows
-        S.pw[wv][p][lane] = (_Float16)(pr * vrt);
+        // P' = P * ruler_v * 2^-ve, rounded to fp16 once (the V codes are exact integers);
+        // tokens past the tile's end have P = 0 and all-zero decoded rows
+        S.pw[wv][p][lane] = (_Float16)(pr * vrs);
       }
 #pragma unroll
       for (int mi = 0; mi < 2; ++mi) oacc[mi] *= amul;
@@ -755,6 +774,12 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
     }
   }
 
+  // the V-ruler scale 2^-ve taken back (exact)
+  if (ve != 0) {
+    const float vsc = ldexpf(1.f, ve);
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi) oacc[mi] *= vsc;
+  }
   // ---- normalisers: the per-lane partial sums over the wave (every wave holds the same)
 #pragma unroll
   for (int p = 0; p < G; ++p) l_lane[p] = wave_sum(l_lane[p]);

@@ -51,10 +51,10 @@ int write_paged(const Geom& g, const void* key, int k_dtype, int64_t k_row_strid
                 int v_dtype, int64_t v_row_stride, const int64_t* slot_mapping, int num_tokens,
                 const int32_t* qsl, int num_reqs, const int32_t* bt, int64_t bt_row_stride,
                 const int32_t* dec_map, int64_t num_blocks, const float* dec_pool,
-                const float* pinv_pool, int64_t n_dec_slots, const int8_t* cq_in,
-                const float* cs_in, uint8_t* page, int64_t n_slots, int64_t slot_stride,
-                float* c_out, float* r_out, void* ws, int64_t ws_bytes, int32_t* err,
-                hipStream_t st);
+                const float* pinv_pool, int64_t n_dec_slots, int32_t* dec_used,
+                const int8_t* cq_in, const float* cs_in, uint8_t* page, int64_t n_slots,
+                int64_t slot_stride, float* c_out, float* r_out, void* ws, int64_t ws_bytes,
+                int32_t* err, hipStream_t st);
 int64_t write_workspace_bytes(const Geom& g, int num_tokens);
 }  // namespace ttkv
 

@@ -27,8 +27,9 @@
 // and the rotated key is split hi + lo too, so each score is the fp32 dot of the fp16 query with
 // the fp32 key up to fp32 rounding. Rounding either operand to a single fp16 instead moves the
 // attention output by up to ~1.5e-3 (decoder) and ~3e-3 (rotated key) on the benchmark's keys,
-// which have x8 outlier channels -- beyond the 2e-3 budget. P * ruler_v is rounded to fp16 once
-// for the P.V contraction (the V codes themselves are exact small integers).
+// which have x8 outlier channels -- beyond the 2e-3 budget. P * ruler_v * 2^-ve is rounded to
+// fp16 once for the P.V contraction (the V codes themselves are exact small integers); ve >= 0
+// grows with the largest V ruler seen so that the product stays below 2^15 (P <= 2^8).
 //
 // Reference semantics: vllm_ttkv/impl.py:725-778 (_prefill_continuation: p0 = seq_len - q_len,
 // scores over the whole store, softmax, V readout), vllm_ttkv/reference.py:112-146
@@ -231,6 +232,8 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
 #pragma unroll
     for (int dt = 0; dt < (SCORES ? 1 : 8); ++dt) o[dt][gg] = float4v{0.f, 0.f, 0.f, 0.f};
   }
+  int ve = 0;  // V-ruler exponent of the P.V operand (see the softmax)
+  float v_thr = 128.f, v_mul = 1.f;
 
   const int k_row_off = g.k_field + h * g.k_row;
   const int v_row_off = g.k_slot + h * g.v_row;
@@ -478,6 +481,26 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
       float4v vr[4];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) vr[kt] = *(const float4v*)&S.vrul[16 * kt + 4 * gq];
+      {
+        // P * ruler_v is carried at scale 2^-ve (ve grows, behind a ballot, with the largest
+        // ruler seen) so that it stays an fp16 normal below 2^15; rulers are >= 0
+        float vmx = 0.f;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) vmx = fmaxf(vmx, max3_mfma(vr[kt][0], vr[kt][1], fmaxf(vr[kt][2], vr[kt][3])));
+        if (__builtin_amdgcn_ballot_w64(vmx >= v_thr) != 0) {  // rare: a large V ruler
+          const int ve_new = wave_max_i((int)(__float_as_uint(vmx) >> 23) - 127) - 6;
+          const float f = ldexpf(1.f, ve - ve_new);
+#pragma unroll
+          for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+            for (int gg = 0; gg < G; ++gg) o[dt][gg] *= f;
+          ve = ve_new;
+          v_thr = ldexpf(1.f, 7 + ve);
+          v_mul = ldexpf(1.f, -ve);
+        }
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) vr[kt] *= v_mul;
+      }
       half8 pb[G][2];
 #pragma unroll
       for (int gg = 0; gg < G; ++gg) {
@@ -529,7 +552,17 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
     }
     __syncthreads();  // Kp / Vt / coef are overwritten by the next tile
   }
-  if constexpr (SCORES) return;
+  if constexpr (SCORES) {
+    return;
+  } else {
+    if (ve != 0) {  // the V-ruler scale taken back (exact)
+      const float vsc = ldexpf(1.f, ve);
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int gg = 0; gg < G; ++gg) o[dt][gg] *= vsc;
+    }
+  }
 
   // ---------------------------------------------------------------- output / split-K hand-off
   if (nparts == 1) {

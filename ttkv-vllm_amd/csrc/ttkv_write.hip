@@ -51,6 +51,7 @@ struct WriteArgs {
   const float* dec_pool;
   const float* pinv_pool;
   int64_t n_dec_slots;
+  int32_t* dec_used;  // [n_dec_slots] or null: set to 1 for every decoder slot a token uses
   const int8_t* cq_in;
   const float* cs_in;
   uint8_t* page;
@@ -253,11 +254,17 @@ __global__ __launch_bounds__(kWThreads) void write_pack_kernel(WriteArgs a) {
   const int h = blockIdx.x % g.H;
   const int HD = g.H * kD;
   const int64_t slot = a.slot_mapping[i];
-  const bool slot_ok = slot >= 0 && slot < a.n_slots;
+  // A negative slot id is vLLM's PAD_SLOT_ID (the padded tokens of a replayed graph): nothing
+  // is written and nothing is refused, as vLLM's own cache writers skip them. Ids past the
+  // cache are refused.
+  if (slot < 0) return;
+  const bool slot_ok = slot < a.n_slots;
   const int ds = token_decoder(a, i);
   if (h == 0 && tid == 0) {
     if (!slot_ok) atomicOr(a.err, TTKV_ERR_BAD_SLOT);
     if (ds < 0) atomicOr(a.err, TTKV_ERR_NO_DECODER);
+    // the decoder registry's use flag (its eviction follows the last use, read by the host)
+    if (ds >= 0 && a.dec_used) a.dec_used[ds] = 1;
   }
   if (ds < 0 || !slot_ok) return;
   // this head's decoder columns (rows a = wv, wv + 4, ...) do not depend on the coefficients:
@@ -356,7 +363,8 @@ int write_paged(const Geom& g, const void* key, int k_dtype, int64_t k_row_strid
                 int v_dtype, int64_t v_row_stride, const int64_t* slot_mapping, int num_tokens,
                 const int32_t* qsl, int num_reqs, const int32_t* bt, int64_t bt_row_stride,
                 const int32_t* dec_map, int64_t num_blocks, const float* dec_pool,
-                const float* pinv_pool, int64_t n_dec_slots, const int8_t* cq_in,
+                const float* pinv_pool, int64_t n_dec_slots, int32_t* dec_used,
+                const int8_t* cq_in,
                 const float* cs_in, uint8_t* page, int64_t n_slots, int64_t slot_stride,
                 float* c_out, float* r_out, void* ws, int64_t ws_bytes, int32_t* err,
                 hipStream_t st) {
@@ -402,6 +410,7 @@ int write_paged(const Geom& g, const void* key, int k_dtype, int64_t k_row_strid
   a.dec_pool = dec_pool;
   a.pinv_pool = pinv_pool;
   a.n_dec_slots = n_dec_slots;
+  a.dec_used = dec_used;
   a.cq_in = cq_in;
   a.cs_in = cs_in;
   a.page = page;

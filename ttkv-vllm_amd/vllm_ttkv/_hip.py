@@ -92,7 +92,7 @@ def lib():
         P, I32, I64,                  # value, v_dtype, v_row_stride
         P, I32, P, I32,               # slot_mapping, num_tokens, query_start_loc, num_reqs
         P, I64, P, I64,               # block_table, bt_row_stride, dec_slot_of_block, num_blocks
-        P, P, I64,                    # dec_pool, pinv_pool, n_dec_slots
+        P, P, I64, P,                 # dec_pool, pinv_pool, n_dec_slots, dec_slot_used
         P, P,                         # coeff_q_in, coeff_scale_in
         P, I64, I64,                  # page, n_slots, slot_stride
         P, P,                         # coeff_out, resid_out

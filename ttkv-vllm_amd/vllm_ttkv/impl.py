@@ -286,7 +286,8 @@ class TTKVAttentionImpl(_ImplBase):
             # decode-only step: every request has a decoder; one launch, no host reads
             kernels.write_paged(lay, K, V, slots, qsl_d, bt, store.dec_map, store.dec_pool,
                                 store.pinv_pool, cache, error_word=self.error_word,
-                                workspace=self._write_workspace(lay, N, K.device, fixed=True))
+                                workspace=self._write_workspace(lay, N, K.device, fixed=True),
+                                dec_used=store.dec_used)
             return
         # A step with prefill chunks. A request whose whole context arrives in this step
         # (seq_len == q_len) is on its first chunk and is fitted (encode.py:257-298) -- ALWAYS,
@@ -325,7 +326,7 @@ class TTKVAttentionImpl(_ImplBase):
             kernels.write_paged(lay, K[idx].contiguous(), V[idx].contiguous(), slots[idx], sub_qsl,
                                 bt[rows].contiguous(), store.dec_map, store.dec_pool,
                                 store.pinv_pool, cache, coeff_q_in=cq, coeff_scale_in=cs,
-                                error_word=self.error_word,
+                                error_word=self.error_word, dec_used=store.dec_used,
                                 workspace=None if cq is not None else
                                 self._write_workspace(lay, len(idx), dev))
 

@@ -122,11 +122,13 @@ def write_paged(lay: TTKLayout, key: torch.Tensor, value: torch.Tensor,
                 coeff_scale_in: torch.Tensor | None = None,
                 coeff_out: torch.Tensor | None = None, resid_out: torch.Tensor | None = None,
                 error_word: torch.Tensor | None = None,
-                workspace: torch.Tensor | None = None) -> None:
+                workspace: torch.Tensor | None = None,
+                dec_used: torch.Tensor | None = None) -> None:
     """K3: encode + pack `key`/`value` ([N, H, d], raw pre-RoPE keys) into their slots.
 
     See `ttkv_write_paged` in include/ttkv_hip.h. `pinv_pool` [slots, H*d, r1] fp32 drives the
-    frozen projection; `coeff_q_in`/`coeff_scale_in` replace it with a fit's coefficients."""
+    frozen projection; `coeff_q_in`/`coeff_scale_in` replace it with a fit's coefficients.
+    `dec_used` ([slots] int32, optional) receives 1 for every decoder slot a token used."""
     _need_device(key, value, slot_mapping, query_start_loc, block_table, dec_slot_of_block,
                  dec_pool, pinv_pool, page)
     N = key.shape[0]
@@ -151,6 +153,10 @@ def write_paged(lay: TTKLayout, key: torch.Tensor, value: torch.Tensor,
     flat = page_bytes(page, lay.compressed_bytes_per_token())
     if error_word is None:
         error_word = torch.zeros(1, dtype=torch.int32, device=key.device)
+    if dec_used is not None:
+        _i32(dec_used, "dec_used")
+        if dec_used.numel() < dec_pool.shape[0]:
+            raise ValueError("dec_used needs one flag per decoder pool slot")
     cq = None
     if coeff_q_in is not None:
         cq = coeff_q_in.to(torch.int8).contiguous()
@@ -165,7 +171,7 @@ def write_paged(lay: TTKLayout, key: torch.Tensor, value: torch.Tensor,
         slot_mapping.data_ptr(), N, query_start_loc.data_ptr(), query_start_loc.numel() - 1,
         block_table.data_ptr(), block_table.stride(0), dec_slot_of_block.data_ptr(),
         dec_slot_of_block.numel(), dec_pool.data_ptr(), _hip.ptr(pinv_pool), dec_pool.shape[0],
-        _hip.ptr(cq), _hip.ptr(coeff_scale_in), flat.data_ptr(), flat.shape[0], flat.stride(0),
+        _hip.ptr(dec_used), _hip.ptr(cq), _hip.ptr(coeff_scale_in), flat.data_ptr(), flat.shape[0], flat.stride(0),
         _hip.ptr(coeff_out), _hip.ptr(resid_out), _hip.ptr(workspace),
         0 if workspace is None else workspace.numel(), error_word.data_ptr(),
         _hip.stream_ptr(key.device))

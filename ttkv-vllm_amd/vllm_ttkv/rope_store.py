@@ -16,8 +16,11 @@ request's decoder through that map themselves, so a step needs no host read of t
 The pools are allocated ONCE, at a fixed capacity (argument, or `VLLM_TTKV_MAX_DECODERS`, default
 64 requests per layer), and the map once the cache's block count is known. Nothing is ever
 reallocated, so a HIP graph captured over the kernels keeps valid pointers for the store's
-lifetime. A full pool evicts the oldest registration that the caller does not name as live (the
-impl names the current step's requests); if every slot is live, registration raises.
+lifetime. A full pool evicts the least recently USED registration that the caller does not name
+as live (the impl names the current step's requests): the write kernel flags every slot a written
+token uses (`dec_used`, read back only when a registration happens), so a running request that
+sits out a few steps outlives requests that finished earlier. `release_decoder` frees a finished
+request's slot at once. If every slot is live, registration raises.
 """
 from __future__ import annotations
 
@@ -158,6 +161,14 @@ class TTKVRopeStore:
         self.decoders: "OrderedDict[int, KDecoder]" = OrderedDict()  # key -> decoder, oldest first
         self._slot_of: dict[int, int] = {}
         self._free = list(range(cap - 1, -1, -1))
+        # Last use: the write kernel sets dec_used[slot] = 1 for every slot a written token used
+        # (every scheduled request writes every step, decode-only steps included, with no host
+        # read). A registration reads the flags back (it runs in a fitting step, which
+        # synchronises anyway), stamps the flagged slots with the current tick and clears them;
+        # eviction then takes the least recently used slot not in the step.
+        self.dec_used = torch.zeros(cap, dtype=torch.int32, device=dev)
+        self._last_use: dict[int, int] = {}   # slot -> tick of its last observed use
+        self._tick = 0
         if num_blocks is not None:
             self.bind_blocks(num_blocks)
         _STORES[layer_name] = self
@@ -181,10 +192,30 @@ class TTKVRopeStore:
         self.dec_map = m.to(self.dec_pool.device)
         return self.dec_map
 
+    def observe_use(self) -> None:
+        """Fold the write kernel's use flags into the last-use record (one small read back)."""
+        self._tick += 1
+        used = self.dec_used.tolist()
+        for slot, u in enumerate(used):
+            if u:
+                self._last_use[slot] = self._tick
+        if any(used):
+            self.dec_used.zero_()
+
+    def eviction_order(self, live=()) -> list:
+        """Registered keys that may be evicted, least recently used first as last observed
+        (`observe_use`; ties: the older registration first); keys in `live` (this step's
+        requests) never appear."""
+        live = {int(k) for k in live}
+        keys = [k for k in self.decoders if k not in live]     # registration order
+        return sorted(keys, key=lambda k: self._last_use.get(self._slot_of[k], 0))
+
     def register(self, key: int, dec: KDecoder, live=()) -> int:
         """Copy `dec` into the pool under request key `key` and map the key to it. A key that is
         already registered keeps its slot (a recycled first block, re-fitted). When the pool is
-        full, the oldest registration whose key is not in `live` is evicted."""
+        full, the least recently used registration whose key is not in `live` is evicted: use is
+        what the write kernel flags (every scheduled request writes every step), so a running
+        request that sits out a few steps outlives requests that finished before its last step."""
         key = int(key)
         lay = self.layout
         if tuple(dec.decoder_f.shape) != (lay.r1, lay.H * lay.d):
@@ -193,16 +224,16 @@ class TTKVRopeStore:
         if self.dec_map is not None and not 0 <= key < self.dec_map.numel():
             raise IndexError(f"request key (first block) {key} outside the cache's "
                              f"{self.dec_map.numel()} blocks")
+        self.observe_use()
         slot = self._slot_of.get(key)
         if slot is None:
             if not self._free:
-                live = {int(k) for k in live}
-                victim = next((k for k in self.decoders if k not in live), None)
-                if victim is None:
+                order = self.eviction_order(live)
+                if not order:
                     raise RuntimeError(
                         f"layer {self.layer_name!r}: all {self.capacity} decoder slots belong "
                         f"to live requests; raise {CAPACITY_ENV} or release finished requests")
-                self.release(victim)
+                self.release(order[0])
             slot = self._free.pop()
             self._slot_of[key] = slot
         self.dec_pool[slot].copy_(dec.decoder_f)
@@ -211,6 +242,7 @@ class TTKVRopeStore:
             self.dec_map[key] = slot
         self.decoders.pop(key, None)
         self.decoders[key] = dec
+        self._last_use[slot] = self._tick
         return slot
 
     def release(self, key: int) -> None:
@@ -220,6 +252,7 @@ class TTKVRopeStore:
         if slot is not None:
             if self.dec_map is not None:
                 self.dec_map[key] = -1
+            self._last_use.pop(slot, None)
             self._free.append(slot)
 
 
