@@ -228,10 +228,13 @@ int64_t ttkv_multi_scores_workspace_bytes(const ttkv_layout* lay, int32_t num_he
                                           int32_t max_q_len, int32_t max_seq_len);
 
 /* Benchmark comparator (no counterpart in the compressed path): dense paged decode attention over
- * an uncompressed fp16/bf16 KV cache of the same shapes and launch structure as
- * ttkv_decode_paged, for the "per-cached-token cost vs dense" comparison the reference's bench
- * makes (bench_decode_read.py:132-151).
- * k_cache / v_cache [n_slots, H, d] (dtype = TTKV_DTYPE_F16 or _BF16 for q, caches and out). */
+ * an uncompressed fp16/bf16 KV cache of the same shapes as ttkv_decode_paged's workload, for the
+ * "per-cached-token cost vs dense" comparison the reference's bench makes
+ * (bench_decode_read.py:132-151). Two launches: split-K over (request, token chunk) items that
+ * read whole slot rows (all H heads), with a work plan computed on the device from the batch's
+ * lengths, then a reduction of the chunks' partials.
+ * k_cache / v_cache [n_slots, H, d] (dtype = TTKV_DTYPE_F16 or _BF16 for q, caches and out);
+ * built for H = 8, G = num_heads / H in 1..4, d = 128 and a power-of-two block size. */
 int64_t ttkv_dense_workspace_bytes(int32_t H, int32_t num_heads, int32_t num_reqs,
                                    int32_t max_seq_len, int32_t block_size);
 int ttkv_dense_decode_paged(int32_t H, int32_t num_heads, int32_t d, float scale,

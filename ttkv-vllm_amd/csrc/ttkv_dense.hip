@@ -1,16 +1,31 @@
-// Benchmark comparator: dense fp16/bf16 paged decode attention of the same shapes and launch
-// structure as K1 (one launch per layer over the batch, split-K over token chunks combined in the
-// same launch). It has no counterpart in the compressed path; it measures what a plain paged KV
-// cache costs per cached token on this GPU (the reference's bench compares its read with dense
-// attention too, bench_decode_read.py:132-151).
+// Benchmark comparator: dense fp16/bf16 paged decode attention over an uncompressed KV cache of
+// the same shapes as K1's workload. It has no counterpart in the compressed path; it measures what
+// a plain paged KV cache costs per cached token on this GPU (the reference's bench compares its
+// read with dense attention too, bench_decode_read.py:132-151). It is built as a byte-streaming
+// kernel, the way a dense decode read is best built on this GPU, so that the comparison is
+// against a read near the HBM bound rather than a weak one.
 //
 // Cache layout (vLLM's paged KV): k_cache / v_cache [num_blocks * block_size, H, d] in the model
-// dtype; slot of position t of request r = block_table[r, t / bs] * bs + t % bs.
+// dtype; slot of position t of request r = block_table[r, t / bs] * bs + t % bs. A token's K row
+// of all H heads (H * 256 bytes at d = 128) is one contiguous run, and so is its V row.
 //
-// Work item = (request, KV head, token chunk). 16 lanes own one token (8 dims each, one 16-byte
-// load per lane for K and for V); a wave walks 16 tokens per step with the next step's loads in
-// flight, dots the G query heads of the KV head, rescales its online softmax once per step and
-// accumulates P.V. Lane groups and waves are merged at the end, then chunks as in K1.
+// Two launches (split-K over token chunks, then a reduction; vLLM's own paged attention v2 has
+// the same structure):
+//   dense_decode_kernel : work item = (request, token chunk), ALL KV heads, so every slot row is
+//       read whole and once. The chunk comes from a work plan computed on the device from the
+//       batch's own lengths: the shortest multiple of 16 tokens that spreads the batch's total
+//       tokens over `target` items (each request at least one chunk), so a ragged batch fills
+//       the chip by its total work, not by its longest request. Wave w takes head group w % 2
+//       (4 heads: lane group g = head 4 * hg + g, 16 lanes of 8 dims each, one 16-byte K and V
+//       load per lane and token) and token stream w / 2; per step it loads 4 tokens with the
+//       next step's loads in flight, dots the G query heads of each head (packed fp16 dot
+//       products for fp16 caches), keeps one online softmax per (head, query head) and
+//       accumulates P.V in fp32. The two streams of a head group are merged through LDS. A
+//       request with one chunk is written out directly; otherwise the item's unnormalised
+//       partials (o, max, sum per head and query head) go to the workspace.
+//   dense_reduce_kernel : one workgroup per (request, KV head) with two or more chunks, from the
+//       same device plan: the per-(head, query head) max and normaliser over the chunks, then
+//       each output as one weighted sum of the chunks' partials.
 #include <math.h>
 
 #include "ttkv_device.h"
@@ -18,8 +33,11 @@
 namespace ttkv {
 
 constexpr int kDThreads = 256;
-constexpr int kDSeg = 1026;  // block ids of one chunk staged in LDS
-constexpr int kDUnroll = 4;  // 4-token steps per wave iteration (loads of the next iteration in flight)
+constexpr int kDSeg = 1026;     // block ids of one chunk staged in LDS
+constexpr int kDPlanLanes = 4;  // requests per lane in the work plan (256 per launch)
+constexpr int kDHeads = 8;      // KV heads the kernel is built for (2 head groups of 4)
+constexpr int kDGran = 16;      // chunk granularity in tokens
+constexpr int kDRThreads = 512; // reduction workgroup: one thread per output (G * d <= 512)
 
 struct DenseArgs {
   int H, HQ, G;
@@ -30,7 +48,7 @@ struct DenseArgs {
   const uint16_t* vc;
   int dtype;  // TTKV_DTYPE_F16 or BF16 for q, cache and out
   int64_t n_slots;
-  int block_size;
+  int block_size, bs_shift;
   const int32_t* bt;
   int64_t bt_row_stride;
   const int32_t* seq_lens;
@@ -38,9 +56,10 @@ struct DenseArgs {
   int num_reqs;
   void* out;
   int64_t out_row_stride;
-  float* ws_part;
-  int* ws_cnt;
-  int chunk, max_chunks, nwork, max_seq;
+  float* ws_part;  // [items][H][G][kD + 2]
+  int target;      // work items aimed at (resident workgroups of the launch)
+  int chunk_cap;   // longest chunk in tokens (a multiple of 64 whose block ids fit the LDS stage)
+  int max_seq;     // longest context the launch was sized for
 };
 
 __device__ __forceinline__ void unpack8(uint4 x, int dt, float f[8]) {
@@ -57,43 +76,109 @@ __device__ __forceinline__ void unpack8(uint4 x, int dt, float f[8]) {
   }
 }
 
+// Inclusive prefix sum over the wave's lanes (all lanes active).
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(v, o);
+    v += lane >= o ? t : 0;
+  }
+  return v;
+}
+
+// The device work plan, computed alike by every wave of both kernels: the chunk length and each
+// request's chunk count and first item. Item `it` (or, for the reduction, request `rq`) resolves
+// to its request, chunk, context length and the request's first item and chunk count.
+struct DensePlan {
+  int chunk, n_items;
+  int r, c, seq, first, n_chunks;
+};
+
+__device__ __forceinline__ DensePlan dense_plan(const DenseArgs& a, int it, int rq) {
+  const int lane = threadIdx.x & 63;
+  const int nper = (a.num_reqs + 63) >> 6;
+  int sl[kDPlanLanes], nch[kDPlanLanes], ex[kDPlanLanes];
+  int tiles = 0;
+#pragma unroll
+  for (int i = 0; i < kDPlanLanes; ++i) {
+    const int rr = lane + 64 * i;
+    sl[i] = (i < nper && rr < a.num_reqs) ? min(max(a.seq_lens[rr], 0), a.max_seq) : 0;
+    tiles += (sl[i] + kDGran - 1) / kDGran;
+  }
+  tiles = wave_sum_i(tiles);
+  DensePlan P{};
+  const int m_tiles = min(max(1, (tiles + a.target - 1) / a.target), a.chunk_cap / kDGran);
+  P.chunk = m_tiles * kDGran;
+  int carry = 0;
+#pragma unroll
+  for (int i = 0; i < kDPlanLanes; ++i) {
+    const int rr = lane + 64 * i;
+    nch[i] = (i < nper && rr < a.num_reqs) ? max(1, (sl[i] + P.chunk - 1) / P.chunk) : 0;
+    const int incl = wave_incl_scan(nch[i]);
+    ex[i] = carry + incl - nch[i];
+    carry += __shfl(incl, 63);
+  }
+  P.n_items = carry;
+  P.n_chunks = 0;
+#pragma unroll
+  for (int i = 0; i < kDPlanLanes; ++i) {
+    const int rr = lane + 64 * i;
+    const bool mine = rq >= 0 ? rr == rq : (nch[i] > 0 && ex[i] <= it && it < ex[i] + nch[i]);
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(mine && rr < a.num_reqs);
+    if (hit) {
+      const int ln = __builtin_ctzll(hit);
+      P.r = 64 * i + ln;
+      P.first = __shfl(ex[i], ln);
+      P.c = it - P.first;
+      P.seq = __shfl(sl[i], ln);
+      P.n_chunks = __shfl(nch[i], ln);
+    }
+  }
+  return P;
+}
+
 template <int G, int DT>
-__global__ __launch_bounds__(kDThreads) void dense_decode_kernel(DenseArgs a) {
-  __shared__ float red_o[4][G][kD];
+__global__ __launch_bounds__(kDThreads, 2) void dense_decode_kernel(DenseArgs a) {
+  constexpr int NST = 2;  // token streams per head group
+  __shared__ float red_o[4][4][G][kD];  // [wave][head in group][query head][dim]
   __shared__ float red_m[4][4][G], red_l[4][4][G];
-  __shared__ int is_last;
   __shared__ int seg[kDSeg];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wv = tid >> 6;
-  const int grp = lane >> 4;  // token slot within the wave step
+  const int hl = lane >> 4;   // head within the group
   const int sub = lane & 15;  // dims 8*sub .. 8*sub+7
-  const int per_xcd = gridDim.x >> 3;
-  const int w = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-  if (w >= a.nwork) return;
-  const int h = w % a.H;
-  const int rc = w / a.H;
-  const int r = rc % a.num_reqs;
-  const int c = rc / a.num_reqs;
-  if (c >= a.max_chunks) return;
-  const int seq = min(a.seq_lens[r], a.max_seq);
-  const int n_chunks = (seq + a.chunk - 1) / a.chunk;
-  if (c >= n_chunks) return;
-  const int t0 = c * a.chunk, t1 = min(seq, t0 + a.chunk);
-  const int64_t qrow = a.qsl[r];
-  const int bfirst = t0 / a.block_size;
-  const int nseg = (t1 - 1) / a.block_size - bfirst + 1;
-  for (int i = tid; i < nseg; i += kDThreads)
-    seg[i] = a.bt[(int64_t)r * a.bt_row_stride + bfirst + i];
-  __syncthreads();
+  const int hg = wv & 1, stream = wv >> 1;
+  const int head = 4 * hg + hl;
 
-  float q[G][8];
+  const int per_xcd_slots = gridDim.x >> 3;
+  const int it = (blockIdx.x & 7) * per_xcd_slots + (blockIdx.x >> 3);
+  const DensePlan P = dense_plan(a, it, -1);
+  if (it >= P.n_items) return;
+  const int64_t qrow = a.qsl[P.r];
+  const int t0 = P.c * P.chunk, t1 = min(P.seq, t0 + P.chunk);
+  if (t1 <= t0) {  // empty context: the attention over zero rows is 0
+    for (int i = tid; i < a.HQ * kD; i += kDThreads)
+      store_act(a.out, DT, qrow * a.out_row_stride + i, 0.f);
+    return;
+  }
+  const int bfirst = t0 >> a.bs_shift;
+  const int nseg = ((t1 - 1) >> a.bs_shift) - bfirst + 1;
+  for (int i = tid; i < nseg; i += kDThreads)
+    seg[i] = a.bt[(int64_t)P.r * a.bt_row_stride + bfirst + i];
+
+  // query: fp16 caches take packed fp16 pairs (dot products on v_dot2), bf16 fp32 values
+  uint32_t qp[G][4];
+  float qf[G][8];
 #pragma unroll
   for (int p = 0; p < G; ++p) {
     const uint4 x = ld_global16((const uint16_t*)a.q + qrow * a.q_row_stride +
-                                (int64_t)(h * G + p) * kD + 8 * sub);
-    unpack8(x, DT, q[p]);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) q[p][i] *= a.scale_log2;
+                                (int64_t)(head * G + p) * kD + 8 * sub);
+    qp[p][0] = x.x;
+    qp[p][1] = x.y;
+    qp[p][2] = x.z;
+    qp[p][3] = x.w;
+    if constexpr (DT != TTKV_DTYPE_F16) unpack8(x, DT, qf[p]);
   }
   float o[G][8], m[G], l[G];
 #pragma unroll
@@ -103,71 +188,78 @@ __global__ __launch_bounds__(kDThreads) void dense_decode_kernel(DenseArgs a) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[p][i] = 0.f;
   }
-  const int64_t row_elems = (int64_t)a.H * kD;
-  auto slot_off = [&](int t) -> int64_t {
-    const int bi = t / a.block_size;
-    const int blk = seg[bi - bfirst];
-    return ((int64_t)blk * a.block_size + (t - bi * a.block_size)) * row_elems + (int64_t)h * kD +
-           8 * sub;
-  };
-  // Each wave owns steps of 4 * kDUnroll tokens (4 lane groups x kDUnroll); the next step's K/V loads are
-  // issued before the current step is computed. One softmax rescale per step.
-  constexpr int kStep = 4 * kDUnroll;
-  uint4 kx[kDUnroll], vx[kDUnroll];
+  __syncthreads();  // seg
+  const int bmask = a.block_size - 1;
+  const int lane_off = head * kD + 8 * sub;  // elements within a slot's row
+  constexpr int64_t kRow = (int64_t)kDHeads * kD;
   const uint4 zero4 = make_uint4(0, 0, 0, 0);
-  int tb = t0 + kStep * wv;
+  constexpr int kStep = 4;  // tokens per wave step
+  auto load_step = [&](int tb, uint4* kx, uint4* vx) {
 #pragma unroll
-  for (int u = 0; u < kDUnroll; ++u) {
-    const int t = tb + 4 * u + grp;
-    const int64_t off = t < t1 ? slot_off(t) : -1;
-    kx[u] = off >= 0 ? ld_global16(a.kc + off) : zero4;
-    vx[u] = off >= 0 ? ld_global16(a.vc + off) : zero4;
-  }
-  for (; tb < t1; tb += 4 * kStep) {
-    uint4 kn[kDUnroll], vn[kDUnroll];
-#pragma unroll
-    for (int u = 0; u < kDUnroll; ++u) {
-      const int t = tb + 4 * kStep + 4 * u + grp;
-      const int64_t off = t < t1 ? slot_off(t) : -1;
-      kn[u] = off >= 0 ? ld_global16(a.kc + off) : zero4;
-      vn[u] = off >= 0 ? ld_global16(a.vc + off) : zero4;
+    for (int u = 0; u < kStep; ++u) {
+      const int t = tb + u;
+      if (t < t1) {
+        const int64_t slot = (int64_t)seg[(t >> a.bs_shift) - bfirst] * a.block_size + (t & bmask);
+        const int64_t off = slot * kRow + lane_off;
+        kx[u] = ld_stream16(a.kc + off);
+        vx[u] = ld_stream16(a.vc + off);
+      } else {
+        kx[u] = zero4;
+        vx[u] = zero4;
+      }
     }
-    float s[G][kDUnroll];
+  };
+  uint4 kx[kStep], vx[kStep];
+  int tb = t0 + kStep * stream;
+  load_step(tb, kx, vx);
+  for (; tb < t1; tb += kStep * NST) {
+    uint4 kn[kStep], vn[kStep];
+    load_step(tb + kStep * NST, kn, vn);
+    float s[G][kStep];
 #pragma unroll
-    for (int u = 0; u < kDUnroll; ++u) {
+    for (int u = 0; u < kStep; ++u) {
+      const bool ok = tb + u < t1;
       float kf[8];
-      unpack8(kx[u], DT, kf);
-      const bool ok = tb + 4 * u + grp < t1;
+      if constexpr (DT != TTKV_DTYPE_F16) unpack8(kx[u], DT, kf);
+      const uint32_t kw[4] = {kx[u].x, kx[u].y, kx[u].z, kx[u].w};
 #pragma unroll
       for (int p = 0; p < G; ++p) {
         float acc = 0.f;
+        if constexpr (DT == TTKV_DTYPE_F16) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc = fmaf(q[p][i], kf[i], acc);
-        s[p][u] = ok ? row_sum(acc) : -INFINITY;
+          for (int i = 0; i < 4; ++i)
+            acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, qp[p][i]),
+                                         __builtin_bit_cast(half2v, kw[i]), acc, false);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc = fmaf(qf[p][i], kf[i], acc);
+        }
+        s[p][u] = ok ? row_sum(acc) * a.scale_log2 : -INFINITY;
       }
     }
+    // online softmax per (head, query head): the 16 lanes of a head hold the same scores; the
+    // reference point moves only when a score exceeds it by more than 2^8 (p <= 256 otherwise)
 #pragma unroll
     for (int p = 0; p < G; ++p) {
       float mt = s[p][0];
 #pragma unroll
-      for (int u = 1; u < kDUnroll; ++u) mt = fmaxf(mt, s[p][u]);
-      mt = cross_row_max(mt);
-      const float mn = fmaxf(m[p], mt);
-      const float mref = mn == -INFINITY ? 0.f : mn;
-      const float alpha = exp2f(m[p] - mref);
-      m[p] = mn;
-      float ls = 0.f;
+      for (int u = 1; u < kStep; ++u) mt = fmaxf(mt, s[p][u]);
+      if (__builtin_amdgcn_ballot_w64(mt > m[p] + 8.f) != 0) {
+        const float mn = fmaxf(m[p], mt);
+        const float alpha = m[p] == -INFINITY ? 0.f : exp2f(m[p] - mn);
+        m[p] = mn;
+        l[p] *= alpha;
 #pragma unroll
-      for (int u = 0; u < kDUnroll; ++u) {
-        s[p][u] = fast_exp2(s[p][u] - mref);
-        ls += s[p][u];
+        for (int i = 0; i < 8; ++i) o[p][i] *= alpha;
       }
-      l[p] = l[p] * alpha + cross_row_sum(ls);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o[p][i] *= alpha;
+      for (int u = 0; u < kStep; ++u) {
+        s[p][u] = fast_exp2(s[p][u] - m[p]);
+        l[p] += s[p][u];
+      }
     }
 #pragma unroll
-    for (int u = 0; u < kDUnroll; ++u) {
+    for (int u = 0; u < kStep; ++u) {
       float vf[8];
       unpack8(vx[u], DT, vf);
 #pragma unroll
@@ -176,92 +268,112 @@ __global__ __launch_bounds__(kDThreads) void dense_decode_kernel(DenseArgs a) {
         for (int i = 0; i < 8; ++i) o[p][i] = fmaf(s[p][u], vf[i], o[p][i]);
     }
 #pragma unroll
-    for (int u = 0; u < kDUnroll; ++u) {
+    for (int u = 0; u < kStep; ++u) {
       kx[u] = kn[u];
       vx[u] = vn[u];
     }
   }
-  // merge the 4 lane groups of each wave, then the 4 waves, through LDS
-  if (sub == 0) {  // m, l are wave-uniform: the 4 lane groups share one running softmax
+  // ---- merge the two streams of each head group through LDS
+  if (sub == 0) {
 #pragma unroll
     for (int p = 0; p < G; ++p) {
-      red_m[wv][grp][p] = grp == 0 ? m[p] : -INFINITY;
-      red_l[wv][grp][p] = grp == 0 ? l[p] : 0.f;
+      red_m[wv][hl][p] = m[p];
+      red_l[wv][hl][p] = l[p];
     }
   }
   __syncthreads();
-  float M[G];
+  if (stream != 0) {
+#pragma unroll
+    for (int p = 0; p < G; ++p) {
+      const float M = fmaxf(red_m[hg][hl][p], m[p]);
+      const float f = m[p] == -INFINITY ? 0.f : exp2f(m[p] - M);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) red_o[wv][hl][p][8 * sub + i] = o[p][i] * f;
+    }
+  }
+  __syncthreads();
+  if (stream != 0) return;
+  // stream 0 of each head group: merged o, max, sum of its 4 heads
+  const int wo = wv + 2;  // the other stream's wave
+  float* partp = nullptr;
+  if (P.n_chunks > 1)
+    partp = a.ws_part + ((int64_t)it * kDHeads + head) * G * (kD + 2);
 #pragma unroll
   for (int p = 0; p < G; ++p) {
-    M[p] = -INFINITY;
-    for (int i = 0; i < 16; ++i) M[p] = fmaxf(M[p], red_m[i >> 2][i & 3][p]);
-  }
-  for (int i = tid; i < 4 * G * kD; i += kDThreads) (&red_o[0][0][0])[i] = 0.f;
-  __syncthreads();
+    const float mo = red_m[wo][hl][p];
+    const float M = fmaxf(m[p], mo);
+    const float f = m[p] == -INFINITY ? 0.f : exp2f(m[p] - M);
+    const float L = l[p] * f + (mo == -INFINITY ? 0.f : red_l[wo][hl][p] * exp2f(mo - M));
+    float v[8];
 #pragma unroll
-  for (int p = 0; p < G; ++p) {
-    const float f = m[p] == -INFINITY ? 0.f : exp2f(m[p] - M[p]);
+    for (int i = 0; i < 8; ++i) v[i] = fmaf(o[p][i], f, red_o[wo][hl][p][8 * sub + i]);
+    if (P.n_chunks == 1) {
+      const float inv = 1.f / L;
+      const int64_t ob = qrow * a.out_row_stride + (int64_t)(head * G + p) * kD + 8 * sub;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) atomicAdd(&red_o[wv][p][8 * sub + i], o[p][i] * f);
-  }
-  __syncthreads();
-  float L[G];
+      for (int i = 0; i < 8; ++i) store_act(a.out, DT, ob + i, v[i] * inv);
+    } else {
+      float* pp = partp + p * (kD + 2);
 #pragma unroll
-  for (int p = 0; p < G; ++p) {
-    L[p] = 0.f;
-    for (int i = 0; i < 16; ++i) {
-      const float mi = red_m[i >> 2][i & 3][p];
-      L[p] += mi == -INFINITY ? 0.f : red_l[i >> 2][i & 3][p] * exp2f(mi - M[p]);
+      for (int i = 0; i < 8; ++i) pp[8 * sub + i] = v[i];
+      if (sub == 0) {
+        pp[kD] = M;
+        pp[kD + 1] = L;
+      }
     }
   }
-  if (n_chunks == 1) {
-    for (int i = tid; i < G * kD; i += kDThreads) {
-      const int p = i / kD, d = i % kD;
-      const float v = red_o[0][p][d] + red_o[1][p][d] + red_o[2][p][d] + red_o[3][p][d];
-      store_act(a.out, DT, qrow * a.out_row_stride + (int64_t)(h * G + p) * kD + d, v / L[p]);
+}
+
+// One workgroup per (request, KV head) whose request has two or more chunks: the chunks'
+// partials combined into the output. The partials were written by the previous launch.
+template <int G, int DT>
+__global__ __launch_bounds__(kDRThreads) void dense_reduce_kernel(DenseArgs a) {
+  __shared__ float comb[G][2];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int rq = blockIdx.x / kDHeads, h = blockIdx.x % kDHeads;
+  if (rq >= a.num_reqs) return;
+  const DensePlan P = dense_plan(a, 0, rq);
+  if (P.n_chunks <= 1) return;
+  const int64_t hstride = (int64_t)G * (kD + 2);
+  const int64_t cstride = (int64_t)kDHeads * hstride;  // between consecutive items
+  const float* pbase = a.ws_part + ((int64_t)P.first * kDHeads + h) * hstride;
+  if (wv < G) {  // wave p: max and normaliser of query head p
+    const int p = wv;
+    float mx = -INFINITY;
+    for (int cc = lane; cc < P.n_chunks; cc += 64)
+      mx = fmaxf(mx, pbase[cc * cstride + p * (kD + 2) + kD]);
+    mx = wave_max(mx);
+    float Ls = 0.f;
+    for (int cc = lane; cc < P.n_chunks; cc += 64) {
+      const float* pc = pbase + cc * cstride + p * (kD + 2);
+      Ls = fmaf(pc[kD + 1], exp2f(pc[kD] - mx), Ls);
     }
-    return;
-  }
-  const int64_t pstride = (int64_t)G * (kD + 2);
-  float* partp = a.ws_part + ((int64_t)(r * a.H + h) * a.max_chunks + c) * pstride;
-  for (int i = tid; i < G * kD; i += kDThreads) {
-    const int p = i / kD, d = i % kD;
-    const float v = red_o[0][p][d] + red_o[1][p][d] + red_o[2][p][d] + red_o[3][p][d];
-    __hip_atomic_store(&partp[p * (kD + 2) + d], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  if (tid < G) {
-    __hip_atomic_store(&partp[tid * (kD + 2) + kD], M[tid], __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(&partp[tid * (kD + 2) + kD + 1], L[tid], __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (tid == 0) {
-    const int prev = __hip_atomic_fetch_add(&a.ws_cnt[r * a.H + h], 1, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-    is_last = (prev == n_chunks - 1);
-  }
-  __syncthreads();
-  if (!is_last) return;
-  const float* pbase = a.ws_part + (int64_t)(r * a.H + h) * a.max_chunks * pstride;
-  for (int i = tid; i < G * kD; i += kDThreads) {
-    const int p = i / kD, d = i % kD;
-    float Mx = -INFINITY;
-    for (int cc = 0; cc < n_chunks; ++cc)
-      Mx = fmaxf(Mx, __hip_atomic_load(&pbase[cc * pstride + p * (kD + 2) + kD], __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT));
-    float Lx = 0.f, Ox = 0.f;
-    for (int cc = 0; cc < n_chunks; ++cc) {
-      const float* pc = pbase + cc * pstride + p * (kD + 2);
-      const float f = exp2f(__hip_atomic_load(&pc[kD], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - Mx);
-      Lx = fmaf(__hip_atomic_load(&pc[kD + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), f, Lx);
-      Ox = fmaf(__hip_atomic_load(&pc[d], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), f, Ox);
+    Ls = wave_sum(Ls);
+    if (lane == 0) {
+      comb[p][0] = mx;
+      comb[p][1] = 1.f / Ls;
     }
-    store_act(a.out, DT, qrow * a.out_row_stride + (int64_t)(h * G + p) * kD + d, Ox / Lx);
   }
-  if (tid == 0)
-    __hip_atomic_store(&a.ws_cnt[r * a.H + h], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (tid >= G * kD) return;
+  const int64_t qrow = a.qsl[P.r];
+  const int p = tid / kD, d = tid % kD;
+  const float mx = comb[p][0];
+  const float* ph = pbase + p * (kD + 2);
+  float O = 0.f;
+  int cc = 0;
+  for (; cc + 16 <= P.n_chunks; cc += 16) {  // 16 chunks' loads in flight together
+    float mv[16], ov[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      mv[j] = ph[(cc + j) * cstride + kD];
+      ov[j] = ph[(cc + j) * cstride + d];
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) O = fmaf(ov[j], exp2f(mv[j] - mx), O);
+  }
+  for (; cc < P.n_chunks; ++cc) O = fmaf(ph[cc * cstride + d], exp2f(ph[cc * cstride + kD] - mx), O);
+  store_act(a.out, DT, qrow * a.out_row_stride + (int64_t)(h * G + p) * kD + d, O * comb[p][1]);
 }
 
 }  // namespace ttkv
@@ -270,38 +382,58 @@ __global__ __launch_bounds__(kDThreads) void dense_decode_kernel(DenseArgs a) {
 
 namespace ttkv {
 
-int dense_chunk_for(int num_reqs, int H, int max_seq_len, int block_size) {
-  const int64_t work = (int64_t)num_reqs * H * std::max(max_seq_len, 1);
-  const int64_t target = 2LL * device_cu_count();  // 2 resident workgroups per CU
-  int64_t chunk = (work + target - 1) / target;
-  chunk = (chunk + 255) / 256 * 256;
-  chunk = std::min<int64_t>(std::max<int64_t>(chunk, 256), 8192);
-  const int64_t seg_cap = (int64_t)(kDSeg - 2) * std::max(block_size, 1) / 256 * 256;
-  return (int)std::max<int64_t>(std::min(chunk, seg_cap), 256);
+// Resident workgroups of the G/DT build on this device (the plan's item target), at most two per
+// CU: longer chunks stream longer runs per workgroup.
+template <int G, int DT>
+static int dense_slots() {
+  static int slots = 0;
+  if (!slots) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, dense_decode_kernel<G, DT>,
+                                                     kDThreads, 0) != hipSuccess || per_cu < 1)
+      per_cu = 2;
+    slots = std::min(per_cu, 2) * device_cu_count();
+  }
+  return slots;
 }
 
-// Requests per launch: one arrival counter per (request, head).
-static int dense_slice_reqs(int H, int num_reqs) {
-  return std::min(num_reqs, std::max(1, kMaxCounters / std::max(H, 1)));
+static int dense_target(int G, int dtype) {
+  const bool f16 = dtype == TTKV_DTYPE_F16;
+  switch (G) {
+    case 1: return f16 ? dense_slots<1, TTKV_DTYPE_F16>() : dense_slots<1, TTKV_DTYPE_BF16>();
+    case 2: return f16 ? dense_slots<2, TTKV_DTYPE_F16>() : dense_slots<2, TTKV_DTYPE_BF16>();
+    case 3: return f16 ? dense_slots<3, TTKV_DTYPE_F16>() : dense_slots<3, TTKV_DTYPE_BF16>();
+    default: return f16 ? dense_slots<4, TTKV_DTYPE_F16>() : dense_slots<4, TTKV_DTYPE_BF16>();
+  }
 }
 
-static int64_t dense_part_bytes(int H, int G, int nr, int max_seq_len, int block_size) {
-  const int chunk = dense_chunk_for(nr, H, max_seq_len, block_size);
-  const int max_chunks = std::max(1, (max_seq_len + chunk - 1) / chunk);
-  return (int64_t)nr * H * max_chunks * G * (kD + 2) * 4;
+static int dense_chunk_cap(int block_size) {
+  return (int)std::max<int64_t>(kDGran, (int64_t)(kDSeg - 2) * std::max(block_size, 1) / kDGran *
+                                            kDGran);
+}
+
+// Requests per launch: the plan's 256.
+static int dense_slice_reqs(int num_reqs) { return std::min(num_reqs, kDPlanLanes * 64); }
+
+// (request, chunk) items a launch can plan: at most target + one per request from rounding,
+// more when the chunk cap binds
+static int64_t dense_max_items(int nr, int max_seq_len, int block_size, int target) {
+  const int64_t cap = dense_chunk_cap(block_size);
+  return (int64_t)target + 1 + (int64_t)nr * (2 + (std::max(max_seq_len, 1) + cap - 1) / cap);
 }
 
 int64_t dense_workspace_bytes(int H, int G, int num_reqs, int max_seq_len, int block_size) {
-  if (num_reqs <= 0) return kCounterBytes;
-  const int slice = dense_slice_reqs(H, num_reqs);
-  return kCounterBytes +
-         std::max(dense_part_bytes(H, G, slice, max_seq_len, block_size),
-                  dense_part_bytes(H, G, (num_reqs - 1) % slice + 1, max_seq_len, block_size));
+  if (num_reqs <= 0 || G < 1 || G > 4 || H != kDHeads) return 256;
+  const int slice = std::max(1, dense_slice_reqs(num_reqs));
+  const int target = std::max(dense_target(G, TTKV_DTYPE_F16), dense_target(G, TTKV_DTYPE_BF16));
+  return dense_max_items(slice, max_seq_len, block_size, target) * kDHeads * G * (kD + 2) * 4;
 }
 
 template <int G, int DT>
 static int launch_dense_t(const DenseArgs& a, int grid, hipStream_t st) {
   hipLaunchKernelGGL((dense_decode_kernel<G, DT>), dim3(grid), dim3(kDThreads), 0, st, a);
+  hipLaunchKernelGGL((dense_reduce_kernel<G, DT>), dim3(a.num_reqs * kDHeads), dim3(kDRThreads), 0,
+                     st, a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return host_fail(TTKV_E_LAUNCH, std::string("dense launch: ") + hipGetErrorString(e));
@@ -316,6 +448,7 @@ int dense_decode_paged(int H, int HQ, int d, float scale, const void* q, int64_t
                        hipStream_t st) {
   if (d != kD) return host_fail(TTKV_E_UNSUPPORTED, "head dim must be 128");
   if (H <= 0 || HQ % H) return host_fail(TTKV_E_INVALID, "num_heads is not a multiple of H");
+  if (H != kDHeads) return host_fail(TTKV_E_UNSUPPORTED, "the dense comparator is built for H = 8");
   if (dtype != TTKV_DTYPE_F16 && dtype != TTKV_DTYPE_BF16)
     return host_fail(TTKV_E_INVALID, "dense cache dtype must be fp16 or bf16");
   if (!q || !k_cache || !v_cache || !bt || !seq_lens || !qsl || !out)
@@ -323,12 +456,20 @@ int dense_decode_paged(int H, int HQ, int d, float scale, const void* q, int64_t
   if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) % 16 || q_row_stride % 8)
     return host_fail(TTKV_E_INVALID, "q / caches must be 16-byte aligned");
   if (num_reqs == 0) return TTKV_OK;
+  if (block_size <= 0 || (block_size & (block_size - 1)))
+    return host_fail(TTKV_E_UNSUPPORTED, "the dense comparator takes a power-of-two block size");
   if ((int64_t)max_blocks * block_size < max_seq_len)
     return host_fail(TTKV_E_INVALID, "max_seq_len needs more blocks than the block table holds");
+  const int G = HQ / H;
+  if (G < 1 || G > 4) return host_fail(TTKV_E_UNSUPPORTED, "G must be 1..4 for the dense comparator");
+  const int64_t need = dense_workspace_bytes(H, G, num_reqs, max_seq_len, block_size);
+  if (!ws || ws_bytes < need || (uintptr_t)ws % 256)
+    return host_fail(TTKV_E_WORKSPACE, "dense workspace needs " + std::to_string(need) +
+                                           " bytes, 256-aligned");
   DenseArgs a{};
   a.H = H;
   a.HQ = HQ;
-  a.G = HQ / H;
+  a.G = G;
   a.scale_log2 = scale * 1.4426950408889634f;
   a.q = q;
   a.q_row_stride = q_row_stride;
@@ -337,42 +478,27 @@ int dense_decode_paged(int H, int HQ, int d, float scale, const void* q, int64_t
   a.dtype = dtype;
   a.n_slots = n_slots;
   a.block_size = block_size;
+  a.bs_shift = __builtin_ctz((unsigned)block_size);
   a.bt = bt;
   a.bt_row_stride = bt_row_stride;
-  a.seq_lens = seq_lens;
-  a.qsl = qsl;
-  a.num_reqs = num_reqs;
   a.out = out;
   a.out_row_stride = out_row_stride;
   a.max_seq = max_seq_len;
-  if (a.G < 1 || a.G > 4) return host_fail(TTKV_E_UNSUPPORTED, "G must be 1..4 for the dense comparator");
-  if (H > kMaxCounters) return host_fail(TTKV_E_UNSUPPORTED, "H");
-  const bool multi = dense_chunk_for(dense_slice_reqs(H, num_reqs), H, max_seq_len, block_size) <
-                     max_seq_len;
-  if (multi) {
-    const int64_t need = dense_workspace_bytes(H, a.G, num_reqs, max_seq_len, block_size);
-    if (!ws || ws_bytes < need || (uintptr_t)ws % 256)
-      return host_fail(TTKV_E_WORKSPACE, "dense workspace needs " + std::to_string(need) +
-                                             " bytes, 256-aligned");
-  }
-  const int slice = dense_slice_reqs(H, num_reqs);
+  a.target = dense_target(G, dtype);
+  a.chunk_cap = dense_chunk_cap(block_size);
+  a.ws_part = (float*)ws;
+  const int slice = dense_slice_reqs(num_reqs);
   for (int r0 = 0; r0 < num_reqs; r0 += slice) {
     DenseArgs b = a;
     b.num_reqs = std::min(slice, num_reqs - r0);
     b.seq_lens = seq_lens + r0;
     b.qsl = qsl + r0;
     b.bt = bt + (int64_t)r0 * bt_row_stride;
-    b.chunk = dense_chunk_for(b.num_reqs, H, max_seq_len, block_size);
-    b.max_chunks = std::max(1, (max_seq_len + b.chunk - 1) / b.chunk);
-    if (b.max_chunks > 1) {  // counters [r * H + h] <= kMaxCounters
-      b.ws_cnt = (int*)ws;
-      b.ws_part = (float*)((char*)ws + kCounterBytes);
-    }
-    b.nwork = b.num_reqs * b.max_chunks * H;
-    const int grid = (b.nwork + 7) / 8 * 8;
+    const int64_t items = dense_max_items(b.num_reqs, max_seq_len, block_size, a.target);
+    const int grid = (int)((items + 7) / 8 * 8);
     const bool f16 = dtype == TTKV_DTYPE_F16;
     int rc = TTKV_OK;
-    switch (a.G) {
+    switch (G) {
       case 1: rc = f16 ? launch_dense_t<1, TTKV_DTYPE_F16>(b, grid, st) : launch_dense_t<1, TTKV_DTYPE_BF16>(b, grid, st); break;
       case 2: rc = f16 ? launch_dense_t<2, TTKV_DTYPE_F16>(b, grid, st) : launch_dense_t<2, TTKV_DTYPE_BF16>(b, grid, st); break;
       case 3: rc = f16 ? launch_dense_t<3, TTKV_DTYPE_F16>(b, grid, st) : launch_dense_t<3, TTKV_DTYPE_BF16>(b, grid, st); break;
