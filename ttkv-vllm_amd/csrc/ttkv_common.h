@@ -188,6 +188,27 @@ __device__ __forceinline__ void store_agent8(float* p, float2v v) {
   __asm__ volatile("global_store_dwordx2 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
 }
 
+// Split-K hand-off, read side. The partials were stored write-through at agent scope (above, or
+// agent-scope atomic stores) and completed (s_waitcnt vmcnt(0)) before their workgroup's
+// arrival-counter RMW, so once the last workgroup sees the count complete it reads them with
+// agent-scope loads, which are coherent across the XCDs' L2 caches. Neither side needs a
+// cache-wide operation: an acquire-release RMW writes back the XCD's whole L2 before the RMW and
+// invalidates it after, which measured ~2.7 us per workgroup on the release side and 7-14 us of
+// the combining workgroup's tail on the acquire side (K1 headline: 136 -> 125 us per launch).
+// K1 and K3 use this; the continuation kernels keep the acquire-release counter and plain loads
+// after the acquire, which their combine loops batch better (agent-scope loads there measured
+// 280 against 254 us per config-4 launch).
+__device__ __forceinline__ float ld_agent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float4v ld_agent4(const float* p) {
+  return float4v{ld_agent(p), ld_agent(p + 1), ld_agent(p + 2), ld_agent(p + 3)};
+}
+// The arrival counter: relaxed (the ordering comes from the completed write-through stores).
+__device__ __forceinline__ int arrive(int* cnt) {
+  return __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Four consecutive activations from element i (a multiple of 4) with one store, where `vec` says
 // the tensor's rows are aligned for it; element stores otherwise.
 __device__ __forceinline__ void store_act4(void* p, int dt, int64_t i, float4v v, bool vec);

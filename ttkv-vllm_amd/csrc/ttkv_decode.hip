@@ -36,7 +36,8 @@
 //             (c - 2^(b-1)). The V^T operand is read straight from the decoded code rows with
 //             the gfx950 LDS transpose read (ds_read_tr8_b64); P'^T from a per-wave LDS row.
 // Chunks of one (r, h) are combined in the same launch by the last workgroup to finish
-// (device-scope fence + counter), which also resets the counter to zero. The counters sit at the
+// (write-through partials + a relaxed arrival counter, agent-scope loads), which also resets the
+// counter to zero. The counters sit at the
 // workspace's fixed 64 KiB head, the partials after it, indexed by (chunk item) so their count
 // follows the plan.
 //
@@ -118,7 +119,7 @@ struct DecodeSmem {
 // One-round split-K combine for up to NC chunks: each thread requests every chunk's (max, sum,
 // output) value for its outputs (it = tid + u * kThreads) in one round, then combines them in
 // registers. Chunks past n_chunks re-read the last one and are not used. The partials were
-// written through to the device-coherent level and an agent-scope acquire precedes this.
+// written through to the device-coherent level and are read with agent-scope loads.
 template <int G, int NC>
 __device__ __forceinline__ void combine_regs(const float* pbase, int64_t cstride, int n_chunks,
                                              int tid, void* out, int out_dtype, int64_t orow,
@@ -133,9 +134,9 @@ __device__ __forceinline__ void combine_regs(const float* pbase, int64_t cstride
 #pragma unroll
     for (int cc = 0; cc < NC; ++cc) {
       const float* pc = pbase + min(cc, n_chunks - 1) * cstride + p * (kD + 2);
-      mv[u][cc] = pc[kD];
-      lv[u][cc] = pc[kD + 1];
-      ov[u][cc] = pc[dim];
+      mv[u][cc] = ld_agent(&pc[kD]);
+      lv[u][cc] = ld_agent(&pc[kD + 1]);
+      ov[u][cc] = ld_agent(&pc[dim]);
     }
   }
 #pragma unroll
@@ -827,17 +828,15 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (tid == 0) {
-    const int prev = __hip_atomic_fetch_add(&a.ws_cnt[r * g.H + h], 1, __ATOMIC_ACQ_REL,
-                                            __HIP_MEMORY_SCOPE_AGENT);
+    const int prev = arrive(&a.ws_cnt[r * g.H + h]);
     S.is_last = (prev == n_chunks - 1);
   }
   __syncthreads();
   if (!S.is_last) return;
-  // Every partial is complete in L2 (write-through stores, waited on before their counter
-  // update). An agent-scope acquire drops this CU's L1 copies, after which plain loads see the
-  // partials -- and, unlike atomic loads, the loads of all chunks can be in flight together.
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  auto ld_agent = [](const float* p) { return *p; };
+  // Every partial was stored write-through and completed before its counter update, so the
+  // agent-scope loads below (ld_agent: coherent across the XCDs' L2s, with no L2 invalidate) see
+  // them; the loads of all chunks are in flight together.
+
   const float* pbase = a.ws_part + ((int64_t)base * g.H + h) * pstride;
   const int64_t cstride = (int64_t)g.H * pstride;  // between chunks of one request and head
   // Many chunks: weights in LDS (the tile buffers are free now) -- every chunk's (max, sum) in

@@ -205,16 +205,15 @@ __global__ __launch_bounds__(kWThreads) void write_project_kernel(WriteArgs a) {
   }
   // Hand-off to the token's last workgroup: the partials above are agent-scope (write-through)
   // stores, completed (vmcnt) and ordered before the counter update by the barrier; the counter
-  // update is an acquire-release RMW, and the last workgroup takes an agent-scope acquire before
-  // it reads the other heads' partials.
+  // update is relaxed, and the last workgroup reads the other heads' partials with agent-scope
+  // loads (no cache-wide writeback or invalidate on either side).
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (tid == 0)
-    is_last = __hip_atomic_fetch_add(&a.ws_cnt[il], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
-              g.H - 1;
+    is_last = arrive(&a.ws_cnt[il]) == g.H - 1;
   __syncthreads();
   if (!is_last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+
   // c[a] = sum over heads in head order
   float* cq = a.ws_q + (int64_t)il * (g.r1 + 1);
   float mx = 0.f;
