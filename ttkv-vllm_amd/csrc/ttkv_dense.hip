@@ -23,9 +23,10 @@
 //       accumulates P.V in fp32. The two streams of a head group are merged through LDS. A
 //       request with one chunk is written out directly; otherwise the item's unnormalised
 //       partials (o, max, sum per head and query head) go to the workspace.
-//   dense_reduce_kernel : one workgroup per (request, KV head) with two or more chunks, from the
-//       same device plan: the per-(head, query head) max and normaliser over the chunks, then
-//       each output as one weighted sum of the chunks' partials.
+//   dense_reduce_kernel : one wave per (request, query head) with two or more chunks: the
+//       chunks' maxima and sums one per lane, their weights through LDS, two output dims per
+//       lane with a batch of up to 64 chunks' loads in flight together. The decode launch
+//       leaves each request's (first item, chunk count) at the head of the workspace.
 #include <math.h>
 
 #include "ttkv_device.h"
@@ -37,7 +38,7 @@ constexpr int kDSeg = 1026;     // block ids of one chunk staged in LDS
 constexpr int kDPlanLanes = 4;  // requests per lane in the work plan (256 per launch)
 constexpr int kDHeads = 8;      // KV heads the kernel is built for (2 head groups of 4)
 constexpr int kDGran = 16;      // chunk granularity in tokens
-constexpr int kDRThreads = 512; // reduction workgroup: one thread per output (G * d <= 512)
+constexpr int kDMetaBytes = 4096;  // workspace head: (first item, chunk count) per request
 
 struct DenseArgs {
   int H, HQ, G;
@@ -56,6 +57,7 @@ struct DenseArgs {
   int num_reqs;
   void* out;
   int64_t out_row_stride;
+  int2* ws_meta;   // [requests] (first item, chunk count), written by the decode launch
   float* ws_part;  // [items][H][G][kD + 2]
   int target;      // work items aimed at (resident workgroups of the launch)
   int chunk_cap;   // longest chunk in tokens (a multiple of 64 whose block ids fit the LDS stage)
@@ -88,14 +90,18 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
 }
 
 // The device work plan, computed alike by every wave of both kernels: the chunk length and each
-// request's chunk count and first item. Item `it` (or, for the reduction, request `rq`) resolves
-// to its request, chunk, context length and the request's first item and chunk count.
+// request's chunk count and first item. Block `blk` of the decode launch (rq < 0), or request
+// `rq` of the reduction, resolves to its item, request, chunk, context length and the request's
+// first item and chunk count. Blocks are dealt to the 8 XCDs round-robin, so each XCD takes a
+// contiguous range of ceil(items / 8) items: sized by the items, not by the grid (which is sized
+// for the most items any batch of the launch's shape can plan), so that no XCD receives more
+// items than it has resident slots while another idles.
 struct DensePlan {
   int chunk, n_items;
-  int r, c, seq, first, n_chunks;
+  int it, r, c, seq, first, n_chunks;
 };
 
-__device__ __forceinline__ DensePlan dense_plan(const DenseArgs& a, int it, int rq) {
+__device__ __forceinline__ DensePlan dense_plan(const DenseArgs& a, int blk, int rq) {
   const int lane = threadIdx.x & 63;
   const int nper = (a.num_reqs + 63) >> 6;
   int sl[kDPlanLanes], nch[kDPlanLanes], ex[kDPlanLanes];
@@ -121,6 +127,12 @@ __device__ __forceinline__ DensePlan dense_plan(const DenseArgs& a, int it, int 
   }
   P.n_items = carry;
   P.n_chunks = 0;
+  int it = 0;
+  if (rq < 0) {
+    const int per_xcd = (P.n_items + 7) >> 3;
+    it = (blk >> 3) < per_xcd ? (blk & 7) * per_xcd + (blk >> 3) : P.n_items;
+  }
+  P.it = it;
 #pragma unroll
   for (int i = 0; i < kDPlanLanes; ++i) {
     const int rr = lane + 64 * i;
@@ -145,18 +157,21 @@ __global__ __launch_bounds__(kDThreads, 2) void dense_decode_kernel(DenseArgs a)
   __shared__ float red_m[4][4][G], red_l[4][4][G];
   __shared__ int seg[kDSeg];
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wv = tid >> 6;
+  // the wave index and the item's bounds in scalar registers: the streaming loop's trip count is
+  // uniform (scalar branches, no exec-mask bookkeeping around the loads)
+  const int lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hl = lane >> 4;   // head within the group
   const int sub = lane & 15;  // dims 8*sub .. 8*sub+7
   const int hg = wv & 1, stream = wv >> 1;
   const int head = 4 * hg + hl;
 
-  const int per_xcd_slots = gridDim.x >> 3;
-  const int it = (blockIdx.x & 7) * per_xcd_slots + (blockIdx.x >> 3);
-  const DensePlan P = dense_plan(a, it, -1);
+  const DensePlan P = dense_plan(a, blockIdx.x, -1);
+  const int it = P.it;
   if (it >= P.n_items) return;
+  if (P.c == 0 && tid == 0) a.ws_meta[P.r] = make_int2(P.first, P.n_chunks);
   const int64_t qrow = a.qsl[P.r];
-  const int t0 = P.c * P.chunk, t1 = min(P.seq, t0 + P.chunk);
+  const int t0 = __builtin_amdgcn_readfirstlane(P.c * P.chunk);
+  const int t1 = __builtin_amdgcn_readfirstlane(min(P.seq, t0 + P.chunk));
   if (t1 <= t0) {  // empty context: the attention over zero rows is 0
     for (int i = tid; i < a.HQ * kD; i += kDThreads)
       store_act(a.out, DT, qrow * a.out_row_stride + i, 0.f);
@@ -192,29 +207,27 @@ __global__ __launch_bounds__(kDThreads, 2) void dense_decode_kernel(DenseArgs a)
   const int bmask = a.block_size - 1;
   const int lane_off = head * kD + 8 * sub;  // elements within a slot's row
   constexpr int64_t kRow = (int64_t)kDHeads * kD;
-  const uint4 zero4 = make_uint4(0, 0, 0, 0);
   constexpr int kStep = 4;  // tokens per wave step
+  // Loads are unconditional (positions past the chunk re-read its last row, whose scores are
+  // masked to -inf), issued in the same order in every copy of the step, from a wave-uniform row
+  // address plus the lane's 32-bit offset: with a branch per token the compiler could not count
+  // the loads in flight across the join and waited for all of them, the next step's included,
+  // before any use (headline 100 -> 83 us per launch with the two register sets below).
+  const uint32_t lane_byte = (uint32_t)lane_off * 2u;
   auto load_step = [&](int tb, uint4* kx, uint4* vx) {
 #pragma unroll
     for (int u = 0; u < kStep; ++u) {
-      const int t = tb + u;
-      if (t < t1) {
-        const int64_t slot = (int64_t)seg[(t >> a.bs_shift) - bfirst] * a.block_size + (t & bmask);
-        const int64_t off = slot * kRow + lane_off;
-        kx[u] = ld_stream16(a.kc + off);
-        vx[u] = ld_stream16(a.vc + off);
-      } else {
-        kx[u] = zero4;
-        vx[u] = zero4;
-      }
+      const int t = min(tb + u, t1 - 1);
+      const int blk = __builtin_amdgcn_readfirstlane(seg[(t >> a.bs_shift) - bfirst]);
+      const int64_t slot = (int64_t)blk * a.block_size + (t & bmask);
+      const char* kr = (const char*)a.kc + slot * (kRow * 2);
+      const char* vr = (const char*)a.vc + slot * (kRow * 2);
+      kx[u] = ld_stream16(kr + lane_byte);
+      vx[u] = ld_stream16(vr + lane_byte);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
-  uint4 kx[kStep], vx[kStep];
-  int tb = t0 + kStep * stream;
-  load_step(tb, kx, vx);
-  for (; tb < t1; tb += kStep * NST) {
-    uint4 kn[kStep], vn[kStep];
-    load_step(tb + kStep * NST, kn, vn);
+  auto step = [&](int tb, const uint4* kx, const uint4* vx) {
     float s[G][kStep];
 #pragma unroll
     for (int u = 0; u < kStep; ++u) {
@@ -267,11 +280,23 @@ __global__ __launch_bounds__(kDThreads, 2) void dense_decode_kernel(DenseArgs a)
 #pragma unroll
         for (int i = 0; i < 8; ++i) o[p][i] = fmaf(s[p][u], vf[i], o[p][i]);
     }
-#pragma unroll
-    for (int u = 0; u < kStep; ++u) {
-      kx[u] = kn[u];
-      vx[u] = vn[u];
-    }
+  };
+  // Two register sets in turn, so the next step's loads are in flight during a step; the
+  // scheduling barriers keep the compiler from hoisting a step's arithmetic above them.
+  constexpr int kAdv = kStep * NST;  // tokens between a stream's consecutive steps
+  uint4 ka[kStep], va[kStep], kb[kStep], vb[kStep];
+  int tb = t0 + kStep * stream;
+  load_step(tb, ka, va);
+  while (tb < t1) {
+    load_step(tb + kAdv, kb, vb);
+    __builtin_amdgcn_sched_barrier(0);
+    step(tb, ka, va);
+    tb += kAdv;
+    if (tb >= t1) break;
+    load_step(tb + kAdv, ka, va);
+    __builtin_amdgcn_sched_barrier(0);
+    step(tb, kb, vb);
+    tb += kAdv;
   }
   // ---- merge the two streams of each head group through LDS
   if (sub == 0) {
@@ -324,56 +349,59 @@ __global__ __launch_bounds__(kDThreads, 2) void dense_decode_kernel(DenseArgs a)
   }
 }
 
-// One workgroup per (request, KV head) whose request has two or more chunks: the chunks'
-// partials combined into the output. The partials were written by the previous launch.
+// One wave per (request, query head) whose request has two or more chunks: the chunks' partials
+// combined into the output, in batches of up to 64 chunks. Lane c holds chunk c's max and sum;
+// the chunk weights go through LDS to every lane, and each lane combines two output dims, with
+// all of the batch's output loads in flight together. The request's item range comes from the
+// decode launch (no plan here).
 template <int G, int DT>
-__global__ __launch_bounds__(kDRThreads) void dense_reduce_kernel(DenseArgs a) {
-  __shared__ float comb[G][2];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int rq = blockIdx.x / kDHeads, h = blockIdx.x % kDHeads;
+__global__ __launch_bounds__(64) void dense_reduce_kernel(DenseArgs a) {
+  __shared__ float wgt[64];
+  const int lane = threadIdx.x;
+  const int rq = blockIdx.x / a.HQ, hq = blockIdx.x % a.HQ;
   if (rq >= a.num_reqs) return;
-  const DensePlan P = dense_plan(a, 0, rq);
-  if (P.n_chunks <= 1) return;
-  const int64_t hstride = (int64_t)G * (kD + 2);
-  const int64_t cstride = (int64_t)kDHeads * hstride;  // between consecutive items
-  const float* pbase = a.ws_part + ((int64_t)P.first * kDHeads + h) * hstride;
-  if (wv < G) {  // wave p: max and normaliser of query head p
-    const int p = wv;
-    float mx = -INFINITY;
-    for (int cc = lane; cc < P.n_chunks; cc += 64)
-      mx = fmaxf(mx, pbase[cc * cstride + p * (kD + 2) + kD]);
-    mx = wave_max(mx);
-    float Ls = 0.f;
-    for (int cc = lane; cc < P.n_chunks; cc += 64) {
-      const float* pc = pbase + cc * cstride + p * (kD + 2);
-      Ls = fmaf(pc[kD + 1], exp2f(pc[kD] - mx), Ls);
-    }
-    Ls = wave_sum(Ls);
-    if (lane == 0) {
-      comb[p][0] = mx;
-      comb[p][1] = 1.f / Ls;
-    }
-  }
-  __syncthreads();
-  if (tid >= G * kD) return;
-  const int64_t qrow = a.qsl[P.r];
-  const int p = tid / kD, d = tid % kD;
-  const float mx = comb[p][0];
-  const float* ph = pbase + p * (kD + 2);
-  float O = 0.f;
-  int cc = 0;
-  for (; cc + 16 <= P.n_chunks; cc += 16) {  // 16 chunks' loads in flight together
-    float mv[16], ov[16];
+  const int2 meta = a.ws_meta[rq];
+  const int first = meta.x, nch = meta.y;
+  if (nch <= 1) return;
+  const int h = hq / G, p = hq % G;
+  const int64_t cstride = (int64_t)kDHeads * G * (kD + 2);  // between consecutive items
+  const float* ph = a.ws_part + ((int64_t)first * kDHeads + h) * G * (kD + 2) + p * (kD + 2);
+  float M = -INFINITY, L = 0.f, O0 = 0.f, O1 = 0.f;
+  for (int c0 = 0; c0 < nch; c0 += 64) {
+    const int nb = min(64, nch - c0);
+    // chunks past the batch re-read its last chunk (valid, finite) and get weight 0
+    const float* pl = ph + (int64_t)(c0 + min(lane, nb - 1)) * cstride;
+    const float mc = lane < nb ? pl[kD] : -INFINITY;
+    const float lc = pl[kD + 1];
+    float2v ov[64];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      mv[j] = ph[(cc + j) * cstride + kD];
-      ov[j] = ph[(cc + j) * cstride + d];
-    }
+    for (int j = 0; j < 64; ++j)
+      ov[j] = *(const float2v*)(ph + (int64_t)(c0 + min(j, nb - 1)) * cstride + 2 * lane);
+    const float mb = fmaxf(M, wave_max(mc));
+    // a non-empty chunk's max is finite, so mb is; the running terms start at zero
+    const float f = M == -INFINITY ? 0.f : exp2f(M - mb);
+    const float wc = mc == -INFINITY ? 0.f : exp2f(mc - mb);
+    L = fmaf(L, f, wave_sum(lc * wc));
+    wgt[lane] = wc;
+    __syncthreads();
+    O0 *= f;
+    O1 *= f;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) O = fmaf(ov[j], exp2f(mv[j] - mx), O);
+    for (int j = 0; j < 64; j += 4) {
+      const float4v w = *(const float4v*)&wgt[j];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        O0 = fmaf(ov[j + k][0], w[k], O0);
+        O1 = fmaf(ov[j + k][1], w[k], O1);
+      }
+    }
+    __syncthreads();  // wgt is rewritten by the next batch
+    M = mb;
   }
-  for (; cc < P.n_chunks; ++cc) O = fmaf(ph[cc * cstride + d], exp2f(ph[cc * cstride + kD] - mx), O);
-  store_act(a.out, DT, qrow * a.out_row_stride + (int64_t)(h * G + p) * kD + d, O * comb[p][1]);
+  const float inv = 1.f / L;
+  const int64_t ob = (int64_t)a.qsl[rq] * a.out_row_stride + (int64_t)hq * kD + 2 * lane;
+  store_act(a.out, DT, ob, O0 * inv);
+  store_act(a.out, DT, ob + 1, O1 * inv);
 }
 
 }  // namespace ttkv
@@ -426,13 +454,14 @@ int64_t dense_workspace_bytes(int H, int G, int num_reqs, int max_seq_len, int b
   if (num_reqs <= 0 || G < 1 || G > 4 || H != kDHeads) return 256;
   const int slice = std::max(1, dense_slice_reqs(num_reqs));
   const int target = std::max(dense_target(G, TTKV_DTYPE_F16), dense_target(G, TTKV_DTYPE_BF16));
-  return dense_max_items(slice, max_seq_len, block_size, target) * kDHeads * G * (kD + 2) * 4;
+  return kDMetaBytes + dense_max_items(slice, max_seq_len, block_size, target) * kDHeads * G *
+                            (kD + 2) * 4;
 }
 
 template <int G, int DT>
 static int launch_dense_t(const DenseArgs& a, int grid, hipStream_t st) {
   hipLaunchKernelGGL((dense_decode_kernel<G, DT>), dim3(grid), dim3(kDThreads), 0, st, a);
-  hipLaunchKernelGGL((dense_reduce_kernel<G, DT>), dim3(a.num_reqs * kDHeads), dim3(kDRThreads), 0,
+  hipLaunchKernelGGL((dense_reduce_kernel<G, DT>), dim3(a.num_reqs * a.HQ), dim3(64), 0,
                      st, a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess)
@@ -486,7 +515,8 @@ int dense_decode_paged(int H, int HQ, int d, float scale, const void* q, int64_t
   a.max_seq = max_seq_len;
   a.target = dense_target(G, dtype);
   a.chunk_cap = dense_chunk_cap(block_size);
-  a.ws_part = (float*)ws;
+  a.ws_meta = (int2*)ws;
+  a.ws_part = (float*)((char*)ws + kDMetaBytes);
   const int slice = dense_slice_reqs(num_reqs);
   for (int r0 = 0; r0 < num_reqs; r0 += slice) {
     DenseArgs b = a;
