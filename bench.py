@@ -444,7 +444,8 @@ def bench_dense(torch, lens, q, dev, steps=3, warmup=1, n_layers=L_LAYERS):
     ms = time_back_to_back(torch, run, steps * n_layers, warmup * n_layers)
     ms_ev = time_launches(torch, run, steps * n_layers, warmup * n_layers)
     del kcs, vcs
-    res = dict(us_per_layer=ms * 1e3, hbm_gbps=sum(lens) * H * D * 2 * 2 / (ms * 1e-3) / 1e9,
+    gbps = sum(lens) * H * D * 2 * 2 / (ms * 1e-3) / 1e9
+    res = dict(us_per_layer=ms * 1e3, hbm_gbps=gbps, hbm_frac=gbps / HBM_PEAK_GBPS,
                ns_per_cached_token=ms * 1e6 / sum(lens), layers_cycled=n_layers,
                us_per_layer_launch_events=ms_ev * 1e3)
     try:
@@ -784,12 +785,12 @@ def main():
         dn["compressed_ns_per_cached_token"] = ml * 1e6 / sum(lens3)
         extra["config3_dense_fp16_comparator"] = dn
         log(f"dense fp16 comparator (config 3 shapes): {dn['us_per_layer']:.1f} us/layer, "
-            f"{dn['hbm_gbps']:.0f} GB/s")
+            f"{dn['hbm_gbps']:.0f} GB/s ({100 * dn['hbm_frac']:.0f} % of HBM peak)")
         dh = bench_dense(torch, lens, q, dev)
         dh["compressed_ns_per_cached_token"] = ms_launch * 1e6 / sum(lens)
         extra["headline_dense_fp16_comparator"] = dh
         log(f"dense fp16 comparator (8x14402): {dh['us_per_layer']:.1f} us/layer, "
-            f"{dh['hbm_gbps']:.0f} GB/s")
+            f"{dh['hbm_gbps']:.0f} GB/s ({100 * dh['hbm_frac']:.0f} % of HBM peak)")
         extra["config4_continuation"] = bench_config4(torch, lay, cfg, cache, dev,
                                                       cpu=not args.no_cpu)
         extra["config5_4bit_read_write"] = bench_config5(torch, cache, dev, cpu=not args.no_cpu)

@@ -141,10 +141,12 @@ int ttkv_decode_paged_noalloc(const ttkv_layout* lay, int32_t num_heads, float s
  *   written, so the host registry can evict decoders by last use (the caller clears it).
  * slot_mapping entries < 0 are vLLM's PAD_SLOT_ID (padded tokens of a replayed graph): skipped
  *   silently, as vLLM's cache writers do; entries past the cache set TTKV_ERR_BAD_SLOT.
- * key/value: [N, H, d] rows with the given element stride between tokens.
+ * key/value: [N, H, d] rows with the given element stride between tokens. dec_pool must be
+ *   8-byte aligned (TTKV_E_INVALID otherwise).
  * Work is spread over (token, KV head) workgroups in two launches: per-head partial projections
  * (the token's last workgroup sums them in head order and quantises) and, per head, the residual
- * and the K and V rows. The partials live in `workspace` (ttkv_write_workspace_bytes). */
+ * and the K and V rows. The partials and each token's decoder slot live in `workspace`
+ * (ttkv_write_workspace_bytes). */
 int ttkv_write_paged(const ttkv_layout* lay, const void* key, int32_t k_dtype, int64_t k_row_stride,
                      const void* value, int32_t v_dtype, int64_t v_row_stride,
                      const int64_t* slot_mapping, int32_t num_tokens,

@@ -101,7 +101,7 @@ def _write_call(lay, **kw):
     L = _hip.lib()
     a = dict(key=1, k_dtype=1, k_row_stride=1024, value=1, v_dtype=1, v_row_stride=1024,
              slot_mapping=1, num_tokens=4, qsl=1, num_reqs=1, block_table=1, bt_row_stride=1,
-             dec_map=1, num_blocks=1, dec_pool=1, pinv_pool=1, n_dec=1, dec_used=0, cq_in=0,
+             dec_map=1, num_blocks=1, dec_pool=16, pinv_pool=1, n_dec=1, dec_used=0, cq_in=0,
              cs_in=0,
              page=4096, n_slots=16, slot_stride=912, c_out=0, r_out=0, ws=256, ws_bytes=1 << 20,
              err=1)
@@ -150,6 +150,7 @@ def test_write_host_refusals_before_launch():
     assert _write_call(safe, key=0) == 1 and b"null" in L.ttkv_last_error()
     assert _write_call(safe, v_dtype=5) == 1 and b"dtype" in L.ttkv_last_error()
     assert _write_call(safe, ws=0) == 4 and b"workspace" in L.ttkv_last_error()
+    assert _write_call(safe, dec_pool=4) == 1 and b"8-byte aligned" in L.ttkv_last_error()
     assert _write_call(safe, num_tokens=0) == 0                          # nothing to do
 
 

@@ -63,26 +63,34 @@ struct WriteArgs {
   int* ws_cnt;      // [num_tokens] arrival counters (zero between calls)
   float* ws_part;   // [num_tokens][H][r1] per-head partial projections
   float* ws_q;      // [num_tokens][r1 + 1] cq (as floats) then cs
+  int* ws_ds;       // [num_tokens] each token's decoder slot (or -1), from K3a for K3b
   float inv127, inv_rk, inv_rv;
 };
 
 // Request of token i (qsl[r] <= i < qsl[r+1]; qsl is non-decreasing) and its decoder slot, or
-// -1: r + 1 = the number of qsl[0..num_reqs) <= i, counted 64 at a time with one load per lane
-// (one memory round trip for a decode batch instead of a dependent binary search). Every lane of
-// the wave must call it; all get the same answer.
+// -1. Decode tokens come first in a step, one per request, so token i is usually request i: that
+// guess, its first block id and the general count (r + 1 = the number of qsl[0..num_reqs) <= i,
+// 64 per lane with one load each) are requested in one round trip; a confirmed guess leaves only
+// the decoder map's round trip (two in all instead of three). Every lane of the wave must call
+// it; all get the same answer.
 __device__ int token_decoder(const WriteArgs& a, int i) {
   const int lane = threadIdx.x & 63;
+  const bool guess = i < a.num_reqs;
+  const int glo = guess ? a.qsl[i] : 0, ghi = guess ? a.qsl[i + 1] : 0;
+  const int gblk = guess ? a.bt[(int64_t)i * a.bt_row_stride] : -1;
   int cnt = 0;
   for (int j0 = 0; j0 < a.num_reqs; j0 += 64) {
     const int j = j0 + lane;
     cnt += __builtin_popcountll(__ballot(j < a.num_reqs && a.qsl[j] <= i));
   }
-  const int r = cnt - 1;
-  int ds = -1;
-  if (r >= 0 && i < a.qsl[r + 1]) {
-    const int blk0 = a.bt[(int64_t)r * a.bt_row_stride];
-    if (blk0 >= 0 && blk0 < a.num_blocks) ds = a.dec_map[blk0];
+  int blk0 = -1;
+  if (guess && glo <= i && i < ghi) {
+    blk0 = gblk;
+  } else {
+    const int r = cnt - 1;
+    if (r >= 0 && i < a.qsl[r + 1]) blk0 = a.bt[(int64_t)r * a.bt_row_stride];
   }
+  const int ds = blk0 >= 0 && blk0 < a.num_blocks ? a.dec_map[blk0] : -1;
   return (ds < 0 || ds >= a.n_dec_slots) ? -1 : ds;
 }
 
@@ -179,6 +187,7 @@ __global__ __launch_bounds__(kWThreads) void write_project_kernel(WriteArgs a) {
   const float kv = tid < kD ? load_act(a.key, a.k_dtype, (int64_t)i * a.k_row_stride + h * kD + tid)
                             : 0.f;
   const int ds = token_decoder(a, i);
+  if (h == 0 && tid == 0) a.ws_ds[il] = ds;
   if (ds < 0 || slot < 0 || slot >= a.n_slots) return;  // K3b reports it
   if (tid < kD) mk[tid] = kv;
   __syncthreads();
@@ -220,9 +229,17 @@ __global__ __launch_bounds__(kWThreads) void write_project_kernel(WriteArgs a) {
   float cv = 0.f;
   const bool mine = tid < g.r1;
   if (mine) {
+    // every head's partial requested in one round trip (H <= 8, host-checked), then summed in
+    // head order
     const float* base = a.ws_part + (int64_t)il * g.H * g.r1;
-    for (int hh = 0; hh < g.H; ++hh)
-      cv += __hip_atomic_load(&base[hh * g.r1 + tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    float ph[8];
+#pragma unroll
+    for (int hh = 0; hh < 8; ++hh) {
+      const float x = ld_agent(&base[min(hh, g.H - 1) * g.r1 + tid]);
+      ph[hh] = hh < g.H ? x : 0.f;
+    }
+#pragma unroll
+    for (int hh = 0; hh < 8; ++hh) cv += ph[hh];
     mx = fabsf(cv);
     if (a.c_out) a.c_out[(int64_t)i * g.r1 + tid] = cv;
   }
@@ -258,7 +275,23 @@ __global__ __launch_bounds__(kWThreads) void write_pack_kernel(WriteArgs a) {
   // cache are refused.
   if (slot < 0) return;
   const bool slot_ok = slot < a.n_slots;
-  const int ds = token_decoder(a, i);
+  // the rows wave 0 (key) and wave 1 (value) pack, requested now: they depend on nothing
+  float xr0 = 0.f, xr1 = 0.f;
+  if (wv == 0) {
+    const int64_t kb = (int64_t)i * a.k_row_stride + h * kD;
+    xr0 = load_act(a.key, a.k_dtype, kb + lane);
+    xr1 = load_act(a.key, a.k_dtype, kb + 64 + lane);
+  } else if (wv == 1) {
+    const int64_t vb = (int64_t)i * a.v_row_stride + h * kD;
+    xr0 = load_act(a.val, a.v_dtype, vb + lane);
+    xr1 = load_act(a.val, a.v_dtype, vb + 64 + lane);
+  }
+  // the decoder slot: from K3a's lookup when it ran (one load), else looked up here; the
+  // coefficients (K3a's or the fit's) are requested in the same round trip
+  const int ds = a.cq_in ? token_decoder(a, i) : a.ws_ds[il];
+  const float* wq = a.ws_q + (int64_t)il * (g.r1 + 1);
+  const float cs = a.cq_in ? a.cs_in[i] : wq[g.r1];
+  const float qv = tid < g.r1 ? (a.cq_in ? (float)a.cq_in[(int64_t)i * g.r1 + tid] : wq[tid]) : 0.f;
   if (h == 0 && tid == 0) {
     if (!slot_ok) atomicOr(a.err, TTKV_ERR_BAD_SLOT);
     if (ds < 0) atomicOr(a.err, TTKV_ERR_NO_DECODER);
@@ -266,32 +299,22 @@ __global__ __launch_bounds__(kWThreads) void write_pack_kernel(WriteArgs a) {
     if (ds >= 0 && a.dec_used) a.dec_used[ds] = 1;
   }
   if (ds < 0 || !slot_ok) return;
-  // this head's decoder columns (rows a = wv, wv + 4, ...) do not depend on the coefficients:
-  // their loads are issued before the coefficients' round trip (r1 <= kDecRows * 4 here)
-  const float* dec = a.dec_pool + (int64_t)ds * g.r1 * HD + h * kD;
+  // this head's decoder columns (rows a = wv, wv + 4, ...; lane l holds dims 2l and 2l + 1, one
+  // 8-byte load per row), requested before the coefficients are needed (r1 <= kDecRows * 4
+  // here). Rows past r1 re-read row r1 - 1 and are multiplied by 0.
+  const float* dec = a.dec_pool + (int64_t)ds * g.r1 * HD + h * kD + 2 * lane;
   constexpr int kDecRows = 32;
-  float d0[kDecRows], d1[kDecRows];
+  float2v dr[kDecRows];
   const bool dec_regs = g.r1 <= 4 * kDecRows;
   if (dec_regs) {
 #pragma unroll
-    for (int u = 0; u < kDecRows; ++u) {
-      const int ar = wv + 4 * u;
-      d0[u] = ar < g.r1 ? dec[(int64_t)ar * HD + lane] : 0.f;
-      d1[u] = ar < g.r1 ? dec[(int64_t)ar * HD + 64 + lane] : 0.f;
-    }
+    for (int u = 0; u < kDecRows; ++u)
+      dr[u] = *(const float2v*)&dec[(int64_t)min(wv + 4 * u, g.r1 - 1) * HD];
   }
-  const float* wq = a.ws_q + (int64_t)il * (g.r1 + 1);
-  const float cs = a.cq_in ? a.cs_in[i] : wq[g.r1];
-  for (int ar = tid; ar < g.r1; ar += kWThreads) {
-    const float q = a.cq_in ? (float)a.cq_in[(int64_t)i * g.r1 + ar] : wq[ar];
-    cqs[ar] = q * cs;
-  }
+  if (tid < g.r1) cqs[tid] = qv * cs;  // r1 <= 256 threads (host-checked)
   uint8_t* base = a.page + slot * a.slot_stride;
   if (h == 0) {
-    for (int ar = tid; ar < g.r1; ar += kWThreads) {
-      const float q = a.cq_in ? (float)a.cq_in[(int64_t)i * g.r1 + ar] : wq[ar];
-      base[ar] = (uint8_t)(int8_t)(int)q;
-    }
+    if (tid < g.r1) base[tid] = (uint8_t)(int8_t)(int)qv;
     if (tid == 0) {
       const uint16_t hb = __builtin_bit_cast(uint16_t, (_Float16)cs);
       base[g.coeff_bytes] = (uint8_t)(hb & 0xff);
@@ -301,52 +324,45 @@ __global__ __launch_bounds__(kWThreads) void write_pack_kernel(WriteArgs a) {
     for (int b = g.k_slot + g.H * g.v_row + tid; b < g.blob; b += kWThreads) base[b] = 0;
   }
   __syncthreads();
-  // R[j] = K[h*d+j] - sum_a cqs[a] * dec[a][h*d+j]: wave w sums a = w, w+4, ...; lanes own j, j+64
+  // R[j] = K[h*d+j] - sum_a cqs[a] * dec[a][h*d+j]: wave w sums a = w, w+4, ...; lane l owns
+  // dims 2l and 2l + 1
   float acc0 = 0.f, acc1 = 0.f;
   if (dec_regs) {
 #pragma unroll
     for (int u = 0; u < kDecRows; ++u) {
       const int ar = wv + 4 * u;
       const float c = ar < g.r1 ? cqs[ar] : 0.f;
-      acc0 = fmaf(c, d0[u], acc0);
-      acc1 = fmaf(c, d1[u], acc1);
+      acc0 = fmaf(c, dr[u][0], acc0);
+      acc1 = fmaf(c, dr[u][1], acc1);
     }
   }
   // larger ranks: rows in batches of 16 whose loads are all issued before their sums
   for (int a0 = wv; !dec_regs && a0 < g.r1; a0 += 64) {
-    float d0[16], d1[16];
+    float2v db[16];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const int ar = a0 + 4 * u;
-      d0[u] = ar < g.r1 ? dec[(int64_t)ar * HD + lane] : 0.f;
-      d1[u] = ar < g.r1 ? dec[(int64_t)ar * HD + 64 + lane] : 0.f;
-    }
+    for (int u = 0; u < 16; ++u)
+      db[u] = *(const float2v*)&dec[(int64_t)min(a0 + 4 * u, g.r1 - 1) * HD];
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
       const int ar = a0 + 4 * u;
       const float c = ar < g.r1 ? cqs[ar] : 0.f;
-      acc0 = fmaf(c, d0[u], acc0);
-      acc1 = fmaf(c, d1[u], acc1);
+      acc0 = fmaf(c, db[u][0], acc0);
+      acc1 = fmaf(c, db[u][1], acc1);
     }
   }
-  rp[wv][lane] = acc0;
-  rp[wv][64 + lane] = acc1;
+  rp[wv][2 * lane] = acc0;
+  rp[wv][2 * lane + 1] = acc1;
   __syncthreads();
   if (wv == 0) {
-    const int64_t kb = (int64_t)i * a.k_row_stride + h * kD;
-    float r0 = load_act(a.key, a.k_dtype, kb + lane) -
-               (((rp[0][lane] + rp[1][lane]) + rp[2][lane]) + rp[3][lane]);
-    float r1v = load_act(a.key, a.k_dtype, kb + 64 + lane) -
-                (((rp[0][64 + lane] + rp[1][64 + lane]) + rp[2][64 + lane]) + rp[3][64 + lane]);
+    float r0 = xr0 - (((rp[0][lane] + rp[1][lane]) + rp[2][lane]) + rp[3][lane]);
+    float r1v = xr1 - (((rp[0][64 + lane] + rp[1][64 + lane]) + rp[2][64 + lane]) + rp[3][64 + lane]);
     if (a.r_out) {
       a.r_out[(int64_t)i * HD + h * kD + lane] = r0;
       a.r_out[(int64_t)i * HD + h * kD + 64 + lane] = r1v;
     }
     pack_row<RB>(r0, r1v, g.res_k, a.inv_rk, base + g.k_field + h * g.k_row, codes[0]);
   } else if (wv == 1) {
-    const int64_t vb = (int64_t)i * a.v_row_stride + h * kD;
-    pack_row<VB>(load_act(a.val, a.v_dtype, vb + lane), load_act(a.val, a.v_dtype, vb + 64 + lane),
-                 g.v_lanes, a.inv_rv, base + g.k_slot + h * g.v_row, codes[1]);
+    pack_row<VB>(xr0, xr1, g.v_lanes, a.inv_rv, base + g.k_slot + h * g.v_row, codes[1]);
   }
 }
 
@@ -355,7 +371,7 @@ static float inv_ruler_f32(int bits) { return (float)(1.0 / (double)((1 << (bits
 // Tokens per launch: one arrival counter each.
 int64_t write_workspace_bytes(const Geom& g, int num_tokens) {
   const int64_t nt = std::min(std::max(num_tokens, 0), kMaxCounters);
-  return kCounterBytes + nt * (g.H * g.r1 + g.r1 + 1) * 4;
+  return kCounterBytes + nt * (g.H * g.r1 + g.r1 + 2) * 4;
 }
 
 int write_paged(const Geom& g, const void* key, int k_dtype, int64_t k_row_stride, const void* val,
@@ -390,6 +406,8 @@ int write_paged(const Geom& g, const void* key, int k_dtype, int64_t k_row_strid
                                              " bytes (256-aligned), got " +
                                              std::to_string(ws_bytes));
   }
+  if ((uintptr_t)dec_pool % 8)
+    return host_fail(TTKV_E_INVALID, "dec_pool must be 8-byte aligned");
   WriteArgs a{};
   a.g = g;
   a.key = key;
@@ -429,6 +447,7 @@ int write_paged(const Geom& g, const void* key, int k_dtype, int64_t k_row_strid
       b.ws_cnt = (int*)ws;
       b.ws_part = (float*)((char*)ws + kCounterBytes);
       b.ws_q = b.ws_part + (int64_t)b.num_tokens * g.H * g.r1;
+      b.ws_ds = (int*)(b.ws_q + (int64_t)b.num_tokens * (g.r1 + 1));
     }
     const int grid = b.num_tokens * g.H;
     if (!cq_in) hipLaunchKernelGGL(write_project_kernel, dim3(grid), dim3(kWThreads), 0, st, b);
