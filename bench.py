@@ -664,6 +664,8 @@ def main():
                     help="only the container-layout reads (krt + v_out at 8 x 14402); prints its line")
     ap.add_argument("--first-chunk-only", action="store_true",
                     help="only the first-chunk timings (attention, fit, write at 2048 / 8192)")
+    ap.add_argument("--dense-only", action="store_true",
+                    help="only the dense fp16 paged comparator (headline and config 3 shapes)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 1 GiB device copy (HBM-counter calibration for rocprofv3)")
     args = ap.parse_args()
@@ -682,6 +684,15 @@ def main():
     lay = layout_for_config(cfg, r1=R1)
     cache = rope.cos_sin_cache(32768, D, device=dev)
     extra = {}
+
+    if args.calib_copy:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log("calibration copy: 1073741824 bytes read + written")
+        del src, dst
 
     if args.config4_only:
         c4 = bench_config4(torch, lay, cfg, cache, dev, args.steps, args.warmup)
@@ -709,6 +720,16 @@ def main():
                               higher_is_better=False, data="synthetic", **fc)))
         return
 
+    if args.dense_only:
+        qd = synth.queries(8, seed=5, device=dev)
+        dh = bench_dense(torch, [14402] * 8, qd, dev, args.steps, args.warmup)
+        d3 = bench_dense(torch, config3_lens(), qd, dev, args.steps, args.warmup)
+        print(json.dumps(dict(metric="dense fp16 paged decode us/layer (comparator)",
+                              value=dh["us_per_layer"], unit="us", n_gpus=1,
+                              higher_is_better=False, dtype="fp16 in/out, fp32 accumulate",
+                              data="synthetic", headline=dh, config3=d3)))
+        return
+
     if args.config5_only:
         c5 = bench_config5(torch, cache, dev, args.steps, args.warmup)
         print(json.dumps(dict(metric="4-bit decode step us/layer, K3 write + K1 read (BASELINE "
@@ -719,15 +740,6 @@ def main():
                                     "accumulate and softmax",
                               data="synthetic", **c5)))
         return
-
-    if args.calib_copy:
-        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        log("calibration copy: 1073741824 bytes read + written")
-        del src, dst
 
     # ---------------------------------------------------------------- headline: B=8 @ 14402
     lens = [14402] * 8
