@@ -50,8 +50,12 @@ def _compare(fit, K, cfg_name):
     step = ref["decoder_f"].abs().amax(1, keepdim=True) / qm
     derr = (dec * sign[:, None] - ref["decoder_f"]).abs()
     assert bool((derr <= 2.01 * step + 1e-6).all())
+    # entries one code apart: the fits' leading vectors near the rank cut converge to ~1e-4 on
+    # flat spectra, so codes near a rounding boundary flip; the share depends on the host BLAS's
+    # thread count for both fits (0.2-1.1 % measured at 1, 8 and 16 threads), hence the same 2 %
+    # bound as the coefficients below
     ulp = 2e-3 * ref["decoder_f"].abs() + 1e-3 * step
-    assert float((derr > ulp).float().mean()) < 1e-2
+    assert float((derr > ulp).float().mean()) < 2e-2
     dq = (cq.to(torch.int32) * sign.to(torch.int32) - ref["coeff_q"].to(torch.int32)).abs()
     assert int(dq.max()) <= 1 and float((dq != 0).float().mean()) < 0.02
     e_mine = _keys_err(fit.coeff_q, fit.coeff_scale, fit.decoder.decoder_f, K)
