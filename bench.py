@@ -330,6 +330,9 @@ def bench_first_chunk(torch, lay, cfg, dev, lengths=(2048, 8192), reps=5):
         dec_map = torch.full((nblk,), -1, dtype=torch.int32, device=dev)
         dec_map[0] = 0
         dec_pool = fk[0].decoder.decoder_f.unsqueeze(0).contiguous()
+        # the decoder's registration (its pseudo-inverse, for the frozen projection of the
+        # request's later tokens; rope_store.register)
+        us_reg = timed(lambda: encode.KDecoder(fk[0].decoder.decoder_f).pinv)
         pinv_pool = fk[0].decoder.pinv.unsqueeze(0).contiguous()
         qsl = torch.tensor([0, T], dtype=torch.int32, device=dev)
         slots = torch.arange(T, dtype=torch.int64, device=dev)
@@ -338,13 +341,15 @@ def bench_first_chunk(torch, lay, cfg, dev, lengths=(2048, 8192), reps=5):
             lay, Kt, V, slots, qsl, bt, dec_map, dec_pool, pinv_pool, page,
             coeff_q_in=fk[0].coeff_q, coeff_scale_in=fk[0].coeff_scale))
         row = dict(tokens=T, sdpa_fp32_us=us_sdpa, sdpa_fp16_us=us_sdpa16, fit_us=us_fit,
-                   write_us=us_write, total_us=us_sdpa + us_fit + us_write)
+                   register_us=us_reg, write_us=us_write,
+                   total_us=us_sdpa + us_fit + us_reg + us_write)
         log(f"first chunk {T}: SDPA fp32 {us_sdpa:.0f} us (fp16 {us_sdpa16:.0f}), fit "
-            f"{us_fit:.0f} us, write {us_write:.0f} us per layer")
+            f"{us_fit:.0f} us, registration {us_reg:.0f} us, write {us_write:.0f} us per layer")
         out.append(row)
         del K, V, q, k, v, qh, kh, vh, page
     return dict(per_layer=out, note="one request's first chunk per layer: attention over the "
-                "chunk (fp32 causal SDPA, the reference's precision), device fit, K3 write")
+                "chunk (fp32 causal SDPA, the reference's precision), device fit, the decoder's "
+                "registration (pseudo-inverse), K3 write")
 
 
 def bench_config4(torch, lay, cfg, cache, dev, steps=10, warmup=3, cpu=False):

@@ -29,8 +29,32 @@ def _ruler(x: torch.Tensor, divisor: int) -> torch.Tensor:
     return x * inv
 
 
+def _pinv_rows(D: torch.Tensor) -> torch.Tensor:
+    """Moore-Penrose pseudo-inverse `[k, r]` of a wide float32 matrix D `[r, k]` (r <= k), as
+    `torch.linalg.pinv(D)` defines it -- singular values at or below max(r, k) * eps(fp32) times
+    the largest treated as zero -- computed from the r x r Gram matrix instead of an SVD of D:
+    with D D^T = U diag(s^2) U^T, pinv(D) = D^T U diag(1 / s^2) U^T over the kept s. The Gram
+    matrix is formed in float64 (its eigenvalues are the squared singular values, so float64
+    keeps them to ~1e-8 relative) and solved by the host's LAPACK (~0.5 ms at r = 110, where the
+    device SVD of D takes ~5 ms). Rows of D that are exactly zero (rank below the budget) get
+    exactly zero columns."""
+    r, k = D.shape
+    nz = D.abs().amax(1) > 0
+    out = torch.zeros(k, r, dtype=torch.float32, device=D.device)
+    if not bool(nz.any()):
+        return out
+    Dn = D[nz].to(torch.float64)
+    lam, U = torch.linalg.eigh((Dn @ Dn.T).cpu())
+    cut = (max(r, k) * torch.finfo(torch.float32).eps * lam.max().clamp(min=0.0).sqrt()) ** 2
+    inv = torch.where(lam > cut, 1.0 / lam, torch.zeros_like(lam))
+    Ginv = ((U * inv) @ U.T).to(D.device)
+    out[:, nz] = (Dn.T @ Ginv).to(torch.float32)
+    return out
+
+
 class KDecoder:
-    """A request's frozen decoder `[r1, H*d]` fp32 and its cached pseudo-inverse `[H*d, r1]`."""
+    """A request's frozen decoder `[r1, H*d]` fp32 and its cached pseudo-inverse `[H*d, r1]`
+    (encode.py:198-208 uses `torch.linalg.pinv`; `_pinv_rows` computes the same matrix)."""
 
     __slots__ = ("decoder_f", "_pinv")
 
@@ -43,7 +67,9 @@ class KDecoder:
     @property
     def pinv(self) -> torch.Tensor:
         if self._pinv is None:
-            self._pinv = torch.linalg.pinv(self.decoder_f).contiguous()
+            D = self.decoder_f
+            self._pinv = (_pinv_rows(D) if D.shape[0] <= D.shape[1]
+                          else torch.linalg.pinv(D)).contiguous()
         return self._pinv
 
 
