@@ -57,26 +57,41 @@ def _check(got, want, what):
 
 @pytest.mark.parametrize("n", [1082, 4322, 8642, 14402])
 def test_config2_batch1_contexts(n):
-    """Config 2: B = 1 at each context, two layers (independent stores and queries)."""
+    """Config 2: B = 1 at each context, four layers (independent stores and queries)."""
     torch.set_num_threads(16)
-    for layer in range(2):
+    for layer in range(4):
         print(f"config2 n={n} layer={layer}", flush=True)
         st = device_store("safe", [n], seed=200 + 10 * layer + n % 97)
         q = synth.queries(1, seed=layer + n)
         _check(_k1(st, q), _oracle_decode(st, q), f"config2 n={n} layer {layer}")
 
 
-def test_config3_batch8_random_contexts():
-    """Config 3: 8 requests, contexts seeded U[1000, 14400], shuffled block table, one launch."""
+@pytest.mark.parametrize("layer", range(3))
+def test_config3_batch8_random_contexts(layer):
+    """Config 3: 8 requests, contexts seeded U[1000, 14400], shuffled block table, one launch;
+    three layers (independent stores and queries over the same contexts)."""
     torch.set_num_threads(16)
     lens = config3_lens()
-    print(f"config3 contexts {lens}", flush=True)
-    st = device_store("safe", lens, seed=3)
-    q = synth.queries(8, seed=5)
+    print(f"config3 contexts {lens} layer {layer}", flush=True)
+    st = device_store("safe", lens, seed=3 + 100 * layer)
+    q = synth.queries(8, seed=5 + layer)
     got = _k1(st, q)
     want = _oracle_decode(st, q)
     for r in range(8):
-        _check(got[r:r + 1], want[r:r + 1], f"config3 request {r} (n={lens[r]})")
+        _check(got[r:r + 1], want[r:r + 1], f"config3 layer {layer} request {r} (n={lens[r]})")
+
+
+def test_headline_batch8_at_14402():
+    """The bench's headline shape: 8 requests of 14,402 tokens in one launch (8 chunks per
+    (request, head), the in-launch combine of each), against the oracle."""
+    torch.set_num_threads(16)
+    lens = [14402] * 8
+    st = device_store("safe", lens, seed=77)
+    q = synth.queries(8, seed=78)
+    got = _k1(st, q)
+    want = _oracle_decode(st, q)
+    for r in range(8):
+        _check(got[r:r + 1], want[r:r + 1], f"headline request {r}")
 
 
 def _config4_store():
