@@ -48,6 +48,7 @@ def log(*a):
 def build_store(torch, lay, cfg, lens, n_layers, seed, dev, fit_on=FIT_ON, distinct=4):
     """Per-layer paged caches for requests of `lens` tokens. Returns a dict of device tensors."""
     from vllm_ttkv import encode, kernels, synth
+    from vllm_ttkv.decoder_pool import DecoderPool, empty_pool
     bt, nblk = synth.shuffled_block_table(lens, BS, seed=seed, extra_blocks=4)
     B = len(lens)
     C = lay.compressed_bytes_per_token()
@@ -66,11 +67,14 @@ def build_store(torch, lay, cfg, lens, n_layers, seed, dev, fit_on=FIT_ON, disti
         if li >= distinct:
             # replicate a built layer into this layer's own pages (distinct HBM addresses)
             src = layers[li % distinct]
-            layers.append(dict(page=src["page"].clone(), dec_pool=src["dec_pool"].clone(),
-                               pinv_pool=src["pinv_pool"].clone()))
+            layers.append(dict(page=src["page"].clone(),
+                               dec_pool=DecoderPool(src["dec_pool"].q.clone(),
+                                                    src["dec_pool"].scale.clone()),
+                               pinv_pool=src["pinv_pool"].clone(), dec_f=src["dec_f"]))
             continue
         page = torch.zeros(nblk * BS, C, dtype=torch.uint8, device=dev)
-        dec_pool = torch.zeros(B, lay.r1, H * D, dtype=torch.float32, device=dev)
+        dec_pool = empty_pool(B, lay.r1, H, D, dev)
+        dec_f = torch.zeros(B, lay.r1, H * D, dtype=torch.float32, device=dev)  # CPU baselines
         pinv_pool = torch.zeros(B, H * D, lay.r1, dtype=torch.float32, device=dev)
         first_k, first_v, first_cq, first_cs, first_slot, rest = [], [], [], [], [], []
         for r, n in enumerate(lens):
@@ -80,7 +84,9 @@ def build_store(torch, lay, cfg, lens, n_layers, seed, dev, fit_on=FIT_ON, disti
             f = min(fit_on, n)
             t0 = time.perf_counter()
             fk = encode.fit_into_budget(K[:, :f], lay, cfg)
-            dec_pool[r] = fk.decoder.decoder_f
+            dec_f[r] = fk.decoder.decoder_f
+            dec_pool.q[r].copy_(fk.decoder.packed.q)
+            dec_pool.scale[r].copy_(fk.decoder.packed.scale)
             pinv_pool[r] = fk.decoder.pinv
             torch.cuda.synchronize()
             t_fit += time.perf_counter() - t0
@@ -107,7 +113,7 @@ def build_store(torch, lay, cfg, lens, n_layers, seed, dev, fit_on=FIT_ON, disti
         torch.cuda.synchronize()
         t_write += time.perf_counter() - t0
         del first_k, first_v, rest
-        layers.append(dict(page=page, dec_pool=dec_pool, pinv_pool=pinv_pool))
+        layers.append(dict(page=page, dec_pool=dec_pool, pinv_pool=pinv_pool, dec_f=dec_f))
     if int(err.item()):
         raise RuntimeError(f"store build: device error word {int(err.item())}")
     return dict(layers=layers, bt=bt_d, dec_map=dec_map_d, nblk=nblk, B=B,
@@ -123,10 +129,11 @@ def config3_lens(seed=3, B=8):
 
 
 def k1_bytes(lay, lens, r1, cs_rows):
-    """Algorithmic HBM bytes of one K1 launch: every slot once, each request's fp32 decoder
-    once, the angle table rows once, q and out once (fp16)."""
+    """Algorithmic HBM bytes of one K1 launch: every slot once, each request's decoder once in
+    the pool's form (r1 x H*d int8 values and r1 fp32 rank rulers), the angle table rows once, q
+    and out once (fp16)."""
     B = len(lens)
-    return (sum(lens) * lay.compressed_bytes_per_token() + B * r1 * H * D * 4
+    return (sum(lens) * lay.compressed_bytes_per_token() + B * r1 * (H * D + 4)
             + cs_rows * D * 4 + 2 * B * HQ * D * 2)
 
 
@@ -257,7 +264,7 @@ def cpu_k2_sample(torch, lay, st, L, q_chunk, cache, n, Q):
     slots = (bt[0, p // BS].long() * BS + p % BS)
     blob = L["page"][slots.to(L["page"].device)].cpu()
     k_s, v_s = blob[:, :olay.k_slot_bytes].contiguous(), blob[:, olay.k_slot_bytes:].contiguous()
-    dec = L["dec_pool"][0].cpu()
+    dec = L["dec_f"][0].cpu()
     cos, sin = orope.cos_sin_from_cache(cache.cpu(), p, D)
     qq = q_chunk.float().cpu().permute(1, 0, 2).contiguous()                # [HQ, Q, d]
     t0 = time.perf_counter()
@@ -265,7 +272,7 @@ def cpu_k2_sample(torch, lay, st, L, q_chunk, cache, n, Q):
     return (time.perf_counter() - t0) * 1e3, torch.get_num_threads()
 
 
-def cpu_k3_sample(torch, lay, k_new, v_new, dec_pool, pinv_pool):
+def cpu_k3_sample(torch, lay, k_new, v_new, dec_f, pinv_pool):
     """The torch-CPU oracle's write (encode.py:301-443 restated: projection, quantisation,
     residual, top-k select and pack of K and V rows) for the B new tokens of one config-5
     step-layer, each against its own request's decoder as the reference's request loop does
@@ -275,7 +282,7 @@ def cpu_k3_sample(torch, lay, k_new, v_new, dec_pool, pinv_pool):
     torch.set_num_threads(os.cpu_count() or 1)
     K = k_new.float().cpu().permute(1, 0, 2).contiguous()                  # [H, B, d]
     V = v_new.float().cpu().permute(1, 0, 2).contiguous()
-    dec, pinv = dec_pool.cpu(), pinv_pool.cpu()
+    dec, pinv = dec_f.cpu(), pinv_pool.cpu()
     t0 = time.perf_counter()
     for r in range(K.shape[1]):
         ef = oenc.encode_frozen(K[:, r:r + 1].contiguous(), dec[r], olay, pinv[r])
@@ -291,6 +298,7 @@ def bench_first_chunk(torch, lay, cfg, dev, lengths=(2048, 8192), reps=5):
     write of its tokens with the fit's coefficients. The fp16 SDPA (model dtype, not the
     reference's arithmetic) is timed beside it for scale."""
     from vllm_ttkv import encode, kernels, synth
+    from vllm_ttkv.decoder_pool import DecoderPool
     from vllm_ttkv.impl import TTKVAttentionImpl
     im = TTKVAttentionImpl(HQ, D, D ** -0.5, H)
     out = []
@@ -329,7 +337,8 @@ def bench_first_chunk(torch, lay, cfg, dev, lengths=(2048, 8192), reps=5):
         bt = torch.arange(nblk, dtype=torch.int32, device=dev).reshape(1, nblk)
         dec_map = torch.full((nblk,), -1, dtype=torch.int32, device=dev)
         dec_map[0] = 0
-        dec_pool = fk[0].decoder.decoder_f.unsqueeze(0).contiguous()
+        dec_pool = DecoderPool(fk[0].decoder.packed.q.unsqueeze(0).contiguous(),
+                               fk[0].decoder.packed.scale.unsqueeze(0).contiguous())
         # the decoder's registration (its pseudo-inverse, for the frozen projection of the
         # request's later tokens; rope_store.register)
         us_reg = timed(lambda: encode.KDecoder(fk[0].decoder.decoder_f).pinv)
@@ -597,7 +606,7 @@ def bench_config5(torch, cache, dev, steps=10, warmup=3, n_layers=L_LAYERS, cpu=
     if cpu:
         L = st["layers"][0]
         slots, k_new, v_new, _ = plans[0]
-        cms, cores = cpu_k3_sample(torch, lay5, k_new, v_new, L["dec_pool"], L["pinv_pool"])
+        cms, cores = cpu_k3_sample(torch, lay5, k_new, v_new, L["dec_f"], L["pinv_pool"])
         res["k3_cpu_baseline"] = dict(value=cms, unit="ms per 8-token write", cores=cores,
                                       kind="port",
                                       sample="one step-layer's 8 new tokens through the "
@@ -624,7 +633,7 @@ def cpu_baseline(torch, lay, store, q, cache, n, budget_s=12.0):
         p = torch.arange(n, device=bt.device)
         slots = (bt[r, p // BS].long() * BS + p % BS)
         blob = L["page"][slots.to(L["page"].device)].cpu()
-        dec = L["dec_pool"][r].cpu()
+        dec = L["dec_f"][r].cpu()
         k_s, v_s = blob[:, :lay.k_slot_bytes].contiguous(), blob[:, lay.k_slot_bytes:].contiguous()
         qq = q[r].float().cpu()
         t0 = time.perf_counter()

@@ -55,6 +55,12 @@ typedef struct ttkv_layout {
  * Replaces TTKLayout.compressed_bytes_per_token (vllm_ttkv/layout.py:152-154). */
 int64_t ttkv_blob_bytes(const ttkv_layout* lay);
 
+/* Ranks R each decoder column holds in the decoder pool (dec_q [n_dec_slots, H*d, R]): 64 for
+ * r1 <= 64, 128 for r1 <= 128, else r1 rounded up to a multiple of 32; -1 for r1 <= 0. Replaces
+ * the reference's [r1, H*d] decoder shape (codec/ttkv_packed_cache.py:284-293), padded so that
+ * every kernel reads whole 8- and 16-byte groups of ranks. */
+int32_t ttkv_decoder_ranks(int32_t r1);
+
 /* Workspaces (all four `*_workspace_bytes`): the first 64 KiB of a workspace are arrival
  * counters at a fixed place, followed by per-call partial results. A workspace must be
  * zero-filled before its first use; every call leaves the counters zero again, and no call writes
@@ -81,7 +87,11 @@ int64_t ttkv_decode_workspace_bytes(const ttkv_layout* lay, int32_t num_heads,
  * block_table  [num_reqs, bt_row_stride] int32; slot of position t = bt[r, t/bs]*bs + t%bs.
  * dec_slot_of_block [num_blocks] int32: the registry rope_store.register_decoder keys by
  *              block_table[r, 0] (rope_store.py:148-237), as a device map; -1 = none.
- * dec_pool     [n_dec_slots, r1, H*d] fp32 decoder_f rows (encode.py:178-211).
+ * dec_q, dec_scale  the decoder pool: each slot holds one decoder_f (encode.py:178-211) in the
+ *              codec's own form (ttkv_packed_cache.py:284-293), decoder_f[a, j] =
+ *              float(dec_q[slot, j, a]) * dec_scale[slot, a], laid out column-major:
+ *              dec_q [n_dec_slots, H*d, R] int8, dec_scale [n_dec_slots, R] fp32, R =
+ *              ttkv_decoder_ranks(r1); ranks a >= r1 hold 0. Both 16-byte aligned.
  * cos_sin_cache [max_position, d] fp32, vLLM layout: cos in columns [0,d/2), sin in [d/2,d)
  *              (decode.py:54-122).
  * out          [N, num_heads, d] (dtype out_dtype); only the decode rows are written.
@@ -96,7 +106,7 @@ int ttkv_decode_paged(const ttkv_layout* lay, int32_t num_heads, float scale,
                       int32_t max_blocks, const int32_t* seq_lens,
                       const int32_t* query_start_loc, int32_t num_reqs, int32_t max_seq_len,
                       const int32_t* dec_slot_of_block, int64_t num_blocks,
-                      const float* dec_pool, int64_t n_dec_slots,
+                      const int8_t* dec_q, const float* dec_scale, int64_t n_dec_slots,
                       const float* cos_sin_cache, int64_t max_position,
                       void* out, int32_t out_dtype, int64_t out_row_stride,
                       void* workspace, int64_t workspace_bytes, int32_t* error_word,
@@ -117,7 +127,7 @@ int ttkv_decode_paged_noalloc(const ttkv_layout* lay, int32_t num_heads, float s
                               int64_t bt_row_stride, int32_t max_blocks, const int32_t* seq_lens,
                               const int32_t* query_start_loc, int32_t num_reqs,
                               int32_t max_seq_len, const int32_t* dec_slot_of_block,
-                              int64_t num_blocks, const float* dec_pool, int64_t n_dec_slots,
+                              int64_t num_blocks, const int8_t* dec_q, const float* dec_scale, int64_t n_dec_slots,
                               const float* cos_sin_cache, int64_t max_position, void* out,
                               int32_t out_dtype, int64_t out_row_stride, int32_t* error_word,
                               ttkv_stream_t stream);
@@ -141,8 +151,9 @@ int ttkv_decode_paged_noalloc(const ttkv_layout* lay, int32_t num_heads, float s
  *   written, so the host registry can evict decoders by last use (the caller clears it).
  * slot_mapping entries < 0 are vLLM's PAD_SLOT_ID (padded tokens of a replayed graph): skipped
  *   silently, as vLLM's cache writers do; entries past the cache set TTKV_ERR_BAD_SLOT.
- * key/value: [N, H, d] rows with the given element stride between tokens. dec_pool must be
- *   8-byte aligned (TTKV_E_INVALID otherwise).
+ * key/value: [N, H, d] rows with the given element stride between tokens. The decoder pool
+ *   (dec_q, dec_scale) is laid out as for ttkv_decode_paged; pinv_pool [n_dec_slots, H*d, r1]
+ *   fp32 holds each decoder's pseudo-inverse (encode.py:193-206).
  * Work is spread over (token, KV head) workgroups in two launches: per-head partial projections
  * (the token's last workgroup sums them in head order and quantises) and, per head, the residual
  * and the K and V rows. The partials and each token's decoder slot live in `workspace`
@@ -152,7 +163,8 @@ int ttkv_write_paged(const ttkv_layout* lay, const void* key, int32_t k_dtype, i
                      const int64_t* slot_mapping, int32_t num_tokens,
                      const int32_t* query_start_loc, int32_t num_reqs, const int32_t* block_table,
                      int64_t bt_row_stride, const int32_t* dec_slot_of_block, int64_t num_blocks,
-                     const float* dec_pool, const float* pinv_pool, int64_t n_dec_slots,
+                     const int8_t* dec_q, const float* dec_scale, const float* pinv_pool,
+                     int64_t n_dec_slots,
                      int32_t* dec_slot_used, const int8_t* coeff_q_in,
                      const float* coeff_scale_in, uint8_t* page, int64_t n_slots,
                      int64_t slot_stride, float* coeff_out, float* resid_out, void* workspace,
@@ -197,7 +209,7 @@ int ttkv_prefill_paged(const ttkv_layout* lay, int32_t num_heads, float scale,
                        const int32_t* query_start_loc, const int32_t* req_index,
                        int32_t num_reqs, int32_t max_q_len, int32_t max_seq_len,
                        const int32_t* dec_slot_of_block, int64_t num_blocks,
-                       const float* dec_pool, int64_t n_dec_slots,
+                       const int8_t* dec_q, const float* dec_scale, int64_t n_dec_slots,
                        const float* cos_sin_cache, int64_t max_position,
                        void* out, int32_t out_dtype, int64_t out_row_stride,
                        void* workspace, int64_t workspace_bytes, int32_t* error_word,
@@ -217,7 +229,7 @@ int ttkv_multi_scores_paged(const ttkv_layout* lay, int32_t num_heads, float sca
                             int64_t bt_row_stride, int32_t max_blocks, const int32_t* seq_lens,
                             const int32_t* query_start_loc, int32_t max_q_len,
                             int32_t max_seq_len, const int32_t* dec_slot_of_block,
-                            int64_t num_blocks, const float* dec_pool, int64_t n_dec_slots,
+                            int64_t num_blocks, const int8_t* dec_q, const float* dec_scale, int64_t n_dec_slots,
                             const float* cos_sin_cache, int64_t max_position, float* scores,
                             int64_t s_head_stride, int64_t s_q_stride, void* workspace,
                             int64_t workspace_bytes, int32_t* error_word, ttkv_stream_t stream);

@@ -46,6 +46,13 @@ def paged(stores, block_size: int = 16, seed: int = 0, width_pad: int = 0):
                 num_blocks=nblk)
 
 
+def dec_pool_of(decoders, dev: str = "cuda"):
+    """The product's decoder pool (`DecoderPool`, int8 + rank rulers) holding fp32 `decoders`
+    ([r1, H*d] each, fitted, so exactly int8 x ruler), one slot per decoder, on `dev`."""
+    from vllm_ttkv.decoder_pool import pack_decoders
+    return pack_decoders(torch.stack([d.to(torch.float32) for d in decoders]).to(dev))
+
+
 def llama3_cache(max_pos: int):
     inv = orope.inv_freq_llama3(D, **orope.LLAMA32_3B_ROPE)
     return orope.vllm_cos_sin_cache(inv, max_pos)
@@ -61,7 +68,8 @@ def device_store(cfg_name: str, lens, seed: int, r1: int = 110, block_size: int 
     as on a store the oracle built.
 
     Returns dict(lay (oracle Layout), play (product TTKLayout), page [n_slots, C] u8 (device),
-    block_table, seq_lens, dec_map, dec_pool, pinv_pool (device), decoders (CPU list), num_blocks).
+    block_table, seq_lens, dec_map, dec_pool (DecoderPool), pinv_pool (device), decoders (CPU
+    fp32 list), num_blocks).
     """
     from vllm_ttkv import encode as penc, kernels
     from vllm_ttkv.layout import CONFIGS as PCONFIGS, layout_for_config as play_for
@@ -73,7 +81,9 @@ def device_store(cfg_name: str, lens, seed: int, r1: int = 110, block_size: int 
     bt, nblk = synth.shuffled_block_table(lens, block_size, seed=seed, extra_blocks=3)
     C = lay.compressed_bytes_per_token()
     page = torch.zeros(nblk * block_size, C, dtype=torch.uint8, device=dev)
-    dec_pool = torch.zeros(B, r1, H * D, dtype=torch.float32, device=dev)
+    from vllm_ttkv.decoder_pool import empty_pool
+    dec_pool = empty_pool(B, r1, H, D, dev)
+    dec_f = torch.zeros(B, r1, H * D, dtype=torch.float32, device=dev)
     pinv_pool = torch.zeros(B, H * D, r1, dtype=torch.float32, device=dev)
     dec_map = torch.full((nblk,), -1, dtype=torch.int32)
     for r in range(B):
@@ -87,7 +97,9 @@ def device_store(cfg_name: str, lens, seed: int, r1: int = 110, block_size: int 
         V = synth.values(n, seed=s, device=dev).permute(1, 0, 2)
         f = min(fit_on, n)
         fk = penc.fit_into_budget(K[:f].permute(1, 0, 2).contiguous(), play, PCONFIGS[cfg_name])
-        dec_pool[r] = fk.decoder.decoder_f
+        dec_f[r] = fk.decoder.decoder_f
+        dec_pool.q[r].copy_(fk.decoder.packed.q)
+        dec_pool.scale[r].copy_(fk.decoder.packed.scale)
         pinv_pool[r] = fk.decoder.pinv
         p = torch.arange(n)
         slot = (bt[r, p // block_size].long() * block_size + p % block_size).to(dev)
@@ -117,7 +129,7 @@ def device_store(cfg_name: str, lens, seed: int, r1: int = 110, block_size: int 
         raise RuntimeError(f"store build: device error word {int(err.item())}")
     return dict(lay=lay, play=play, page=page, block_table=bt_d, seq_lens=torch.tensor(
         lens, dtype=torch.int32, device=dev), dec_map=dec_map_d, dec_pool=dec_pool,
-        pinv_pool=pinv_pool, decoders=[dec_pool[r].cpu() for r in range(B)], num_blocks=nblk,
+        pinv_pool=pinv_pool, decoders=[dec_f[r].cpu() for r in range(B)], num_blocks=nblk,
         block_size=block_size)
 
 

@@ -45,7 +45,7 @@ def _decode_call(lay, **kw):
     args = dict(num_heads=24, scale=0.088, query=1, q_dtype=1, q_row_stride=3072, page=4096,
                 n_slots=16, slot_stride=912, block_size=16, block_table=1, bt_row_stride=1,
                 max_blocks=1, seq_lens=1, qsl=1, num_reqs=1, max_seq_len=16, dec_map=1,
-                num_blocks=1, dec_pool=1, n_dec=1, cs=16, max_pos=64, out=1, out_dtype=1,
+                num_blocks=1, dec_q=16, dec_scale=16, n_dec=1, cs=16, max_pos=64, out=1, out_dtype=1,
                 out_row_stride=3072, ws=256, ws_bytes=1 << 20, err=1)
     args.update(kw)
     a = args
@@ -54,7 +54,8 @@ def _decode_call(lay, **kw):
                                a["slot_stride"], a["block_size"], a["block_table"],
                                a["bt_row_stride"], a["max_blocks"], a["seq_lens"], a["qsl"],
                                a["num_reqs"], a["max_seq_len"], a["dec_map"], a["num_blocks"],
-                               a["dec_pool"], a["n_dec"], a["cs"], a["max_pos"], a["out"],
+                               a["dec_q"], a["dec_scale"], a["n_dec"], a["cs"], a["max_pos"],
+                               a["out"],
                                a["out_dtype"], a["out_row_stride"], a["ws"], a["ws_bytes"],
                                a["err"], None)
 
@@ -73,6 +74,8 @@ def test_host_refusals_before_launch():
     assert _decode_call(safe, slot_stride=900) == 1                     # narrower than the blob
     assert _decode_call(safe, page=4097) == 1                           # misaligned page
     assert _decode_call(safe, err=0) == 1                               # no error word
+    assert _decode_call(safe, dec_scale=20) == 1 and b"16-byte" in L.ttkv_last_error()
+    assert _decode_call(safe, dec_q=0) == 1 and b"decoder pool" in L.ttkv_last_error()
     big = layout_for_config(CONFIGS["safe"], 200)
     assert _decode_call(big) == 2 and b"r1" in L.ttkv_last_error()
     mixed = TTKLayout(H=8, d=128, r1=110, qbits=8, res_k=81, res_bits=3, v_lanes=64, v_bits=4)
@@ -84,7 +87,8 @@ def _prefill_call(lay, **kw):
     a = dict(num_heads=24, scale=0.088, query=1, q_dtype=1, q_row_stride=3072, page=4096,
              n_slots=64, slot_stride=912, block_size=16, block_table=1, bt_row_stride=4,
              max_blocks=4, seq_lens=1, qsl=1, req_index=0, num_reqs=1, max_q_len=8,
-             max_seq_len=64, dec_map=1, num_blocks=4, dec_pool=1, n_dec=1, cs=16, max_pos=64,
+             max_seq_len=64, dec_map=1, num_blocks=4, dec_q=16, dec_scale=16, n_dec=1, cs=16,
+             max_pos=64,
              out=1, out_dtype=1, out_row_stride=3072, ws=256, ws_bytes=1 << 24, err=1)
     a.update(kw)
     return L.ttkv_prefill_paged(_hip.Layout.of(lay), a["num_heads"], a["scale"], a["query"],
@@ -92,7 +96,8 @@ def _prefill_call(lay, **kw):
                                 a["slot_stride"], a["block_size"], a["block_table"],
                                 a["bt_row_stride"], a["max_blocks"], a["seq_lens"], a["qsl"],
                                 a["req_index"], a["num_reqs"], a["max_q_len"], a["max_seq_len"],
-                                a["dec_map"], a["num_blocks"], a["dec_pool"], a["n_dec"], a["cs"],
+                                a["dec_map"], a["num_blocks"], a["dec_q"], a["dec_scale"],
+                                a["n_dec"], a["cs"],
                                 a["max_pos"], a["out"], a["out_dtype"], a["out_row_stride"],
                                 a["ws"], a["ws_bytes"], a["err"], None)
 
@@ -101,7 +106,8 @@ def _write_call(lay, **kw):
     L = _hip.lib()
     a = dict(key=1, k_dtype=1, k_row_stride=1024, value=1, v_dtype=1, v_row_stride=1024,
              slot_mapping=1, num_tokens=4, qsl=1, num_reqs=1, block_table=1, bt_row_stride=1,
-             dec_map=1, num_blocks=1, dec_pool=16, pinv_pool=1, n_dec=1, dec_used=0, cq_in=0,
+             dec_map=1, num_blocks=1, dec_q=16, dec_scale=16, pinv_pool=1, n_dec=1, dec_used=0,
+             cq_in=0,
              cs_in=0,
              page=4096, n_slots=16, slot_stride=912, c_out=0, r_out=0, ws=256, ws_bytes=1 << 20,
              err=1)
@@ -109,8 +115,8 @@ def _write_call(lay, **kw):
     return L.ttkv_write_paged(_hip.Layout.of(lay), a["key"], a["k_dtype"], a["k_row_stride"],
                               a["value"], a["v_dtype"], a["v_row_stride"], a["slot_mapping"],
                               a["num_tokens"], a["qsl"], a["num_reqs"], a["block_table"],
-                              a["bt_row_stride"], a["dec_map"], a["num_blocks"], a["dec_pool"],
-                              a["pinv_pool"], a["n_dec"], a["dec_used"], a["cq_in"],
+                              a["bt_row_stride"], a["dec_map"], a["num_blocks"], a["dec_q"],
+                              a["dec_scale"], a["pinv_pool"], a["n_dec"], a["dec_used"], a["cq_in"],
                               a["cs_in"], a["page"],
                               a["n_slots"], a["slot_stride"], a["c_out"], a["r_out"], a["ws"],
                               a["ws_bytes"], a["err"], None)
@@ -132,6 +138,7 @@ def test_prefill_host_refusals_before_launch():
     assert _prefill_call(safe, cs=17) == 1 and b"16-aligned" in L.ttkv_last_error()
     assert _prefill_call(layout_for_config(CONFIGS["safe"], 200)) == 2
     assert _prefill_call(safe, q_dtype=7) == 1 and b"dtype" in L.ttkv_last_error()
+    assert _prefill_call(safe, dec_q=24) == 1 and b"16-byte" in L.ttkv_last_error()
 
 
 def test_write_host_refusals_before_launch():
@@ -150,7 +157,8 @@ def test_write_host_refusals_before_launch():
     assert _write_call(safe, key=0) == 1 and b"null" in L.ttkv_last_error()
     assert _write_call(safe, v_dtype=5) == 1 and b"dtype" in L.ttkv_last_error()
     assert _write_call(safe, ws=0) == 4 and b"workspace" in L.ttkv_last_error()
-    assert _write_call(safe, dec_pool=4) == 1 and b"8-byte aligned" in L.ttkv_last_error()
+    assert _write_call(safe, dec_q=8) == 1 and b"16-byte aligned" in L.ttkv_last_error()
+    assert _write_call(safe, dec_scale=0) == 1 and b"decoder pool" in L.ttkv_last_error()
     assert _write_call(safe, num_tokens=0) == 0                          # nothing to do
 
 

@@ -117,6 +117,18 @@ def test_product_fit_matches_exact_fit(cfg_name, T):
     _compare(fit, K, cfg_name)
 
 
+def _pool_form_is_exact(fit):
+    """The fit's pool form (int8 ranks and rulers, the codec's dec_q / dec_scale) holds exactly
+    its fp32 decoder, and the form derived from the fp32 decoder alone holds the same values."""
+    from vllm_ttkv.decoder_pool import pack_decoders, unpack_decoders
+    r1 = fit.decoder.decoder_f.shape[0]
+    p = fit.decoder.packed
+    assert p.q.dtype == torch.int8 and p.q.shape == (1024, 128)
+    assert torch.equal(unpack_decoders(p, r1), fit.decoder.decoder_f)
+    assert torch.equal(unpack_decoders(pack_decoders(fit.decoder.decoder_f), r1),
+                       fit.decoder.decoder_f)
+
+
 def test_low_rank_keys():
     """Keys of exact rank 7. The reference's rule keeps the first component whose tail energy is
     below tol^2, here the 8th, of zero energy, whose left vector is arbitrary (LAPACK returns some
@@ -132,6 +144,7 @@ def test_low_rank_keys():
     assert fit.fitted_rank == ref["fitted_rank"] == 8
     assert not bool(fit.coeff_q[:, 8:].any()) and not bool(fit.decoder.decoder_f[8:].any())
     assert bool(torch.isfinite(fit.decoder.decoder_f).all())
+    _pool_form_is_exact(fit)
     X = K.permute(1, 2, 0).contiguous()
     mine = _approx(penc._tt_factors(X, cfg["tols"], R1), 900)
     exact = _approx(oc.tt_svd(X.double(), cfg["tols"], R1)[0], 900)
@@ -156,6 +169,7 @@ def test_product_fit_on_device(cfg_name):
     ms = (time.perf_counter() - t0) * 1e3
     print(f"[fit] {cfg_name} T={T} rank={fit.fitted_rank} device fit {ms:.1f} ms", flush=True)
     assert fit.coeff_q.is_cuda and fit.decoder.decoder_f.is_cuda
+    _pool_form_is_exact(fit)
     sign = _compare(fit, K, cfg_name)
     cpu = penc.fit_into_budget(K, lay, CONFIGS[cfg_name])
     sign_cpu = torch.where((cpu.decoder.decoder_f * fit.decoder.decoder_f.cpu()).sum(1) < 0,

@@ -11,6 +11,7 @@ import numpy as np
 import pytest
 import torch
 
+from helpers import dec_pool_of
 from oracle import attend
 from oracle.codec import CONFIGS
 from vllm_ttkv import kernels, synth
@@ -53,7 +54,7 @@ def test_k1_matches_reference_attend_raw_store():
     kernels.decode_paged(lay, q.cuda(), page.cuda(), bs, bt.cuda(),
                          torch.tensor([n], dtype=torch.int32).cuda(),
                          torch.tensor([0, 1], dtype=torch.int32).cuda(), n, dec_map.cuda(),
-                         f["decoder_f"].unsqueeze(0).float().cuda(), cache.cuda(), 128 ** -0.5,
+                         dec_pool_of([f["decoder_f"]]), cache.cuda(), 128 ** -0.5,
                          out=out, error_word=err)
     torch.cuda.synchronize()
     assert int(err.item()) == 0
@@ -71,7 +72,7 @@ def test_k2_scores_match_reference_raw_scores_multi_causal():
                                      page.cuda(), bs, bt.cuda(),
                                      torch.tensor([n], dtype=torch.int32).cuda(),
                                      torch.tensor([0, Q], dtype=torch.int32).cuda(), Q, n,
-                                     dec_map.cuda(), f["decoder_f"].unsqueeze(0).float().cuda(),
+                                     dec_map.cuda(), dec_pool_of([f["decoder_f"]]),
                                      cache.cuda(), 128 ** -0.5, error_word=err)
     torch.cuda.synchronize()
     assert int(err.item()) == 0
@@ -94,7 +95,7 @@ def test_k2_attention_matches_reference_scores_softmax_readout():
     kernels.prefill_paged(lay, q.cuda(), page.cuda(), bs, bt.cuda(),
                           torch.tensor([n], dtype=torch.int32).cuda(),
                           torch.tensor([0, Q], dtype=torch.int32).cuda(), Q, n, dec_map.cuda(),
-                          f["decoder_f"].unsqueeze(0).float().cuda(), cache.cuda(), 128 ** -0.5,
+                          dec_pool_of([f["decoder_f"]]), cache.cuda(), 128 ** -0.5,
                           out=out, error_word=err)
     torch.cuda.synchronize()
     assert int(err.item()) == 0

@@ -141,6 +141,15 @@ def test_backend_flags():
     assert "bfloat16" in B.supported_kv_cache_dtypes
 
 
+def _codec_dec(r1=16, hd=8 * 128, seed=0):
+    """A decoder in the codec's form (int8 rows times an fp16 ruler per rank), as every fit
+    produces (encode.py:257-298)."""
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randint(-128, 128, (r1, hd), generator=g).float()
+    ruler = (torch.rand(r1, generator=g) * 1e-2 + 1e-4).half().float()
+    return q * ruler[:, None]
+
+
 def test_decoder_registry_round_trip():
     """Fixed-capacity pool: registration, release, slot reuse, eviction of the oldest
     registration that is not live, and refusal when every slot is live. The pools are never
@@ -150,20 +159,20 @@ def test_decoder_registry_round_trip():
     rope_store.clear_stores()
     st = rope_store.TTKVRopeStore(24, 8, 128, torch.zeros(8, 128), "L0", lay, num_blocks=10,
                                   capacity=2)
-    pools = (st.dec_pool.data_ptr(), st.pinv_pool.data_ptr(), st.dec_map.data_ptr())
-    d1 = KDecoder(torch.randn(16, 8 * 128))
-    d2 = KDecoder(torch.randn(16, 8 * 128))
-    d3 = KDecoder(torch.randn(16, 8 * 128))
+    from vllm_ttkv.decoder_pool import unpack_decoders
+    pools = (st.dec_pool.q.data_ptr(), st.dec_pool.scale.data_ptr(), st.pinv_pool.data_ptr(),
+             st.dec_map.data_ptr())
+    d1, d2, d3 = (KDecoder(_codec_dec(seed=i)) for i in range(3))
     s1 = st.register(3, d1)
     s2 = st.register(7, d2)
     assert st.dec_map[3] == s1 and st.dec_map[7] == s2 and s1 != s2
-    assert torch.equal(st.dec_pool[s2], d2.decoder_f)
+    assert torch.equal(unpack_decoders(st.dec_pool.slot(s2), 16), d2.decoder_f)
     assert torch.allclose(st.pinv_pool[s2], d2.pinv)
     st.release(3)
     assert st.dec_map[3] == -1 and 3 not in st.decoders
     assert st.register(5, d1) == s1               # freed slot reused
     assert st.register(5, d3) == s1               # re-registering a key keeps its slot
-    assert torch.equal(st.dec_pool[s1], d3.decoder_f)
+    assert torch.equal(unpack_decoders(st.dec_pool.slot(s1), 16), d3.decoder_f)
     # full: the oldest registration not named live is evicted (7, registered before 5)
     s9 = st.register(9, d1, live=[5, 9])
     assert s9 == s2 and st.dec_map[7] == -1 and 7 not in st.decoders and st.dec_map[9] == s9
@@ -171,7 +180,8 @@ def test_decoder_registry_round_trip():
         st.register(2, d2, live=[5, 9, 2])
     with pytest.raises(IndexError):
         st.register(10, d1)
-    assert (st.dec_pool.data_ptr(), st.pinv_pool.data_ptr(), st.dec_map.data_ptr()) == pools
+    assert (st.dec_pool.q.data_ptr(), st.dec_pool.scale.data_ptr(), st.pinv_pool.data_ptr(),
+            st.dec_map.data_ptr()) == pools
     rope_store.clear_stores()
 
 
@@ -186,7 +196,7 @@ def test_decoder_eviction_follows_last_use():
     rope_store.clear_stores()
     st = rope_store.TTKVRopeStore(24, 8, 128, torch.zeros(8, 128), "L0", lay, num_blocks=40,
                                   capacity=3)
-    dec = KDecoder(torch.randn(16, 8 * 128))
+    dec = KDecoder(_codec_dec())
     a = st.register(1, dec, live=[1])                  # the running request
     for step, key in enumerate(range(10, 20)):         # 10 short requests, one per even step
         st.dec_used[a] = 1                             # odd step: request 1 decodes
@@ -216,7 +226,8 @@ def test_reference_calling_sequence_binds():
     lay = layout_for_config(CONFIGS["safe"], 16)
     rope_store.clear_stores()
     name = "model.layers.4.self_attn"
-    dec_a, dec_b = torch.randn(16, 1024), torch.randn(16, 1024)
+    from vllm_ttkv.decoder_pool import unpack_decoders
+    dec_a, dec_b = _codec_dec(seed=1), _codec_dec(seed=2)
     bt = torch.tensor([[6, 2, 9], [4, 0, -1]], dtype=torch.int32)
     rope_store.register_decoder(name, rope_store.request_key(bt[0]), KDecoder(dec_a))  # pending
     assert rope_store.decoder_for_request(name, 6).decoder_f is not None
@@ -229,7 +240,7 @@ def test_reference_calling_sequence_binds():
     assert again is store and store.dec_map.numel() == 12
     for key, dec in ((6, dec_a), (4, dec_b)):
         slot = int(store.dec_map[key])
-        assert slot >= 0 and torch.equal(store.dec_pool[slot], dec)
+        assert slot >= 0 and torch.equal(unpack_decoders(store.dec_pool.slot(slot), 16), dec)
         assert rope_store.decoder_for_request(name, key).decoder_f is not None
     assert rope_store.decoder_for_layer(name) is None              # no layer-level decoder
     rope_store.release_decoder(name, 6)

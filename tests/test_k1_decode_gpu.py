@@ -5,7 +5,7 @@ fp32 (here float64) oracle, with the kernel writing fp16."""
 import pytest
 import torch
 
-from helpers import HQ, fitted_store, llama3_cache, paged
+from helpers import HQ, dec_pool_of, fitted_store, llama3_cache, paged
 from oracle import attend, rope as orope
 from vllm_ttkv import kernels, synth
 
@@ -18,7 +18,7 @@ def _run_k1(stores, q, cache, block_size=16, seed=0, out_dtype=torch.float16, wo
     dev = "cuda"
     lay = stores[0]["lay"]
     B = len(stores)
-    dec_pool = torch.stack([s["decoder"] for s in stores]).to(dev)
+    dec_pool = dec_pool_of([s["decoder"] for s in stores], dev)
     dec_map = torch.full((pg["num_blocks"],), -1, dtype=torch.int32)
     for r in range(B):
         dec_map[pg["block_table"][r, 0]] = r
@@ -129,7 +129,7 @@ def test_write_then_read_loop():
     dec_map = torch.full((nblk,), -1, dtype=torch.int32)
     dec_map[bt[0, 0]] = 0
     args = dict(block_table=bt.to(dev), dec_slot_of_block=dec_map.to(dev),
-                dec_pool=dec.unsqueeze(0).to(dev), pinv_pool=encode.pinv(dec).unsqueeze(0).to(dev),
+                dec_pool=dec_pool_of([dec], dev), pinv_pool=encode.pinv(dec).unsqueeze(0).to(dev),
                 page=page)
     Kt = K.permute(1, 0, 2).contiguous()
     Vt = V.permute(1, 0, 2).contiguous()
@@ -149,7 +149,7 @@ def test_write_then_read_loop():
     kernels.decode_paged(lay, q.to(dev), page, bs, bt.to(dev),
                          torch.tensor([T], dtype=torch.int32, device=dev),
                          torch.tensor([0, 1], dtype=torch.int32, device=dev), T,
-                         dec_map.to(dev), dec.unsqueeze(0).to(dev), cache.to(dev), 128 ** -0.5,
+                         dec_map.to(dev), args["dec_pool"], cache.to(dev), 128 ** -0.5,
                          out=out, error_word=err)
     torch.cuda.synchronize()
     assert int(err.item()) == 0
@@ -195,7 +195,7 @@ def test_empty_context_and_missing_decoder():
     lay = stores[0]["lay"]
     seq_lens = pg["seq_lens"].clone()
     seq_lens[1] = 0                                      # request 1: empty
-    dec_pool = torch.stack([s["decoder"] for s in stores]).to(dev)
+    dec_pool = dec_pool_of([s["decoder"] for s in stores], dev)
     dec_map = torch.full((pg["num_blocks"],), -1, dtype=torch.int32)
     dec_map[pg["block_table"][0, 0]] = 0                 # request 2 left unregistered
     dec_map[pg["block_table"][1, 0]] = 1
@@ -267,7 +267,7 @@ def test_length_past_max_seq_len_is_flagged_and_clamped():
     pg = paged(stores, 16, 4)
     dev = "cuda"
     lay = stores[0]["lay"]
-    dec_pool = torch.stack([s["decoder"] for s in stores]).to(dev)
+    dec_pool = dec_pool_of([s["decoder"] for s in stores], dev)
     dec_map = torch.full((pg["num_blocks"],), -1, dtype=torch.int32)
     for r in range(2):
         dec_map[pg["block_table"][r, 0]] = r

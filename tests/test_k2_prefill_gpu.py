@@ -9,7 +9,7 @@ float64 oracle; the masked pattern is compared exactly."""
 import pytest
 import torch
 
-from helpers import HQ, fitted_store, llama3_cache, paged
+from helpers import HQ, dec_pool_of, fitted_store, llama3_cache, paged
 from oracle import attend
 from oracle.rope import cos_sin_from_cache
 from vllm_ttkv import kernels, synth
@@ -22,7 +22,7 @@ SCALE = 128 ** -0.5
 def _dev_inputs(stores, block_size=16, seed=0):
     pg = paged(stores, block_size, seed)
     B = len(stores)
-    dec_pool = torch.stack([s["decoder"] for s in stores]).cuda()
+    dec_pool = dec_pool_of([s["decoder"] for s in stores])
     dec_map = torch.full((pg["num_blocks"],), -1, dtype=torch.int32)
     for r in range(B):
         dec_map[pg["block_table"][r, 0]] = r

@@ -7,7 +7,7 @@ stages (projection, reconstruction) are checked at fp32 tolerance against the or
 import pytest
 import torch
 
-from helpers import D, H
+from helpers import D, H, dec_pool_of
 from oracle import codec, encode
 from oracle.layout import layout_for_config, unpack_v_slots
 from oracle import attend
@@ -41,7 +41,7 @@ def _run(lay, dec, pinv, Knew, V, slots, n_slots, v_dtype=torch.float32, cq_in=N
     err = torch.zeros(1, dtype=torch.int32, device=DEV)
     kernels.write_paged(lay, Knew.permute(1, 0, 2).contiguous().to(DEV),
                         V.permute(1, 0, 2).contiguous().to(v_dtype).to(DEV),
-                        slots.to(DEV), qsl, bt, dec_map, dec.unsqueeze(0).to(DEV),
+                        slots.to(DEV), qsl, bt, dec_map, dec_pool_of([dec], DEV),
                         pinv.unsqueeze(0).to(DEV), page,
                         coeff_q_in=None if cq_in is None else cq_in.to(DEV),
                         coeff_scale_in=None if cs_in is None else cs_in.to(DEV),
@@ -230,7 +230,7 @@ def test_workspace_shared_across_token_counts():
         err = torch.zeros(1, dtype=torch.int32, device=DEV)
         kernels.write_paged(lay, Kt[lo:hi], Vt[lo:hi], torch.arange(n, dtype=torch.int64, device=DEV),
                             torch.tensor([0, n], dtype=torch.int32, device=DEV), bt, dec_map,
-                            dec.unsqueeze(0).to(DEV), pinv.unsqueeze(0).to(DEV), page,
+                            dec_pool_of([dec], DEV), pinv.unsqueeze(0).to(DEV), page,
                             error_word=err, workspace=ws)
         torch.cuda.synchronize()
         assert int(err.item()) == 0
@@ -251,7 +251,7 @@ def test_write_flags_the_decoder_slots_it_uses():
     page = torch.zeros(16, C, dtype=torch.uint8, device=DEV)
     bt = torch.tensor([[3], [1]], dtype=torch.int32, device=DEV)   # request keys 3 and 1
     dec_map = torch.tensor([-1, 4, -1, 2, -1], dtype=torch.int32, device=DEV)
-    pool = dec.unsqueeze(0).repeat(6, 1, 1).to(DEV)
+    pool = dec_pool_of([dec] * 6, DEV)
     pinvs = pinv.unsqueeze(0).repeat(6, 1, 1).to(DEV)
     used = torch.zeros(6, dtype=torch.int32, device=DEV)
     err = torch.zeros(1, dtype=torch.int32, device=DEV)

@@ -11,7 +11,7 @@ enter). A request of ordinary values rides in the same launch and keeps the abso
 import pytest
 import torch
 
-from helpers import HQ, fitted_store, llama3_cache, paged
+from helpers import HQ, dec_pool_of, fitted_store, llama3_cache, paged
 from oracle import attend, codec, container as ocont
 from vllm_ttkv import container, kernels, synth
 
@@ -36,7 +36,7 @@ def _check(got, want, vs, what):
 
 def _dev(stores, seed):
     pg = paged(stores, 16, seed)
-    dec_pool = torch.stack([s["decoder"] for s in stores]).cuda()
+    dec_pool = dec_pool_of([s["decoder"] for s in stores])
     dec_map = torch.full((pg["num_blocks"],), -1, dtype=torch.int32)
     for r in range(len(stores)):
         dec_map[pg["block_table"][r, 0]] = r

@@ -26,8 +26,9 @@ def _noalloc(st, q, cos_sin, out, err, max_len=None):
         flat.data_ptr(), flat.shape[0], flat.stride(0),
         st["block_size"], st["block_table"].data_ptr(), st["block_table"].stride(0),
         st["block_table"].shape[1], st["seq_lens"].data_ptr(), qsl.data_ptr(), B, max_len,
-        st["dec_map"].data_ptr(), st["dec_map"].numel(), st["dec_pool"].data_ptr(),
-        st["dec_pool"].shape[0], cos_sin.data_ptr(), cos_sin.shape[0],
+        st["dec_map"].data_ptr(), st["dec_map"].numel(), st["dec_pool"].q.data_ptr(),
+        st["dec_pool"].scale.data_ptr(), st["dec_pool"].slots, cos_sin.data_ptr(),
+        cos_sin.shape[0],
         out.data_ptr(), _hip.DTYPE_CODE[out.dtype], out.stride(0), err.data_ptr(),
         _hip.stream_ptr(q.device))
     return rc

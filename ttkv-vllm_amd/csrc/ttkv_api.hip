@@ -55,6 +55,8 @@ extern "C" {
 
 const char* ttkv_last_error(void) { return t_err.c_str(); }
 
+int32_t ttkv_decoder_ranks(int32_t r1) { return r1 > 0 ? dec_ranks(r1) : -1; }
+
 int64_t ttkv_blob_bytes(const ttkv_layout* lay) {
   Geom g;
   return make_geom(lay, &g) ? g.blob : -1;
@@ -73,8 +75,8 @@ int ttkv_decode_paged(const ttkv_layout* lay, int32_t num_heads, float scale, co
                       int64_t slot_stride, int32_t block_size, const int32_t* block_table,
                       int64_t bt_row_stride, int32_t max_blocks, const int32_t* seq_lens,
                       const int32_t* query_start_loc, int32_t num_reqs, int32_t max_seq_len,
-                      const int32_t* dec_slot_of_block, int64_t num_blocks,
-                      const float* dec_pool, int64_t n_dec_slots, const float* cos_sin_cache,
+                      const int32_t* dec_slot_of_block, int64_t num_blocks, const int8_t* dec_q,
+                      const float* dec_scale, int64_t n_dec_slots, const float* cos_sin_cache,
                       int64_t max_position, void* out, int32_t out_dtype, int64_t out_row_stride,
                       void* workspace, int64_t workspace_bytes, int32_t* error_word,
                       ttkv_stream_t stream) {
@@ -83,7 +85,7 @@ int ttkv_decode_paged(const ttkv_layout* lay, int32_t num_heads, float scale, co
   return decode_paged(g, num_heads, scale, query, q_dtype, q_row_stride, page, n_slots,
                       slot_stride, block_size, block_table, bt_row_stride, max_blocks, seq_lens,
                       query_start_loc, num_reqs, max_seq_len, dec_slot_of_block, num_blocks,
-                      dec_pool, n_dec_slots, cos_sin_cache, max_position, out, out_dtype,
+                      dec_q, dec_scale, n_dec_slots, cos_sin_cache, max_position, out, out_dtype,
                       out_row_stride, workspace, workspace_bytes, error_word,
                       (hipStream_t)stream);
 }
@@ -91,11 +93,11 @@ int ttkv_decode_paged(const ttkv_layout* lay, int32_t num_heads, float scale, co
 int ttkv_decode_paged_noalloc(const ttkv_layout* lay, int32_t num_heads, float scale,
                               const void* query, int32_t q_dtype, int64_t q_row_stride,
                               const uint8_t* page, int64_t n_slots, int64_t slot_stride,
-                              int32_t block_size, const int32_t* block_table,
-                              int64_t bt_row_stride, int32_t max_blocks, const int32_t* seq_lens,
-                              const int32_t* query_start_loc, int32_t num_reqs,
-                              int32_t max_seq_len, const int32_t* dec_slot_of_block,
-                              int64_t num_blocks, const float* dec_pool, int64_t n_dec_slots,
+                              int32_t block_size, const int32_t* block_table, int64_t bt_row_stride,
+                              int32_t max_blocks, const int32_t* seq_lens,
+                              const int32_t* query_start_loc, int32_t num_reqs, int32_t max_seq_len,
+                              const int32_t* dec_slot_of_block, int64_t num_blocks,
+                              const int8_t* dec_q, const float* dec_scale, int64_t n_dec_slots,
                               const float* cos_sin_cache, int64_t max_position, void* out,
                               int32_t out_dtype, int64_t out_row_stride, int32_t* error_word,
                               ttkv_stream_t stream) {
@@ -103,8 +105,8 @@ int ttkv_decode_paged_noalloc(const ttkv_layout* lay, int32_t num_heads, float s
   if (!make_geom(lay, &g)) return host_fail(TTKV_E_INVALID, "invalid layout");
   return decode_paged_noalloc(g, num_heads, scale, query, q_dtype, q_row_stride, page, n_slots,
                               slot_stride, block_size, block_table, bt_row_stride, max_blocks,
-                              seq_lens, query_start_loc, num_reqs, max_seq_len,
-                              dec_slot_of_block, num_blocks, dec_pool, n_dec_slots, cos_sin_cache,
+                              seq_lens, query_start_loc, num_reqs, max_seq_len, dec_slot_of_block,
+                              num_blocks, dec_q, dec_scale, n_dec_slots, cos_sin_cache,
                               max_position, out, out_dtype, out_row_stride, error_word,
                               (hipStream_t)stream);
 }
@@ -114,8 +116,8 @@ int ttkv_write_paged(const ttkv_layout* lay, const void* key, int32_t k_dtype, i
                      const int64_t* slot_mapping, int32_t num_tokens,
                      const int32_t* query_start_loc, int32_t num_reqs, const int32_t* block_table,
                      int64_t bt_row_stride, const int32_t* dec_slot_of_block, int64_t num_blocks,
-                     const float* dec_pool, const float* pinv_pool, int64_t n_dec_slots,
-                     int32_t* dec_slot_used, const int8_t* coeff_q_in,
+                     const int8_t* dec_q, const float* dec_scale, const float* pinv_pool,
+                     int64_t n_dec_slots, int32_t* dec_slot_used, const int8_t* coeff_q_in,
                      const float* coeff_scale_in, uint8_t* page, int64_t n_slots,
                      int64_t slot_stride, float* coeff_out, float* resid_out, void* workspace,
                      int64_t workspace_bytes, int32_t* error_word, ttkv_stream_t stream) {
@@ -123,7 +125,7 @@ int ttkv_write_paged(const ttkv_layout* lay, const void* key, int32_t k_dtype, i
   if (!make_geom(lay, &g)) return host_fail(TTKV_E_INVALID, "invalid layout");
   return write_paged(g, key, k_dtype, k_row_stride, value, v_dtype, v_row_stride, slot_mapping,
                      num_tokens, query_start_loc, num_reqs, block_table, bt_row_stride,
-                     dec_slot_of_block, num_blocks, dec_pool, pinv_pool, n_dec_slots,
+                     dec_slot_of_block, num_blocks, dec_q, dec_scale, pinv_pool, n_dec_slots,
                      dec_slot_used, coeff_q_in,
                      coeff_scale_in, page, n_slots, slot_stride, coeff_out, resid_out, workspace,
                      workspace_bytes, error_word, (hipStream_t)stream);
@@ -144,22 +146,21 @@ int64_t ttkv_prefill_workspace_bytes(const ttkv_layout* lay, int32_t num_heads, 
 }
 
 int ttkv_prefill_paged(const ttkv_layout* lay, int32_t num_heads, float scale, const void* query,
-                       int32_t q_dtype, int64_t q_row_stride, const uint8_t* page,
-                       int64_t n_slots, int64_t slot_stride, int32_t block_size,
-                       const int32_t* block_table, int64_t bt_row_stride, int32_t max_blocks,
-                       const int32_t* seq_lens, const int32_t* query_start_loc,
-                       const int32_t* req_index, int32_t num_reqs, int32_t max_q_len,
-                       int32_t max_seq_len, const int32_t* dec_slot_of_block, int64_t num_blocks,
-                       const float* dec_pool, int64_t n_dec_slots, const float* cos_sin_cache,
-                       int64_t max_position, void* out, int32_t out_dtype, int64_t out_row_stride,
-                       void* workspace, int64_t workspace_bytes, int32_t* error_word,
-                       ttkv_stream_t stream) {
+                       int32_t q_dtype, int64_t q_row_stride, const uint8_t* page, int64_t n_slots,
+                       int64_t slot_stride, int32_t block_size, const int32_t* block_table,
+                       int64_t bt_row_stride, int32_t max_blocks, const int32_t* seq_lens,
+                       const int32_t* query_start_loc, const int32_t* req_index, int32_t num_reqs,
+                       int32_t max_q_len, int32_t max_seq_len, const int32_t* dec_slot_of_block,
+                       int64_t num_blocks, const int8_t* dec_q, const float* dec_scale,
+                       int64_t n_dec_slots, const float* cos_sin_cache, int64_t max_position,
+                       void* out, int32_t out_dtype, int64_t out_row_stride, void* workspace,
+                       int64_t workspace_bytes, int32_t* error_word, ttkv_stream_t stream) {
   Geom g;
   if (!make_geom(lay, &g)) return host_fail(TTKV_E_INVALID, "invalid layout");
   return prefill_paged(g, num_heads, scale, query, q_dtype, q_row_stride, page, n_slots,
                        slot_stride, block_size, block_table, bt_row_stride, max_blocks, seq_lens,
                        query_start_loc, req_index, num_reqs, max_q_len, max_seq_len,
-                       dec_slot_of_block, num_blocks, dec_pool, n_dec_slots, cos_sin_cache,
+                       dec_slot_of_block, num_blocks, dec_q, dec_scale, n_dec_slots, cos_sin_cache,
                        max_position, out, out_dtype, out_row_stride, nullptr, 0, 0, workspace,
                        workspace_bytes, error_word, (hipStream_t)stream);
 }
@@ -167,11 +168,11 @@ int ttkv_prefill_paged(const ttkv_layout* lay, int32_t num_heads, float scale, c
 int ttkv_multi_scores_paged(const ttkv_layout* lay, int32_t num_heads, float scale,
                             const void* query, int32_t q_dtype, int64_t q_row_stride,
                             const uint8_t* page, int64_t n_slots, int64_t slot_stride,
-                            int32_t block_size, const int32_t* block_table,
-                            int64_t bt_row_stride, int32_t max_blocks, const int32_t* seq_lens,
-                            const int32_t* query_start_loc, int32_t max_q_len,
-                            int32_t max_seq_len, const int32_t* dec_slot_of_block,
-                            int64_t num_blocks, const float* dec_pool, int64_t n_dec_slots,
+                            int32_t block_size, const int32_t* block_table, int64_t bt_row_stride,
+                            int32_t max_blocks, const int32_t* seq_lens,
+                            const int32_t* query_start_loc, int32_t max_q_len, int32_t max_seq_len,
+                            const int32_t* dec_slot_of_block, int64_t num_blocks,
+                            const int8_t* dec_q, const float* dec_scale, int64_t n_dec_slots,
                             const float* cos_sin_cache, int64_t max_position, float* scores,
                             int64_t s_head_stride, int64_t s_q_stride, void* workspace,
                             int64_t workspace_bytes, int32_t* error_word, ttkv_stream_t stream) {
@@ -182,8 +183,8 @@ int ttkv_multi_scores_paged(const ttkv_layout* lay, int32_t num_heads, float sca
   return prefill_paged(g, num_heads, scale, query, q_dtype, q_row_stride, page, n_slots,
                        slot_stride, block_size, block_table, bt_row_stride, max_blocks, seq_lens,
                        query_start_loc, nullptr, 1, max_q_len, max_seq_len, dec_slot_of_block,
-                       num_blocks, dec_pool, n_dec_slots, cos_sin_cache, max_position, nullptr, 0,
-                       0, scores, s_head_stride, s_q_stride, workspace, workspace_bytes,
+                       num_blocks, dec_q, dec_scale, n_dec_slots, cos_sin_cache, max_position,
+                       nullptr, 0, 0, scores, s_head_stride, s_q_stride, workspace, workspace_bytes,
                        error_word, (hipStream_t)stream);
 }
 

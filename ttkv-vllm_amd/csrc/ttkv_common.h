@@ -39,6 +39,22 @@ struct Geom {
 
 __host__ inline int align_up16(int n) { return (n + 15) / 16 * 16; }
 
+// Decoder pool (the codec's int8 decoder, ttkv_packed_cache.py:284-293, laid out for the kernels):
+//   dec_q     [slots, H*d, R] int8: column j = h*d + dim holds its R rank values contiguously
+//   dec_scale [slots, R] fp32: the rank's ruler
+// R = 64 for r1 <= 64, 128 for r1 <= 128, else r1 rounded up to 32: every kernel's rank window
+// (16-rank units in K1, 32-rank steps in K2 and K3) lies inside it. Ranks >= r1 hold 0 with ruler
+// 0. A decoder value is float(dec_q) * dec_scale, exact in fp32 (8 bits times the codec's 11-bit
+// fp16 ruler).
+__host__ __device__ inline int dec_ranks(int r1) {
+  return r1 <= 64 ? 64 : r1 <= 128 ? 128 : (r1 + 31) & ~31;
+}
+
+// Decoder value of rank 4m + k (k = 0..3) from the dword of ranks 4m .. 4m+3 and its ruler.
+__device__ __forceinline__ float dec_value(uint32_t q4, int k, float ruler) {
+  return (float)(int8_t)(q4 >> (8 * k)) * ruler;
+}
+
 __host__ inline bool make_geom(const ttkv_layout* l, Geom* g) {
   if (!l) return false;
   g->H = l->H; g->d = l->d; g->r1 = l->r1; g->qbits = l->qbits;

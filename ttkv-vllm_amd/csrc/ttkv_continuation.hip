@@ -78,7 +78,8 @@ struct ExpandArgs {
   int ri0, num_reqs;
   const int32_t* dec_map;
   int64_t num_blocks;
-  const float* dec_pool;
+  const int8_t* dec_q;  // decoder pool (see dec_ranks)
+  const float* dec_scale;
   int64_t n_dec_slots;
   const float* cs_cache;
   uint8_t* tiles;     // [num_reqs][H][ntl] tiles of kTileBytes
@@ -144,18 +145,33 @@ __global__ __launch_bounds__(kXThreads, 2) void expand_kernel(ExpandArgs a) {
   build_luts(S.lut, (RB == 3 || VB == 3) ? lut3s : nullptr, tid, kXThreads);
 
   // decoder fragments (A operand, M = dims), hi + lo fp16, resident in registers
+  // (int8 ranks 32s + 8gq .. +7 of the lane's two columns, 8 bytes per step, and their rulers;
+  // 32 KSTEPS <= R, so every load is inside the decoder)
   const int HD = g.H * kD;
-  const float* dec = a.dec_pool + (int64_t)dslot * g.r1 * HD + h * kD;
+  const int R = dec_ranks(g.r1);
+  const int8_t* decq = a.dec_q + ((int64_t)dslot * HD + h * kD) * R;
+  const float* decs = a.dec_scale + (int64_t)dslot * R;
+  u32x2v dq[2][KSTEPS];
+  float4v dsc[2 * KSTEPS];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi) {
+    const int8_t* col = decq + (int64_t)(16 * (wv + 4 * mi) + n) * R;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) dq[mi][s] = *gbl((const u32x2v*)(col + 32 * s + 8 * gq));
+  }
+#pragma unroll
+  for (int s = 0; s < 2 * KSTEPS; ++s)
+    dsc[s] = *gbl((const float4v*)(decs + 32 * (s >> 1) + 8 * gq + 4 * (s & 1)));
   half8 ahi[2][KSTEPS], alo[2][KSTEPS];
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi) {
-    const int dim = 16 * (wv + 4 * mi) + n;
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int ar = 32 * s + 8 * gq + j;
-        const float f = ar < g.r1 ? dec[(int64_t)ar * HD + dim] : 0.f;
+        const float f =
+            ar < g.r1 ? dec_value(dq[mi][s][j >> 2], j & 3, dsc[2 * s + (j >> 2)][j & 3]) : 0.f;
         const _Float16 hi = (_Float16)f;
         ahi[mi][s][j] = hi;
         alo[mi][s][j] = (_Float16)(f - (float)hi);
@@ -1049,9 +1065,9 @@ int launch_scores_t(const ScoresArgs& a, int grid, hipStream_t st) {
 int expand_rows(const Geom& g, const uint8_t* page, int64_t n_slots, int64_t slot_stride,
                 int block_size, const int32_t* bt, int64_t bt_row_stride, const int32_t* seq_lens,
                 const int32_t* req_index, int ri0, int nr, int ntl, int max_seq_len,
-                const int32_t* dec_map, int64_t num_blocks, const float* dec_pool,
-                int64_t n_dec_slots, const float* cs_cache, uint8_t* tiles, int32_t* err,
-                hipStream_t st) {
+                const int32_t* dec_map, int64_t num_blocks, const int8_t* dec_q,
+                const float* dec_scale, int64_t n_dec_slots, const float* cs_cache, uint8_t* tiles,
+                int32_t* err, hipStream_t st) {
   ExpandArgs e{};
   e.g = g;
   e.page = page;
@@ -1066,7 +1082,8 @@ int expand_rows(const Geom& g, const uint8_t* page, int64_t n_slots, int64_t slo
   e.num_reqs = nr;
   e.dec_map = dec_map;
   e.num_blocks = num_blocks;
-  e.dec_pool = dec_pool;
+  e.dec_q = dec_q;
+  e.dec_scale = dec_scale;
   e.n_dec_slots = n_dec_slots;
   e.cs_cache = cs_cache;
   e.tiles = tiles;
@@ -1099,14 +1116,14 @@ int continuation_scores(const Geom& g, int HQ, float scale, const void* q, int q
                         int64_t slot_stride, int block_size, const int32_t* bt,
                         int64_t bt_row_stride, const int32_t* seq_lens, const int32_t* qsl,
                         int max_q_len, int max_seq_len, const int32_t* dec_map, int64_t num_blocks,
-                        const float* dec_pool, int64_t n_dec_slots, const float* cs_cache,
-                        float* s_out, int64_t s_head_stride, int64_t s_q_stride, void* ws,
-                        int32_t* err, hipStream_t st) {
+                        const int8_t* dec_q, const float* dec_scale, int64_t n_dec_slots,
+                        const float* cs_cache, float* s_out, int64_t s_head_stride,
+                        int64_t s_q_stride, void* ws, int32_t* err, hipStream_t st) {
   const int G = HQ / g.H;
   const int ntl = ceil_div(max_seq_len, kXTile);
   uint8_t* tiles = (uint8_t*)ws;
   if (int rc = expand_rows(g, page, n_slots, slot_stride, block_size, bt, bt_row_stride, seq_lens,
-                           nullptr, 0, 1, ntl, max_seq_len, dec_map, num_blocks, dec_pool,
+                           nullptr, 0, 1, ntl, max_seq_len, dec_map, num_blocks, dec_q, dec_scale,
                            n_dec_slots, cs_cache, tiles, err, st))
     return rc;
   ScoresArgs b{};
@@ -1171,9 +1188,10 @@ int continuation_paged(const Geom& g, int HQ, float scale, const void* q, int q_
                        int64_t slot_stride, int block_size, const int32_t* bt,
                        int64_t bt_row_stride, const int32_t* seq_lens, const int32_t* qsl,
                        const int32_t* req_index, int num_reqs, int max_q_len, int max_seq_len,
-                       const int32_t* dec_map, int64_t num_blocks, const float* dec_pool,
-                       int64_t n_dec_slots, const float* cs_cache, void* out, int out_dtype,
-                       int64_t out_row_stride, void* ws, int32_t* err, hipStream_t st) {
+                       const int32_t* dec_map, int64_t num_blocks, const int8_t* dec_q,
+                       const float* dec_scale, int64_t n_dec_slots, const float* cs_cache,
+                       void* out, int out_dtype, int64_t out_row_stride, void* ws, int32_t* err,
+                       hipStream_t st) {
   const int G = HQ / g.H;
   const int slice = cont_slice_reqs(g, num_reqs, max_q_len, max_seq_len);
   for (int ri0 = 0; ri0 < num_reqs; ri0 += slice) {
@@ -1183,7 +1201,7 @@ int continuation_paged(const Geom& g, int HQ, float scale, const void* q, int q_
 
     if (int rc = expand_rows(g, page, n_slots, slot_stride, block_size, bt, bt_row_stride,
                              seq_lens, req_index, ri0, nr, s.ntl, max_seq_len, dec_map,
-                             num_blocks, dec_pool, n_dec_slots, cs_cache, tiles, err, st))
+                             num_blocks, dec_q, dec_scale, n_dec_slots, cs_cache, tiles, err, st))
       return rc;
 
     AttendArgs b{};

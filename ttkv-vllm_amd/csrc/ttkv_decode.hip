@@ -79,7 +79,8 @@ struct DecodeArgs {
   int num_reqs;
   const int32_t* dec_map;
   int64_t num_blocks;
-  const float* dec_pool;
+  const int8_t* dec_q;  // decoder pool (see dec_ranks)
+  const float* dec_scale;
   int64_t n_dec_slots;
   const float* cs_cache;
   int64_t max_pos;
@@ -388,24 +389,29 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   // overlaps the table and block-id staging
   const int dl = 16 * wv + 4 * gq;
   const int HD = g.H * kD;
-  const float* dec = a.dec_pool + (int64_t)dslot * g.r1 * HD + h * kD;
-  float draw[2][KSTEPS * 8 + 4];
+  // int8 ranks 32s + 8gq .. +7 of each of the lane's two columns (one 8-byte load per step; the
+  // k = 16 tail step: ranks 32 KSTEPS + 4gq .. +3, 4 bytes) and their rulers (one float4 per 4
+  // ranks, the same for both columns). 16 KU <= R, so every load is inside the decoder.
+  const int R = dec_ranks(g.r1);
+  const int8_t* decq = a.dec_q + ((int64_t)dslot * HD + h * kD) * R;
+  const float* decs = a.dec_scale + (int64_t)dslot * R;
+  u32x2v dq[2][KSTEPS];
+  uint32_t dqt[2] = {0u, 0u};
+  float4v dsc[2 * KSTEPS + 1];
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi) {
-    const int dim = 16 * (wv + 4 * mi) + n;
+    const int8_t* col = decq + (int64_t)(16 * (wv + 4 * mi) + n) * R;
 #pragma unroll
-    for (int s = 0; s < KSTEPS; ++s)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int ar = 32 * s + 8 * gq + j;
-        draw[mi][8 * s + j] = ar < g.r1 ? dec[(int64_t)ar * HD + dim] : 0.f;
-      }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int ar = 32 * KSTEPS + 4 * gq + j;
-      draw[mi][8 * KSTEPS + j] = KTAIL && ar < g.r1 ? dec[(int64_t)ar * HD + dim] : 0.f;
-    }
+    for (int s = 0; s < KSTEPS; ++s) dq[mi][s] = *gbl((const u32x2v*)(col + 32 * s + 8 * gq));
+    if constexpr (KTAIL) dqt[mi] = *gbl((const uint32_t*)(col + 32 * KSTEPS + 4 * gq));
   }
+#pragma unroll
+  for (int s = 0; s < KSTEPS; ++s) {
+    dsc[2 * s] = *gbl((const float4v*)(decs + 32 * s + 8 * gq));
+    dsc[2 * s + 1] = *gbl((const float4v*)(decs + 32 * s + 8 * gq + 4));
+  }
+  dsc[2 * KSTEPS] = KTAIL ? *gbl((const float4v*)(decs + 32 * KSTEPS + 4 * gq))
+                          : float4v{0.f, 0.f, 0.f, 0.f};
   // (rows n >= G of the fragment are zero: they load head G - 1 and discard it, so the loads
   // carry no branch and go out together)
   float qraw[8];
@@ -463,14 +469,18 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
     for (int s = 0; s < KSTEPS; ++s)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float f = draw[mi][8 * s + j];
+        const int ar = 32 * s + 8 * gq + j;
+        const uint32_t q4 = dq[mi][s][j >> 2];
+        const float f = ar < g.r1 ? dec_value(q4, j & 3, dsc[2 * s + (j >> 2)][j & 3]) : 0.f;
         const _Float16 hi = (_Float16)f;
         ahi[mi][s][j] = hi;
         alo[mi][s][j] = (_Float16)(f - (float)hi);
       }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float f = j < 4 ? draw[mi][8 * KSTEPS + j] : 0.f;
+      const int ar = 32 * KSTEPS + 4 * gq + j;
+      const float f =
+          j < 4 && ar < g.r1 ? dec_value(dqt[mi], j & 3, dsc[2 * KSTEPS][j & 3]) : 0.f;
       const _Float16 hi = (_Float16)f;
       thi[mi][j] = hi;
       tlo[mi][j] = (_Float16)(f - (float)hi);
@@ -999,10 +1009,10 @@ int decode_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype,
                  int64_t q_row_stride, const uint8_t* page, int64_t n_slots, int64_t slot_stride,
                  int block_size, const int32_t* bt, int64_t bt_row_stride, int max_blocks,
                  const int32_t* seq_lens, const int32_t* qsl, int num_reqs, int max_seq_len,
-                 const int32_t* dec_map, int64_t num_blocks, const float* dec_pool,
-                 int64_t n_dec_slots, const float* cs_cache, int64_t max_pos, void* out,
-                 int out_dtype, int64_t out_row_stride, void* ws, int64_t ws_bytes, int32_t* err,
-                 hipStream_t st) {
+                 const int32_t* dec_map, int64_t num_blocks, const int8_t* dec_q,
+                 const float* dec_scale, int64_t n_dec_slots, const float* cs_cache,
+                 int64_t max_pos, void* out, int out_dtype, int64_t out_row_stride, void* ws,
+                 int64_t ws_bytes, int32_t* err, hipStream_t st) {
   if (g.d != kD) return host_fail(TTKV_E_UNSUPPORTED, "head dim must be 128");
   if (g.qbits != 8) return host_fail(TTKV_E_UNSUPPORTED, "coefficient width must be 8 bits");
   if (!((g.res_bits == 3 && g.v_bits == 3) || (g.res_bits == 4 && g.v_bits == 4)))
@@ -1019,8 +1029,9 @@ int decode_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype,
     return host_fail(TTKV_E_UNSUPPORTED, "a head row of " + std::to_string(g.k_row) + "/" +
                                              std::to_string(g.v_row) +
                                              " bytes straddles its 64-byte load window");
-  if (!q || !page || !bt || !seq_lens || !qsl || !dec_map || !dec_pool || !cs_cache || !out || !err)
+  if (!q || !page || !bt || !seq_lens || !qsl || !dec_map || !cs_cache || !out || !err)
     return host_fail(TTKV_E_INVALID, "null pointer argument");
+  if (int rc = check_dec_pool(dec_q, dec_scale)) return rc;
   if ((uintptr_t)page % 16 || slot_stride % 16 || slot_stride < g.blob)
     return host_fail(TTKV_E_INVALID,
                      "page must be 16-byte aligned with a slot stride that is a multiple of 16 and "
@@ -1059,7 +1070,8 @@ int decode_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype,
   a.num_reqs = num_reqs;
   a.dec_map = dec_map;
   a.num_blocks = num_blocks;
-  a.dec_pool = dec_pool;
+  a.dec_q = dec_q;
+  a.dec_scale = dec_scale;
   a.n_dec_slots = n_dec_slots;
   a.cs_cache = cs_cache;
   a.max_pos = max_pos;
@@ -1160,8 +1172,8 @@ int decode_paged_noalloc(const Geom& g, int HQ, float scale, const void* q, int 
                          int64_t q_row_stride, const uint8_t* page, int64_t n_slots,
                          int64_t slot_stride, int block_size, const int32_t* bt,
                          int64_t bt_row_stride, int max_blocks, const int32_t* seq_lens,
-                         const int32_t* qsl, int num_reqs, int max_seq_len,
-                         const int32_t* dec_map, int64_t num_blocks, const float* dec_pool,
+                         const int32_t* qsl, int num_reqs, int max_seq_len, const int32_t* dec_map,
+                         int64_t num_blocks, const int8_t* dec_q, const float* dec_scale,
                          int64_t n_dec_slots, const float* cs_cache, int64_t max_pos, void* out,
                          int out_dtype, int64_t out_row_stride, int32_t* err, hipStream_t st) {
   if (g.H <= 0 || HQ <= 0 || HQ % g.H) return host_fail(TTKV_E_INVALID, "num_heads is not a multiple of H");
@@ -1177,8 +1189,8 @@ int decode_paged_noalloc(const Geom& g, int HQ, float scale, const void* q, int 
   if (!ws) return TTKV_E_LAUNCH;
   return decode_paged(g, HQ, scale, q, q_dtype, q_row_stride, page, n_slots, slot_stride,
                       block_size, bt, bt_row_stride, max_blocks, seq_lens, qsl, num_reqs,
-                      max_seq_len, dec_map, num_blocks, dec_pool, n_dec_slots, cs_cache, max_pos,
-                      out, out_dtype, out_row_stride, ws, kScratchBytes, err, st);
+                      max_seq_len, dec_map, num_blocks, dec_q, dec_scale, n_dec_slots, cs_cache,
+                      max_pos, out, out_dtype, out_row_stride, ws, kScratchBytes, err, st);
 }
 
 }  // namespace ttkv

@@ -68,7 +68,8 @@ struct PrefillArgs {
   int num_reqs;
   const int32_t* dec_map;
   int64_t num_blocks;
-  const float* dec_pool;
+  const int8_t* dec_q;  // decoder pool (see dec_ranks)
+  const float* dec_scale;
   int64_t n_dec_slots;
   const float* cs_cache;
   void* out;
@@ -204,18 +205,25 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
   }
 
   // ---- decoder fragments (A operand of the reconstruction, M = dims), resident in registers
+  // (int8 ranks 32s + 8gq .. +7 of the lane's two columns, 8 bytes per step, and their rulers;
+  // 32 KSTEPS <= R, so every load is inside the decoder)
   const int HD = g.H * kD;
-  const float* dec = a.dec_pool + (int64_t)dslot * g.r1 * HD + h * kD;
+  const int R = dec_ranks(g.r1);
+  const int8_t* decq = a.dec_q + ((int64_t)dslot * HD + h * kD) * R;
+  const float* decs = a.dec_scale + (int64_t)dslot * R;
   half8 ahi[2][KSTEPS], alo[2][EXACT ? KSTEPS : 1];
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi) {
-    const int dim = 16 * (wv + 4 * mi) + n;
+    const int8_t* col = decq + (int64_t)(16 * (wv + 4 * mi) + n) * R;
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) {
+      const u32x2v q8 = *gbl((const u32x2v*)(col + 32 * s + 8 * gq));
+      const float4v s0 = *gbl((const float4v*)(decs + 32 * s + 8 * gq));
+      const float4v s1 = *gbl((const float4v*)(decs + 32 * s + 8 * gq + 4));
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int ar = 32 * s + 8 * gq + j;
-        const float f = ar < g.r1 ? dec[(int64_t)ar * HD + dim] : 0.f;
+        const float f = ar < g.r1 ? dec_value(q8[j >> 2], j & 3, j < 4 ? s0[j] : s1[j - 4]) : 0.f;
         const _Float16 hi = (_Float16)f;
         ahi[mi][s][j] = hi;
         if constexpr (EXACT) alo[mi][s][j] = (_Float16)(f - (float)hi);
@@ -738,10 +746,10 @@ int prefill_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype
                   int block_size, const int32_t* bt, int64_t bt_row_stride, int max_blocks,
                   const int32_t* seq_lens, const int32_t* qsl, const int32_t* req_index,
                   int num_reqs, int max_q_len, int max_seq_len, const int32_t* dec_map,
-                  int64_t num_blocks, const float* dec_pool, int64_t n_dec_slots,
-                  const float* cs_cache, int64_t max_pos, void* out, int out_dtype,
-                  int64_t out_row_stride, float* s_out, int64_t s_head_stride, int64_t s_q_stride,
-                  void* ws, int64_t ws_bytes, int32_t* err, hipStream_t st) {
+                  int64_t num_blocks, const int8_t* dec_q, const float* dec_scale,
+                  int64_t n_dec_slots, const float* cs_cache, int64_t max_pos, void* out,
+                  int out_dtype, int64_t out_row_stride, float* s_out, int64_t s_head_stride,
+                  int64_t s_q_stride, void* ws, int64_t ws_bytes, int32_t* err, hipStream_t st) {
   const bool scores = s_out != nullptr;
   if (g.d != kD) return host_fail(TTKV_E_UNSUPPORTED, "head dim must be 128");
   if (g.qbits != 8) return host_fail(TTKV_E_UNSUPPORTED, "coefficient width must be 8 bits");
@@ -757,8 +765,9 @@ int prefill_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype
     return host_fail(TTKV_E_UNSUPPORTED, "a head row of " + std::to_string(g.k_row) + "/" +
                                              std::to_string(g.v_row) +
                                              " bytes straddles its 64-byte load window");
-  if (!q || !page || !bt || !seq_lens || !qsl || !dec_map || !dec_pool || !cs_cache || !err)
+  if (!q || !page || !bt || !seq_lens || !qsl || !dec_map || !cs_cache || !err)
     return host_fail(TTKV_E_INVALID, "null pointer argument");
+  if (int rc = check_dec_pool(dec_q, dec_scale)) return rc;
   if (!scores && !out) return host_fail(TTKV_E_INVALID, "out is null");
   if ((uintptr_t)page % 16 || slot_stride % 16 || slot_stride < g.blob)
     return host_fail(TTKV_E_INVALID,
@@ -803,7 +812,8 @@ int prefill_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype
   a.num_reqs = num_reqs;
   a.dec_map = dec_map;
   a.num_blocks = num_blocks;
-  a.dec_pool = dec_pool;
+  a.dec_q = dec_q;
+  a.dec_scale = dec_scale;
   a.n_dec_slots = n_dec_slots;
   a.cs_cache = cs_cache;
   a.out = out;
@@ -836,15 +846,15 @@ int prefill_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype
     if (need && ws_bytes >= need && (uintptr_t)ws % 256 == 0)
       return continuation_scores(g, HQ, scale, q, q_dtype, q_row_stride, page, n_slots,
                                  slot_stride, block_size, bt, bt_row_stride, seq_lens, qsl,
-                                 max_q_len, max_seq_len, dec_map, num_blocks, dec_pool,
+                                 max_q_len, max_seq_len, dec_map, num_blocks, dec_q, dec_scale,
                                  n_dec_slots, cs_cache, s_out, s_head_stride, s_q_stride, ws, err,
                                  st);
   }
   if (!scores && continuation_applies(g, G, max_q_len))
     return continuation_paged(g, HQ, scale, q, q_dtype, q_row_stride, page, n_slots, slot_stride,
                               block_size, bt, bt_row_stride, seq_lens, qsl, req_index, num_reqs,
-                              max_q_len, max_seq_len, dec_map, num_blocks, dec_pool, n_dec_slots,
-                              cs_cache, out, out_dtype, out_row_stride, ws, err, st);
+                              max_q_len, max_seq_len, dec_map, num_blocks, dec_q, dec_scale,
+                              n_dec_slots, cs_cache, out, out_dtype, out_row_stride, ws, err, st);
   const int slice = prefill_slice_reqs(g, num_reqs, max_q_len);
   for (int ri0 = 0; ri0 < num_reqs; ri0 += slice) {
     PrefillArgs b = a;

@@ -48,7 +48,8 @@ struct WriteArgs {
   int64_t bt_row_stride;
   const int32_t* dec_map;
   int64_t num_blocks;
-  const float* dec_pool;
+  const int8_t* dec_q;  // decoder pool (see dec_ranks)
+  const float* dec_scale;
   const float* pinv_pool;
   int64_t n_dec_slots;
   int32_t* dec_used;  // [n_dec_slots] or null: set to 1 for every decoder slot a token uses
@@ -299,18 +300,25 @@ __global__ __launch_bounds__(kWThreads) void write_pack_kernel(WriteArgs a) {
     if (ds >= 0 && a.dec_used) a.dec_used[ds] = 1;
   }
   if (ds < 0 || !slot_ok) return;
-  // this head's decoder columns (rows a = wv, wv + 4, ...; lane l holds dims 2l and 2l + 1, one
-  // 8-byte load per row), requested before the coefficients are needed (r1 <= kDecRows * 4
-  // here). Rows past r1 re-read row r1 - 1 and are multiplied by 0.
-  const float* dec = a.dec_pool + (int64_t)ds * g.r1 * HD + h * kD + 2 * lane;
-  constexpr int kDecRows = 32;
-  float2v dr[kDecRows];
-  const bool dec_regs = g.r1 <= 4 * kDecRows;
-  if (dec_regs) {
+  // this head's decoder columns h*d + 2l and h*d + 2l + 1 (lane l): wave w sums ranks
+  // 32w .. 32w + 31 of each 128-rank block, 32 int8 per column (two 16-byte loads) times their 32
+  // rulers (the same for every lane of the wave). The first block is requested before the
+  // coefficients are needed.
+  const int R = dec_ranks(g.r1);
+  const int8_t* dcol = a.dec_q + ((int64_t)ds * HD + h * kD + 2 * lane) * R;
+  const float* drul = a.dec_scale + (int64_t)ds * R;
+  u32x4 dqv[4];
+  float4v dsv[8];
+  auto load_ranks = [&](int b0) {
 #pragma unroll
-    for (int u = 0; u < kDecRows; ++u)
-      dr[u] = *(const float2v*)&dec[(int64_t)min(wv + 4 * u, g.r1 - 1) * HD];
-  }
+    for (int c = 0; c < 2; ++c) {
+      dqv[2 * c] = *gbl((const u32x4*)(dcol + c * R + b0));
+      dqv[2 * c + 1] = *gbl((const u32x4*)(dcol + c * R + b0 + 16));
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) dsv[k] = *gbl((const float4v*)(drul + b0 + 4 * k));
+  };
+  if (32 * wv < R) load_ranks(32 * wv);
   if (tid < g.r1) cqs[tid] = qv * cs;  // r1 <= 256 threads (host-checked)
   uint8_t* base = a.page + slot * a.slot_stride;
   if (h == 0) {
@@ -324,30 +332,20 @@ __global__ __launch_bounds__(kWThreads) void write_pack_kernel(WriteArgs a) {
     for (int b = g.k_slot + g.H * g.v_row + tid; b < g.blob; b += kWThreads) base[b] = 0;
   }
   __syncthreads();
-  // R[j] = K[h*d+j] - sum_a cqs[a] * dec[a][h*d+j]: wave w sums a = w, w+4, ...; lane l owns
-  // dims 2l and 2l + 1
+  // R[j] = K[h*d+j] - sum_a cqs[a] * dec[a][h*d+j]: wave w sums its ranks in increasing order,
+  // lane l owns dims 2l and 2l + 1
   float acc0 = 0.f, acc1 = 0.f;
-  if (dec_regs) {
+  for (int b0 = 32 * wv; b0 < R; b0 += 128) {
+    if (b0 != 32 * wv) load_ranks(b0);
 #pragma unroll
-    for (int u = 0; u < kDecRows; ++u) {
-      const int ar = wv + 4 * u;
+    for (int k = 0; k < 32; ++k) {
+      const int ar = b0 + k;
+      const float rul = dsv[k >> 2][k & 3];
       const float c = ar < g.r1 ? cqs[ar] : 0.f;
-      acc0 = fmaf(c, dr[u][0], acc0);
-      acc1 = fmaf(c, dr[u][1], acc1);
-    }
-  }
-  // larger ranks: rows in batches of 16 whose loads are all issued before their sums
-  for (int a0 = wv; !dec_regs && a0 < g.r1; a0 += 64) {
-    float2v db[16];
-#pragma unroll
-    for (int u = 0; u < 16; ++u)
-      db[u] = *(const float2v*)&dec[(int64_t)min(a0 + 4 * u, g.r1 - 1) * HD];
-#pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const int ar = a0 + 4 * u;
-      const float c = ar < g.r1 ? cqs[ar] : 0.f;
-      acc0 = fmaf(c, db[u][0], acc0);
-      acc1 = fmaf(c, db[u][1], acc1);
+      const float d0 = ar < g.r1 ? dec_value(dqv[k >> 4][(k >> 2) & 3], k & 3, rul) : 0.f;
+      const float d1 = ar < g.r1 ? dec_value(dqv[2 + (k >> 4)][(k >> 2) & 3], k & 3, rul) : 0.f;
+      acc0 = fmaf(c, d0, acc0);
+      acc1 = fmaf(c, d1, acc1);
     }
   }
   rp[wv][2 * lane] = acc0;
@@ -377,12 +375,11 @@ int64_t write_workspace_bytes(const Geom& g, int num_tokens) {
 int write_paged(const Geom& g, const void* key, int k_dtype, int64_t k_row_stride, const void* val,
                 int v_dtype, int64_t v_row_stride, const int64_t* slot_mapping, int num_tokens,
                 const int32_t* qsl, int num_reqs, const int32_t* bt, int64_t bt_row_stride,
-                const int32_t* dec_map, int64_t num_blocks, const float* dec_pool,
-                const float* pinv_pool, int64_t n_dec_slots, int32_t* dec_used,
-                const int8_t* cq_in,
-                const float* cs_in, uint8_t* page, int64_t n_slots, int64_t slot_stride,
-                float* c_out, float* r_out, void* ws, int64_t ws_bytes, int32_t* err,
-                hipStream_t st) {
+                const int32_t* dec_map, int64_t num_blocks, const int8_t* dec_q,
+                const float* dec_scale, const float* pinv_pool, int64_t n_dec_slots,
+                int32_t* dec_used, const int8_t* cq_in, const float* cs_in, uint8_t* page,
+                int64_t n_slots, int64_t slot_stride, float* c_out, float* r_out, void* ws,
+                int64_t ws_bytes, int32_t* err, hipStream_t st) {
   if (g.d != kD) return host_fail(TTKV_E_UNSUPPORTED, "head dim must be 128");
   if (g.H > 8) return host_fail(TTKV_E_UNSUPPORTED, "H > 8 KV heads is not built");
   if (g.qbits != 8) return host_fail(TTKV_E_UNSUPPORTED, "coefficient width must be 8 bits");
@@ -390,7 +387,7 @@ int write_paged(const Geom& g, const void* key, int k_dtype, int64_t k_row_strid
   if (g.res_k < 1) return host_fail(TTKV_E_UNSUPPORTED, "res_k must be >= 1");
   if (!((g.res_bits == 3 && g.v_bits == 3) || (g.res_bits == 4 && g.v_bits == 4)))
     return host_fail(TTKV_E_UNSUPPORTED, "res_bits/v_bits must be 3/3 or 4/4");
-  if (!key || !val || !slot_mapping || !qsl || !bt || !dec_map || !dec_pool || !page || !err)
+  if (!key || !val || !slot_mapping || !qsl || !bt || !dec_map || !page || !err)
     return host_fail(TTKV_E_INVALID, "null pointer argument");
   if (!cq_in && !pinv_pool) return host_fail(TTKV_E_INVALID, "need pinv_pool or coeff_q_in");
   if (cq_in && !cs_in) return host_fail(TTKV_E_INVALID, "coeff_q_in needs coeff_scale_in");
@@ -406,8 +403,7 @@ int write_paged(const Geom& g, const void* key, int k_dtype, int64_t k_row_strid
                                              " bytes (256-aligned), got " +
                                              std::to_string(ws_bytes));
   }
-  if ((uintptr_t)dec_pool % 8)
-    return host_fail(TTKV_E_INVALID, "dec_pool must be 8-byte aligned");
+  if (int rc = check_dec_pool(dec_q, dec_scale)) return rc;
   WriteArgs a{};
   a.g = g;
   a.key = key;
@@ -424,7 +420,8 @@ int write_paged(const Geom& g, const void* key, int k_dtype, int64_t k_row_strid
   a.bt_row_stride = bt_row_stride;
   a.dec_map = dec_map;
   a.num_blocks = num_blocks;
-  a.dec_pool = dec_pool;
+  a.dec_q = dec_q;
+  a.dec_scale = dec_scale;
   a.pinv_pool = pinv_pool;
   a.n_dec_slots = n_dec_slots;
   a.dec_used = dec_used;

@@ -56,6 +56,8 @@ def lib():
     LP = ctypes.POINTER(Layout)
     L.ttkv_last_error.restype = ctypes.c_char_p
     L.ttkv_last_error.argtypes = []
+    L.ttkv_decoder_ranks.restype = I32
+    L.ttkv_decoder_ranks.argtypes = [I32]
     L.ttkv_blob_bytes.restype = I64
     L.ttkv_blob_bytes.argtypes = [LP]
     L.ttkv_decode_workspace_bytes.restype = I64
@@ -67,7 +69,8 @@ def lib():
         P, I64, I64,                  # page, n_slots, slot_stride
         I32, P, I64, I32,             # block_size, block_table, bt_row_stride, max_blocks
         P, P, I32, I32,               # seq_lens, query_start_loc, num_reqs, max_seq_len
-        P, I64, P, I64,               # dec_slot_of_block, num_blocks, dec_pool, n_dec_slots
+        P, I64,                       # dec_slot_of_block, num_blocks
+        P, P, I64,                    # dec_q, dec_scale, n_dec_slots
         P, I64,                       # cos_sin_cache, max_position
         P, I32, I64,                  # out, out_dtype, out_row_stride
         P, I64, P,                    # workspace, workspace_bytes, error_word
@@ -80,7 +83,8 @@ def lib():
         P, I64, I64,                  # page, n_slots, slot_stride
         I32, P, I64, I32,             # block_size, block_table, bt_row_stride, max_blocks
         P, P, I32, I32,               # seq_lens, query_start_loc, num_reqs, max_seq_len
-        P, I64, P, I64,               # dec_slot_of_block, num_blocks, dec_pool, n_dec_slots
+        P, I64,                       # dec_slot_of_block, num_blocks
+        P, P, I64,                    # dec_q, dec_scale, n_dec_slots
         P, I64,                       # cos_sin_cache, max_position
         P, I32, I64,                  # out, out_dtype, out_row_stride
         P,                            # error_word
@@ -92,7 +96,7 @@ def lib():
         P, I32, I64,                  # value, v_dtype, v_row_stride
         P, I32, P, I32,               # slot_mapping, num_tokens, query_start_loc, num_reqs
         P, I64, P, I64,               # block_table, bt_row_stride, dec_slot_of_block, num_blocks
-        P, P, I64, P,                 # dec_pool, pinv_pool, n_dec_slots, dec_slot_used
+        P, P, P, I64, P,              # dec_q, dec_scale, pinv_pool, n_dec_slots, dec_slot_used
         P, P,                         # coeff_q_in, coeff_scale_in
         P, I64, I64,                  # page, n_slots, slot_stride
         P, P,                         # coeff_out, resid_out
@@ -110,7 +114,8 @@ def lib():
         I32, P, I64, I32,             # block_size, block_table, bt_row_stride, max_blocks
         P, P, P,                      # seq_lens, query_start_loc, req_index
         I32, I32, I32,                # num_reqs, max_q_len, max_seq_len
-        P, I64, P, I64,               # dec_slot_of_block, num_blocks, dec_pool, n_dec_slots
+        P, I64,                       # dec_slot_of_block, num_blocks
+        P, P, I64,                    # dec_q, dec_scale, n_dec_slots
         P, I64,                       # cos_sin_cache, max_position
         P, I32, I64,                  # out, out_dtype, out_row_stride
         P, I64, P,                    # workspace, workspace_bytes, error_word
@@ -123,7 +128,8 @@ def lib():
         P, I64, I64,                  # page, n_slots, slot_stride
         I32, P, I64, I32,             # block_size, block_table, bt_row_stride, max_blocks
         P, P, I32, I32,               # seq_lens, query_start_loc, max_q_len, max_seq_len
-        P, I64, P, I64,               # dec_slot_of_block, num_blocks, dec_pool, n_dec_slots
+        P, I64,                       # dec_slot_of_block, num_blocks
+        P, P, I64,                    # dec_q, dec_scale, n_dec_slots
         P, I64,                       # cos_sin_cache, max_position
         P, I64, I64,                  # scores, s_head_stride, s_q_stride
         P, I64, P, P,                 # workspace, workspace_bytes, error_word, stream
@@ -161,9 +167,9 @@ def lib():
 
 
 # Every symbol include/ttkv_hip.h declares (checked by tests/test_abi.py).
-EXPORTS = ("ttkv_last_error", "ttkv_blob_bytes", "ttkv_decode_workspace_bytes",
-           "ttkv_decode_paged", "ttkv_decode_paged_noalloc", "ttkv_write_paged", "ttkv_prefill_workspace_bytes",
-           "ttkv_prefill_paged", "ttkv_multi_scores_paged", "ttkv_multi_scores_workspace_bytes",
+EXPORTS = ("ttkv_last_error", "ttkv_decoder_ranks", "ttkv_blob_bytes",
+           "ttkv_decode_workspace_bytes", "ttkv_decode_paged", "ttkv_decode_paged_noalloc",
+           "ttkv_write_paged", "ttkv_prefill_workspace_bytes", "ttkv_prefill_paged", "ttkv_multi_scores_paged", "ttkv_multi_scores_workspace_bytes",
            "ttkv_dense_workspace_bytes",
            "ttkv_dense_decode_paged", "ttkv_write_workspace_bytes", "ttkv_container_krt",
            "ttkv_container_v_out")

@@ -19,6 +19,7 @@ import math
 
 import torch
 
+from .decoder_pool import DecoderPool, decoder_ranks, pack_decoders
 from .layout import TTKLayout
 
 
@@ -54,15 +55,24 @@ def _pinv_rows(D: torch.Tensor) -> torch.Tensor:
 
 class KDecoder:
     """A request's frozen decoder `[r1, H*d]` fp32 and its cached pseudo-inverse `[H*d, r1]`
-    (encode.py:198-208 uses `torch.linalg.pinv`; `_pinv_rows` computes the same matrix)."""
+    (encode.py:198-208 uses `torch.linalg.pinv`; `_pinv_rows` computes the same matrix), plus
+    its pool form (`packed`: the codec's int8 decoder as the kernels read it), given by the fit
+    or derived exactly from `decoder_f` on first use."""
 
-    __slots__ = ("decoder_f", "_pinv")
+    __slots__ = ("decoder_f", "_pinv", "_packed")
 
-    def __init__(self, decoder_f: torch.Tensor):
+    def __init__(self, decoder_f: torch.Tensor, packed: DecoderPool | None = None):
         if decoder_f.dim() != 2:
             raise ValueError(f"a decoder is [r1, H*d]; got {tuple(decoder_f.shape)}")
         self.decoder_f = decoder_f.to(torch.float32).contiguous()
         self._pinv = None
+        self._packed = packed
+
+    @property
+    def packed(self) -> DecoderPool:
+        if self._packed is None:
+            self._packed = pack_decoders(self.decoder_f)
+        return self._packed
 
     @property
     def pinv(self) -> torch.Tensor:
@@ -288,10 +298,17 @@ def fit_into_budget(K: torch.Tensor, lay: TTKLayout, cfg: dict) -> FittedK:
     rmax = dec.abs().amax(1, keepdim=True)
     sc = _ruler(torch.where(rmax == 0, torch.ones_like(rmax), rmax), qm)
     dec_q = torch.clamp(torch.round(dec / sc), -(qm + 1), qm)
-    dec_f = dec_q * sc.to(torch.float16).to(torch.float32)          # int8 * fp16 row ruler
+    s16 = sc.to(torch.float16).to(torch.float32)
+    dec_f = dec_q * s16                                              # int8 * fp16 row ruler
     coeff_q = torch.zeros(n, lay.r1, dtype=torch.int8, device=K.device)
     coeff_q[:, :r1] = cq
     padded = torch.zeros(lay.r1, H * d, dtype=torch.float32, device=K.device)
     padded[:r1] = dec_f
-    return FittedK(coeff_q=coeff_q, coeff_scale=cs.reshape(n), decoder=KDecoder(padded),
-                   fitted_rank=r1, budget=lay.r1)
+    # the pool form of the same decoder: column-major int8 ranks and their rulers
+    R = decoder_ranks(lay.r1)
+    pq = torch.zeros(H * d, R, dtype=torch.int8, device=K.device)
+    ps = torch.zeros(R, dtype=torch.float32, device=K.device)
+    pq[:, :r1] = dec_q.t().to(torch.int8)
+    ps[:r1] = s16.reshape(r1)
+    return FittedK(coeff_q=coeff_q, coeff_scale=cs.reshape(n),
+                   decoder=KDecoder(padded, DecoderPool(pq, ps)), fitted_rank=r1, budget=lay.r1)

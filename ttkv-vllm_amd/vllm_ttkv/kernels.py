@@ -9,10 +9,12 @@ from __future__ import annotations
 import torch
 
 from . import _hip
+from .decoder_pool import DecoderPool, decoder_ranks
 from .layout import TTKLayout
 
 
 def _need_device(*ts):
+    ts = [u for t in ts for u in (t if isinstance(t, DecoderPool) else (t,))]
     for t in ts:
         if t is not None and t.device.type != "cuda":
             raise RuntimeError("libttkv_hip kernels take device tensors; got a "
@@ -23,6 +25,26 @@ def _i32(t, name):
     if t.dtype != torch.int32 or not t.is_contiguous():
         raise ValueError(f"{name} must be a contiguous int32 tensor, got {t.dtype}")
     return t
+
+
+def pool_args(lay: TTKLayout, dec_pool: DecoderPool) -> tuple[int, int, int]:
+    """(dec_q pointer, dec_scale pointer, slots) of a decoder pool, after checking it has the
+    layout's shape: `q [slots, H*d, R]` int8 and `scale [slots, R]` fp32, both contiguous, R =
+    decoder_ranks(r1) (see `decoder_pool`)."""
+    if not isinstance(dec_pool, DecoderPool):
+        raise TypeError("dec_pool must be a DecoderPool (a store's `dec_pool`, or "
+                        "decoder_pool.pack_decoders of fp32 decoders)")
+    q, sc = dec_pool
+    R = decoder_ranks(lay.r1)
+    if (q.dtype != torch.int8 or q.dim() != 3 or tuple(q.shape[1:]) != (lay.H * lay.d, R)
+            or not q.is_contiguous()):
+        raise ValueError(f"dec_pool.q must be contiguous int8 [slots, {lay.H * lay.d}, {R}], got "
+                         f"{q.dtype} {tuple(q.shape)} (a decoder written at one rank cannot be "
+                         f"read at another)")
+    if sc.dtype != torch.float32 or tuple(sc.shape) != (q.shape[0], R) or not sc.is_contiguous():
+        raise ValueError(f"dec_pool.scale must be contiguous fp32 [{q.shape[0]}, {R}], got "
+                         f"{sc.dtype} {tuple(sc.shape)}")
+    return q.data_ptr(), sc.data_ptr(), int(q.shape[0])
 
 
 def page_bytes(page: torch.Tensor, blob: int) -> torch.Tensor:
@@ -52,7 +74,7 @@ def decode_workspace(lay: TTKLayout, num_heads: int, num_reqs: int, max_seq_len:
 def decode_paged(lay: TTKLayout, query: torch.Tensor, page: torch.Tensor, block_size: int,
                  block_table: torch.Tensor, seq_lens: torch.Tensor,
                  query_start_loc: torch.Tensor, max_seq_len: int,
-                 dec_slot_of_block: torch.Tensor, dec_pool: torch.Tensor,
+                 dec_slot_of_block: torch.Tensor, dec_pool: DecoderPool,
                  cos_sin_cache: torch.Tensor, scale: float, out: torch.Tensor | None = None,
                  workspace: torch.Tensor | None = None,
                  error_word: torch.Tensor | None = None) -> torch.Tensor:
@@ -60,8 +82,9 @@ def decode_paged(lay: TTKLayout, query: torch.Tensor, page: torch.Tensor, block_
 
     query [N, HQ, d]; page: the layer's cache (bytes reinterpreted); block_table [B, max_blocks]
     int32; seq_lens [B] int32; query_start_loc [>=B] int32 (row of request r's query);
-    dec_slot_of_block [num_blocks] int32; dec_pool [slots, r1, H*d] fp32; cos_sin_cache
-    [max_pos, d] fp32 (vLLM layout). Returns `out` [N, HQ, d] with the decode rows written."""
+    dec_slot_of_block [num_blocks] int32; dec_pool: the decoder pool (`DecoderPool`);
+    cos_sin_cache [max_pos, d] fp32 (vLLM layout). Returns `out` [N, HQ, d] with the decode rows
+    written."""
     _need_device(query, page, block_table, seq_lens, query_start_loc, dec_slot_of_block,
                  dec_pool, cos_sin_cache)
     L = _hip.lib()
@@ -77,12 +100,7 @@ def decode_paged(lay: TTKLayout, query: torch.Tensor, page: torch.Tensor, block_
     _i32(seq_lens, "seq_lens")
     _i32(query_start_loc, "query_start_loc")
     _i32(dec_slot_of_block, "dec_slot_of_block")
-    if dec_pool.dtype != torch.float32 or not dec_pool.is_contiguous():
-        raise ValueError("dec_pool must be contiguous fp32 [slots, r1, H*d]")
-    if dec_pool.dim() != 3 or dec_pool.shape[1] != lay.r1 or dec_pool.shape[2] != lay.H * lay.d:
-        raise ValueError(f"dec_pool is {tuple(dec_pool.shape)}; expected [slots, {lay.r1}, "
-                         f"{lay.H * lay.d}] (a decoder written at one rank cannot be read at "
-                         f"another)")
+    dq, ds, n_dec = pool_args(lay, dec_pool)
     if cos_sin_cache.dtype != torch.float32 or not cos_sin_cache.is_contiguous():
         raise ValueError("cos_sin_cache must be contiguous fp32 [max_pos, d]")
     if cos_sin_cache.shape[-1] != lay.d:
@@ -105,8 +123,8 @@ def decode_paged(lay: TTKLayout, query: torch.Tensor, page: torch.Tensor, block_
         flat.data_ptr(), flat.shape[0], flat.stride(0),
         int(block_size), block_table.data_ptr(), block_table.stride(0), block_table.shape[1],
         seq_lens.data_ptr(), query_start_loc.data_ptr(), num_reqs, int(max_seq_len),
-        dec_slot_of_block.data_ptr(), dec_slot_of_block.numel(), dec_pool.data_ptr(),
-        dec_pool.shape[0], cos_sin_cache.data_ptr(), cos_sin_cache.shape[0],
+        dec_slot_of_block.data_ptr(), dec_slot_of_block.numel(), dq, ds, n_dec,
+        cos_sin_cache.data_ptr(), cos_sin_cache.shape[0],
         out.data_ptr(), _hip.DTYPE_CODE[out.dtype], out.stride(0),
         workspace.data_ptr(), workspace.numel(), error_word.data_ptr(),
         _hip.stream_ptr(query.device))
@@ -117,7 +135,7 @@ def decode_paged(lay: TTKLayout, query: torch.Tensor, page: torch.Tensor, block_
 def write_paged(lay: TTKLayout, key: torch.Tensor, value: torch.Tensor,
                 slot_mapping: torch.Tensor, query_start_loc: torch.Tensor,
                 block_table: torch.Tensor, dec_slot_of_block: torch.Tensor,
-                dec_pool: torch.Tensor, pinv_pool: torch.Tensor | None, page: torch.Tensor,
+                dec_pool: DecoderPool, pinv_pool: torch.Tensor | None, page: torch.Tensor,
                 coeff_q_in: torch.Tensor | None = None,
                 coeff_scale_in: torch.Tensor | None = None,
                 coeff_out: torch.Tensor | None = None, resid_out: torch.Tensor | None = None,
@@ -145,8 +163,7 @@ def write_paged(lay: TTKLayout, key: torch.Tensor, value: torch.Tensor,
     _i32(query_start_loc, "query_start_loc")
     _i32(block_table, "block_table")
     _i32(dec_slot_of_block, "dec_slot_of_block")
-    if dec_pool.dtype != torch.float32 or tuple(dec_pool.shape[1:]) != (lay.r1, lay.H * lay.d):
-        raise ValueError("dec_pool must be fp32 [slots, r1, H*d]")
+    dq, ds, n_dec = pool_args(lay, dec_pool)
     if pinv_pool is not None and (pinv_pool.dtype != torch.float32 or
                                   tuple(pinv_pool.shape[1:]) != (lay.H * lay.d, lay.r1)):
         raise ValueError("pinv_pool must be fp32 [slots, H*d, r1]")
@@ -155,7 +172,7 @@ def write_paged(lay: TTKLayout, key: torch.Tensor, value: torch.Tensor,
         error_word = torch.zeros(1, dtype=torch.int32, device=key.device)
     if dec_used is not None:
         _i32(dec_used, "dec_used")
-        if dec_used.numel() < dec_pool.shape[0]:
+        if dec_used.numel() < n_dec:
             raise ValueError("dec_used needs one flag per decoder pool slot")
     cq = None
     if coeff_q_in is not None:
@@ -170,8 +187,9 @@ def write_paged(lay: TTKLayout, key: torch.Tensor, value: torch.Tensor,
         value.data_ptr(), _hip.DTYPE_CODE[value.dtype], value.stride(0),
         slot_mapping.data_ptr(), N, query_start_loc.data_ptr(), query_start_loc.numel() - 1,
         block_table.data_ptr(), block_table.stride(0), dec_slot_of_block.data_ptr(),
-        dec_slot_of_block.numel(), dec_pool.data_ptr(), _hip.ptr(pinv_pool), dec_pool.shape[0],
-        _hip.ptr(dec_used), _hip.ptr(cq), _hip.ptr(coeff_scale_in), flat.data_ptr(), flat.shape[0], flat.stride(0),
+        dec_slot_of_block.numel(), dq, ds, _hip.ptr(pinv_pool), n_dec,
+        _hip.ptr(dec_used), _hip.ptr(cq), _hip.ptr(coeff_scale_in), flat.data_ptr(),
+        flat.shape[0], flat.stride(0),
         _hip.ptr(coeff_out), _hip.ptr(resid_out), _hip.ptr(workspace),
         0 if workspace is None else workspace.numel(), error_word.data_ptr(),
         _hip.stream_ptr(key.device))
@@ -202,10 +220,7 @@ def _read_checks(lay: TTKLayout, query, page, block_table, seq_lens, query_start
     _i32(seq_lens, "seq_lens")
     _i32(query_start_loc, "query_start_loc")
     _i32(dec_slot_of_block, "dec_slot_of_block")
-    if (dec_pool.dtype != torch.float32 or not dec_pool.is_contiguous() or dec_pool.dim() != 3
-            or tuple(dec_pool.shape[1:]) != (lay.r1, lay.H * lay.d)):
-        raise ValueError(f"dec_pool must be contiguous fp32 [slots, {lay.r1}, {lay.H * lay.d}], "
-                         f"got {tuple(dec_pool.shape)} {dec_pool.dtype}")
+    pool_args(lay, dec_pool)
     if cos_sin_cache.dtype != torch.float32 or not cos_sin_cache.is_contiguous():
         raise ValueError("cos_sin_cache must be contiguous fp32 [max_pos, d]")
     if cos_sin_cache.shape[-1] != lay.d:
@@ -227,7 +242,7 @@ def prefill_workspace(lay: TTKLayout, num_heads: int, num_reqs: int, max_q_len: 
 def prefill_paged(lay: TTKLayout, query: torch.Tensor, page: torch.Tensor, block_size: int,
                   block_table: torch.Tensor, seq_lens: torch.Tensor,
                   query_start_loc: torch.Tensor, max_q_len: int, max_seq_len: int,
-                  dec_slot_of_block: torch.Tensor, dec_pool: torch.Tensor,
+                  dec_slot_of_block: torch.Tensor, dec_pool: DecoderPool,
                   cos_sin_cache: torch.Tensor, scale: float,
                   req_index: torch.Tensor | None = None, out: torch.Tensor | None = None,
                   workspace: torch.Tensor | None = None,
@@ -263,8 +278,8 @@ def prefill_paged(lay: TTKLayout, query: torch.Tensor, page: torch.Tensor, block
         int(block_size), block_table.data_ptr(), block_table.stride(0), block_table.shape[1],
         seq_lens.data_ptr(), query_start_loc.data_ptr(), _hip.ptr(req_index), num_reqs,
         int(max_q_len), int(max_seq_len),
-        dec_slot_of_block.data_ptr(), dec_slot_of_block.numel(), dec_pool.data_ptr(),
-        dec_pool.shape[0], cos_sin_cache.data_ptr(), cos_sin_cache.shape[0],
+        dec_slot_of_block.data_ptr(), dec_slot_of_block.numel(), *pool_args(lay, dec_pool),
+        cos_sin_cache.data_ptr(), cos_sin_cache.shape[0],
         out.data_ptr(), _hip.DTYPE_CODE[out.dtype], out.stride(0),
         workspace.data_ptr(), workspace.numel(), error_word.data_ptr(),
         _hip.stream_ptr(query.device))
@@ -275,7 +290,7 @@ def prefill_paged(lay: TTKLayout, query: torch.Tensor, page: torch.Tensor, block
 def multi_scores_paged(lay: TTKLayout, query: torch.Tensor, page: torch.Tensor,
                        block_size: int, block_table: torch.Tensor, seq_lens: torch.Tensor,
                        query_start_loc: torch.Tensor, max_q_len: int, max_seq_len: int,
-                       dec_slot_of_block: torch.Tensor, dec_pool: torch.Tensor,
+                       dec_slot_of_block: torch.Tensor, dec_pool: DecoderPool,
                        cos_sin_cache: torch.Tensor, scale: float,
                        scores: torch.Tensor | None = None,
                        error_word: torch.Tensor | None = None,
@@ -311,8 +326,8 @@ def multi_scores_paged(lay: TTKLayout, query: torch.Tensor, page: torch.Tensor,
         flat.data_ptr(), flat.shape[0], flat.stride(0),
         int(block_size), block_table.data_ptr(), block_table.stride(0), block_table.shape[1],
         seq_lens.data_ptr(), query_start_loc.data_ptr(), int(max_q_len), int(max_seq_len),
-        dec_slot_of_block.data_ptr(), dec_slot_of_block.numel(), dec_pool.data_ptr(),
-        dec_pool.shape[0], cos_sin_cache.data_ptr(), cos_sin_cache.shape[0],
+        dec_slot_of_block.data_ptr(), dec_slot_of_block.numel(), *pool_args(lay, dec_pool),
+        cos_sin_cache.data_ptr(), cos_sin_cache.shape[0],
         scores.data_ptr(), scores.stride(0), scores.stride(1), ws_ptr, ws_bytes,
         error_word.data_ptr(), _hip.stream_ptr(query.device))
     _hip.check(rc, "ttkv_multi_scores_paged")

@@ -8,8 +8,10 @@ Same surface as the reference's `vllm_ttkv/rope_store.py:70-300`: `load_calibrat
 layout)` and `ensure_store(layer_name, cos_sin_cache, num_heads, num_kv_heads, head_dim, layout)`.
 
 What is different underneath: a registered decoder is copied into its layer's DEVICE pool
-(`dec_pool [capacity, r1, H*d]`, `pinv_pool [capacity, H*d, r1]`, fp32) and the request key ->
-pool slot map is a device array (`dec_map [num_blocks]`, -1 = none), keyed by `block_table[r, 0]`
+(`dec_pool`: the codec's int8 decoder with its per-rank rulers, `q [capacity, H*d, R]` int8 +
+`scale [capacity, R]` fp32, see `decoder_pool`; `pinv_pool [capacity, H*d, r1]` fp32) and the
+request key -> pool slot map is a device array (`dec_map [num_blocks]`, -1 = none), keyed by
+`block_table[r, 0]`
 as in the reference (rope_store.py:148-163). The decode, continuation and write kernels resolve a
 request's decoder through that map themselves, so a step needs no host read of the block table.
 
@@ -32,6 +34,7 @@ from collections import OrderedDict
 
 import torch
 
+from .decoder_pool import empty_pool
 from .encode import KDecoder
 from .layout import CONFIGS, TTKLayout, layout_for_config
 
@@ -155,7 +158,7 @@ class TTKVRopeStore:
             raise ValueError(f"decoder pool capacity must be positive, got {cap}")
         H, d, r1 = layout.H, layout.d, layout.r1
         self.capacity = cap
-        self.dec_pool = torch.zeros(cap, r1, H * d, dtype=torch.float32, device=dev)
+        self.dec_pool = empty_pool(cap, r1, H, d, dev)
         self.pinv_pool = torch.zeros(cap, H * d, r1, dtype=torch.float32, device=dev)
         self.dec_map: torch.Tensor | None = None
         self.decoders: "OrderedDict[int, KDecoder]" = OrderedDict()  # key -> decoder, oldest first
@@ -189,7 +192,7 @@ class TTKVRopeStore:
                 raise IndexError(f"request key (first block) {key} outside the cache's "
                                  f"{num_blocks} blocks")
             m[key] = slot
-        self.dec_map = m.to(self.dec_pool.device)
+        self.dec_map = m.to(self.pinv_pool.device)
         return self.dec_map
 
     def observe_use(self) -> None:
@@ -236,7 +239,9 @@ class TTKVRopeStore:
                 self.release(order[0])
             slot = self._free.pop()
             self._slot_of[key] = slot
-        self.dec_pool[slot].copy_(dec.decoder_f)
+        packed = dec.packed
+        self.dec_pool.q[slot].copy_(packed.q)
+        self.dec_pool.scale[slot].copy_(packed.scale)
         self.pinv_pool[slot].copy_(dec.pinv)
         if self.dec_map is not None:
             self.dec_map[key] = slot
