@@ -50,9 +50,14 @@ __host__ __device__ inline int dec_ranks(int r1) {
   return r1 <= 64 ? 64 : r1 <= 128 ? 128 : (r1 + 31) & ~31;
 }
 
-// Decoder value of rank 4m + k (k = 0..3) from the dword of ranks 4m .. 4m+3 and its ruler.
-__device__ __forceinline__ float dec_value(uint32_t q4, int k, float ruler) {
-  return (float)(int8_t)(q4 >> (8 * k)) * ruler;
+// Decoder values of ranks 4m .. 4m+3 from their dword of int8 codes and their rulers: float(q) *
+// ruler, exactly, as u * ruler - 128 * ruler with u = q + 128 (a byte convert and an fma per
+// value: the fma's exact result is float(q) * ruler, which is representable, so nothing rounds).
+__device__ __forceinline__ void dec_values4(uint32_t q4, float4v ruler, float out[4]) {
+  const uint32_t u = q4 ^ 0x80808080u;
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    out[k] = fmaf((float)((u >> (8 * k)) & 0xffu), ruler[k], -128.0f * ruler[k]);
 }
 
 __host__ inline bool make_geom(const ttkv_layout* l, Geom* g) {

@@ -166,16 +166,18 @@ __global__ __launch_bounds__(kXThreads, 2) void expand_kernel(ExpandArgs a) {
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi) {
 #pragma unroll
-    for (int s = 0; s < KSTEPS; ++s)
+    for (int s = 0; s < KSTEPS; ++s) {
+      float v[8];
+      dec_values4(dq[mi][s][0], dsc[2 * s], v);
+      dec_values4(dq[mi][s][1], dsc[2 * s + 1], v + 4);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int ar = 32 * s + 8 * gq + j;
-        const float f =
-            ar < g.r1 ? dec_value(dq[mi][s][j >> 2], j & 3, dsc[2 * s + (j >> 2)][j & 3]) : 0.f;
+        const float f = 32 * s + 8 * gq + j < g.r1 ? v[j] : 0.f;
         const _Float16 hi = (_Float16)f;
         ahi[mi][s][j] = hi;
         alo[mi][s][j] = (_Float16)(f - (float)hi);
       }
+    }
   }
 
   const int k_row_off = g.k_field + h * g.k_row;

@@ -466,21 +466,23 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi) {
 #pragma unroll
-    for (int s = 0; s < KSTEPS; ++s)
+    for (int s = 0; s < KSTEPS; ++s) {
+      float v[8];
+      dec_values4(dq[mi][s][0], dsc[2 * s], v);
+      dec_values4(dq[mi][s][1], dsc[2 * s + 1], v + 4);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int ar = 32 * s + 8 * gq + j;
-        const uint32_t q4 = dq[mi][s][j >> 2];
-        const float f = ar < g.r1 ? dec_value(q4, j & 3, dsc[2 * s + (j >> 2)][j & 3]) : 0.f;
+        const float f = 32 * s + 8 * gq + j < g.r1 ? v[j] : 0.f;
         const _Float16 hi = (_Float16)f;
         ahi[mi][s][j] = hi;
         alo[mi][s][j] = (_Float16)(f - (float)hi);
       }
+    }
+    float vt[4];
+    dec_values4(dqt[mi], dsc[2 * KSTEPS], vt);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int ar = 32 * KSTEPS + 4 * gq + j;
-      const float f =
-          j < 4 && ar < g.r1 ? dec_value(dqt[mi], j & 3, dsc[2 * KSTEPS][j & 3]) : 0.f;
+      const float f = KTAIL && j < 4 && 32 * KSTEPS + 4 * gq + j < g.r1 ? vt[j & 3] : 0.f;
       const _Float16 hi = (_Float16)f;
       thi[mi][j] = hi;
       tlo[mi][j] = (_Float16)(f - (float)hi);

@@ -220,10 +220,12 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
       const u32x2v q8 = *gbl((const u32x2v*)(col + 32 * s + 8 * gq));
       const float4v s0 = *gbl((const float4v*)(decs + 32 * s + 8 * gq));
       const float4v s1 = *gbl((const float4v*)(decs + 32 * s + 8 * gq + 4));
+      float v[8];
+      dec_values4(q8[0], s0, v);
+      dec_values4(q8[1], s1, v + 4);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int ar = 32 * s + 8 * gq + j;
-        const float f = ar < g.r1 ? dec_value(q8[j >> 2], j & 3, j < 4 ? s0[j] : s1[j - 4]) : 0.f;
+        const float f = 32 * s + 8 * gq + j < g.r1 ? v[j] : 0.f;
         const _Float16 hi = (_Float16)f;
         ahi[mi][s][j] = hi;
         if constexpr (EXACT) alo[mi][s][j] = (_Float16)(f - (float)hi);

@@ -261,8 +261,9 @@ __global__ __launch_bounds__(kWThreads) void write_project_kernel(WriteArgs a) {
 // K3b: residual of head h, then its K row and V row; head 0 also writes the coefficients.
 template <int RB, int VB>
 __global__ __launch_bounds__(kWThreads) void write_pack_kernel(WriteArgs a) {
-  __shared__ float cqs[256];
-  __shared__ float rp[4][kD];
+  __shared__ __align__(16) float cqs[256];  // c * cs by rank (0 past r1)
+  __shared__ __align__(16) float rul[256];  // decoder rank rulers (0 past r1)
+  __shared__ float rp[kD];    // sum_a cqs[a] * dec[a][h*d + j]
   __shared__ uint8_t codes[2][kD];
   const Geom& g = a.g;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -300,26 +301,26 @@ __global__ __launch_bounds__(kWThreads) void write_pack_kernel(WriteArgs a) {
     if (ds >= 0 && a.dec_used) a.dec_used[ds] = 1;
   }
   if (ds < 0 || !slot_ok) return;
-  // this head's decoder columns h*d + 2l and h*d + 2l + 1 (lane l): wave w sums ranks
-  // 32w .. 32w + 31 of each 128-rank block, 32 int8 per column (two 16-byte loads) times their 32
-  // rulers (the same for every lane of the wave). The first block is requested before the
-  // coefficients are needed.
+  // this head's decoder: wave w owns dims 32w .. 32w + 31; lane l reads column h*d + 32w + l/2,
+  // ranks 64 (l & 1) .. + 63 of each 128-rank block (a lane pair reads one whole 128-byte column
+  // line), requested before the coefficients are needed. The rank rulers are staged in LDS beside
+  // the coefficients (thread t: rank t; r1 <= 256 threads, host-checked).
   const int R = dec_ranks(g.r1);
-  const int8_t* dcol = a.dec_q + ((int64_t)ds * HD + h * kD + 2 * lane) * R;
-  const float* drul = a.dec_scale + (int64_t)ds * R;
+  const int cdim = 32 * wv + (lane >> 1);
+  const int half = lane & 1;
+  const int8_t* dcol = a.dec_q + ((int64_t)ds * HD + h * kD + cdim) * R + 64 * half;
   u32x4 dqv[4];
-  float4v dsv[8];
   auto load_ranks = [&](int b0) {
+    if (b0 + 64 * half < R) {  // R = 64 (or 192): the second half has no ranks in the last block
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      dqv[2 * c] = *gbl((const u32x4*)(dcol + c * R + b0));
-      dqv[2 * c + 1] = *gbl((const u32x4*)(dcol + c * R + b0 + 16));
+      for (int c = 0; c < 4; ++c) dqv[c] = *gbl((const u32x4*)(dcol + b0 + 16 * c));
     }
-#pragma unroll
-    for (int k = 0; k < 8; ++k) dsv[k] = *gbl((const float4v*)(drul + b0 + 4 * k));
   };
-  if (32 * wv < R) load_ranks(32 * wv);
-  if (tid < g.r1) cqs[tid] = qv * cs;  // r1 <= 256 threads (host-checked)
+  load_ranks(0);
+  if (tid < R) {
+    rul[tid] = tid < g.r1 ? a.dec_scale[(int64_t)ds * R + tid] : 0.f;
+    cqs[tid] = qv * cs;  // qv = 0 past r1
+  }
   uint8_t* base = a.page + slot * a.slot_stride;
   if (h == 0) {
     if (tid < g.r1) base[tid] = (uint8_t)(int8_t)(int)qv;
@@ -332,28 +333,32 @@ __global__ __launch_bounds__(kWThreads) void write_pack_kernel(WriteArgs a) {
     for (int b = g.k_slot + g.H * g.v_row + tid; b < g.blob; b += kWThreads) base[b] = 0;
   }
   __syncthreads();
-  // R[j] = K[h*d+j] - sum_a cqs[a] * dec[a][h*d+j]: wave w sums its ranks in increasing order,
-  // lane l owns dims 2l and 2l + 1
-  float acc0 = 0.f, acc1 = 0.f;
-  for (int b0 = 32 * wv; b0 < R; b0 += 128) {
-    if (b0 != 32 * wv) load_ranks(b0);
+  // R[j] = K[h*d+j] - sum_a cqs[a] * dec[a][h*d+j], dec = float(q) * ruler exactly: each lane sums
+  // its ranks in increasing order, then the two halves of the column are added
+  float acc = 0.f;
+  for (int b0 = 0; b0 < R; b0 += 128) {
+    if (b0) load_ranks(b0);
+    const int r0 = b0 + 64 * half;
+    if (r0 < R) {
 #pragma unroll
-    for (int k = 0; k < 32; ++k) {
-      const int ar = b0 + k;
-      const float rul = dsv[k >> 2][k & 3];
-      const float c = ar < g.r1 ? cqs[ar] : 0.f;
-      const float d0 = ar < g.r1 ? dec_value(dqv[k >> 4][(k >> 2) & 3], k & 3, rul) : 0.f;
-      const float d1 = ar < g.r1 ? dec_value(dqv[2 + (k >> 4)][(k >> 2) & 3], k & 3, rul) : 0.f;
-      acc0 = fmaf(c, d0, acc0);
-      acc1 = fmaf(c, d1, acc1);
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const int r = r0 + 16 * c + 4 * m;
+          const float4v c4 = *(const float4v*)&cqs[r];
+          float d[4];
+          dec_values4(dqv[c][m], *(const float4v*)&rul[r], d);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) acc = fmaf(c4[k], d[k], acc);
+        }
     }
   }
-  rp[wv][2 * lane] = acc0;
-  rp[wv][2 * lane + 1] = acc1;
+  acc += __shfl_xor(acc, 1);
+  if (half == 0) rp[cdim] = acc;
   __syncthreads();
   if (wv == 0) {
-    float r0 = xr0 - (((rp[0][lane] + rp[1][lane]) + rp[2][lane]) + rp[3][lane]);
-    float r1v = xr1 - (((rp[0][64 + lane] + rp[1][64 + lane]) + rp[2][64 + lane]) + rp[3][64 + lane]);
+    const float r0 = xr0 - rp[lane];
+    const float r1v = xr1 - rp[64 + lane];
     if (a.r_out) {
       a.r_out[(int64_t)i * HD + h * kD + lane] = r0;
       a.r_out[(int64_t)i * HD + h * kD + 64 + lane] = r1v;
