@@ -56,9 +56,9 @@ typedef struct ttkv_layout {
 int64_t ttkv_blob_bytes(const ttkv_layout* lay);
 
 /* Ranks R each decoder column holds in the decoder pool (dec_q [n_dec_slots, H*d, R]): 64 for
- * r1 <= 64, 128 for r1 <= 128, else r1 rounded up to a multiple of 32; -1 for r1 <= 0. Replaces
+ * r1 <= 64, 128 for r1 <= 128, else r1 rounded up to a multiple of 64; -1 for r1 <= 0. Replaces
  * the reference's [r1, H*d] decoder shape (codec/ttkv_packed_cache.py:284-293), padded so that
- * every kernel reads whole 8- and 16-byte groups of ranks. */
+ * every kernel reads whole 8-, 16- and 64-byte groups of ranks. */
 int32_t ttkv_decoder_ranks(int32_t r1);
 
 /* Workspaces (all four `*_workspace_bytes`): the first 64 KiB of a workspace are arrival

@@ -90,13 +90,13 @@ def test_non_codec_decoders_are_refused(bad):
 def test_decoder_ranks_matches_the_c_abi():
     """`decoder_ranks` is the C ABI's `ttkv_decoder_ranks` (the library loads without a GPU),
     and every kernel's rank window fits inside it: K1's 16-rank units (r1 padded to 64, 112, 128
-    or 160) and K2/K3's 32-rank steps."""
+    or 160), K2's 32-rank steps and K3's whole 64-rank chunks."""
     from vllm_ttkv import _hip
     L = _hip.lib()
     for r1 in range(1, 300):
         R = decoder_ranks(r1)
         assert L.ttkv_decoder_ranks(r1) == R
-        assert R >= r1 and R % 32 == 0
+        assert R >= r1 and R % 64 == 0
         ku = 4 if r1 <= 64 else 7 if r1 <= 112 else 8 if r1 <= 128 else 10 if r1 <= 160 else 0
         if ku:
             assert 16 * ku <= R

@@ -53,7 +53,28 @@ def _run(lay, dec, pinv, Knew, V, slots, n_slots, v_dtype=torch.float32, cq_in=N
 @pytest.mark.parametrize("cfg", ["safe", "tight", "campaign4x"])
 def test_write_bytes_exact_from_quantiser_inputs(cfg):
     lay, dec, pinv, Knew, V = _setup(cfg, 9, seed=21)
+    _check_write(lay, dec, pinv, Knew, V, cfg)
+
+
+@pytest.mark.parametrize("r1", [150, 200])
+def test_write_large_rank_budgets(r1):
+    """Rank budgets past 128 (the decoder pool pads them to 192 / 256 ranks, read as whole
+    64-rank chunks per lane in the residual): a codec-form decoder with every rank active
+    (int8 rows times fp16 rank rulers, as the codec stores them) and its pseudo-inverse."""
+    lay = layout_for_config(codec.CONFIGS["safe"], r1=r1)
+    g = torch.Generator().manual_seed(r1)
+    q = torch.randint(-127, 128, (r1, H * D), generator=g).float()
+    ruler = (torch.rand(r1, generator=g) * 0.02 + 0.005).half().float()
+    dec = q * ruler[:, None]
+    pinv = encode.pinv(dec)
+    Knew = synth.keys(9, seed=r1 + 1)
+    V = synth.values(9, seed=r1 + 2) * 0.3
+    _check_write(lay, dec, pinv, Knew, V, f"r1={r1}")
+
+
+def _check_write(lay, dec, pinv, Knew, V, label):
     slots = torch.tensor([5, 0, 17, 3, 30, 8, 11, 2, 25], dtype=torch.int64)
+    print(f"[k3] {label}", flush=True)
     page, c, R, err = _run(lay, dec, pinv, Knew, V, slots, 32)
     assert err == 0
     # float stages at fp32 tolerance
@@ -70,7 +91,7 @@ def test_write_bytes_exact_from_quantiser_inputs(cfg):
     want = torch.cat([k_slots, v_slots], dim=1)
     got = page[slots]
     nbad = int((got != want).sum())
-    assert nbad == 0, f"{cfg}: {nbad} of {want.numel()} bytes differ"
+    assert nbad == 0, f"{label}: {nbad} of {want.numel()} bytes differ"
     untouched = torch.ones(32, dtype=torch.bool)
     untouched[slots] = False
     assert int(page[untouched].abs().sum()) == 0, "bytes outside the written slots changed"

@@ -42,12 +42,12 @@ __host__ inline int align_up16(int n) { return (n + 15) / 16 * 16; }
 // Decoder pool (the codec's int8 decoder, ttkv_packed_cache.py:284-293, laid out for the kernels):
 //   dec_q     [slots, H*d, R] int8: column j = h*d + dim holds its R rank values contiguously
 //   dec_scale [slots, R] fp32: the rank's ruler
-// R = 64 for r1 <= 64, 128 for r1 <= 128, else r1 rounded up to 32: every kernel's rank window
-// (16-rank units in K1, 32-rank steps in K2 and K3) lies inside it. Ranks >= r1 hold 0 with ruler
-// 0. A decoder value is float(dec_q) * dec_scale, exact in fp32 (8 bits times the codec's 11-bit
-// fp16 ruler).
+// R = 64 for r1 <= 64, 128 for r1 <= 128, else r1 rounded up to 64: every kernel's rank window
+// lies inside it (K1: 16-rank units up to 16 KU; K2: 32-rank steps; K3: whole 64-rank chunks of a
+// column per lane). Ranks >= r1 hold 0 with ruler 0. A decoder value is float(dec_q) *
+// dec_scale, exact in fp32 (8 bits times the codec's 11-bit fp16 ruler).
 __host__ __device__ inline int dec_ranks(int r1) {
-  return r1 <= 64 ? 64 : r1 <= 128 ? 128 : (r1 + 31) & ~31;
+  return r1 <= 64 ? 64 : r1 <= 128 ? 128 : (r1 + 63) & ~63;
 }
 
 // Decoder values of ranks 4m .. 4m+3 from their dword of int8 codes and their rulers: float(q) *

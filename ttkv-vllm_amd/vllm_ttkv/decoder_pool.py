@@ -22,12 +22,12 @@ import torch
 
 def decoder_ranks(r1: int) -> int:
     """Ranks R a pool column holds: 64 for r1 <= 64, 128 for r1 <= 128, else r1 rounded up to
-    32 (the kernels read whole 8- and 16-byte groups of a column's ranks; `ttkv_decoder_ranks`
-    in the C ABI returns the same)."""
+    64 (the kernels read a column's ranks in whole 8-, 16- and 64-byte groups;
+    `ttkv_decoder_ranks` in the C ABI returns the same)."""
     r1 = int(r1)
     if r1 <= 0:
         raise ValueError(f"r1 must be positive, got {r1}")
-    return 64 if r1 <= 64 else 128 if r1 <= 128 else (r1 + 31) // 32 * 32
+    return 64 if r1 <= 64 else 128 if r1 <= 128 else (r1 + 63) // 64 * 64
 
 
 class DecoderPool(NamedTuple):
