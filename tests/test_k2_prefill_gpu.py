@@ -125,6 +125,39 @@ def test_attend_mode_ragged_batch_with_splits():
         _check(out[s:e].float(), want[r], f"attend req {r} {shapes[r]}", exact_inf=False)
 
 
+@pytest.mark.parametrize("r1", [64, 160])
+def test_attend_mode_rank_budgets(r1):
+    """Rank budgets of 2 and 5 reconstruction k-steps: r1 = 64 through the two-launch path
+    (expand + attend) and r1 = 160 through the fused kernel (r1 > 128), each with a chunk of
+    several queries and a single query, against the oracle. The output is fp32 here: an fp16
+    output row of magnitude 4 or more is rounded by up to 2^-9 by its format alone, which would
+    leave no room for the kernel's own error under the 2e-3 bound."""
+    shapes = [(700, 70), (1200, 1)]
+    stores = [fitted_store("safe", n, seed=60 + i, r1=r1) for i, (n, _) in enumerate(shapes)]
+    cache = llama3_cache(2048)
+    pg, dec_pool, dec_map = _dev_inputs(stores, seed=4)
+    q = torch.cat([synth.queries(Q, seed=200 + i).reshape(Q, HQ, 128)
+                   for i, (_, Q) in enumerate(shapes)])
+    qsl = torch.tensor([0] + list(torch.tensor([Q for _, Q in shapes]).cumsum(0)),
+                       dtype=torch.int32)
+    out = torch.zeros(q.shape, dtype=torch.float32, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    print(f"[k2] r1={r1}", flush=True)
+    lay = stores[0]["lay"]
+    kernels.prefill_paged(lay, q.cuda(), pg["page"].cuda(), 16, pg["block_table"].cuda(),
+                          pg["seq_lens"].cuda(), qsl.cuda(), max(Q for _, Q in shapes),
+                          max(n for n, _ in shapes), dec_map, dec_pool, cache.cuda(), SCALE,
+                          out=out, error_word=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    want = attend.paged_continuation(lay, pg["page"], pg["block_table"], pg["seq_lens"], qsl,
+                                     q.double(), [s["decoder"] for s in stores], cache, 16, SCALE,
+                                     dtype=torch.float64)
+    for r in range(len(shapes)):
+        s, e = int(qsl[r]), int(qsl[r + 1])
+        _check(out[s:e].float(), want[r], f"r1={r1} req {r} {shapes[r]}", exact_inf=False)
+
+
 def test_attend_mode_queries_in_rows_that_are_not_16_byte_aligned():
     """Query rows at a stride of HQ*d + 2 elements (a view into a wider buffer): the kernel loads
     them element by element instead of in wide loads, with the same result."""
