@@ -116,7 +116,7 @@ class FittedK:
 _OVERSAMPLE = 128     # extra subspace columns beyond the rank budget
 _ITERS = 24           # multiplications by G: the error decays like (s_{r+p+1} / s_r)^(2 * iters)
 _RANGE_SEED = 0x7E5   # fixed start-block seed: the fit is deterministic
-_QR_SPREAD = 1e6      # largest diagonal spread of R accepted for a block of several multiplications
+_QR_SPREAD = 1e8      # largest diagonal spread of R accepted for a block of several multiplications
 _MAX_STEP = 8         # multiplications between two Cholesky QRs at most
 
 
@@ -172,8 +172,9 @@ def _leading_eigh(G: torch.Tensor, count: int):
     diagonal gives the growth per multiplication g, and the next block takes
     log(_QR_SPREAD) / log(g) multiplications (at most _MAX_STEP). A block whose factor comes out
     more spread than _QR_SPREAD (or whose factorisation fails) is redone one multiplication at a
-    time. On the spectra of key blocks (g ~ 50-60) that is 3 multiplications per QR: 11 QRs
-    instead of 26 for the same 24 multiplications and the same span to rounding. The final basis
+    time. On the spectra of key blocks (g ~ 50-60) that is 4 multiplications per QR: 9 QRs
+    instead of 26 for the same 24 multiplications and the same span to rounding (a spread of at
+    most 10^8 leaves the block's smallest direction ~10^-8 of float64's precision lost). The final basis
     gets a second QR (CholeskyQR2: orthonormal to working precision). If a single-step
     factorisation meets a numerically rank-deficient block, the iteration is redone with
     Householder QR."""
