@@ -121,14 +121,17 @@ _MAX_STEP = 8         # multiplications between two Cholesky QRs at most
 
 
 def _chol_qr_spread(Y: torch.Tensor):
-    """Cholesky QR of Y with its status read back: (Y R^-1, spread of |diag R|, ok). One host
-    sync, for the 6 numbers; the factorisation itself stays on the device."""
-    R, info = torch.linalg.cholesky_ex(Y.T @ Y, upper=True)
+    """Cholesky QR of Y with its status: (Y R^-1, spread of |diag R|, ok). The small Gram matrix
+    Y^T Y (<= 238 x 238, float64) goes to the host, whose LAPACK factors it and inverts R; Y R^-1
+    is then one GEMM on Y's device. At 1024 x 238 that takes 0.45 ms per QR where the device's
+    potrf + triangular solve take 0.67 ms, with the same one host round trip (the status read)."""
+    W = (Y.T @ Y).cpu()
+    R, info = torch.linalg.cholesky_ex(W, upper=True)
     d = R.diagonal().abs()
-    dmax, dmin, bad = torch.stack([d.max(), d.min(), info.to(d.dtype)]).cpu().tolist()
-    ok = bad == 0 and dmin > 0.0
-    Q = torch.linalg.solve_triangular(R, Y, upper=True, left=False) if ok else None
-    return Q, (dmax / dmin if ok else float("inf")), ok
+    if int(info) != 0 or not float(d.min()) > 0.0:
+        return None, float("inf"), False
+    Ri = torch.linalg.solve_triangular(R, torch.eye(R.shape[0], dtype=R.dtype), upper=True)
+    return Y @ Ri.to(Y.device), float(d.max() / d.min()), True
 def _energy_rank(e: torch.Tensor, total: float, tol: float) -> int | None:
     """The reference's rank rule on a descending energy spectrum e (squared singular values):
     r = 1 + the first index i at which the energy of components i, i+1, ... is <= tol^2 of the
