@@ -185,6 +185,27 @@ def test_decoder_registry_round_trip():
     rope_store.clear_stores()
 
 
+def test_registry_refuses_a_decoder_the_pool_cannot_hold():
+    """The pool stores the codec's int8 decoder (int8 rows times one ruler per rank, as every
+    fit produces): a decoder of another form is refused with an error, and the pool and map are
+    left as they were."""
+    lay = layout_for_config(CONFIGS["safe"], 16)
+    from vllm_ttkv.encode import KDecoder
+    rope_store.clear_stores()
+    st = rope_store.TTKVRopeStore(24, 8, 128, torch.zeros(8, 128), "L0", lay, num_blocks=10,
+                                  capacity=2)
+    ok = st.register(1, KDecoder(_codec_dec(seed=4)))
+    before = (st.dec_pool.q.clone(), st.dec_pool.scale.clone(), st.dec_map.clone())
+    with pytest.raises(ValueError, match="int8"):
+        st.register(2, KDecoder(torch.randn(16, 8 * 128)))
+    assert torch.equal(st.dec_pool.q, before[0]) and torch.equal(st.dec_pool.scale, before[1])
+    assert torch.equal(st.dec_map, before[2]) and int(st.dec_map[1]) == ok
+    assert 2 not in st.decoders and st.register(3, KDecoder(_codec_dec(seed=5))) != ok
+    with pytest.raises(RuntimeError, match="live requests"):       # both slots now in use
+        st.register(4, KDecoder(_codec_dec(seed=6)), live=[1, 3, 4])
+    rope_store.clear_stores()
+
+
 def test_decoder_eviction_follows_last_use():
     """A full pool evicts the least recently USED key that is not live. Use comes from the write
     kernel's flags (`dec_used`, one per slot, set here by hand as the kernel would): a running

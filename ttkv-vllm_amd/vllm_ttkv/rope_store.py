@@ -227,6 +227,9 @@ class TTKVRopeStore:
         if self.dec_map is not None and not 0 <= key < self.dec_map.numel():
             raise IndexError(f"request key (first block) {key} outside the cache's "
                              f"{self.dec_map.numel()} blocks")
+        # the pool form and the pseudo-inverse first: a decoder the pool cannot hold is refused
+        # before any slot is taken or evicted
+        packed, pinv = dec.packed, dec.pinv
         self.observe_use()
         slot = self._slot_of.get(key)
         if slot is None:
@@ -239,10 +242,9 @@ class TTKVRopeStore:
                 self.release(order[0])
             slot = self._free.pop()
             self._slot_of[key] = slot
-        packed = dec.packed
         self.dec_pool.q[slot].copy_(packed.q)
         self.dec_pool.scale[slot].copy_(packed.scale)
-        self.pinv_pool[slot].copy_(dec.pinv)
+        self.pinv_pool[slot].copy_(pinv)
         if self.dec_map is not None:
             self.dec_map[key] = slot
         self.decoders.pop(key, None)
