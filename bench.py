@@ -100,7 +100,9 @@ def build_store(torch, lay, cfg, lens, n_layers, seed, dev, fit_on=FIT_ON, disti
         qsl = torch.tensor([0] + list(torch.tensor(fl).cumsum(0)), dtype=torch.int32, device=dev)
         kernels.write_paged(lay, torch.cat(first_k).contiguous(), torch.cat(first_v).contiguous(),
                             torch.cat(first_slot), qsl, bt_d, dec_map_d, dec_pool, pinv_pool,
-                            page, coeff_q_in=torch.cat(first_cq), coeff_scale_in=torch.cat(first_cs),
+                            page,
+                            coeff_q_in=torch.cat(first_cq) if lay.qbits == 8 else None,
+                            coeff_scale_in=torch.cat(first_cs) if lay.qbits == 8 else None,
                             error_word=err)
         rl = [x[0].shape[0] for x in rest]
         if sum(rl):
@@ -119,6 +121,32 @@ def build_store(torch, lay, cfg, lens, n_layers, seed, dev, fit_on=FIT_ON, disti
     return dict(layers=layers, bt=bt_d, dec_map=dec_map_d, nblk=nblk, B=B,
                 seq_lens=torch.tensor(lens, dtype=torch.int32, device=dev), max_len=max(lens),
                 t_fit=t_fit, t_write=t_write)
+
+
+def bench_coef_modes(torch, cache, dev, steps=10, warmup=3, n_layers=L_LAYERS):
+    """K1 at the headline shape (8 x 14,402, 28 layers back to back) over stores in this
+    library's own coefficient modes (`EXTENSION_CONFIGS`: fp16 coefficients on the safe
+    geometry, 4-bit group-32 coefficients on campaign4x's), each fitted and written on the device
+    like the headline store."""
+    from vllm_ttkv import synth
+    from vllm_ttkv.layout import EXTENSION_CONFIGS, layout_for_config
+    lens = [14402] * 8
+    q = synth.queries(8, seed=5, device=dev)
+    res = {}
+    for name, mcfg in EXTENSION_CONFIGS.items():
+        mlay = layout_for_config(mcfg, R1)
+        st = build_store(torch, mlay, mcfg, lens, n_layers, seed=9, dev=dev)
+        _, ml = time_k1(torch, mlay, st, q, cache, steps, warmup, n_layers, per_launch=False)
+        b = k1_bytes(mlay, lens, R1, max(lens))
+        res[name] = dict(slot_bytes=mlay.compressed_bytes_per_token(), qbits=mlay.qbits,
+                         us_per_layer=ml * 1e3, algorithmic_bytes=b,
+                         hbm_gbps=b / (ml * 1e-3) / 1e9,
+                         roofline_frac=b / (ml * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+                         ns_per_cached_token=ml * 1e6 / sum(lens))
+        log(f"K1 B=8x14402 {name} ({mlay.compressed_bytes_per_token()} B/token): "
+            f"{ml * 1e3:.1f} us/launch back to back")
+        del st
+    return res
 
 
 def config3_lens(seed=3, B=8):
@@ -676,6 +704,8 @@ def main():
                     help="only the continuation workload (BASELINE config 4, K2); prints its line")
     ap.add_argument("--container-only", action="store_true",
                     help="only the container-layout reads (krt + v_out at 8 x 14402); prints its line")
+    ap.add_argument("--coef-modes-only", action="store_true",
+                    help="only K1 over the fp16 / 4-bit coefficient-mode stores")
     ap.add_argument("--first-chunk-only", action="store_true",
                     help="only the first-chunk timings (attention, fit, write at 2048 / 8192)")
     ap.add_argument("--dense-only", action="store_true",
@@ -742,6 +772,13 @@ def main():
                               value=dh["us_per_layer"], unit="us", n_gpus=1,
                               higher_is_better=False, dtype="fp16 in/out, fp32 accumulate",
                               data="synthetic", headline=dh, config3=d3)))
+        return
+
+    if args.coef_modes_only:
+        cm = bench_coef_modes(torch, cache, dev, args.steps, args.warmup)
+        print(json.dumps(dict(metric="K1 us/layer at 8 x 14402, fp16 and 4-bit coefficient modes",
+                              value=cm["safe_fp16"]["us_per_layer"], unit="us", n_gpus=1,
+                              higher_is_better=False, data="synthetic", modes=cm)))
         return
 
     if args.config5_only:
@@ -822,6 +859,7 @@ def main():
         extra["config5_4bit_read_write"] = bench_config5(torch, cache, dev, cpu=not args.no_cpu)
         extra["container_reads_b8_ctx14402"] = bench_container(torch, dev)
         extra["first_chunk"] = bench_first_chunk(torch, lay, cfg, dev)
+        extra["coefficient_modes_b8_ctx14402"] = bench_coef_modes(torch, cache, dev)
 
     cpu = None
     if not args.no_cpu:

@@ -46,7 +46,12 @@ enum {
 
 /* One layer's allocation. Mirrors TTKLayout(H, d, r1, qbits, res_k, res_bits, v_lanes, v_bits)
  * (vllm_ttkv/layout.py:56-74); all byte offsets are derived from these by layout.py:98-157's
- * formulas. The kernels are built for d == 128, qbits == 8, res_bits/v_bits in {3, 4}. */
+ * formulas. The kernels are built for d == 128 and res_bits/v_bits in {3, 4}.
+ * qbits selects the coefficient field: 8 is the reference's (r1 int8 values + one fp16 ruler);
+ * 16 (r1 fp16 values, no ruler) and 4 (4-bit values in [-7, 7] as 4 * ceil(r1/8) bytes of
+ * word-interleaved nibbles, then one fp16 scale per 32 ranks) are this library's own modes, with
+ * no counterpart in the reference, built for num_heads / H == 3 and 64 < r1 <= 128 (other
+ * shapes: TTKV_E_UNSUPPORTED). The residual rows follow the coefficient field in every mode. */
 typedef struct ttkv_layout {
   int32_t H, d, r1, qbits, res_k, res_bits, v_lanes, v_bits;
 } ttkv_layout;
@@ -144,6 +149,10 @@ int ttkv_decode_paged_noalloc(const ttkv_layout* lay, int32_t num_heads, float s
  * written at slot_mapping[i] as the reference slot bytes (layout.py:161-239), padding zeroed.
  * When coeff_q_in/coeff_scale_in ([N, r1] int8, [N] fp32) are given, they replace the projection
  * (a first chunk written with its fit's own coefficients, encode.py:257-298).
+ * In the qbits 16 / 4 modes (see ttkv_layout) c is stored as fp16(c) (round to nearest even), or
+ * as q * scale per group of 32 ranks (scale = max|c| / 7 rounded up to 8 significant bits, within
+ * [2^-14, 9344]; q = clamp(rint(c / scale), -7, 7)), and R = key[i] - value(c) @ decoder_f;
+ * coeff_q_in must then be null (TTKV_E_INVALID).
  * Bytes are bit-exact functions of R and value (select_triton.py:24-91): exact top-k by magnitude
  * (ties -> lowest lane), ruler = rowmax * fp32(1/(2^(b-1)-1)), q = rint(x / ruler) (IEEE div).
  * coeff_out [N, r1] and resid_out [N, H*d] (optional, fp32) receive c and R.

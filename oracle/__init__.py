@@ -15,6 +15,9 @@ Modules
   attend   -- dense reconstruction, per-row RoPE, scores, softmax,
               V readout, paged batch decode, continuation scores     (reference.py, decode.py, impl.py)
   rope     -- llama3 frequency table and vLLM's cos_sin_cache layout  (decode.py; public Llama 3 config)
+  coef_modes -- fp16 and 4-bit (group-32) coefficient fields: this build's own storage modes,
+              not the reference's (parity unpinned against it; pinned by closed forms, brute
+              force and round trips in tests/test_coef_modes.py)
 
 Pinning (what each part is checked against; see `tests/test_oracle_*.py`):
   * layout geometry: closed-form table of byte offsets (safe/tight/campaign4x) and the

@@ -20,7 +20,10 @@ def dense_k_from_slots(lay: Layout, k_slots, decoder_f, dtype=torch.float32):
     """reference.py:63-76 -> RAW K [H, n, d]."""
     n, H, d = k_slots.shape[0], lay.H, lay.d
     cq, cs, (bm, pk, sc) = unpack_k_slots(lay, k_slots)
-    kflat = (cq.to(dtype) * cs.to(dtype).unsqueeze(1)) @ decoder_f.to(dtype)
+    if lay.qbits == 8:
+        kflat = (cq.to(dtype) * cs.to(dtype).unsqueeze(1)) @ decoder_f.to(dtype)
+    else:  # this build's fp16 / 4-bit coefficient modes: cq holds the stored values themselves
+        kflat = cq.to(dtype) @ decoder_f.to(dtype)
     R = codec.packed_rows_materialise(bm, pk, sc, d, lay.res_k, lay.res_bits).to(dtype)
     return (kflat.reshape(n, H, d).permute(1, 0, 2) + R.reshape(H, n, d)).contiguous()
 

@@ -77,6 +77,24 @@ def encode_frozen(K: torch.Tensor, decoder_f: torch.Tensor, lay: Layout, pinv_m=
     return dict(coeff_q=cq, coeff_scale=cs.to(torch.float16).reshape(-1), c=c, R=R, resid=resid)
 
 
+def encode_frozen_mode(K: torch.Tensor, decoder_f: torch.Tensor, lay: Layout, pinv_m=None,
+                       c=None):
+    """The frozen write in this build's fp16 / 4-bit coefficient modes (`coef_modes`): c as
+    `encode_frozen` projects it (or as given), quantised by the mode, and the residual against the
+    stored values. -> dict(coeff_q, coeff_scale, values, c, R, resid) for `k_slots_from`."""
+    from . import coef_modes
+    if decoder_f.shape[0] != lay.r1:
+        raise ValueError("decoder rank != layout r1")
+    if c is None:
+        c = project(K, pinv(decoder_f) if pinv_m is None else pinv_m)
+    vals, q, s = coef_modes.quantise(c, lay.qbits)
+    H, n, d = K.shape
+    kd = (vals @ decoder_f.to(torch.float32)).reshape(n, H, d).permute(1, 0, 2)
+    R = (K.to(torch.float32) - kd).reshape(H * n, d)
+    resid = codec.build_rows(R, lay.res_k, lay.res_bits, "gpu")
+    return dict(coeff_q=q, coeff_scale=s, values=vals, c=c, R=R, resid=resid)
+
+
 def encode_v(V: torch.Tensor, lay: Layout, ruler_mode: str = "gpu"):
     """encode.py:431-443 -> (bitmap, packed, scale) over H*n rows; V in [H,n,d]."""
     return codec.build_v_layer(V.to(torch.float32), lay.v_lanes, lay.v_bits, ruler_mode)

@@ -50,9 +50,17 @@ class Layout:
 
     @property
     def coeff_bytes(self) -> int:
-        if (self.r1 * self.qbits) % 8:
-            raise ValueError("coefficient row is not a whole number of bytes")
-        return self.r1 * self.qbits // 8
+        """layout.py:98-101 for qbits 8; qbits 16 and 4 are this build's own modes
+        (`coef_modes`)."""
+        if self.qbits == 8:
+            return self.r1
+        from .coef_modes import coeff_bytes
+        return coeff_bytes(self.qbits, self.r1)
+
+    @property
+    def coeff_scale_bytes(self) -> int:
+        from .coef_modes import coeff_scale_bytes
+        return coeff_scale_bytes(self.qbits, self.r1)
 
     @property
     def k_pb(self) -> int:
@@ -73,11 +81,11 @@ class Layout:
     @property
     def k_field_off(self) -> int:
         """Byte offset of head 0's residual row inside the K slot."""
-        return self.coeff_bytes + 2
+        return self.coeff_bytes + self.coeff_scale_bytes
 
     @property
     def k_slot_bytes(self) -> int:
-        return align_up(self.coeff_bytes + 2 + self.H * self.k_row_bytes, self.align)
+        return align_up(self.k_field_off + self.H * self.k_row_bytes, self.align)
 
     @property
     def v_slot_bytes(self) -> int:
@@ -110,13 +118,18 @@ def _f16_bytes(x: torch.Tensor) -> torch.Tensor:
 
 def pack_k_slots(lay: Layout, coeff_q, coeff_scale, bitmap, packed, scale) -> torch.Tensor:
     """layout.py:161-193. coeff_q [n,r1] int8, coeff_scale [n] fp16, residual rows over H*n
-    rows in (head, token) order -> [n, k_slot_bytes] uint8."""
+    rows in (head, token) order -> [n, k_slot_bytes] uint8. For qbits 16 / 4 (`coef_modes`),
+    coeff_q / coeff_scale are `coef_modes.quantise`'s q and scales."""
     n = coeff_q.shape[0]
     if bitmap.shape[0] != lay.H * n:
         raise ValueError("residual rows != H*n")
     out = torch.zeros(n, lay.k_slot_bytes, dtype=torch.uint8)
-    out[:, :lay.coeff_bytes] = coeff_q.contiguous().view(torch.uint8)
-    out[:, lay.coeff_bytes:lay.coeff_bytes + 2] = _f16_bytes(coeff_scale)
+    if lay.qbits == 8:
+        out[:, :lay.coeff_bytes] = coeff_q.contiguous().view(torch.uint8)
+        out[:, lay.coeff_bytes:lay.coeff_bytes + 2] = _f16_bytes(coeff_scale)
+    else:  # this build's fp16 / 4-bit modes: coeff_q, coeff_scale as coef_modes.quantise gives
+        from .coef_modes import field_bytes
+        out[:, :lay.k_field_off] = field_bytes(lay.qbits, lay.r1, coeff_q, coeff_scale)
     for h in range(lay.H):
         base = lay.k_field_off + h * lay.k_row_bytes
         rows = slice(h * n, (h + 1) * n)
@@ -127,11 +140,16 @@ def pack_k_slots(lay: Layout, coeff_q, coeff_scale, bitmap, packed, scale) -> to
 
 
 def unpack_k_slots(lay: Layout, slots: torch.Tensor):
-    """layout.py:196-219 -> (coeff_q int8 [n,r1], coeff_scale fp16 [n], (bitmap, packed, scale))."""
+    """layout.py:196-219 -> (coeff_q int8 [n,r1], coeff_scale fp16 [n], (bitmap, packed, scale)).
+    For qbits 16 / 4 (`coef_modes`): (the stored coefficient values fp32 [n, r1], None, rows)."""
     n = slots.shape[0]
-    coeff_q = slots[:, :lay.coeff_bytes].clone().view(torch.int8)
-    coeff_scale = slots[:, lay.coeff_bytes:lay.coeff_bytes + 2].clone().view(
-        torch.float16).reshape(n)
+    if lay.qbits == 8:
+        coeff_q = slots[:, :lay.coeff_bytes].clone().view(torch.int8)
+        coeff_scale = slots[:, lay.coeff_bytes:lay.coeff_bytes + 2].clone().view(
+            torch.float16).reshape(n)
+    else:
+        from .coef_modes import values_from_field
+        coeff_q, coeff_scale = values_from_field(lay.qbits, lay.r1, slots[:, :lay.k_field_off]), None
     bm, pk, sc = [], [], []
     for h in range(lay.H):
         base = lay.k_field_off + h * lay.k_row_bytes

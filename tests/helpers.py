@@ -63,7 +63,7 @@ def device_store(cfg_name: str, lens, seed: int, r1: int = 110, block_size: int 
     """A paged store for requests of `lens` tokens, built the way serving builds it: each
     request's first `fit_on` tokens fitted on the device (`vllm_ttkv.encode.fit_into_budget`) and
     every token packed by the K3 write kernel (the first chunk from the fit's coefficients, the
-    rest by frozen projection). Full-size stores in seconds, where the CPU oracle's fit would take
+    rest by frozen projection; in the fp16 / 4-bit coefficient modes every token is projected). Full-size stores in seconds, where the CPU oracle's fit would take
     minutes; the oracle then reads the SAME slot bytes, so K1/K2 are checked against it exactly
     as on a store the oracle built.
 
@@ -72,11 +72,11 @@ def device_store(cfg_name: str, lens, seed: int, r1: int = 110, block_size: int 
     fp32 list), num_blocks).
     """
     from vllm_ttkv import encode as penc, kernels
-    from vllm_ttkv.layout import CONFIGS as PCONFIGS, layout_for_config as play_for
+    from vllm_ttkv.layout import config_named, layout_for_config as play_for
 
-    cfg = codec.CONFIGS[cfg_name]
-    lay = layout_for_config(cfg, r1=r1)
-    play = play_for(PCONFIGS[cfg_name], r1)
+    pcfg = config_named(cfg_name)  # a shipped allocation or a coefficient-mode extension
+    lay = layout_for_config(pcfg, r1=r1)
+    play = play_for(pcfg, r1)
     B = len(lens)
     bt, nblk = synth.shuffled_block_table(lens, block_size, seed=seed, extra_blocks=3)
     C = lay.compressed_bytes_per_token()
@@ -96,7 +96,7 @@ def device_store(cfg_name: str, lens, seed: int, r1: int = 110, block_size: int 
         K = synth.keys(n, seed=s, device=dev).permute(1, 0, 2)      # [n, H, d]
         V = synth.values(n, seed=s, device=dev).permute(1, 0, 2)
         f = min(fit_on, n)
-        fk = penc.fit_into_budget(K[:f].permute(1, 0, 2).contiguous(), play, PCONFIGS[cfg_name])
+        fk = penc.fit_into_budget(K[:f].permute(1, 0, 2).contiguous(), play, pcfg)
         dec_f[r] = fk.decoder.decoder_f
         dec_pool.q[r].copy_(fk.decoder.packed.q)
         dec_pool.scale[r].copy_(fk.decoder.packed.scale)
@@ -122,7 +122,10 @@ def device_store(cfg_name: str, lens, seed: int, r1: int = 110, block_size: int 
                             coeff_scale_in=None if cs is None else torch.cat([cs[i] for i in reqs]),
                             error_word=err)
 
-    _write(fk_all, [x[3] for x in fk_all], [x[4] for x in fk_all])
+    if play.qbits == 8:
+        _write(fk_all, [x[3] for x in fk_all], [x[4] for x in fk_all])
+    else:  # fp16 / 4-bit coefficients: the first chunk is projected too
+        _write(fk_all)
     _write(rest)
     torch.cuda.synchronize()
     if int(err.item()):

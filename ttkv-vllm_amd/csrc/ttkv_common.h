@@ -5,6 +5,15 @@
 //   K slot = r1 int8 coefficients, fp16 coefficient ruler (LE), H rows of
 //            [bitmap d/8 B | MSB-first code stream ceil(k*bits/8) B | fp16 ruler (LE)]
 //   V slot = H rows of the same shape
+// Two more coefficient fields, selected by the layout's qbits, are this library's own storage
+// modes (the reference writes only qbits = 8, layout.py:179):
+//   qbits 16: r1 fp16 coefficients (LE), no ruler
+//   qbits 4 : 4-bit two's complement coefficients in [-7, 7], 4 * ceil(r1/8) bytes of
+//             little-endian words: word w holds rank 8w + 2m at bits 4m .. 4m+3 and rank
+//             8w + 2m + 1 at bits 16 + 4m .. 16 + 4m + 3 (m = 0..3; pad nibbles 0), then one fp16
+//             scale per group of 32 ranks (ceil(r1/32) of them, LE). A scale has at most 8
+//             significant bits and lies in [2^-14, 9344] (or is 0 for an all-zero group), so
+//             q * scale is exact in fp16. The coefficient value is q * scale.
 // Bitmap: lane j <-> byte j>>3, bit 7-(j&7). The stream holds the kept lanes in increasing lane
 // order, `bits` bits each, MSB first; the stored code is q + 2^(bits-1). Decoded value
 // (code - 2^(bits-1)) * float(ruler) on kept lanes, 0 elsewhere.
@@ -28,9 +37,14 @@ constexpr int kD = 128;           // head dim the kernels are built for
 constexpr int kBitmapBytes = kD / 8;
 
 // Byte geometry of one layer, derived exactly as layout.py:98-157.
+// Coefficient storage modes, by the layout's qbits (8, 16, 4 above).
+enum CoefMode { kCoefI8 = 0, kCoefF16 = 1, kCoefI4G32 = 2 };
+
 struct Geom {
   int H, d, r1, qbits, res_k, res_bits, v_lanes, v_bits;
-  int coeff_bytes;   // r1 * qbits / 8
+  int coef_mode;     // CoefMode
+  int coeff_bytes;   // coefficient values: r1 (int8), 2 * r1 (fp16), 4 * ceil(r1 / 8) (4-bit)
+  int coef_groups;   // 4-bit mode: scales (groups of 32 ranks) after the values; else 0
   int k_pb, v_pb;    // packed code bytes per row
   int k_row, v_row;  // bytes per head row
   int k_field;       // offset of head 0's K row in the slot
@@ -65,15 +79,30 @@ __host__ inline bool make_geom(const ttkv_layout* l, Geom* g) {
   g->H = l->H; g->d = l->d; g->r1 = l->r1; g->qbits = l->qbits;
   g->res_k = l->res_k; g->res_bits = l->res_bits; g->v_lanes = l->v_lanes; g->v_bits = l->v_bits;
   if (g->d <= 0 || g->d % 8 || g->H <= 0 || g->r1 <= 0) return false;
-  if ((g->r1 * g->qbits) % 8) return false;
   if (g->res_k < 0 || g->res_k > g->d || g->v_lanes < 1 || g->v_lanes > g->d) return false;
-  g->coeff_bytes = g->r1 * g->qbits / 8;
+  int scale_bytes = 2;
+  g->coef_groups = 0;
+  if (g->qbits == 8) {
+    g->coef_mode = kCoefI8;
+    g->coeff_bytes = g->r1;
+  } else if (g->qbits == 16) {
+    g->coef_mode = kCoefF16;
+    g->coeff_bytes = 2 * g->r1;
+    scale_bytes = 0;
+  } else if (g->qbits == 4) {
+    g->coef_mode = kCoefI4G32;
+    g->coeff_bytes = 4 * ((g->r1 + 7) / 8);
+    g->coef_groups = (g->r1 + 31) / 32;
+    scale_bytes = 2 * g->coef_groups;
+  } else {
+    return false;
+  }
   g->k_pb = (g->res_k * g->res_bits + 7) / 8;
   g->v_pb = (g->v_lanes * g->v_bits + 7) / 8;
   g->k_row = g->d / 8 + g->k_pb + 2;
   g->v_row = g->d / 8 + g->v_pb + 2;
-  g->k_field = g->coeff_bytes + 2;
-  g->k_slot = align_up16(g->coeff_bytes + 2 + g->H * g->k_row);
+  g->k_field = g->coeff_bytes + scale_bytes;
+  g->k_slot = align_up16(g->k_field + g->H * g->k_row);
   g->v_slot = align_up16(g->H * g->v_row);
   g->blob = g->k_slot + g->v_slot;
   return true;

@@ -103,7 +103,7 @@ struct ExpandSmem {
   float cs[kXTile], krul[kXTile], vrul[kXTile];
 };
 
-template <int RB, int VB, int KSTEPS>
+template <int RB, int VB, int KSTEPS, int CM>
 __global__ __launch_bounds__(kXThreads, 2) void expand_kernel(ExpandArgs a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   __shared__ uint16_t lut3s[kLut3Entries];  // static: its address folds into the loads
@@ -210,29 +210,16 @@ __global__ __launch_bounds__(kXThreads, 2) void expand_kernel(ExpandArgs a) {
     return slot < a.n_slots ? a.page + slot * a.slot_stride : nullptr;
   };
   const int k_win = k_row_off & ~15, v_win = v_row_off & ~15;
-  RawSlotW<2 * KSTEPS> P;
-  fetch_raw_slot_w<2 * KSTEPS>(P, slot_base(k0), part, g, k_win, v_win);
+  RawSlotW<2 * KSTEPS, CM> P;
+  fetch_raw_slot_w<2 * KSTEPS, CM>(P, slot_base(k0), part, g, k_win, v_win);
   uint8_t* tile_out = a.tiles + (((int64_t)ri * g.H + h) * a.ntl + t_lo) * kTileBytes;
 
   for (int tt = k0; tt < k1; tt += kXTile, tile_out += kTileBytes) {
     const int ntile = min(kXTile, k1 - tt);
     // ------------------------------------------------------------ commit this tile's bytes
     {
-      uint32_t* crow = (uint32_t*)&S.coef[ptok][0];
-#pragma unroll
-      for (int i = 0; i < RawSlotW<2 * KSTEPS>::kChunks; ++i) {
-        // bytes past r1 are finite int8 values that meet zero decoder rows: they contribute 0
-        const int cch = part + 4 * i;
-        if (cch < 2 * KSTEPS) {
-          uint32_t hh[8];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) i8x4_to_f16(P.coef[i][j], hh[2 * j], hh[2 * j + 1]);
-          *(u32x4*)&crow[8 * cch] = u32x4{hh[0], hh[1], hh[2], hh[3]};
-          *(u32x4*)&crow[8 * cch + 4] = u32x4{hh[4], hh[5], hh[6], hh[7]};
-        }
-      }
-      if (part == 0)
-        S.cs[ptok] = f16_bits_to_float((g.coeff_bytes & 2) ? P.rul >> 16 : P.rul & 0xffffu);
+      const float cs = commit_coef<2 * KSTEPS, CM>(P, (uint32_t*)&S.coef[ptok][0], part, g);
+      if (part == 0) S.cs[ptok] = cs;
       stage_row_w(P.krow, (k_row_off & 15) >> 2, ksel, &S.rawk[ptok][part * 4]);
       stage_row_w(P.vrow, (v_row_off & 15) >> 2, vsel, &S.rawv[ptok][part * 4]);
     }
@@ -248,7 +235,7 @@ __global__ __launch_bounds__(kXThreads, 2) void expand_kernel(ExpandArgs a) {
       svA[nb] = *gbl((const float4v*)&a.cs_cache[(int64_t)pos * kD + 64 + dl]);
     }
     if (tt + kXTile < k1)
-      fetch_raw_slot_w<2 * KSTEPS>(P, slot_base(tt + kXTile), part, g, k_win, v_win);
+      fetch_raw_slot_w<2 * KSTEPS, CM>(P, slot_base(tt + kXTile), part, g, k_win, v_win);
     // No barrier: wave w commits and decodes the same 16 keys (16w .. 16w+15), and LDS accesses
     // of one wave complete in order (the fences only keep the compiler from moving them); the
     // previous tile's readers finished before its closing barrier.
@@ -1018,10 +1005,10 @@ ContShape cont_shape(const Geom& g, int G, int nr, int max_q_len, int max_seq_le
 
 int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
-template <int RB, int VB, int KSTEPS>
+template <int RB, int VB, int KSTEPS, int CM = kCoefI8>
 int launch_expand_t(const ExpandArgs& a, int grid, hipStream_t st) {
   const size_t smem = sizeof(ExpandSmem<KSTEPS>);
-  auto kfn = expand_kernel<RB, VB, KSTEPS>;
+  auto kfn = expand_kernel<RB, VB, KSTEPS, CM>;
   if (int rc = raise_smem_limit((const void*)kfn, smem)) return rc;
   hipLaunchKernelGGL(kfn, dim3(grid), dim3(kXThreads), smem, st, a);
   const hipError_t e = hipGetLastError();
@@ -1032,6 +1019,15 @@ int launch_expand_t(const ExpandArgs& a, int grid, hipStream_t st) {
 
 int launch_expand(const ExpandArgs& a, int ksteps, int grid, hipStream_t st) {
   const bool b3 = a.g.res_bits == 3;
+  // the fp16 and 4-bit coefficient modes are built for 64 < r1 <= 128
+  if (a.g.coef_mode != kCoefI8 && ksteps != 4)
+    return host_fail(TTKV_E_UNSUPPORTED, "fp16 and 4-bit coefficients are built for 64 < r1 <= 128");
+  if (a.g.coef_mode == kCoefF16)
+    return b3 ? launch_expand_t<3, 3, 4, kCoefF16>(a, grid, st)
+              : launch_expand_t<4, 4, 4, kCoefF16>(a, grid, st);
+  if (a.g.coef_mode == kCoefI4G32)
+    return b3 ? launch_expand_t<3, 3, 4, kCoefI4G32>(a, grid, st)
+              : launch_expand_t<4, 4, 4, kCoefI4G32>(a, grid, st);
   switch (ksteps) {
     case 2: return b3 ? launch_expand_t<3, 3, 2>(a, grid, st) : launch_expand_t<4, 4, 2>(a, grid, st);
     case 4: return b3 ? launch_expand_t<3, 3, 4>(a, grid, st) : launch_expand_t<4, 4, 4>(a, grid, st);

@@ -7,8 +7,9 @@
 // waves) walks its chunk in 64-token tiles with the next tile's raw bytes prefetched into
 // registers while the current one is computed:
 //   commit  : prefetched bytes -> LDS: coefficients as fp16 MFMA B-fragments (int8 is exact in
-//             fp16); this head's K and V rows realigned, the code streams byte-reversed per dword
-//             (one v_perm each) so that a code window is one v_alignbit.
+//             fp16; the fp16 mode's values are copied; the 4-bit mode's q * group scale is exact
+//             in fp16, commit_coef); this head's K and V rows realigned, the code streams
+//             byte-reversed per dword (one v_perm each) so that a code window is one v_alignbit.
 //   decode  : one thread per half row. Per bitmap byte, the next 8 codes are spread one per byte
 //             through a 64-entry two-code table (3-bit) or nibble perms (4-bit) and scattered onto their
 //             lanes with one v_perm driven by a 256-entry selector table (both tables built in
@@ -163,7 +164,7 @@ __device__ __forceinline__ void combine_regs(const float* pbase, int64_t cstride
 
 // QLO: the query's low fp16 part can be non-zero (fp32 / bf16 queries), so the scores take the
 // third product qlo * yhi; an fp16 query is its own hi part and skips it.
-template <int G, int RB, int VB, int KU, bool QLO>
+template <int G, int RB, int VB, int KU, bool QLO, int CM>
 __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   __shared__ uint16_t lut3s[kLut3Entries];  // static: its address folds into the loads
@@ -368,14 +369,14 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
   const int v_row_off = g.k_slot + h * g.v_row;
   // the rows' 64-byte windows (16-aligned; each row lies inside its window, host-checked)
   const int k_win = k_row_off & ~15, v_win = v_row_off & ~15;
-  RawSlotW<KU> P;
+  RawSlotW<KU, CM> P;
   {
     const uint8_t* base = nullptr;
     if (ptok < min(kTile, t1 - t0) && blk_t0 >= 0 && blk_t0 < a.num_blocks) {
       const int64_t slot = (int64_t)blk_t0 * a.block_size + (pos0 - bi0 * a.block_size);
       if (slot < a.n_slots) base = a.page + slot * a.slot_stride;
     }
-    fetch_raw_slot_w<KU>(P, base, part, g, k_win, v_win);
+    fetch_raw_slot_w<KU, CM>(P, base, part, g, k_win, v_win);
   }
   if (dslot < 0 || dslot >= a.n_dec_slots) {
     if (tid == 0) atomicOr(a.err, TTKV_ERR_NO_DECODER);
@@ -543,23 +544,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
     const uint8_t* next_base = tt + kTile < t1 ? slot_base(tt + kTile) : nullptr;
     // ---------------------------------------------------------------- commit prefetched bytes
     {
-      uint32_t* crow = (uint32_t*)&S.coef[ptok][0];
-#pragma unroll
-      for (int i = 0; i < RawSlotW<KU>::kChunks; ++i) {
-        // coefficient chunk part + 4i -> 16 fp16 values; bytes past r1 (the ruler, head 0's row)
-        // are converted too: they are finite, and the decoder fragments are zero for k >= r1,
-        // so they contribute exactly 0
-        const int cch = part + 4 * i;
-        if (cch < KU) {
-          uint32_t h[8];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) i8x4_to_f16(P.coef[i][j], h[2 * j], h[2 * j + 1]);
-          *(u32x4*)&crow[8 * cch] = u32x4{h[0], h[1], h[2], h[3]};
-          *(u32x4*)&crow[8 * cch + 4] = u32x4{h[4], h[5], h[6], h[7]};
-        }
-      }
-      if (part == 0)
-        S.cs[ptok] = f16_bits_to_float((g.coeff_bytes & 2) ? P.rul >> 16 : P.rul & 0xffffu);
+      const float cs = commit_coef<KU, CM>(P, (uint32_t*)&S.coef[ptok][0], part, g);
+      if (part == 0) S.cs[ptok] = cs;
       stage_row_w(P.krow, (k_row_off & 15) >> 2, ksel, &S.rawk[ptok][part * 4]);
       stage_row_w(P.vrow, (v_row_off & 15) >> 2, vsel, &S.rawv[ptok][part * 4]);
     }
@@ -574,7 +560,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
     // the decode and reconstruction instead of stalling the next commit (measured: the bytes took
     // ~2k cycles, longer than the softmax and P.V they used to overlap). The reconstruction's
     // angle loads queue behind them (loads complete in order) but are issued a decode later.
-    if (tt + kTile < t1) fetch_raw_slot_w<KU>(P, next_base, part, g, k_win, v_win);
+    if (tt + kTile < t1) fetch_raw_slot_w<KU, CM>(P, next_base, part, g, k_win, v_win);
     // ---------------------------------------------------------------- decode (thread = half row)
     // The decode and reconstruction are each workgroup's critical chain; the co-resident
     // workgroup's softmax, P.V and commit fill the issue slots they leave. Raising this wave's
@@ -932,11 +918,11 @@ __global__ __launch_bounds__(kThreads, 2) void decode_paged_kernel(DecodeArgs a)
 
 namespace ttkv {
 
-template <int G, int RB, int VB, int KU>
+template <int G, int RB, int VB, int KU, int CM = kCoefI8>
 static int launch_decode_t(const DecodeArgs& a, int grid, hipStream_t st) {
   const size_t smem = sizeof(DecodeSmem<KU, G>);
-  auto kfn = a.q_dtype == TTKV_DTYPE_F16 ? decode_paged_kernel<G, RB, VB, KU, false>
-                                         : decode_paged_kernel<G, RB, VB, KU, true>;
+  auto kfn = a.q_dtype == TTKV_DTYPE_F16 ? decode_paged_kernel<G, RB, VB, KU, false, CM>
+                                         : decode_paged_kernel<G, RB, VB, KU, true, CM>;
   if (int rc = raise_smem_limit((const void*)kfn, smem)) return rc;
   hipLaunchKernelGGL(kfn, dim3(grid), dim3(kThreads), smem, st, a);
   const hipError_t e = hipGetLastError();
@@ -958,8 +944,20 @@ static int dispatch_g(const DecodeArgs& a, int grid, hipStream_t st) {
                                            " query heads per KV head is not built (1,2,3,4,8)");
 }
 
+// The fp16 and 4-bit coefficient modes are built for G = 3 and r1 in 65..128 (the shapes their
+// tests and benchmark use).
+template <int RB, int VB, int CM>
+static int dispatch_mode(const DecodeArgs& a, int ku, int grid, hipStream_t st) {
+  if (a.G == 3 && ku == 7) return launch_decode_t<3, RB, VB, 7, CM>(a, grid, st);
+  if (a.G == 3 && ku == 8) return launch_decode_t<3, RB, VB, 8, CM>(a, grid, st);
+  return host_fail(TTKV_E_UNSUPPORTED, "fp16 and 4-bit coefficients are built for num_heads / H "
+                                       "= 3 and 64 < r1 <= 128");
+}
+
 template <int RB, int VB>
 static int dispatch_k(const DecodeArgs& a, int ku, int grid, hipStream_t st) {
+  if (a.g.coef_mode == kCoefF16) return dispatch_mode<RB, VB, kCoefF16>(a, ku, grid, st);
+  if (a.g.coef_mode == kCoefI4G32) return dispatch_mode<RB, VB, kCoefI4G32>(a, ku, grid, st);
   switch (ku) {
     case 4: return dispatch_g<RB, VB, 4>(a, grid, st);
     case 7: return dispatch_g<RB, VB, 7>(a, grid, st);
@@ -1016,7 +1014,6 @@ int decode_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype,
                  int64_t max_pos, void* out, int out_dtype, int64_t out_row_stride, void* ws,
                  int64_t ws_bytes, int32_t* err, hipStream_t st) {
   if (g.d != kD) return host_fail(TTKV_E_UNSUPPORTED, "head dim must be 128");
-  if (g.qbits != 8) return host_fail(TTKV_E_UNSUPPORTED, "coefficient width must be 8 bits");
   if (!((g.res_bits == 3 && g.v_bits == 3) || (g.res_bits == 4 && g.v_bits == 4)))
     return host_fail(TTKV_E_UNSUPPORTED, "res_bits/v_bits must be 3/3 or 4/4");
   if (HQ <= 0 || HQ % g.H) return host_fail(TTKV_E_INVALID, "num_heads is not a multiple of H");
@@ -1025,7 +1022,13 @@ int decode_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype,
   // coefficient window in 16-wide k units (r1 padded to 16 * ku)
   const int ku = g.r1 <= 64 ? 4 : g.r1 <= 112 ? 7 : g.r1 <= 128 ? 8 : g.r1 <= 160 ? 10 : 0;
   if (!ku) return host_fail(TTKV_E_UNSUPPORTED, "r1 > 160 is not built");
-  if (ku * 16 > g.k_slot)
+  if (g.coef_mode != kCoefI8 && (G != 3 || (ku != 7 && ku != 8)))
+    return host_fail(TTKV_E_UNSUPPORTED, "fp16 and 4-bit coefficients are built for num_heads / "
+                                         "H = 3 and 64 < r1 <= 128");
+  // the coefficient window (16 * ku ranks) is read in 16-byte chunks from the slot's start
+  const int win_bytes = g.coef_mode == kCoefI8 ? 16 * ku : g.coef_mode == kCoefF16 ? 32 * ku
+                                                                                 : 16 * ((ku + 1) / 2);
+  if (win_bytes > g.k_slot)
     return host_fail(TTKV_E_UNSUPPORTED, "padded coefficient block exceeds the K slot");
   if (!rows_in_windows(g))
     return host_fail(TTKV_E_UNSUPPORTED, "a head row of " + std::to_string(g.k_row) + "/" +

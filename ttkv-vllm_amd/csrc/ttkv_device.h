@@ -54,71 +54,28 @@ __device__ __forceinline__ void spread8(uint32_t w, uint32_t& e0, uint32_t& e1) 
   }
 }
 
-// The slot bytes one of a token's 4 loader threads needs for one KV head: its quarter of the
-// coefficient window (NCW dwords), source dwords part*4 .. part*4+4 of the head's K and V rows
-// (4 output dwords + the funnel for realignment), and the fp16 coefficient ruler (part 0).
-template <int NCW>
-struct RawSlot {
-  uint32_t coef[NCW];
-  uint32_t krow[5], vrow[5];
-  uint32_t rul;
-};
-
-// Fetch a token's RawSlot (all zero for a null slot base).
-template <int NCW>
-__device__ __forceinline__ void fetch_raw_slot(RawSlot<NCW>& P, const uint8_t* base, int part,
-                                               const Geom& g, int k_row_off, int v_row_off) {
-  constexpr int kCPP = NCW * 4;
-  if (!base) {
-#pragma unroll
-    for (int i = 0; i < NCW; ++i) P.coef[i] = 0u;
-#pragma unroll
-    for (int i = 0; i < 5; ++i) P.krow[i] = P.vrow[i] = 0u;
-    P.rul = 0u;
-    return;
-  }
-  const auto* cs = gbl((const uint32_t*)(base + part * kCPP));
-#pragma unroll
-  for (int i = 0; i < NCW; ++i) P.coef[i] = cs[i];
-  {
-    const uintptr_t A = (uintptr_t)(base + k_row_off);
-    const auto* src = gbl((const uint32_t*)(A & ~(uintptr_t)3));
-    const int nsrc = (int)((A & 3) + g.k_row + 3) >> 2;
-    // clamped index: every load stays inside the row's dwords (the extra ones are never decoded)
-#pragma unroll
-    for (int i = 0; i < 5; ++i) P.krow[i] = src[min(part * 4 + i, nsrc - 1)];
-  }
-  {
-    const uintptr_t A = (uintptr_t)(base + v_row_off);
-    const auto* src = gbl((const uint32_t*)(A & ~(uintptr_t)3));
-    const int nsrc = (int)((A & 3) + g.v_row + 3) >> 2;
-#pragma unroll
-    for (int i = 0; i < 5; ++i) P.vrow[i] = src[min(part * 4 + i, nsrc - 1)];
-  }
-  // every part loads the ruler (the 4 loads of a token hit one line), so the load is not
-  // conditional and the compiler's wait counts stay exact across the prefetch pipeline
-  P.rul = *gbl((const uint16_t*)(base + g.coeff_bytes));  // 2-aligned (r1 even)
-}
-
 // Wide fetch of the slot bytes one of a token's 4 loader threads needs for one KV head: 16-byte
 // loads only (5 per thread instead of one per dword). Part p loads coefficient chunks p, p+4,
-// p+8 (bytes 16c .. 16c+15 of the 16*KU-byte window; a chunk past the window is clamped to the
-// window's last one and never committed), chunk p of the 64-byte-aligned windows holding this
-// head's K row and V row (each row lies inside its window: misalignment + row length <= 64,
-// checked by the host; a chunk past the blob is clamped inside it and covers no row byte), and
-// the dword holding the coefficient ruler.
-template <int KU>
+// p+8 (bytes 16c .. 16c+15 of the coefficient window: 16 ranks of int8, 8 of fp16 or 32 of 4-bit
+// values per chunk; a chunk past the window is clamped to the window's last one and never
+// committed), chunk p of the 64-byte-aligned windows holding this head's K row and V row (each
+// row lies inside its window: misalignment + row length <= 64, checked by the host; a chunk past
+// the blob is clamped inside it and covers no row byte), and the dword holding the coefficient
+// ruler (int8 mode) or the scale of group p (4-bit mode; the fp16 mode has neither).
+template <int KU, int CM = kCoefI8>
 struct RawSlotW {
-  static constexpr int kChunks = (KU + 3) / 4;  // coefficient chunks per part
+  // coefficient chunks of the 16*KU-rank window
+  static constexpr int kCoefChunks = CM == kCoefI8 ? KU : CM == kCoefF16 ? 2 * KU : (KU + 1) / 2;
+  static constexpr int kChunks = (kCoefChunks + 3) / 4;  // coefficient chunks per part
   u32x4 coef[kChunks];
   u32x4 krow, vrow;
   uint32_t rul;
 };
 
-template <int KU>
-__device__ __forceinline__ void fetch_raw_slot_w(RawSlotW<KU>& P, const uint8_t* base, int part,
-                                                 const Geom& g, int k_win, int v_win) {
-  using R = RawSlotW<KU>;
+template <int KU, int CM = kCoefI8>
+__device__ __forceinline__ void fetch_raw_slot_w(RawSlotW<KU, CM>& P, const uint8_t* base,
+                                                 int part, const Geom& g, int k_win, int v_win) {
+  using R = RawSlotW<KU, CM>;
   if (!base) {
 #pragma unroll
     for (int i = 0; i < R::kChunks; ++i) P.coef[i] = u32x4{0u, 0u, 0u, 0u};
@@ -128,10 +85,76 @@ __device__ __forceinline__ void fetch_raw_slot_w(RawSlotW<KU>& P, const uint8_t*
   }
 #pragma unroll
   for (int i = 0; i < R::kChunks; ++i)
-    P.coef[i] = *gbl((const u32x4*)(base + 16 * min(part + 4 * i, KU - 1)));
+    P.coef[i] = *gbl((const u32x4*)(base + 16 * min(part + 4 * i, R::kCoefChunks - 1)));
   P.krow = *gbl((const u32x4*)(base + min(k_win + 16 * part, g.blob - 16)));
   P.vrow = *gbl((const u32x4*)(base + min(v_win + 16 * part, g.blob - 16)));
-  P.rul = *gbl((const uint32_t*)(base + (g.coeff_bytes & ~3)));
+  if constexpr (CM == kCoefI4G32)
+    P.rul = *gbl((const uint32_t*)(base + ((g.coeff_bytes + 2 * min(part, g.coef_groups - 1)) & ~3)));
+  else if constexpr (CM == kCoefI8)
+    P.rul = *gbl((const uint32_t*)(base + (g.coeff_bytes & ~3)));
+  else
+    P.rul = 0u;
+}
+
+// Commit of one token's coefficients: this part's chunks become fp16 MFMA B values in the token's
+// LDS row `crow` (one dword = two consecutive ranks, ranks 0 .. 16*KU-1), exactly. Returns the
+// coefficient ruler the key is scaled by afterwards: the int8 mode's fp16 ruler, 1 for the fp16
+// and 4-bit modes (their values are the coefficients themselves).
+//  - int8: 16 ranks per chunk; bytes past r1 (the ruler, head 0's row) are finite int8 values
+//    that meet zero decoder ranks, so they contribute exactly 0.
+//  - fp16: 8 ranks per chunk, copied; ranks >= r1 (other fields' bytes, maybe not finite) are
+//    zeroed.
+//  - 4-bit: 32 ranks (one group) per chunk. Per word, each pair of ranks (2m, 2m+1) becomes
+//    fp16 1024 + (q + 8) by one shift-and-or into the exponent of 1024, then (x - 1032) * scale,
+//    both exact (|q| <= 8 and the scale's 8 significant bits need 11). Words past the values
+//    (the scales, head 0's row) are taken as zero and groups past the last have scale 0.
+template <int KU, int CM>
+__device__ __forceinline__ float commit_coef(const RawSlotW<KU, CM>& P, uint32_t* crow, int part,
+                                             const Geom& g) {
+  using R = RawSlotW<KU, CM>;
+  static_assert(CM != kCoefI4G32 || R::kChunks == 1, "4-bit mode: one group per loader part");
+#pragma unroll
+  for (int i = 0; i < R::kChunks; ++i) {
+    const int cch = part + 4 * i;
+    if (cch >= R::kCoefChunks) continue;
+    if constexpr (CM == kCoefI8) {
+      uint32_t h[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) i8x4_to_f16(P.coef[i][j], h[2 * j], h[2 * j + 1]);
+      *(u32x4*)&crow[8 * cch] = u32x4{h[0], h[1], h[2], h[3]};
+      *(u32x4*)&crow[8 * cch + 4] = u32x4{h[4], h[5], h[6], h[7]};
+    } else if constexpr (CM == kCoefF16) {
+      uint32_t h[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = 8 * cch + 2 * j;
+        h[j] = P.coef[i][j] & ((r < g.r1 ? 0x0000ffffu : 0u) | (r + 1 < g.r1 ? 0xffff0000u : 0u));
+      }
+      *(u32x4*)&crow[4 * cch] = u32x4{h[0], h[1], h[2], h[3]};
+    } else {
+      const uint32_t sb = (g.coeff_bytes + 2 * part) & 2 ? P.rul >> 16 : P.rul & 0xffffu;
+      const _Float16 sc = part < g.coef_groups ? __builtin_bit_cast(_Float16, (uint16_t)sb)
+                                               : (_Float16)0.0f;
+      const half2v s2 = {sc, sc};
+      const half2v bias = {(_Float16)1032.0f, (_Float16)1032.0f};
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        if (32 * cch + 8 * w >= 16 * KU) continue;  // past the window (KU odd)
+        const uint32_t x = (16 * cch + 4 * w < g.coeff_bytes ? P.coef[i][w] : 0u) ^ 0x88888888u;
+        uint32_t o[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const half2v v = __builtin_bit_cast(half2v, ((x >> (4 * m)) & 0x000f000fu) | 0x64006400u);
+          o[m] = __builtin_bit_cast(uint32_t, (v - bias) * s2);
+        }
+        *(u32x4*)&crow[16 * cch + 4 * w] = u32x4{o[0], o[1], o[2], o[3]};
+      }
+    }
+  }
+  if constexpr (CM == kCoefI8)
+    return f16_bits_to_float((g.coeff_bytes & 2) ? P.rul >> 16 : P.rul & 0xffffu);
+  else
+    return 1.f;
 }
 
 // Stage dwords 4*part .. 4*part+3 of a head row for the decode (the big-endian staged layout

@@ -105,7 +105,7 @@ struct PrefillSmem {
   int is_last;
 };
 
-template <int G, int RB, int VB, int KSTEPS, bool SCORES>
+template <int G, int RB, int VB, int KSTEPS, bool SCORES, int CM>
 __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) void prefill_paged_kernel(PrefillArgs a) {
   constexpr bool EXACT = true;  // see the precision note at the top
   extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -279,8 +279,8 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
   };
   // the rows' 64-byte windows (16-aligned; each row lies inside its window, host-checked)
   const int k_win = k_row_off & ~15, v_win = v_row_off & ~15;
-  RawSlotW<2 * KSTEPS> P;
-  fetch_raw_slot_w<2 * KSTEPS>(P, slot_base(k0), part, g, k_win, v_win);
+  RawSlotW<2 * KSTEPS, CM> P;
+  fetch_raw_slot_w<2 * KSTEPS, CM>(P, slot_base(k0), part, g, k_win, v_win);
 
   // score-tensor rows 16-byte aligned: every 4-key group starts on a 16-byte boundary
   const bool s_vec = SCORES && ((uintptr_t)a.s_out % 16 == 0) && a.s_q_stride % 4 == 0 &&
@@ -289,27 +289,13 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
     const int ntile = min(kPTile, k1 - tt);
     // ------------------------------------------------------------ commit this tile's bytes
     {
-      uint32_t* crow = (uint32_t*)&S.coef[ptok][0];
-#pragma unroll
-      for (int i = 0; i < RawSlotW<2 * KSTEPS>::kChunks; ++i) {
-        // coefficient chunk part + 4i -> 16 fp16 values; bytes past r1 are finite int8 values
-        // and meet zero decoder rows: they contribute 0
-        const int cch = part + 4 * i;
-        if (cch < 2 * KSTEPS) {
-          uint32_t hh[8];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) i8x4_to_f16(P.coef[i][j], hh[2 * j], hh[2 * j + 1]);
-          *(u32x4*)&crow[8 * cch] = u32x4{hh[0], hh[1], hh[2], hh[3]};
-          *(u32x4*)&crow[8 * cch + 4] = u32x4{hh[4], hh[5], hh[6], hh[7]};
-        }
-      }
-      if (part == 0)
-        S.cs[ptok] = f16_bits_to_float((g.coeff_bytes & 2) ? P.rul >> 16 : P.rul & 0xffffu);
+      const float cs = commit_coef<2 * KSTEPS, CM>(P, (uint32_t*)&S.coef[ptok][0], part, g);
+      if (part == 0) S.cs[ptok] = cs;
       stage_row_w(P.krow, (k_row_off & 15) >> 2, ksel, &S.u.raw.k[ptok][part * 4]);
       stage_row_w(P.vrow, (v_row_off & 15) >> 2, vsel, &S.u.raw.v[ptok][part * 4]);
     }
     if constexpr (SCORES)
-      if (tt + kPTile < k1) fetch_raw_slot_w<2 * KSTEPS>(P, slot_base(tt + kPTile), part, g, k_win, v_win);
+      if (tt + kPTile < k1) fetch_raw_slot_w<2 * KSTEPS, CM>(P, slot_base(tt + kPTile), part, g, k_win, v_win);
     // No barrier: wave w commits and decodes the same 16 keys (16w .. 16w+15), and LDS accesses
     // of one wave complete in order (the fences only keep the compiler from moving them); the
     // previous tile's readers finished before its closing barrier.
@@ -439,7 +425,7 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
     // angle wait, which would otherwise also wait for them. The score-tensor mode requests them
     // at the commit instead: its score stores count on the same in-order counter (measured).
     if constexpr (!SCORES)
-      if (tt + kPTile < k1) fetch_raw_slot_w<2 * KSTEPS>(P, slot_base(tt + kPTile), part, g, k_win, v_win);
+      if (tt + kPTile < k1) fetch_raw_slot_w<2 * KSTEPS, CM>(P, slot_base(tt + kPTile), part, g, k_win, v_win);
     __syncthreads();
     // ------------------------------------------------------------ scores S^T = Kp Q^T
     float4v sacc[4][G];
@@ -658,10 +644,10 @@ __global__ __launch_bounds__(kPThreads, ((SCORES && G <= 3) || G <= 2) ? 2 : 1) 
 
 namespace ttkv {
 
-template <int G, int RB, int VB, int KSTEPS, bool SCORES>
+template <int G, int RB, int VB, int KSTEPS, bool SCORES, int CM = kCoefI8>
 static int launch_prefill_t(const PrefillArgs& a, int grid, hipStream_t st) {
   const size_t smem = sizeof(PrefillSmem<KSTEPS, true>);
-  auto kfn = prefill_paged_kernel<G, RB, VB, KSTEPS, SCORES>;
+  auto kfn = prefill_paged_kernel<G, RB, VB, KSTEPS, SCORES, CM>;
   if (int rc = raise_smem_limit((const void*)kfn, smem)) return rc;
   hipLaunchKernelGGL(kfn, dim3(grid), dim3(kPThreads), smem, st, a);
   const hipError_t e = hipGetLastError();
@@ -685,6 +671,14 @@ static int prefill_dispatch_g(const PrefillArgs& a, int grid, hipStream_t st) {
 
 template <int RB, int VB, bool SCORES>
 static int prefill_dispatch_k(const PrefillArgs& a, int ksteps, int grid, hipStream_t st) {
+  // the fp16 and 4-bit coefficient modes are built for G = 3 and 64 < r1 <= 128
+  if (a.g.coef_mode != kCoefI8) {
+    if (a.G != 3 || ksteps != 4)
+      return host_fail(TTKV_E_UNSUPPORTED, "fp16 and 4-bit coefficients are built for num_heads "
+                                           "/ H = 3 and 64 < r1 <= 128");
+    return a.g.coef_mode == kCoefF16 ? launch_prefill_t<3, RB, VB, 4, SCORES, kCoefF16>(a, grid, st)
+                                     : launch_prefill_t<3, RB, VB, 4, SCORES, kCoefI4G32>(a, grid, st);
+  }
   switch (ksteps) {
     case 2: return prefill_dispatch_g<RB, VB, 2, SCORES>(a, grid, st);
     case 4: return prefill_dispatch_g<RB, VB, 4, SCORES>(a, grid, st);
@@ -754,14 +748,19 @@ int prefill_paged(const Geom& g, int HQ, float scale, const void* q, int q_dtype
                   int64_t s_q_stride, void* ws, int64_t ws_bytes, int32_t* err, hipStream_t st) {
   const bool scores = s_out != nullptr;
   if (g.d != kD) return host_fail(TTKV_E_UNSUPPORTED, "head dim must be 128");
-  if (g.qbits != 8) return host_fail(TTKV_E_UNSUPPORTED, "coefficient width must be 8 bits");
   if (!((g.res_bits == 3 && g.v_bits == 3) || (g.res_bits == 4 && g.v_bits == 4)))
     return host_fail(TTKV_E_UNSUPPORTED, "res_bits/v_bits must be 3/3 or 4/4");
   if (HQ <= 0 || HQ % g.H) return host_fail(TTKV_E_INVALID, "num_heads is not a multiple of H");
   const int G = HQ / g.H;
   const int ksteps = g.r1 <= 64 ? 2 : g.r1 <= 128 ? 4 : g.r1 <= 160 ? 5 : 0;
   if (!ksteps) return host_fail(TTKV_E_UNSUPPORTED, "r1 > 160 is not built");
-  if (ksteps * 32 > g.k_slot)
+  if (g.coef_mode != kCoefI8 && (G != 3 || ksteps != 4))
+    return host_fail(TTKV_E_UNSUPPORTED, "fp16 and 4-bit coefficients are built for num_heads / "
+                                         "H = 3 and 64 < r1 <= 128");
+  // the coefficient window (32 * ksteps ranks) is read in 16-byte chunks from the slot's start
+  const int win_bytes = g.coef_mode == kCoefI8 ? 32 * ksteps
+                        : g.coef_mode == kCoefF16 ? 64 * ksteps : 16 * ksteps;
+  if (win_bytes > g.k_slot)
     return host_fail(TTKV_E_UNSUPPORTED, "padded coefficient block exceeds the K slot");
   if (!rows_in_windows(g))
     return host_fail(TTKV_E_UNSUPPORTED, "a head row of " + std::to_string(g.k_row) + "/" +

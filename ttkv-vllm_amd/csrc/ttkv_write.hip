@@ -63,7 +63,9 @@ struct WriteArgs {
   int tok0;         // first token of this launch (tokens tok0 .. tok0 + num_tokens - 1)
   int* ws_cnt;      // [num_tokens] arrival counters (zero between calls)
   float* ws_part;   // [num_tokens][H][r1] per-head partial projections
-  float* ws_q;      // [num_tokens][r1 + 1] cq (as floats) then cs
+  float* ws_q;      // [num_tokens][wq_stride]: cq (as floats; the coefficient value itself in
+                    // the fp16 and 4-bit modes), cs (1 in those modes), then the 4-bit mode's
+                    // group scales
   int* ws_ds;       // [num_tokens] each token's decoder slot (or -1), from K3a for K3b
   float inv127, inv_rk, inv_rv;
 };
@@ -171,6 +173,19 @@ __device__ void pack_row(float x0, float x1, int k, float inv_ruler, uint8_t* ds
   }
 }
 
+// Floats per token in ws_q: r1 coefficients, the ruler, up to 8 group scales (r1 <= 256).
+__host__ __device__ inline int wq_stride(const Geom& g) { return g.r1 + 9; }
+
+// Scale of a 4-bit coefficient group whose largest magnitude is m: m / 7 (IEEE) rounded up to 8
+// significant bits, then held within [2^-14, 9344], so that every q * scale (|q| <= 7) is an
+// exact fp16 normal; 0 for an all-zero group.
+__device__ inline float coef_group_scale(float m) {
+  if (!(m > 0.f)) return 0.f;
+  uint32_t u = __builtin_bit_cast(uint32_t, __fdiv_rn(m, 7.f));
+  if (u & 0xffffu) u = (u & ~0xffffu) + 0x10000u;
+  return fminf(fmaxf(__builtin_bit_cast(float, u), 0x1p-14f), 9344.f);
+}
+
 // K3a: per-head partial projections; the token's last workgroup combines and quantises.
 __global__ __launch_bounds__(kWThreads) void write_project_kernel(WriteArgs a) {
   __shared__ float mk[kD];
@@ -225,7 +240,7 @@ __global__ __launch_bounds__(kWThreads) void write_project_kernel(WriteArgs a) {
   if (!is_last) return;
 
   // c[a] = sum over heads in head order
-  float* cq = a.ws_q + (int64_t)il * (g.r1 + 1);
+  float* cq = a.ws_q + (int64_t)il * wq_stride(g);
   float mx = 0.f;
   float cv = 0.f;
   const bool mine = tid < g.r1;
@@ -244,18 +259,30 @@ __global__ __launch_bounds__(kWThreads) void write_project_kernel(WriteArgs a) {
     mx = fabsf(cv);
     if (a.c_out) a.c_out[(int64_t)i * g.r1 + tid] = cv;
   }
+  if (g.coef_mode == kCoefI8) {  // workgroup-uniform
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-  if (lane == 0) red[wv] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  float cs = mx * a.inv127;
-  if (cs == 0.f) cs = 1.f;
-  if (mine) cq[tid] = fminf(fmaxf(rintf(__fdiv_rn(cv, cs)), -128.f), 127.f);
-  if (tid == 0) {
-    cq[g.r1] = cs;
-    __hip_atomic_store(&a.ws_cnt[il], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if (lane == 0) red[wv] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float cs = mx * a.inv127;
+    if (cs == 0.f) cs = 1.f;
+    if (mine) cq[tid] = fminf(fmaxf(rintf(__fdiv_rn(cv, cs)), -128.f), 127.f);
+    if (tid == 0) cq[g.r1] = cs;
+  } else if (g.coef_mode == kCoefF16) {
+    if (mine) cq[tid] = (float)(_Float16)cv;  // round to nearest even
+    if (tid == 0) cq[g.r1] = 1.f;
+  } else {
+    // group k = ranks 32k .. 32k+31 = threads 32k .. 32k+31 (half a wave)
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    const float sc = coef_group_scale(mx);
+    if (mine)
+      cq[tid] = sc > 0.f ? fminf(fmaxf(rintf(__fdiv_rn(cv, sc)), -7.f), 7.f) * sc : 0.f;
+    if (mine && (tid & 31) == 0) cq[g.r1 + 1 + (tid >> 5)] = sc;
+    if (tid == 0) cq[g.r1] = 1.f;
   }
+  if (tid == 0) __hip_atomic_store(&a.ws_cnt[il], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // K3b: residual of head h, then its K row and V row; head 0 also writes the coefficients.
@@ -291,7 +318,7 @@ __global__ __launch_bounds__(kWThreads) void write_pack_kernel(WriteArgs a) {
   // the decoder slot: from K3a's lookup when it ran (one load), else looked up here; the
   // coefficients (K3a's or the fit's) are requested in the same round trip
   const int ds = a.cq_in ? token_decoder(a, i) : a.ws_ds[il];
-  const float* wq = a.ws_q + (int64_t)il * (g.r1 + 1);
+  const float* wq = a.ws_q + (int64_t)il * wq_stride(g);
   const float cs = a.cq_in ? a.cs_in[i] : wq[g.r1];
   const float qv = tid < g.r1 ? (a.cq_in ? (float)a.cq_in[(int64_t)i * g.r1 + tid] : wq[tid]) : 0.f;
   if (h == 0 && tid == 0) {
@@ -323,16 +350,45 @@ __global__ __launch_bounds__(kWThreads) void write_pack_kernel(WriteArgs a) {
   }
   uint8_t* base = a.page + slot * a.slot_stride;
   if (h == 0) {
-    if (tid < g.r1) base[tid] = (uint8_t)(int8_t)(int)qv;
-    if (tid == 0) {
-      const uint16_t hb = __builtin_bit_cast(uint16_t, (_Float16)cs);
-      base[g.coeff_bytes] = (uint8_t)(hb & 0xff);
-      base[g.coeff_bytes + 1] = (uint8_t)(hb >> 8);
+    if (g.coef_mode == kCoefI8) {
+      if (tid < g.r1) base[tid] = (uint8_t)(int8_t)(int)qv;
+      if (tid == 0) {
+        const uint16_t hb = __builtin_bit_cast(uint16_t, (_Float16)cs);
+        base[g.coeff_bytes] = (uint8_t)(hb & 0xff);
+        base[g.coeff_bytes + 1] = (uint8_t)(hb >> 8);
+      }
+    } else if (g.coef_mode == kCoefF16) {
+      if (tid < g.r1) {  // qv is an fp16 value: the conversion is exact
+        const uint16_t hb = __builtin_bit_cast(uint16_t, (_Float16)qv);
+        base[2 * tid] = (uint8_t)(hb & 0xff);
+        base[2 * tid + 1] = (uint8_t)(hb >> 8);
+      }
+    } else if (tid < g.coef_groups) {  // 4-bit: the group scales (exact in fp16)
+      const uint16_t hb = __builtin_bit_cast(uint16_t, (_Float16)wq[g.r1 + 1 + tid]);
+      base[g.coeff_bytes + 2 * tid] = (uint8_t)(hb & 0xff);
+      base[g.coeff_bytes + 2 * tid + 1] = (uint8_t)(hb >> 8);
     }
     for (int b = g.k_field + g.H * g.k_row + tid; b < g.k_slot; b += kWThreads) base[b] = 0;
     for (int b = g.k_slot + g.H * g.v_row + tid; b < g.blob; b += kWThreads) base[b] = 0;
   }
   __syncthreads();
+  if (g.coef_mode == kCoefI4G32 && h == 0 && tid < g.coeff_bytes) {
+    // byte b of word w = b / 4 holds the nibbles of ranks lo (bits 0-3) and lo + 2 (bits 4-7):
+    // lo = 8w + 4j for byte j < 2 of the word, 8w + 4j - 7 for j >= 2; q = value / scale exactly
+    const int j = tid & 3;
+    const int lo = 8 * (tid >> 2) + (j < 2 ? 4 * j : 4 * j - 7);
+    uint32_t byte = 0;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int r = lo + 2 * e;
+      if (r < g.r1) {
+        const float sc = wq[g.r1 + 1 + (r >> 5)];
+        const int q = sc > 0.f ? (int)rintf(__fdiv_rn(cqs[r], sc)) : 0;
+        byte |= ((uint32_t)q & 15u) << (4 * e);
+      }
+    }
+    base[tid] = (uint8_t)byte;
+  }
   // R[j] = K[h*d+j] - sum_a cqs[a] * dec[a][h*d+j], dec = float(q) * ruler exactly: each lane sums
   // its ranks in increasing order, then the two halves of the column are added
   float acc = 0.f;
@@ -374,7 +430,7 @@ static float inv_ruler_f32(int bits) { return (float)(1.0 / (double)((1 << (bits
 // Tokens per launch: one arrival counter each.
 int64_t write_workspace_bytes(const Geom& g, int num_tokens) {
   const int64_t nt = std::min(std::max(num_tokens, 0), kMaxCounters);
-  return kCounterBytes + nt * (g.H * g.r1 + g.r1 + 2) * 4;
+  return kCounterBytes + nt * (g.H * g.r1 + wq_stride(g) + 1) * 4;
 }
 
 int write_paged(const Geom& g, const void* key, int k_dtype, int64_t k_row_stride, const void* val,
@@ -387,7 +443,6 @@ int write_paged(const Geom& g, const void* key, int k_dtype, int64_t k_row_strid
                 int64_t ws_bytes, int32_t* err, hipStream_t st) {
   if (g.d != kD) return host_fail(TTKV_E_UNSUPPORTED, "head dim must be 128");
   if (g.H > 8) return host_fail(TTKV_E_UNSUPPORTED, "H > 8 KV heads is not built");
-  if (g.qbits != 8) return host_fail(TTKV_E_UNSUPPORTED, "coefficient width must be 8 bits");
   if (g.r1 > 256) return host_fail(TTKV_E_UNSUPPORTED, "r1 > 256 is not built");
   if (g.res_k < 1) return host_fail(TTKV_E_UNSUPPORTED, "res_k must be >= 1");
   if (!((g.res_bits == 3 && g.v_bits == 3) || (g.res_bits == 4 && g.v_bits == 4)))
@@ -396,6 +451,9 @@ int write_paged(const Geom& g, const void* key, int k_dtype, int64_t k_row_strid
     return host_fail(TTKV_E_INVALID, "null pointer argument");
   if (!cq_in && !pinv_pool) return host_fail(TTKV_E_INVALID, "need pinv_pool or coeff_q_in");
   if (cq_in && !cs_in) return host_fail(TTKV_E_INVALID, "coeff_q_in needs coeff_scale_in");
+  if (cq_in && g.coef_mode != kCoefI8)
+    return host_fail(TTKV_E_INVALID, "coeff_q_in is int8: the fp16 and 4-bit coefficient modes "
+                                     "quantise the projection themselves (pass pinv_pool)");
   if (slot_stride < g.blob) return host_fail(TTKV_E_INVALID, "slot stride smaller than the blob");
   if (k_dtype < 0 || k_dtype > 2 || v_dtype < 0 || v_dtype > 2)
     return host_fail(TTKV_E_INVALID, "dtype code");
@@ -449,7 +507,7 @@ int write_paged(const Geom& g, const void* key, int k_dtype, int64_t k_row_strid
       b.ws_cnt = (int*)ws;
       b.ws_part = (float*)((char*)ws + kCounterBytes);
       b.ws_q = b.ws_part + (int64_t)b.num_tokens * g.H * g.r1;
-      b.ws_ds = (int*)(b.ws_q + (int64_t)b.num_tokens * (g.r1 + 1));
+      b.ws_ds = (int*)(b.ws_q + (int64_t)b.num_tokens * wq_stride(g));
     }
     const int grid = b.num_tokens * g.H;
     if (!cq_in) hipLaunchKernelGGL(write_project_kernel, dim3(grid), dim3(kWThreads), 0, st, b);

@@ -289,15 +289,18 @@ def fit_into_budget(K: torch.Tensor, lay: TTKLayout, cfg: dict) -> FittedK:
     if K.dtype not in (torch.float32, torch.float16, torch.bfloat16):
         raise TypeError(f"raw keys arrived as {K.dtype}")
     K = K.to(torch.float32)
-    qm = 2 ** (lay.qbits - 1) - 1
+    # The decoder is int8 x fp16 rank ruler in every coefficient mode (the pool's form); the
+    # coefficients below are the int8 mode's. The fp16 and 4-bit modes store the projection
+    # onto this decoder instead (the write kernel quantises it), so they take only the decoder.
+    qm = 127
     cores = _tt_factors(K.permute(1, 2, 0).contiguous(), cfg["tols"], lay.r1)  # [n, d, H]
     r1 = int(cores[0].shape[2])
     c = cores[0].reshape(n, r1)
     cs = _ruler(c.abs().amax(1, keepdim=True), qm)
     cs = torch.where(cs == 0, torch.ones_like(cs), cs)
     cq = torch.clamp(torch.round(c / cs), -(qm + 1), qm).to(torch.int8)
-    g2 = _quant_core(cores[1], lay.qbits)
-    g3 = _quant_core(cores[2], lay.qbits)
+    g2 = _quant_core(cores[1], 8)
+    g3 = _quant_core(cores[2], 8)
     dec = torch.einsum("ajb,bh->ahj", g2, g3[:, :, 0]).reshape(r1, H * d)
     rmax = dec.abs().amax(1, keepdim=True)
     sc = _ruler(torch.where(rmax == 0, torch.ones_like(rmax), rmax), qm)

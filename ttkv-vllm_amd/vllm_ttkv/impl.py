@@ -41,7 +41,7 @@ import torch
 
 from . import _hip, kernels
 from . import encode as enc
-from .layout import CONFIGS, TTKLayout
+from .layout import TTKLayout, config_named
 from .patch import take_raw_k
 from .rope_store import decoder_for_layer, ensure_store, layout_for_layer
 
@@ -299,7 +299,7 @@ class TTKVAttentionImpl(_ImplBase):
         # every key of the batch is live and must survive an eviction. A continuation whose key
         # has no decoder is refused on the device (error bit 1, NaN output rows).
         first = self._first_chunks(md, plan)
-        cfg = CONFIGS[os.environ.get("VLLM_TTKV_CONFIG", "safe")]
+        cfg = config_named(os.environ.get("VLLM_TTKV_CONFIG", "safe"))
         frozen, fitted = [], []
         keys = []
         if any(first):
@@ -332,9 +332,11 @@ class TTKVAttentionImpl(_ImplBase):
 
         if frozen:
             launch(frozen)
-        if fitted:
+        if fitted and lay.qbits == 8:
             launch([r for r, _ in fitted], torch.cat([fk.coeff_q for _, fk in fitted]),
                    torch.cat([fk.coeff_scale for _, fk in fitted]))
+        elif fitted:  # fp16 / 4-bit coefficients: the projection onto the new decoder
+            launch([r for r, _ in fitted])
 
     # ------------------------------------------------------------------ read
     def _first_chunks(self, md, plan) -> list:

@@ -176,6 +176,9 @@ def write_paged(lay: TTKLayout, key: torch.Tensor, value: torch.Tensor,
             raise ValueError("dec_used needs one flag per decoder pool slot")
     cq = None
     if coeff_q_in is not None:
+        if lay.qbits != 8:
+            raise ValueError("coeff_q_in is the int8 mode's; the fp16 and 4-bit coefficient "
+                             "modes quantise the projection themselves (pass pinv_pool)")
         cq = coeff_q_in.to(torch.int8).contiguous()
         if coeff_scale_in is None:
             raise ValueError("coeff_q_in needs coeff_scale_in (fp32)")

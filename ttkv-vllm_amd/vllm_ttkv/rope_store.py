@@ -36,7 +36,7 @@ import torch
 
 from .decoder_pool import empty_pool
 from .encode import KDecoder
-from .layout import CONFIGS, TTKLayout, layout_for_config
+from .layout import TTKLayout, config_named, layout_for_config
 
 CONFIG_ENV = "VLLM_TTKV_CONFIG"
 CAPACITY_ENV = "VLLM_TTKV_MAX_DECODERS"
@@ -68,7 +68,7 @@ def load_calibration(path, cfg_name: str = "safe", cfg: dict | None = None,
     the artifact's metadata. `layer_prefix` is accepted for signature compatibility; layers are
     matched by index (`_layer_index`)."""
     global _CALIBRATION
-    alloc = dict(cfg) if cfg is not None else dict(CONFIGS[cfg_name])
+    alloc = dict(cfg) if cfg is not None else dict(config_named(cfg_name))
     meta = json.loads(pathlib.Path(path).read_text())
     missing = [k for k in ("layers", "heads", "head_dim", "r1") if k not in meta]
     if missing:
