@@ -15,7 +15,7 @@ from oracle.rope import cos_sin_from_cache, rope_apply
 from vllm_ttkv import impl as impl_mod
 from vllm_ttkv import patch, rope_store, synth
 from vllm_ttkv.impl import TTKVAttentionImpl
-from vllm_ttkv.layout import CONFIGS, layout_for_config
+from vllm_ttkv.layout import CONFIGS, config_named, layout_for_config
 from vllm_ttkv.metadata import TTKVAttentionMetadata, TTKVAttentionMetadataBuilder
 from vllm_ttkv.rope import cos_sin_cache
 
@@ -94,9 +94,13 @@ def _sdpa_ref(q, k_post, v):
     return torch.einsum("hts,hsd->htd", torch.softmax(s, -1), vv).transpose(0, 1)
 
 
-def test_forward_write_then_read_loop_and_mixed_batch():
-    lay = layout_for_config(CONFIGS["safe"], 110)
-    olay = oracle_layout(CONFIGS["safe"], 110)
+@pytest.mark.parametrize("alloc", ["safe", "safe_fp16", "campaign4x_int4g32"])
+def test_forward_write_then_read_loop_and_mixed_batch(alloc, monkeypatch):
+    """Also in this library's fp16 and 4-bit coefficient modes (selected like an allocation,
+    by VLLM_TTKV_CONFIG), whose first chunks are written by projection onto the new decoder."""
+    monkeypatch.setenv("VLLM_TTKV_CONFIG", alloc)
+    lay = layout_for_config(config_named(alloc), 110)
+    olay = oracle_layout(config_named(alloc), 110)
     rope_store.clear_stores()
     csc = cos_sin_cache(4096)
     seqs = [_Seq(1100, 1), _Seq(1000, 2), _Seq(400, 3)]
