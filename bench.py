@@ -75,7 +75,7 @@ def build_store(torch, lay, cfg, lens, n_layers, seed, dev, fit_on=FIT_ON, disti
         page = torch.zeros(nblk * BS, C, dtype=torch.uint8, device=dev)
         dec_pool = empty_pool(B, lay.r1, H, D, dev)
         dec_f = torch.zeros(B, lay.r1, H * D, dtype=torch.float32, device=dev)  # CPU baselines
-        pinv_pool = torch.zeros(B, H * D, lay.r1, dtype=torch.float32, device=dev)
+        pinv_pool = torch.zeros(B, lay.r1, H * D, dtype=torch.float32, device=dev)
         first_k, first_v, first_cq, first_cs, first_slot, rest = [], [], [], [], [], []
         for r, n in enumerate(lens):
             s = seed * 1000003 + li * 1009 + r
@@ -87,7 +87,7 @@ def build_store(torch, lay, cfg, lens, n_layers, seed, dev, fit_on=FIT_ON, disti
             dec_f[r] = fk.decoder.decoder_f
             dec_pool.q[r].copy_(fk.decoder.packed.q)
             dec_pool.scale[r].copy_(fk.decoder.packed.scale)
-            pinv_pool[r] = fk.decoder.pinv
+            pinv_pool[r] = fk.decoder.pinv.t()
             torch.cuda.synchronize()
             t_fit += time.perf_counter() - t0
             Kt, Vt = K.permute(1, 0, 2), V.permute(1, 0, 2)
@@ -310,7 +310,7 @@ def cpu_k3_sample(torch, lay, k_new, v_new, dec_f, pinv_pool):
     torch.set_num_threads(os.cpu_count() or 1)
     K = k_new.float().cpu().permute(1, 0, 2).contiguous()                  # [H, B, d]
     V = v_new.float().cpu().permute(1, 0, 2).contiguous()
-    dec, pinv = dec_f.cpu(), pinv_pool.cpu()
+    dec, pinv = dec_f.cpu(), pinv_pool.cpu().transpose(1, 2)   # [B, H*d, r1]
     t0 = time.perf_counter()
     for r in range(K.shape[1]):
         ef = oenc.encode_frozen(K[:, r:r + 1].contiguous(), dec[r], olay, pinv[r])
@@ -370,7 +370,7 @@ def bench_first_chunk(torch, lay, cfg, dev, lengths=(2048, 8192), reps=5):
         # the decoder's registration (its pseudo-inverse, for the frozen projection of the
         # request's later tokens; rope_store.register)
         us_reg = timed(lambda: encode.KDecoder(fk[0].decoder.decoder_f).pinv)
-        pinv_pool = fk[0].decoder.pinv.unsqueeze(0).contiguous()
+        pinv_pool = fk[0].decoder.pinv.t().unsqueeze(0).contiguous()
         qsl = torch.tensor([0, T], dtype=torch.int32, device=dev)
         slots = torch.arange(T, dtype=torch.int64, device=dev)
         Kt = K.permute(1, 0, 2).contiguous()

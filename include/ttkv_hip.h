@@ -161,12 +161,14 @@ int ttkv_decode_paged_noalloc(const ttkv_layout* lay, int32_t num_heads, float s
  * slot_mapping entries < 0 are vLLM's PAD_SLOT_ID (padded tokens of a replayed graph): skipped
  *   silently, as vLLM's cache writers do; entries past the cache set TTKV_ERR_BAD_SLOT.
  * key/value: [N, H, d] rows with the given element stride between tokens. The decoder pool
- *   (dec_q, dec_scale) is laid out as for ttkv_decode_paged; pinv_pool [n_dec_slots, H*d, r1]
- *   fp32 holds each decoder's pseudo-inverse (encode.py:193-206).
- * Work is spread over (token, KV head) workgroups in two launches: per-head partial projections
- * (the token's last workgroup sums them in head order and quantises) and, per head, the residual
- * and the K and V rows. The partials and each token's decoder slot live in `workspace`
- * (ttkv_write_workspace_bytes). */
+ *   (dec_q, dec_scale) is laid out as for ttkv_decode_paged; pinv_pool [n_dec_slots, r1, H*d]
+ *   fp32 holds each decoder's pseudo-inverse (encode.py:193-206) transposed: row a is rank a's
+ *   projection vector (the reference's pinv is [H*d, r1]; rank-major rows let the projection read
+ *   whole rows).
+ * Work is spread over two launches: the projection, one workgroup per (token, 16 ranks), each
+ * rank's sum complete in its workgroup; then, per (token, KV head), the quantisation (every head
+ * alike), the residual and the K and V rows. The projection and each token's decoder slot live in
+ * `workspace` (ttkv_write_workspace_bytes). */
 int ttkv_write_paged(const ttkv_layout* lay, const void* key, int32_t k_dtype, int64_t k_row_stride,
                      const void* value, int32_t v_dtype, int64_t v_row_stride,
                      const int64_t* slot_mapping, int32_t num_tokens,

@@ -84,7 +84,7 @@ def device_store(cfg_name: str, lens, seed: int, r1: int = 110, block_size: int 
     from vllm_ttkv.decoder_pool import empty_pool
     dec_pool = empty_pool(B, r1, H, D, dev)
     dec_f = torch.zeros(B, r1, H * D, dtype=torch.float32, device=dev)
-    pinv_pool = torch.zeros(B, H * D, r1, dtype=torch.float32, device=dev)
+    pinv_pool = torch.zeros(B, r1, H * D, dtype=torch.float32, device=dev)
     dec_map = torch.full((nblk,), -1, dtype=torch.int32)
     for r in range(B):
         dec_map[bt[r, 0]] = r
@@ -100,7 +100,7 @@ def device_store(cfg_name: str, lens, seed: int, r1: int = 110, block_size: int 
         dec_f[r] = fk.decoder.decoder_f
         dec_pool.q[r].copy_(fk.decoder.packed.q)
         dec_pool.scale[r].copy_(fk.decoder.packed.scale)
-        pinv_pool[r] = fk.decoder.pinv
+        pinv_pool[r] = fk.decoder.pinv.t()
         p = torch.arange(n)
         slot = (bt[r, p // block_size].long() * block_size + p % block_size).to(dev)
         fk_all.append((K[:f], V[:f], slot[:f], fk.coeff_q, fk.coeff_scale))

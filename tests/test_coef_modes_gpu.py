@@ -56,8 +56,8 @@ def test_write_bytes_exact_from_kernel_projection(name):
                         torch.tensor([0, n], dtype=torch.int32, device=DEV),
                         torch.zeros(1, 1, dtype=torch.int32, device=DEV),
                         torch.zeros(1, dtype=torch.int32, device=DEV), dec_pool_of([dec], DEV),
-                        pinv.unsqueeze(0).to(DEV), page, coeff_out=c_out, resid_out=r_out,
-                        error_word=err)
+                        pinv.t().unsqueeze(0).contiguous().to(DEV), page, coeff_out=c_out,
+                        resid_out=r_out, error_word=err)
     torch.cuda.synchronize()
     assert int(err.item()) == 0
     page, c, R = page.cpu(), c_out.cpu(), r_out.cpu()

@@ -179,7 +179,7 @@ def test_config5_campaign4x_write_then_read():
     c, R = c_out.cpu(), r_out.cpu()
     # float stages at fp32 tolerance against each request's own decoder
     for r in range(B):
-        pinv = st["pinv_pool"][r].cpu()
+        pinv = st["pinv_pool"][r].cpu().t()
         c_ref = encode.project(Knew[:, r:r + 1].contiguous(), pinv)
         assert (c[r:r + 1] - c_ref).abs().max() <= 1e-4 * c_ref.abs().max() + 1e-7
     cq, cs = encode.quantise_coeffs(c)

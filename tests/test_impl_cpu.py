@@ -167,7 +167,7 @@ def test_decoder_registry_round_trip():
     s2 = st.register(7, d2)
     assert st.dec_map[3] == s1 and st.dec_map[7] == s2 and s1 != s2
     assert torch.equal(unpack_decoders(st.dec_pool.slot(s2), 16), d2.decoder_f)
-    assert torch.allclose(st.pinv_pool[s2], d2.pinv)
+    assert torch.allclose(st.pinv_pool[s2], d2.pinv.t())
     st.release(3)
     assert st.dec_map[3] == -1 and 3 not in st.decoders
     assert st.register(5, d1) == s1               # freed slot reused

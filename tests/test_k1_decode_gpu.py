@@ -129,7 +129,7 @@ def test_write_then_read_loop():
     dec_map = torch.full((nblk,), -1, dtype=torch.int32)
     dec_map[bt[0, 0]] = 0
     args = dict(block_table=bt.to(dev), dec_slot_of_block=dec_map.to(dev),
-                dec_pool=dec_pool_of([dec], dev), pinv_pool=encode.pinv(dec).unsqueeze(0).to(dev),
+                dec_pool=dec_pool_of([dec], dev), pinv_pool=encode.pinv(dec).t().unsqueeze(0).contiguous().to(dev),
                 page=page)
     Kt = K.permute(1, 0, 2).contiguous()
     Vt = V.permute(1, 0, 2).contiguous()

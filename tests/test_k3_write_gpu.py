@@ -42,7 +42,7 @@ def _run(lay, dec, pinv, Knew, V, slots, n_slots, v_dtype=torch.float32, cq_in=N
     kernels.write_paged(lay, Knew.permute(1, 0, 2).contiguous().to(DEV),
                         V.permute(1, 0, 2).contiguous().to(v_dtype).to(DEV),
                         slots.to(DEV), qsl, bt, dec_map, dec_pool_of([dec], DEV),
-                        pinv.unsqueeze(0).to(DEV), page,
+                        pinv.t().unsqueeze(0).contiguous().to(DEV), page,
                         coeff_q_in=None if cq_in is None else cq_in.to(DEV),
                         coeff_scale_in=None if cs_in is None else cs_in.to(DEV),
                         coeff_out=c_out, resid_out=r_out, error_word=err)
@@ -251,7 +251,7 @@ def test_workspace_shared_across_token_counts():
         err = torch.zeros(1, dtype=torch.int32, device=DEV)
         kernels.write_paged(lay, Kt[lo:hi], Vt[lo:hi], torch.arange(n, dtype=torch.int64, device=DEV),
                             torch.tensor([0, n], dtype=torch.int32, device=DEV), bt, dec_map,
-                            dec_pool_of([dec], DEV), pinv.unsqueeze(0).to(DEV), page,
+                            dec_pool_of([dec], DEV), pinv.t().unsqueeze(0).contiguous().to(DEV), page,
                             error_word=err, workspace=ws)
         torch.cuda.synchronize()
         assert int(err.item()) == 0
@@ -273,7 +273,7 @@ def test_write_flags_the_decoder_slots_it_uses():
     bt = torch.tensor([[3], [1]], dtype=torch.int32, device=DEV)   # request keys 3 and 1
     dec_map = torch.tensor([-1, 4, -1, 2, -1], dtype=torch.int32, device=DEV)
     pool = dec_pool_of([dec] * 6, DEV)
-    pinvs = pinv.unsqueeze(0).repeat(6, 1, 1).to(DEV)
+    pinvs = pinv.t().unsqueeze(0).repeat(6, 1, 1).contiguous().to(DEV)
     used = torch.zeros(6, dtype=torch.int32, device=DEV)
     err = torch.zeros(1, dtype=torch.int32, device=DEV)
     kernels.write_paged(lay, Knew.permute(1, 0, 2).contiguous().to(DEV),

@@ -1,12 +1,13 @@
 // K3: write/encode of new tokens into compressed slots, one launch for all tokens of a layer.
 // gfx950 / CDNA4.
 //
-// Two launches, each with one 256-thread workgroup per (token, KV head), so a decode batch of B
-// tokens spreads its 2 x B x 450 KB of pinv / decoder reads over B x H CUs:
-//   K3a project  partial c_h[a] = sum_j M[h*d+j] * pinv[h*d+j][a] per head; the last workgroup of
-//             the token sums the H partials in head order (fixed, deterministic), quantises, and
-//             leaves (cq, cs) in the workspace                    -- skipped when a fit gives them
-//   K3b pack     the rest, per (token, head):
+// Two launches of 256-thread workgroups, so a decode batch of B tokens spreads its B x 450 KB of
+// pinv and B x 113 KB of decoder reads over many CUs:
+//   K3a project  one workgroup per (token, slice of 16 ranks): c[a] for its ranks over all H*d
+//             dims, complete in the workgroup (wave sums, fixed order), left in the workspace
+//                                                                  -- skipped when a fit gives (cq, cs)
+//   K3b pack     one workgroup per (token, KV head): every head's workgroup quantises c alike,
+//             then the rest for its head:
 //   project   c[a] = sum_m M[m] * pinv[m][a], M = the token's raw key flattened m = h*d + j
 //             (encode.py:322-324), fp32 in a fixed order          -- or take (cq, cs) from a fit
 //   quantise  cs = max|c| * fp32(1/127) (1 if 0); cq = clamp(rint(c / cs), -128, 127)
@@ -61,11 +62,7 @@ struct WriteArgs {
   float* r_out;
   int* err;
   int tok0;         // first token of this launch (tokens tok0 .. tok0 + num_tokens - 1)
-  int* ws_cnt;      // [num_tokens] arrival counters (zero between calls)
-  float* ws_part;   // [num_tokens][H][r1] per-head partial projections
-  float* ws_q;      // [num_tokens][wq_stride]: cq (as floats; the coefficient value itself in
-                    // the fp16 and 4-bit modes), cs (1 in those modes), then the 4-bit mode's
-                    // group scales
+  float* ws_c;      // [num_tokens][r1] each token's projection c, from K3a for K3b
   int* ws_ds;       // [num_tokens] each token's decoder slot (or -1), from K3a for K3b
   float inv127, inv_rk, inv_rv;
 };
@@ -173,9 +170,6 @@ __device__ void pack_row(float x0, float x1, int k, float inv_ruler, uint8_t* ds
   }
 }
 
-// Floats per token in ws_q: r1 coefficients, the ruler, up to 8 group scales (r1 <= 256).
-__host__ __device__ inline int wq_stride(const Geom& g) { return g.r1 + 9; }
-
 // Scale of a 4-bit coefficient group whose largest magnitude is m: m / 7 (IEEE) rounded up to 8
 // significant bits, then held within [2^-14, 9344], so that every q * scale (|q| <= 7) is an
 // exact fp16 normal; 0 for an all-zero group.
@@ -186,103 +180,76 @@ __device__ inline float coef_group_scale(float m) {
   return fminf(fmaxf(__builtin_bit_cast(float, u), 0x1p-14f), 9344.f);
 }
 
-// K3a: per-head partial projections; the token's last workgroup combines and quantises.
+// K3a: the projection c = M_i . pinv of token i, one workgroup per (token, slice of 16 ranks).
+// The pool holds each decoder's pseudo-inverse by rank (pinv_pool [slot][r1][H*d], row a = rank
+// a's projection vector), so wave w reads whole rows: ranks a0 + 4w .. a0 + 4w + 3, each lane 16
+// of the H*d dims (four 16-byte loads per rank, 1 KB per wave instruction). The wave sums each
+// rank over its lanes with an xor butterfly, so every rank's sum is complete inside one workgroup
+// and nothing is handed between workgroups; K3b quantises.
+constexpr int kSliceRanks = 16;
+
+__host__ __device__ inline int project_slices(const Geom& g) {
+  return (g.r1 + kSliceRanks - 1) / kSliceRanks;
+}
+
 __global__ __launch_bounds__(kWThreads) void write_project_kernel(WriteArgs a) {
-  __shared__ float mk[kD];
-  __shared__ float part[2][256];
-  __shared__ float red[kWThreads / 64];
-  __shared__ int is_last;
   const Geom& g = a.g;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int il = blockIdx.x / g.H;  // token within this launch: its workspace rows
+  const int ns = project_slices(g);
+  const int il = blockIdx.x / ns;  // token within this launch: its workspace row
   const int i = a.tok0 + il;
-  const int h = blockIdx.x % g.H;
+  const int sl = blockIdx.x % ns;
   const int HD = g.H * kD;
   const int64_t slot = a.slot_mapping[i];
-  // the key does not depend on the decoder lookup: its load overlaps the lookup's round trips
-  const float kv = tid < kD ? load_act(a.key, a.k_dtype, (int64_t)i * a.k_row_stride + h * kD + tid)
-                            : 0.f;
+  // this lane's key dims 256j + 4 lane .. + 3, requested before the decoder lookup's round trips
+  const int64_t kb = (int64_t)i * a.k_row_stride;
+  const bool kvec = act_rows_aligned(a.key, a.k_dtype, a.k_row_stride);
+  float kx[4][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int d0 = 256 * j + 4 * lane;
+    if (d0 < HD) {
+      load_act_n<4>(a.key, a.k_dtype, kb + d0, kvec, kx[j]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) kx[j][e] = 0.f;
+    }
+  }
   const int ds = token_decoder(a, i);
-  if (h == 0 && tid == 0) a.ws_ds[il] = ds;
+  if (sl == 0 && tid == 0) a.ws_ds[il] = ds;
   if (ds < 0 || slot < 0 || slot >= a.n_slots) return;  // K3b reports it
-  if (tid < kD) mk[tid] = kv;
-  __syncthreads();
-  const float* pinv = a.pinv_pool + (int64_t)ds * HD * g.r1 + (int64_t)h * kD * g.r1;
-  float* pp = a.ws_part + ((int64_t)il * g.H + h) * g.r1;
-  const int half = tid >> 7, ar = tid & 127;
-  for (int a0 = 0; a0 < g.r1; a0 += 128) {
-    const int aa = a0 + ar;
-    float acc = 0.f;
-    if (aa < g.r1) {
-      // all 64 loads issued before the dependent sum (one memory round trip)
-      float pv[64];
+  const int a0 = sl * kSliceRanks + 4 * wv;
+  if (a0 >= g.r1) return;
+  const float* prow = a.pinv_pool + (int64_t)ds * g.r1 * HD;
+  float4v pv[4][4];
 #pragma unroll
-      for (int j = 0; j < 64; ++j) pv[j] = pinv[(int64_t)(64 * half + j) * g.r1 + aa];
+  for (int r = 0; r < 4; ++r)
 #pragma unroll
-      for (int j = 0; j < 64; ++j) acc = fmaf(mk[64 * half + j], pv[j], acc);
+    for (int j = 0; j < 4; ++j) {
+      const int d0 = 256 * j + 4 * lane;
+      pv[r][j] = (a0 + r < g.r1 && d0 < HD)
+                     ? *gbl((const float4v*)(prow + (int64_t)(a0 + r) * HD + d0))
+                     : float4v{0.f, 0.f, 0.f, 0.f};
     }
-    part[half][ar] = acc;
-    __syncthreads();
-    if (half == 0 && aa < g.r1)
-      __hip_atomic_store(&pp[aa], part[0][ar] + part[1][ar], __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
+  float acc[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    acc[r] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[r] = fmaf(kx[j][e], pv[r][j][e], acc[r]);
   }
-  // Hand-off to the token's last workgroup: the partials above are agent-scope (write-through)
-  // stores, completed (vmcnt) and ordered before the counter update by the barrier; the counter
-  // update is relaxed, and the last workgroup reads the other heads' partials with agent-scope
-  // loads (no cache-wide writeback or invalidate on either side).
-  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (tid == 0)
-    is_last = arrive(&a.ws_cnt[il]) == g.H - 1;
-  __syncthreads();
-  if (!is_last) return;
-
-  // c[a] = sum over heads in head order
-  float* cq = a.ws_q + (int64_t)il * wq_stride(g);
-  float mx = 0.f;
-  float cv = 0.f;
-  const bool mine = tid < g.r1;
-  if (mine) {
-    // every head's partial requested in one round trip (H <= 8, host-checked), then summed in
-    // head order
-    const float* base = a.ws_part + (int64_t)il * g.H * g.r1;
-    float ph[8];
+  // butterfly: the same tree in every lane (operands only commuted), so every lane holds the sum
 #pragma unroll
-    for (int hh = 0; hh < 8; ++hh) {
-      const float x = ld_agent(&base[min(hh, g.H - 1) * g.r1 + tid]);
-      ph[hh] = hh < g.H ? x : 0.f;
-    }
+  for (int o = 32; o > 0; o >>= 1)
 #pragma unroll
-    for (int hh = 0; hh < 8; ++hh) cv += ph[hh];
-    mx = fabsf(cv);
-    if (a.c_out) a.c_out[(int64_t)i * g.r1 + tid] = cv;
+    for (int r = 0; r < 4; ++r) acc[r] += __shfl_xor(acc[r], o);
+  if (lane < 4 && a0 + lane < g.r1) {
+    const float c = lane == 0 ? acc[0] : lane == 1 ? acc[1] : lane == 2 ? acc[2] : acc[3];
+    a.ws_c[(int64_t)il * g.r1 + a0 + lane] = c;
+    if (a.c_out) a.c_out[(int64_t)i * g.r1 + a0 + lane] = c;
   }
-  if (g.coef_mode == kCoefI8) {  // workgroup-uniform
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    if (lane == 0) red[wv] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    float cs = mx * a.inv127;
-    if (cs == 0.f) cs = 1.f;
-    if (mine) cq[tid] = fminf(fmaxf(rintf(__fdiv_rn(cv, cs)), -128.f), 127.f);
-    if (tid == 0) cq[g.r1] = cs;
-  } else if (g.coef_mode == kCoefF16) {
-    if (mine) cq[tid] = (float)(_Float16)cv;  // round to nearest even
-    if (tid == 0) cq[g.r1] = 1.f;
-  } else {
-    // group k = ranks 32k .. 32k+31 = threads 32k .. 32k+31 (half a wave)
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    const float sc = coef_group_scale(mx);
-    if (mine)
-      cq[tid] = sc > 0.f ? fminf(fmaxf(rintf(__fdiv_rn(cv, sc)), -7.f), 7.f) * sc : 0.f;
-    if (mine && (tid & 31) == 0) cq[g.r1 + 1 + (tid >> 5)] = sc;
-    if (tid == 0) cq[g.r1] = 1.f;
-  }
-  if (tid == 0) __hip_atomic_store(&a.ws_cnt[il], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // K3b: residual of head h, then its K row and V row; head 0 also writes the coefficients.
@@ -292,6 +259,7 @@ __global__ __launch_bounds__(kWThreads) void write_pack_kernel(WriteArgs a) {
   __shared__ __align__(16) float rul[256];  // decoder rank rulers (0 past r1)
   __shared__ float rp[kD];    // sum_a cqs[a] * dec[a][h*d + j]
   __shared__ uint8_t codes[2][kD];
+  __shared__ float gsc[8];  // 4-bit mode: group scales
   const Geom& g = a.g;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int il = blockIdx.x / g.H;  // token within this launch: its workspace rows
@@ -316,11 +284,19 @@ __global__ __launch_bounds__(kWThreads) void write_pack_kernel(WriteArgs a) {
     xr1 = load_act(a.val, a.v_dtype, vb + 64 + lane);
   }
   // the decoder slot: from K3a's lookup when it ran (one load), else looked up here; the
-  // coefficients (K3a's or the fit's) are requested in the same round trip
+  // coefficients (K3a's projection or the fit's quantised ones) in the same round trip
   const int ds = a.cq_in ? token_decoder(a, i) : a.ws_ds[il];
-  const float* wq = a.ws_q + (int64_t)il * wq_stride(g);
-  const float cs = a.cq_in ? a.cs_in[i] : wq[g.r1];
-  const float qv = tid < g.r1 ? (a.cq_in ? (float)a.cq_in[(int64_t)i * g.r1 + tid] : wq[tid]) : 0.f;
+  // K3a's projection: lane l loads ranks l, l + 64, l + 128, l + 192, so that every wave sees all
+  // of them (the int8 ruler's max needs no barrier); thread t's own rank t is among them
+  float cw[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int r = lane + 64 * k;
+    cw[k] = (!a.cq_in && r < g.r1) ? a.ws_c[(int64_t)il * g.r1 + r] : 0.f;
+  }
+  const float cv = wv == 0 ? cw[0] : wv == 1 ? cw[1] : wv == 2 ? cw[2] : cw[3];
+  float cs = a.cq_in ? a.cs_in[i] : 1.f;
+  float qv = (a.cq_in && tid < g.r1) ? (float)a.cq_in[(int64_t)i * g.r1 + tid] : 0.f;
   if (h == 0 && tid == 0) {
     if (!slot_ok) atomicOr(a.err, TTKV_ERR_BAD_SLOT);
     if (ds < 0) atomicOr(a.err, TTKV_ERR_NO_DECODER);
@@ -344,6 +320,26 @@ __global__ __launch_bounds__(kWThreads) void write_pack_kernel(WriteArgs a) {
     }
   };
   load_ranks(0);
+  if (!a.cq_in) {
+    // Quantise the projection (every head's workgroup alike, so all agree): thread t holds rank t
+    if (g.coef_mode == kCoefI8) {  // cs = max|c| * fp32(1/127), cq = clamp(rint(c / cs))
+      float mx = fmaxf(fmaxf(fabsf(cw[0]), fabsf(cw[1])), fmaxf(fabsf(cw[2]), fabsf(cw[3])));
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+      cs = mx * a.inv127;
+      if (cs == 0.f) cs = 1.f;
+      if (tid < g.r1) qv = fminf(fmaxf(rintf(__fdiv_rn(cv, cs)), -128.f), 127.f);
+    } else if (g.coef_mode == kCoefF16) {
+      qv = (float)(_Float16)cv;  // round to nearest even
+    } else {  // group k = ranks 32k .. 32k+31 = threads 32k .. 32k+31 (half a wave)
+      float gm = fabsf(cv);
+#pragma unroll
+      for (int o = 16; o > 0; o >>= 1) gm = fmaxf(gm, __shfl_xor(gm, o));
+      const float sc = coef_group_scale(gm);
+      if (tid < g.r1) qv = sc > 0.f ? fminf(fmaxf(rintf(__fdiv_rn(cv, sc)), -7.f), 7.f) * sc : 0.f;
+      if ((tid & 31) == 0 && tid < g.r1) gsc[tid >> 5] = sc;
+    }
+  }
   if (tid < R) {
     rul[tid] = tid < g.r1 ? a.dec_scale[(int64_t)ds * R + tid] : 0.f;
     cqs[tid] = qv * cs;  // qv = 0 past r1
@@ -363,15 +359,16 @@ __global__ __launch_bounds__(kWThreads) void write_pack_kernel(WriteArgs a) {
         base[2 * tid] = (uint8_t)(hb & 0xff);
         base[2 * tid + 1] = (uint8_t)(hb >> 8);
       }
-    } else if (tid < g.coef_groups) {  // 4-bit: the group scales (exact in fp16)
-      const uint16_t hb = __builtin_bit_cast(uint16_t, (_Float16)wq[g.r1 + 1 + tid]);
-      base[g.coeff_bytes + 2 * tid] = (uint8_t)(hb & 0xff);
-      base[g.coeff_bytes + 2 * tid + 1] = (uint8_t)(hb >> 8);
     }
     for (int b = g.k_field + g.H * g.k_row + tid; b < g.k_slot; b += kWThreads) base[b] = 0;
     for (int b = g.k_slot + g.H * g.v_row + tid; b < g.blob; b += kWThreads) base[b] = 0;
   }
   __syncthreads();
+  if (g.coef_mode == kCoefI4G32 && h == 0 && tid < g.coef_groups) {  // the group scales (exact)
+    const uint16_t hb = __builtin_bit_cast(uint16_t, (_Float16)gsc[tid]);
+    base[g.coeff_bytes + 2 * tid] = (uint8_t)(hb & 0xff);
+    base[g.coeff_bytes + 2 * tid + 1] = (uint8_t)(hb >> 8);
+  }
   if (g.coef_mode == kCoefI4G32 && h == 0 && tid < g.coeff_bytes) {
     // byte b of word w = b / 4 holds the nibbles of ranks lo (bits 0-3) and lo + 2 (bits 4-7):
     // lo = 8w + 4j for byte j < 2 of the word, 8w + 4j - 7 for j >= 2; q = value / scale exactly
@@ -382,7 +379,7 @@ __global__ __launch_bounds__(kWThreads) void write_pack_kernel(WriteArgs a) {
     for (int e = 0; e < 2; ++e) {
       const int r = lo + 2 * e;
       if (r < g.r1) {
-        const float sc = wq[g.r1 + 1 + (r >> 5)];
+        const float sc = gsc[r >> 5];
         const int q = sc > 0.f ? (int)rintf(__fdiv_rn(cqs[r], sc)) : 0;
         byte |= ((uint32_t)q & 15u) << (4 * e);
       }
@@ -430,7 +427,7 @@ static float inv_ruler_f32(int bits) { return (float)(1.0 / (double)((1 << (bits
 // Tokens per launch: one arrival counter each.
 int64_t write_workspace_bytes(const Geom& g, int num_tokens) {
   const int64_t nt = std::min(std::max(num_tokens, 0), kMaxCounters);
-  return kCounterBytes + nt * (g.H * g.r1 + wq_stride(g) + 1) * 4;
+  return kCounterBytes + nt * (g.r1 + 1) * 4;
 }
 
 int write_paged(const Geom& g, const void* key, int k_dtype, int64_t k_row_stride, const void* val,
@@ -504,13 +501,13 @@ int write_paged(const Geom& g, const void* key, int k_dtype, int64_t k_row_strid
     b.tok0 = t0;
     b.num_tokens = std::min(kMaxCounters, num_tokens - t0);
     if (!cq_in) {
-      b.ws_cnt = (int*)ws;
-      b.ws_part = (float*)((char*)ws + kCounterBytes);
-      b.ws_q = b.ws_part + (int64_t)b.num_tokens * g.H * g.r1;
-      b.ws_ds = (int*)(b.ws_q + (int64_t)b.num_tokens * wq_stride(g));
+      b.ws_c = (float*)((char*)ws + kCounterBytes);
+      b.ws_ds = (int*)(b.ws_c + (int64_t)b.num_tokens * g.r1);
     }
     const int grid = b.num_tokens * g.H;
-    if (!cq_in) hipLaunchKernelGGL(write_project_kernel, dim3(grid), dim3(kWThreads), 0, st, b);
+    if (!cq_in)
+      hipLaunchKernelGGL(write_project_kernel, dim3(b.num_tokens * project_slices(g)),
+                         dim3(kWThreads), 0, st, b);
     if (g.res_bits == 3)
       hipLaunchKernelGGL((write_pack_kernel<3, 3>), dim3(grid), dim3(kWThreads), 0, st, b);
     else

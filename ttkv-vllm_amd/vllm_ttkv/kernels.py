@@ -144,7 +144,8 @@ def write_paged(lay: TTKLayout, key: torch.Tensor, value: torch.Tensor,
                 dec_used: torch.Tensor | None = None) -> None:
     """K3: encode + pack `key`/`value` ([N, H, d], raw pre-RoPE keys) into their slots.
 
-    See `ttkv_write_paged` in include/ttkv_hip.h. `pinv_pool` [slots, H*d, r1] fp32 drives the
+    See `ttkv_write_paged` in include/ttkv_hip.h. `pinv_pool` [slots, r1, H*d] fp32 (each decoder's pinv transposed: row a
+    is rank a's projection vector) drives the
     frozen projection; `coeff_q_in`/`coeff_scale_in` replace it with a fit's coefficients.
     `dec_used` ([slots] int32, optional) receives 1 for every decoder slot a token used."""
     _need_device(key, value, slot_mapping, query_start_loc, block_table, dec_slot_of_block,
@@ -165,8 +166,8 @@ def write_paged(lay: TTKLayout, key: torch.Tensor, value: torch.Tensor,
     _i32(dec_slot_of_block, "dec_slot_of_block")
     dq, ds, n_dec = pool_args(lay, dec_pool)
     if pinv_pool is not None and (pinv_pool.dtype != torch.float32 or
-                                  tuple(pinv_pool.shape[1:]) != (lay.H * lay.d, lay.r1)):
-        raise ValueError("pinv_pool must be fp32 [slots, H*d, r1]")
+                                  tuple(pinv_pool.shape[1:]) != (lay.r1, lay.H * lay.d)):
+        raise ValueError("pinv_pool must be fp32 [slots, r1, H*d] (each pinv transposed)")
     flat = page_bytes(page, lay.compressed_bytes_per_token())
     if error_word is None:
         error_word = torch.zeros(1, dtype=torch.int32, device=key.device)

@@ -9,7 +9,8 @@ layout)` and `ensure_store(layer_name, cos_sin_cache, num_heads, num_kv_heads, h
 
 What is different underneath: a registered decoder is copied into its layer's DEVICE pool
 (`dec_pool`: the codec's int8 decoder with its per-rank rulers, `q [capacity, H*d, R]` int8 +
-`scale [capacity, R]` fp32, see `decoder_pool`; `pinv_pool [capacity, H*d, r1]` fp32) and the
+`scale [capacity, R]` fp32, see `decoder_pool`; `pinv_pool [capacity, r1, H*d]` fp32: each decoder's pseudo-inverse by rank, the layout the
+write's projection reads in whole rows) and the
 request key -> pool slot map is a device array (`dec_map [num_blocks]`, -1 = none), keyed by
 `block_table[r, 0]`
 as in the reference (rope_store.py:148-163). The decode, continuation and write kernels resolve a
@@ -159,7 +160,7 @@ class TTKVRopeStore:
         H, d, r1 = layout.H, layout.d, layout.r1
         self.capacity = cap
         self.dec_pool = empty_pool(cap, r1, H, d, dev)
-        self.pinv_pool = torch.zeros(cap, H * d, r1, dtype=torch.float32, device=dev)
+        self.pinv_pool = torch.zeros(cap, r1, H * d, dtype=torch.float32, device=dev)
         self.dec_map: torch.Tensor | None = None
         self.decoders: "OrderedDict[int, KDecoder]" = OrderedDict()  # key -> decoder, oldest first
         self._slot_of: dict[int, int] = {}
@@ -244,7 +245,7 @@ class TTKVRopeStore:
             self._slot_of[key] = slot
         self.dec_pool.q[slot].copy_(packed.q)
         self.dec_pool.scale[slot].copy_(packed.scale)
-        self.pinv_pool[slot].copy_(pinv)
+        self.pinv_pool[slot].copy_(pinv.t())
         if self.dec_map is not None:
             self.dec_map[key] = slot
         self.decoders.pop(key, None)
