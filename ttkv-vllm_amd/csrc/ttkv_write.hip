@@ -267,12 +267,9 @@ __global__ __launch_bounds__(kWThreads) void write_pack_kernel(WriteArgs a) {
   const int h = blockIdx.x % g.H;
   const int HD = g.H * kD;
   const int64_t slot = a.slot_mapping[i];
-  // A negative slot id is vLLM's PAD_SLOT_ID (the padded tokens of a replayed graph): nothing
-  // is written and nothing is refused, as vLLM's own cache writers skip them. Ids past the
-  // cache are refused.
-  if (slot < 0) return;
-  const bool slot_ok = slot < a.n_slots;
-  // the rows wave 0 (key) and wave 1 (value) pack, requested now: they depend on nothing
+  // Everything up to the decoder lookup depends only on the token index, so it is requested in
+  // the same round trip as the slot id (before the PAD test below, which would otherwise wait
+  // for the slot id first). The rows wave 0 (key) and wave 1 (value) pack:
   float xr0 = 0.f, xr1 = 0.f;
   if (wv == 0) {
     const int64_t kb = (int64_t)i * a.k_row_stride + h * kD;
@@ -283,9 +280,8 @@ __global__ __launch_bounds__(kWThreads) void write_pack_kernel(WriteArgs a) {
     xr0 = load_act(a.val, a.v_dtype, vb + lane);
     xr1 = load_act(a.val, a.v_dtype, vb + 64 + lane);
   }
-  // the decoder slot: from K3a's lookup when it ran (one load), else looked up here; the
-  // coefficients (K3a's projection or the fit's quantised ones) in the same round trip
-  const int ds = a.cq_in ? token_decoder(a, i) : a.ws_ds[il];
+  // the decoder slot from K3a's lookup when it ran; K3a's projection or the fit's coefficients
+  const int ds_k3a = a.cq_in ? -1 : a.ws_ds[il];
   // K3a's projection: lane l loads ranks l, l + 64, l + 128, l + 192, so that every wave sees all
   // of them (the int8 ruler's max needs no barrier); thread t's own rank t is among them
   float cw[4];
@@ -297,6 +293,12 @@ __global__ __launch_bounds__(kWThreads) void write_pack_kernel(WriteArgs a) {
   const float cv = wv == 0 ? cw[0] : wv == 1 ? cw[1] : wv == 2 ? cw[2] : cw[3];
   float cs = a.cq_in ? a.cs_in[i] : 1.f;
   float qv = (a.cq_in && tid < g.r1) ? (float)a.cq_in[(int64_t)i * g.r1 + tid] : 0.f;
+  // A negative slot id is vLLM's PAD_SLOT_ID (the padded tokens of a replayed graph): nothing
+  // is written and nothing is refused, as vLLM's own cache writers skip them. Ids past the
+  // cache are refused.
+  if (slot < 0) return;
+  const bool slot_ok = slot < a.n_slots;
+  const int ds = a.cq_in ? token_decoder(a, i) : ds_k3a;
   if (h == 0 && tid == 0) {
     if (!slot_ok) atomicOr(a.err, TTKV_ERR_BAD_SLOT);
     if (ds < 0) atomicOr(a.err, TTKV_ERR_NO_DECODER);
