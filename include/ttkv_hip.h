@@ -165,7 +165,7 @@ int ttkv_decode_paged_noalloc(const ttkv_layout* lay, int32_t num_heads, float s
  *   fp32 holds each decoder's pseudo-inverse (encode.py:193-206) transposed: row a is rank a's
  *   projection vector (the reference's pinv is [H*d, r1]; rank-major rows let the projection read
  *   whole rows).
- * Work is spread over two launches: the projection, one workgroup per (token, 16 ranks), each
+ * Work is spread over two launches: the projection, one workgroup per (token, 4 ranks), each
  * rank's sum complete in its workgroup; then, per (token, KV head), the quantisation (every head
  * alike), the residual and the K and V rows. The projection and each token's decoder slot live in
  * `workspace` (ttkv_write_workspace_bytes). */

@@ -3,7 +3,7 @@
 //
 // Two launches of 256-thread workgroups, so a decode batch of B tokens spreads its B x 450 KB of
 // pinv and B x 113 KB of decoder reads over many CUs:
-//   K3a project  one workgroup per (token, slice of 16 ranks): c[a] for its ranks over all H*d
+//   K3a project  one workgroup per (token, 4 ranks): c[a] for its ranks over all H*d
 //             dims, complete in the workgroup (wave sums, fixed order), left in the workspace
 //                                                                  -- skipped when a fit gives (cq, cs)
 //   K3b pack     one workgroup per (token, KV head): every head's workgroup quantises c alike,
@@ -180,13 +180,16 @@ __device__ inline float coef_group_scale(float m) {
   return fminf(fmaxf(__builtin_bit_cast(float, u), 0x1p-14f), 9344.f);
 }
 
-// K3a: the projection c = M_i . pinv of token i, one workgroup per (token, slice of 16 ranks).
-// The pool holds each decoder's pseudo-inverse by rank (pinv_pool [slot][r1][H*d], row a = rank
-// a's projection vector), so wave w reads whole rows: ranks a0 + 4w .. a0 + 4w + 3, each lane 16
-// of the H*d dims (four 16-byte loads per rank, 1 KB per wave instruction). The wave sums each
+// K3a: the projection c = M_i . pinv of token i, one workgroup per (token, slice of kSliceRanks
+// ranks). The pool holds each decoder's pseudo-inverse by rank (pinv_pool [slot][r1][H*d], row a
+// = rank a's projection vector), so each wave reads whole rows: kWaveRanks ranks from a0 +
+// kWaveRanks * w, each lane 16 of the H*d dims (four 16-byte loads per rank, 1 KB per wave
+// instruction). Slices of 16 / 8 / 4 ranks measured 4.8 / 4.7 / 4.6 us per 8-token launch (more,
+// smaller workgroups spread the pinv reads over more CUs). The wave sums each
 // rank over its lanes with an xor butterfly, so every rank's sum is complete inside one workgroup
 // and nothing is handed between workgroups; K3b quantises.
-constexpr int kSliceRanks = 16;
+constexpr int kSliceRanks = 4;
+constexpr int kWaveRanks = kSliceRanks / 4;  // ranks per wave
 
 __host__ __device__ inline int project_slices(const Geom& g) {
   return (g.r1 + kSliceRanks - 1) / kSliceRanks;
@@ -218,12 +221,12 @@ __global__ __launch_bounds__(kWThreads) void write_project_kernel(WriteArgs a) {
   const int ds = token_decoder(a, i);
   if (sl == 0 && tid == 0) a.ws_ds[il] = ds;
   if (ds < 0 || slot < 0 || slot >= a.n_slots) return;  // K3b reports it
-  const int a0 = sl * kSliceRanks + 4 * wv;
+  const int a0 = sl * kSliceRanks + kWaveRanks * wv;
   if (a0 >= g.r1) return;
   const float* prow = a.pinv_pool + (int64_t)ds * g.r1 * HD;
-  float4v pv[4][4];
+  float4v pv[kWaveRanks][4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
+  for (int r = 0; r < kWaveRanks; ++r)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int d0 = 256 * j + 4 * lane;
@@ -231,9 +234,9 @@ __global__ __launch_bounds__(kWThreads) void write_project_kernel(WriteArgs a) {
                      ? *gbl((const float4v*)(prow + (int64_t)(a0 + r) * HD + d0))
                      : float4v{0.f, 0.f, 0.f, 0.f};
     }
-  float acc[4];
+  float acc[kWaveRanks];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
+  for (int r = 0; r < kWaveRanks; ++r) {
     acc[r] = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
@@ -244,9 +247,11 @@ __global__ __launch_bounds__(kWThreads) void write_project_kernel(WriteArgs a) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) acc[r] += __shfl_xor(acc[r], o);
-  if (lane < 4 && a0 + lane < g.r1) {
-    const float c = lane == 0 ? acc[0] : lane == 1 ? acc[1] : lane == 2 ? acc[2] : acc[3];
+    for (int r = 0; r < kWaveRanks; ++r) acc[r] += __shfl_xor(acc[r], o);
+  if (lane < kWaveRanks && a0 + lane < g.r1) {
+    float c = acc[0];
+#pragma unroll
+    for (int r = 1; r < kWaveRanks; ++r) c = lane == r ? acc[r] : c;
     a.ws_c[(int64_t)il * g.r1 + a0 + lane] = c;
     if (a.c_out) a.c_out[(int64_t)i * g.r1 + a0 + lane] = c;
   }
