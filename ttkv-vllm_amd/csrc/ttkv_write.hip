@@ -431,7 +431,9 @@ __global__ __launch_bounds__(kWThreads) void write_pack_kernel(WriteArgs a) {
 
 static float inv_ruler_f32(int bits) { return (float)(1.0 / (double)((1 << (bits - 1)) - 1)); }
 
-// Tokens per launch: one arrival counter each.
+// Workspace: the shared 64 KiB counter region (unused here; kept so that one buffer can serve
+// every entry point), then per token of a launch its projection (r1 floats) and decoder slot.
+// Launches take at most kMaxCounters tokens each.
 int64_t write_workspace_bytes(const Geom& g, int num_tokens) {
   const int64_t nt = std::min(std::max(num_tokens, 0), kMaxCounters);
   return kCounterBytes + nt * (g.r1 + 1) * 4;

@@ -236,7 +236,7 @@ def pack_k_slots(lay: TTKLayout, coeff_q: torch.Tensor, coeff_scale, resid) -> t
     elif lay.qbits == 16:
         out[:, :cb] = coeff_q.contiguous().view(torch.uint8)
     else:
-        if int(coeff_q.abs().amax()) > 7 if coeff_q.numel() else False:
+        if coeff_q.numel() and int(coeff_q.abs().amax()) > 7:
             raise ValueError("4-bit coefficients lie in [-7, 7]")
         if tuple(coeff_scale.shape) != (n, lay.coef_groups):
             raise ValueError(f"coeff_scale must be [{n}, {lay.coef_groups}] group scales")
