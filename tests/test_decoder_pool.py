@@ -111,3 +111,23 @@ def test_empty_pool_shapes():
     assert p.q.shape == (3, 1024, 128) and p.scale.shape == (3, 128)
     assert not bool(p.q.any()) and not bool(p.scale.any())
     assert p.slot(1).q.shape == (1024, 128)
+
+
+@pytest.mark.gpu
+def test_device_packing_matches_the_host():
+    """Packing on the device gives the host's pool, rows whose largest |q| is not 127 included
+    (the search works in float64: fp32 division on the device need not round correctly, and a
+    row of largest |q| 126 was refused once for that)."""
+    g = torch.Generator().manual_seed(5)
+    q = torch.randint(-127, 128, (110, 512), generator=g).float()
+    q[:, 0] = 126.0
+    q[:40].clamp_(-126, 126)
+    q[40:60].clamp_(-100, 100)
+    q[60:70] = q[60:70].clamp(-128, 127)
+    q[60:70, 1] = -128.0
+    ruler = (torch.rand(110, generator=g) * 0.02 + 0.005).half().float()
+    dec = q * ruler[:, None]
+    host = pack_decoders(dec)
+    dev = pack_decoders(dec.cuda())
+    assert torch.equal(dev.q.cpu(), host.q) and torch.equal(dev.scale.cpu(), host.scale)
+    assert torch.equal(unpack_decoders(dev, 110).cpu(), dec)

@@ -284,3 +284,47 @@ def test_write_flags_the_decoder_slots_it_uses():
     torch.cuda.synchronize()
     assert int(err.item()) == 0
     assert used.cpu().tolist() == [0, 0, 1, 0, 1, 0]
+
+
+@pytest.mark.parametrize("Hk,r1", [(4, 110), (2, 40), (8, 7)])
+def test_write_fewer_kv_heads_and_ranks(Hk, r1):
+    """K3 at other shapes than the serving ones: 4 or 2 KV heads (the projection reads H*d = 512
+    or 256 dims per rank row, so lanes past them stay idle) and a rank budget below one 4-rank
+    slice per wave; bytes exact from the kernel's own c and R, every other slot untouched."""
+    from oracle.layout import Layout
+    lay = Layout(H=Hk, d=D, r1=r1, qbits=8, res_k=81, res_bits=3, v_lanes=81, v_bits=3)
+    g = torch.Generator().manual_seed(100 + Hk + r1)
+    q = torch.randint(-127, 128, (r1, Hk * D), generator=g).float()
+    dec = q * ((torch.rand(r1, generator=g) * 0.02 + 0.005).half().float())[:, None]
+    pinv = encode.pinv(dec)
+    Knew = synth.keys(7, H=Hk, seed=r1)
+    V = synth.values(7, H=Hk, seed=r1 + 1) * 0.3
+    n = 7
+    slots = torch.tensor([4, 0, 9, 2, 11, 6, 1], dtype=torch.int64)
+    print(f"[k3] H={Hk} r1={r1}", flush=True)
+    page = torch.zeros(12, lay.compressed_bytes_per_token(), dtype=torch.uint8, device=DEV)
+    c_out = torch.zeros(n, r1, device=DEV)
+    r_out = torch.zeros(n, Hk * D, device=DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    kernels.write_paged(lay, Knew.permute(1, 0, 2).contiguous().to(DEV),
+                        V.permute(1, 0, 2).contiguous().to(DEV), slots.to(DEV),
+                        torch.tensor([0, n], dtype=torch.int32, device=DEV),
+                        torch.zeros(1, 1, dtype=torch.int32, device=DEV),
+                        torch.zeros(1, dtype=torch.int32, device=DEV), dec_pool_of([dec], DEV),
+                        pinv.t().unsqueeze(0).contiguous().to(DEV), page, coeff_out=c_out,
+                        resid_out=r_out, error_word=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    page, c, R = page.cpu(), c_out.cpu(), r_out.cpu()
+    c_ref = encode.project(Knew, pinv)
+    assert (c - c_ref).abs().max() <= 1e-4 * c_ref.abs().max() + 1e-7
+    cq, cs = encode.quantise_coeffs(c)
+    R_k = R.reshape(n, Hk, D).permute(1, 0, 2).reshape(Hk * n, D)
+    assert (R_k - encode.residual(Knew, cq, cs, dec)).abs().max() <= 1e-4
+    want = torch.cat([encode.k_slots_from(lay, cq, cs.to(torch.float16).reshape(-1),
+                                          codec.build_rows(R_k, lay.res_k, lay.res_bits)),
+                      encode.v_slots_from(lay, encode.encode_v(V, lay))], dim=1)
+    assert int((page[slots] != want).sum()) == 0
+    untouched = torch.ones(12, dtype=torch.bool)
+    untouched[slots] = False
+    assert int(page[untouched].abs().sum()) == 0

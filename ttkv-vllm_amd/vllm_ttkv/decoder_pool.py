@@ -57,18 +57,20 @@ def _exact_int8_rows(x: torch.Tensor):
     s = 0. Raises ValueError when some row has no such form."""
     if not bool(torch.isfinite(x).all()):
         raise ValueError("the decoder holds non-finite values")
-    amax = x.abs().amax(-1)
-    q = torch.zeros_like(x)
+    # float64 throughout: the candidate ruler max|row| / m and the quotients are exact there
+    # whenever the row has the form (fp32 division on the device need not round correctly)
+    x64 = x.double()
+    amax = x64.abs().amax(-1)
+    q = torch.zeros_like(x64)
     s = torch.zeros_like(amax)
     todo = amax > 0
-    x64 = x.double()
     for m in _QMAX_ORDER:
         if not bool(todo.any()):
             break
         sm = amax / m
-        qm = torch.round(x / torch.where(todo, sm, torch.ones_like(sm)).unsqueeze(-1))
-        ok = todo & (qm.double() * sm.double().unsqueeze(-1) == x64).all(-1)
-        ok &= (qm.amax(-1) <= 127) & (qm.amin(-1) >= -128)
+        qm = torch.round(x64 / torch.where(todo, sm, torch.ones_like(sm)).unsqueeze(-1))
+        ok = todo & (qm * sm.unsqueeze(-1) == x64).all(-1)
+        ok &= (qm.amax(-1) <= 127) & (qm.amin(-1) >= -128) & (sm.float().double() == sm)
         q = torch.where(ok.unsqueeze(-1), qm, q)
         s = torch.where(ok, sm, s)
         todo &= ~ok
@@ -77,7 +79,7 @@ def _exact_int8_rows(x: torch.Tensor):
         raise ValueError(
             f"decoder rank row(s) {bad} are not int8 values times one ruler: the pool stores the "
             f"codec's int8 decoder (dec_q * dec_scale), which every fitted decoder is")
-    return q, s
+    return q.float(), s.float()
 
 
 def pack_decoders(decoder_f: torch.Tensor) -> DecoderPool:
