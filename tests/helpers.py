@@ -13,13 +13,14 @@ H, D, HQ = 8, 128, 24
 
 
 def fitted_store(cfg_name: str, T: int, seed: int, r1: int = 110, HQ_: int = HQ,
-                 v_scale=None):
-    """One request's store: fit on the whole context (fit_into_budget), then slots. `v_scale`
-    (a number or a [T] tensor of per-token factors) multiplies the values before encoding."""
+                 v_scale=None, H_: int = H):
+    """One request's store of H_ KV heads: fit on the whole context (fit_into_budget), then
+    slots. `v_scale` (a number or a [T] tensor of per-token factors) multiplies the values before
+    encoding."""
     cfg = codec.CONFIGS[cfg_name]
-    lay = layout_for_config(cfg, r1=r1)
-    K = synth.keys(T, seed=seed)
-    V = synth.values(T, seed=seed)
+    lay = layout_for_config(cfg, r1=r1, H=H_)
+    K = synth.keys(T, H=H_, seed=seed)
+    V = synth.values(T, H=H_, seed=seed)
     if v_scale is not None:
         V = V * (v_scale if not torch.is_tensor(v_scale) else v_scale.reshape(1, T, 1))
     fk = encode.fit_into_budget(K, lay, cfg)

@@ -183,6 +183,18 @@ def test_head_groups_ranks_and_block_sizes(hq, r1, bs):
     _check(got, _oracle(stores, q, cache, pg, block_size=bs), f"hq={hq} r1={r1} bs={bs}")
 
 
+@pytest.mark.parametrize("kvh,hq", [(4, 12), (2, 8)])
+def test_fewer_kv_heads(kvh, hq):
+    """4 and 2 KV heads (a K slot of 4 or 2 residual rows, a plan with fewer heads per request)
+    with 3 and 4 query heads each, against the oracle."""
+    lens = [300, 1100, 70]
+    stores = [fitted_store("safe", n, seed=60 + i, H_=kvh) for i, n in enumerate(lens)]
+    q = synth.queries(len(lens), HQ=hq, seed=8)
+    cache = llama3_cache(2048)
+    got, pg = _run_k1(stores, q, cache, seed=3)
+    _check(got, _oracle(stores, q, cache, pg), f"H={kvh} HQ={hq}")
+
+
 def test_empty_context_and_missing_decoder():
     """A request with no cached tokens reads as zeros (the reference's einsum over zero rows); a
     request whose first block has no registered decoder sets error bit 1 and reads as NaN, and

@@ -355,3 +355,32 @@ def test_attend_and_scores_at_one_and_two_query_heads_per_kv_head(hq):
     want_s = attend.raw_scores_multi(lay, st["k_slots"], st["decoder"], q1.permute(1, 0, 2).double(),
                                      cos, sin, SCALE, p0=n - Q, dtype=torch.float64)
     _check(got, want_s, f"scores HQ={hq}")
+
+
+@pytest.mark.parametrize("kvh,hq", [(4, 12), (2, 8)])
+def test_attend_mode_fewer_kv_heads(kvh, hq):
+    """4 and 2 KV heads (3 and 4 query heads each): a 70-query chunk through the expand + attend
+    pair and single queries through the fused kernel, against the oracle (fp32 output)."""
+    shapes = [(700, 70), (1200, 1), (300, 5)]
+    stores = [fitted_store("safe", n, seed=80 + i, H_=kvh) for i, (n, _) in enumerate(shapes)]
+    cache = llama3_cache(2048)
+    pg, dec_pool, dec_map = _dev_inputs(stores, seed=6)
+    q = torch.cat([synth.queries(Q, HQ=hq, seed=300 + i) for i, (_, Q) in enumerate(shapes)])
+    qsl = torch.tensor([0] + list(torch.tensor([Q for _, Q in shapes]).cumsum(0)),
+                       dtype=torch.int32)
+    out = torch.zeros(q.shape, dtype=torch.float32, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    print(f"[k2] H={kvh} HQ={hq}", flush=True)
+    lay = stores[0]["lay"]
+    kernels.prefill_paged(lay, q.cuda(), pg["page"].cuda(), 16, pg["block_table"].cuda(),
+                          pg["seq_lens"].cuda(), qsl.cuda(), max(Q for _, Q in shapes),
+                          max(n for n, _ in shapes), dec_map, dec_pool, cache.cuda(), SCALE,
+                          out=out, error_word=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    want = attend.paged_continuation(lay, pg["page"], pg["block_table"], pg["seq_lens"], qsl,
+                                     q.double(), [s["decoder"] for s in stores], cache, 16, SCALE,
+                                     dtype=torch.float64)
+    for r in range(len(shapes)):
+        s, e = int(qsl[r]), int(qsl[r + 1])
+        _check(out[s:e].float(), want[r], f"H={kvh} req {r} {shapes[r]}", exact_inf=False)
