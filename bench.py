@@ -149,6 +149,25 @@ def bench_coef_modes(torch, cache, dev, steps=10, warmup=3, n_layers=L_LAYERS):
     return res
 
 
+def batch1_sweep(torch, lay, cfg, cache, dev, flush):
+    """K1 at batch 1 (BASELINE config 2's contexts), 28 layers of distinct pages cycled, the
+    caches flushed between launches (cold HBM), an event pair around each launch."""
+    from vllm_ttkv import synth
+    sweep = []
+    for n in (1082, 4322, 8642, 14402):
+        st = build_store(torch, lay, cfg, [n], L_LAYERS, seed=2, dev=dev)
+        q1 = synth.queries(1, seed=6, device=dev)
+        _, ml = time_k1(torch, lay, st, q1, cache, 3, 1, L_LAYERS, flush=flush)
+        b = k1_bytes(lay, [n], R1, n)
+        log(f"K1 B=1x{n}: {ml * 1e3:.1f} us/launch (cold)")
+        sweep.append(dict(context=n, us_per_layer=ml * 1e3,
+                          hbm_gbps=b / (ml * 1e-3) / 1e9,
+                          tokens_per_s=1.0 / (ml * 1e-3 * L_LAYERS), cold_hbm=True,
+                          layers_cycled=L_LAYERS))
+        del st
+    return sweep
+
+
 def config3_lens(seed=3, B=8):
     """BASELINE config 3's contexts: 8 lengths drawn uniformly from [1000, 14400], seeded."""
     import torch
@@ -713,6 +732,8 @@ def main():
                     help="only the continuation workload (BASELINE config 4, K2); prints its line")
     ap.add_argument("--container-only", action="store_true",
                     help="only the container-layout reads (krt + v_out at 8 x 14402); prints its line")
+    ap.add_argument("--batch1-only", action="store_true",
+                    help="only the batch-1 sweep (cold, 1082 / 4322 / 8642 / 14402 tokens)")
     ap.add_argument("--coef-modes-only", action="store_true",
                     help="only K1 over the fp16 / 4-bit coefficient-mode stores")
     ap.add_argument("--first-chunk-only", action="store_true",
@@ -783,6 +804,13 @@ def main():
                               data="synthetic", headline=dh, config3=d3)))
         return
 
+    if args.batch1_only:
+        sw = batch1_sweep(torch, lay, cfg, cache, dev, cache_flusher(torch, dev))
+        print(json.dumps(dict(metric="K1 us/layer at batch 1 (cold, per context)",
+                              value=sw[0]["us_per_layer"], unit="us", n_gpus=1,
+                              higher_is_better=False, data="synthetic", sweep=sw)))
+        return
+
     if args.coef_modes_only:
         cm = bench_coef_modes(torch, cache, dev, args.steps, args.warmup)
         print(json.dumps(dict(metric="K1 us/layer at 8 x 14402, fp16 and 4-bit coefficient modes",
@@ -825,19 +853,7 @@ def main():
         # across a 28-layer cycle; in serving, the model's weights pass between two reads of a
         # layer's cache)
         flush = cache_flusher(torch, dev)
-        sweep = []
-        for n in (1082, 4322, 8642, 14402):
-            st = build_store(torch, lay, cfg, [n], L_LAYERS, seed=2, dev=dev)
-            q1 = synth.queries(1, seed=6, device=dev)
-            _, ml = time_k1(torch, lay, st, q1, cache, 3, 1, L_LAYERS, flush=flush)
-            b = k1_bytes(lay, [n], R1, n)
-            log(f"K1 B=1x{n}: {ml * 1e3:.1f} us/launch (cold)")
-            sweep.append(dict(context=n, us_per_layer=ml * 1e3,
-                              hbm_gbps=b / (ml * 1e-3) / 1e9,
-                              tokens_per_s=1.0 / (ml * 1e-3 * L_LAYERS), cold_hbm=True,
-                              layers_cycled=L_LAYERS))
-            del st
-        extra["batch1_sweep"] = sweep
+        extra["batch1_sweep"] = batch1_sweep(torch, lay, cfg, cache, dev, flush)
         lens3 = config3_lens()
         st = build_store(torch, lay, cfg, lens3, L_LAYERS, seed=3, dev=dev)
         # 28 layers of ~42 MB each cycle far past the 256 MB Infinity Cache: timed back to back
