@@ -34,10 +34,10 @@ class _Layer:
 class _Seq:
     """One request's raw K/V/q streams (positions 0..T-1)."""
 
-    def __init__(self, T, seed):
-        self.K = synth.keys(T, seed=seed).permute(1, 0, 2).contiguous()     # [T, H, d]
-        self.V = synth.values(T, seed=seed).permute(1, 0, 2).contiguous()
-        self.Q = synth.queries(T, seed=seed).float()                         # [T, HQ, d]
+    def __init__(self, T, seed, kvh=H, hq=HQ):
+        self.K = synth.keys(T, H=kvh, seed=seed).permute(1, 0, 2).contiguous()   # [T, H, d]
+        self.V = synth.values(T, H=kvh, seed=seed).permute(1, 0, 2).contiguous()
+        self.Q = synth.queries(T, HQ=hq, seed=seed).float()                      # [T, HQ, d]
 
 
 def _step(im, layer, cache, csc, bt, reqs):
@@ -65,10 +65,11 @@ def _step(im, layer, cache, csc, bt, reqs):
         query_start_loc_cpu=torch.tensor(qsl, dtype=torch.int32), num_actual_tokens=N,
         max_query_len=max(e - s for _, s, e in reqs), max_seq_len=max(seq_lens))
     q = torch.cat(rows_q).to(torch.float16)
-    patch.stash_raw_k(NAME, raw_k.reshape(N, H * D).to(dev), cos_sin_cache=csc.to(dev))
-    out = torch.full((N, HQ, D), float("nan"), dtype=torch.float16, device=dev)
-    im.forward(layer, q.to(dev), k_post.reshape(N, H * D).to(dev),
-               torch.cat(rows_v).reshape(N, H * D).to(torch.float16).to(dev), cache, md,
+    kvh, hq = raw_k.shape[1], q.shape[1]
+    patch.stash_raw_k(NAME, raw_k.reshape(N, kvh * D).to(dev), cos_sin_cache=csc.to(dev))
+    out = torch.full((N, hq, D), float("nan"), dtype=torch.float16, device=dev)
+    im.forward(layer, q.to(dev), k_post.reshape(N, kvh * D).to(dev),
+               torch.cat(rows_v).reshape(N, kvh * D).to(torch.float16).to(dev), cache, md,
                output=out)
     torch.cuda.synchronize()
     assert int(im.error_word.item()) == 0
@@ -85,13 +86,44 @@ def _check(got, want, what, max_abs=2e-3, mean_abs=1e-3):
 def _sdpa_ref(q, k_post, v):
     """fp64 causal attention over the chunk's own (fp16) post-RoPE keys and values."""
     q, k_post, v = q.double(), k_post.double(), v.half().double()
-    G = HQ // H
+    G = q.shape[1] // k_post.shape[1]
     T = q.shape[0]
     kk = k_post.repeat_interleave(G, dim=1).transpose(0, 1)
     vv = v.repeat_interleave(G, dim=1).transpose(0, 1)
     s = torch.einsum("htd,hsd->hts", q.transpose(0, 1), kk) * SCALE
     s = s.masked_fill(torch.triu(torch.ones(T, T, dtype=torch.bool), 1), float("-inf"))
     return torch.einsum("hts,hsd->htd", torch.softmax(s, -1), vv).transpose(0, 1)
+
+
+@pytest.mark.parametrize("kvh,hq", [(4, 12), (2, 8)])
+def test_forward_with_fewer_kv_heads(kvh, hq):
+    """The drop-in at 4 and 2 KV heads (3 and 4 query heads each): a first chunk (fit, write,
+    SDPA), then decode steps against the oracle reading the bytes they wrote."""
+    lay = layout_for_config(CONFIGS["safe"], 110, H=kvh)
+    olay = oracle_layout(CONFIGS["safe"], 110, H=kvh)
+    rope_store.clear_stores()
+    csc = cos_sin_cache(2048)
+    seqs = [_Seq(600, 11, kvh, hq), _Seq(500, 12, kvh, hq)]
+    bt, nblk = synth.shuffled_block_table([600, 500], BS, seed=4, extra_blocks=2)
+    C = lay.compressed_bytes_per_token()
+    cache = torch.zeros(nblk, 1, BS, C // 2, dtype=torch.bfloat16, device="cuda")
+    im = TTKVAttentionImpl(hq, D, SCALE, kvh)
+    layer = _Layer(NAME, lay)
+    out, q, k_post, qsl, _ = _step(im, layer, cache, csc, bt, [(seqs[0], 0, 400),
+                                                                (seqs[1], 0, 300)])
+    for r, (s, e) in enumerate([(0, 400), (0, 300)]):
+        want = _sdpa_ref(q[qsl[r]:qsl[r + 1]], k_post[qsl[r]:qsl[r + 1]], seqs[r].V[s:e])
+        _check(out[qsl[r]:qsl[r + 1]], want, f"H={kvh} first chunk {r}")
+    for t in range(2):
+        reqs = [(seqs[0], 400 + t, 401 + t), (seqs[1], 300 + t, 301 + t)]
+        out, q, _, qsl, seq_lens = _step(im, layer, cache, csc, bt, reqs)
+        flat = cache.view(torch.uint8).reshape(-1, C).cpu()
+        store = rope_store.store_for_layer(NAME)
+        decs = [store.decoders[int(bt[r, 0])].decoder_f.cpu() for r in range(2)]
+        want = attend.paged_decode(olay, flat, bt[:2], torch.tensor(seq_lens), torch.tensor(qsl),
+                                   q.float(), decs, csc, BS, SCALE, dtype=torch.float64)
+        _check(out, want, f"H={kvh} decode step {t}")
+    rope_store.clear_stores()
 
 
 @pytest.mark.parametrize("alloc", ["safe", "safe_fp16", "campaign4x_int4g32"])
