@@ -140,3 +140,32 @@ def test_continuation_read_matches_oracle(name, Q):
     got = out.cpu()
     for r in range(2):
         _check(got[r * Q:(r + 1) * Q], want[r], f"{name} Q={Q} request {r}")
+
+
+@pytest.mark.parametrize("name", MODES)
+@pytest.mark.parametrize("Q", [5, 200])
+def test_scores_mode_matches_oracle(name, Q):
+    """K2 scores mode (`[HQ, Q, n]`, causal -inf pattern exact) over one request's store in the
+    mode: Q = 5 through the fused kernel, Q = 200 through the expand + scores pair."""
+    from oracle.rope import cos_sin_from_cache
+    torch.set_num_threads(16)
+    n = 1900
+    print(f"[coef-modes scores] {name} Q={Q}", flush=True)
+    st = device_store(name, [n], seed=51, fit_on=1024)
+    q = synth.queries(Q, seed=52)
+    qsl = torch.tensor([0, Q], dtype=torch.int32)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    got = kernels.multi_scores_paged(st["play"], q.to(DEV), st["page"], 16, st["block_table"],
+                                     st["seq_lens"], qsl.to(DEV), Q, n, st["dec_map"],
+                                     st["dec_pool"], _cos_sin().to(DEV), SCALE, error_word=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    ks, _ = attend.gather_request(st["lay"], st["page"].cpu(), st["block_table"][0].cpu(), n, 16)
+    cos, sin = cos_sin_from_cache(_cos_sin(), torch.arange(n), D)
+    want = attend.raw_scores_multi(st["lay"], ks, st["decoders"][0],
+                                   q.permute(1, 0, 2).double(), cos, sin, SCALE, p0=n - Q,
+                                   dtype=torch.float64)
+    got = got.double().cpu()
+    assert torch.equal(torch.isneginf(got), torch.isneginf(want)), "mask pattern"
+    fin = torch.isfinite(want)
+    _check(got[fin], want[fin], f"{name} scores Q={Q}")
