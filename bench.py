@@ -14,15 +14,17 @@ coefficients, the rest by frozen projection).
 Extra fields: the batch-1 context sweep (1082/4322/8642/14402), batch 8 with seeded random
 contexts U[1000, 14400] (config 3), the multi-query continuation score (config 4) and the
 4-bit store with one write per request per layer (config 5) when their kernels are built, the
-dense fp16 paged-attention comparator, the K1 roofline (HBM bytes per launch / measured launch
-time vs 8 TB/s) and the CPU baseline (the torch-CPU oracle timed on a bounded sample on this
-host).
+dense fp16 paged-attention comparator, the container-layout reads, first-chunk timings, K1 over
+this package's fp16 and 4-bit group-32 coefficient modes at the headline shape, the K1 roofline
+(HBM bytes per launch / measured launch time vs 8 TB/s) and the CPU baseline (the torch-CPU
+oracle timed on a bounded sample on this host). `--*-only` flags run one extra alone.
 
 Timing: the headline's K steps (and config 3's, and the dense comparator's launches) run back to
 back with HIP events only around the timed region, so a launch's time includes the gap to the
 next launch but no per-launch event packets; the per-launch event-pair figure is reported beside
 it. The batch-1 sweep flushes the caches between launches (its layers would otherwise stay in
-the Infinity Cache) and so is timed per launch.
+the Infinity Cache) and so is timed per launch. Config 5's K3 / K1 split comes from HIP-graph
+replays of one step's writes alone and reads alone.
 """
 from __future__ import annotations
 
